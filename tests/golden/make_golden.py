@@ -1,0 +1,173 @@
+"""Writes the golden decoder fixtures under tests/golden/.
+
+The expected outputs come from an independent float64 model written here with
+torch library ops (``F.layer_norm``, exact ``F.gelu``, ``torch.softmax``,
+``matmul``) from HuggingFace's WhisperDecoder.forward definition — not from
+oracle/oracle.c — so the oracle is pinned against a second implementation
+rather than against itself. Inputs are regenerated from seeds by
+whispereacp_amd.synthetic; each fixture stores a SHA-256 of the stored input
+bytes so a drifting generator is caught rather than silently re-based.
+
+Run: python tests/golden/make_golden.py
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import math
+import os
+import sys
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+from whispereacp_amd import synthetic as S  # noqa: E402
+
+EPS = float(np.float32(1e-5))  # the float epsilon, widened
+
+
+def input_digest(decoder_file, encoder: np.ndarray) -> str:
+    h = hashlib.sha256()
+    for name in S.canonical_names(max(int(n.split(".")[3]) for n in decoder_file
+                                      if n.startswith("model.decoder.layers.")) + 1):
+        t = decoder_file[name]
+        h.update(name.encode())
+        h.update(t.dtype.encode())
+        h.update(np.ascontiguousarray(t.data).tobytes())
+    h.update(np.ascontiguousarray(encoder, dtype=np.float32).tobytes())
+    return h.hexdigest()
+
+
+def torch_decode(shape: S.DecoderShape, decoder_file, encoder: np.ndarray, tokens, cross_rows=0):
+    """WhisperDecoder.forward in float64 over the whole sequence."""
+    W = {n: torch.from_numpy(t.floats().astype(np.float64)) for n, t in decoder_file.items()}
+    d, H = shape.width, shape.heads
+    D = d // H
+    T = len(tokens)
+    rows = cross_rows or shape.cross_positions
+    enc = torch.from_numpy(encoder.astype(np.float64))[:rows]
+
+    h = W[S.MODEL_NAMES[0]][torch.tensor(tokens)] + W[S.MODEL_NAMES[1]][:T]
+
+    def ln(x, prefix):
+        return F.layer_norm(x, (d,), W[prefix + ".weight"], W[prefix + ".bias"], eps=EPS)
+
+    def attention(q, k, v, causal):
+        qh = q.view(q.shape[0], H, D).transpose(0, 1)
+        kh = k.view(k.shape[0], H, D).transpose(0, 1)
+        vh = v.view(v.shape[0], H, D).transpose(0, 1)
+        scores = torch.matmul(qh, kh.transpose(1, 2)) * (1.0 / math.sqrt(D))
+        if causal:
+            mask = torch.ones(q.shape[0], k.shape[0], dtype=torch.bool).triu(1)
+            scores = scores.masked_fill(mask, float("-inf"))
+        probs = torch.softmax(scores, dim=-1)
+        return torch.matmul(probs, vh).transpose(0, 1).reshape(q.shape[0], d)
+
+    for layer in range(shape.layers):
+        p = lambda s: S.layer_name(layer, s)  # noqa: E731
+        n = ln(h, p("self_attn_layer_norm"))
+        q = n @ W[p("self_attn.q_proj.weight")].T + W[p("self_attn.q_proj.bias")]
+        k = n @ W[p("self_attn.k_proj.weight")].T
+        v = n @ W[p("self_attn.v_proj.weight")].T + W[p("self_attn.v_proj.bias")]
+        a = attention(q, k, v, True)
+        h = h + a @ W[p("self_attn.out_proj.weight")].T + W[p("self_attn.out_proj.bias")]
+
+        n = ln(h, p("encoder_attn_layer_norm"))
+        q = n @ W[p("encoder_attn.q_proj.weight")].T + W[p("encoder_attn.q_proj.bias")]
+        k = enc @ W[p("encoder_attn.k_proj.weight")].T
+        v = enc @ W[p("encoder_attn.v_proj.weight")].T + W[p("encoder_attn.v_proj.bias")]
+        a = attention(q, k, v, False)
+        h = h + a @ W[p("encoder_attn.out_proj.weight")].T + W[p("encoder_attn.out_proj.bias")]
+
+        n = ln(h, p("final_layer_norm"))
+        f = F.gelu(n @ W[p("fc1.weight")].T + W[p("fc1.bias")], approximate="none")
+        h = h + f @ W[p("fc2.weight")].T + W[p("fc2.bias")]
+
+    hidden = ln(h, "model.decoder.layer_norm")
+    logits = hidden @ W[S.MODEL_NAMES[0]].T
+    return hidden.numpy(), logits.numpy()
+
+
+def hexes(a: np.ndarray):
+    return [float(x).hex() for x in np.asarray(a, dtype=np.float64).ravel()]
+
+
+def shape_dict(shape: S.DecoderShape):
+    return dict(zip(("width", "heads", "layers", "feed_forward_width", "vocabulary_size",
+                     "max_positions", "cross_positions"), shape.as_tuple()))
+
+
+def write(name: str, payload: dict):
+    path = os.path.join(HERE, name)
+    with open(path, "w") as f:
+        json.dump(payload, f, indent=1)
+    print("wrote", path)
+
+
+def prompt_fixture(name, storage, encoder_kind, tokens, cross_rows=0):
+    shape = S.small_decoder_shape()
+    decoder_file = S.synthetic_decoder_file(shape, storage)
+    encoder = S.synthetic_encoder_output(shape)
+    if encoder_kind == "second":
+        encoder = (np.float32(-0.5) * encoder + np.float32(0.25)).astype(np.float32)
+    if cross_rows:
+        short = S.DecoderShape(*(shape.as_tuple()[:-1] + (cross_rows,)))
+        encoder = S.synthetic_encoder_output(short)
+        padded = np.full((shape.cross_positions, shape.width), -1234.0, dtype=np.float32)
+        padded[:cross_rows] = encoder
+        encoder = padded
+    hidden, logits = torch_decode(shape, decoder_file, encoder, tokens, cross_rows)
+    write(name, dict(
+        shape=shape_dict(shape), weights=dict(kind="reference-fixture", storage=storage),
+        encoder=encoder_kind, cross_rows=cross_rows, tokens=tokens,
+        input_sha256=input_digest(decoder_file, encoder),
+        hidden=hexes(hidden), logits=hexes(logits)))
+
+
+def greedy_fixture(name, shape, dtype, seed, encoder_seed, prompt, steps):
+    if dtype == "spread":
+        decoder_file = S.synthetic_decoder_file(shape, "Float")
+        encoder = S.synthetic_encoder_output(shape)
+    else:
+        decoder_file = S.workload_decoder_file(shape, dtype, seed)
+        encoder = S.normal_encoder_output(shape.cross_positions, shape.width, encoder_seed)
+    sequence = list(prompt)
+    tokens, margins = [], []
+    logits = None
+    for _ in range(steps):
+        _, logits = torch_decode(shape, decoder_file, encoder, sequence)
+        row = logits[-1]
+        best = int(np.argmax(row))
+        second = float(np.max(np.delete(row, best)))
+        tokens.append(best)
+        margins.append(float(row[best]) - second)
+        sequence.append(best)
+    write(name, dict(
+        shape=shape_dict(shape), weights=dict(kind="workload", dtype=dtype, seed=seed),
+        encoder_seed=encoder_seed, prompt=list(prompt), steps=steps,
+        input_sha256=input_digest(decoder_file, encoder),
+        tokens=tokens, margins=margins, last_logits=hexes(logits[-1])))
+
+
+def main():
+    torch.set_default_dtype(torch.float64)
+    prompt_fixture("small_shape_prompt_float.json", "Float", "sweep", [5, 17, 3, 11])
+    prompt_fixture("small_shape_prompt_packed_half.json", "PackedHalf", "sweep", [5, 17, 3, 11])
+    prompt_fixture("small_shape_prompt_all_half.json", "EveryTensorHalf", "sweep", [5, 17, 3, 11])
+    prompt_fixture("small_shape_second_sequence.json", "Float", "second", [7, 2, 9])
+    prompt_fixture("small_shape_reduced_cross.json", "Float", "sweep", [5, 17, 3, 11, 5],
+                   cross_rows=3)
+    mid = S.DecoderShape(64, 4, 2, 256, 97, 24, 40)
+    greedy_fixture("mid_shape_greedy_f32.json", mid, "F32", 77, 5, [1, 2, 3, 4], 12)
+    greedy_fixture("mid_shape_greedy_bf16.json", mid, "BF16", 78, 6, [9, 8, 7, 6], 12)
+    greedy_fixture("mid_shape_greedy_f16.json", mid, "F16", 79, 7, [4, 40, 60, 80], 12)
+    greedy_fixture("mid_shape_greedy_spread.json", mid, "spread", 0, 0, [3, 1, 4, 1], 16)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,408 @@
+"""The oracle, checked before anything is checked against it (CPU only).
+
+Each oracle function is pinned by something other than itself: the golden
+fixtures written by an independent torch float64 model, the reference test
+suite's known answers (argmax rows, constant-row LayerNorm, counted embedding
+tables), closed forms (one key returns its value row, equal scores average the
+values), library conversions (numpy float16, torch bfloat16) and the C++
+standard's mt19937 known answer. The ``planted`` cases at the end plant a
+plausible mistake (a transposed operand, a dropped bias, a flipped sign, a
+mis-scaled norm) into a copy of the oracle's inputs on the CPU and check that
+the golden comparison rejects it.
+"""
+
+import glob
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from whispereacp_amd import synthetic as S
+from oracle import tensors_in_order
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLDEN = os.path.join(HERE, "golden")
+
+
+def worst_error(actual, expected):
+    """Tests/Encoder/Common.h:731-746: max |a - e| / (1 + |e|)."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    return float(np.max(np.abs(a - e) / (1.0 + np.abs(e))))
+
+
+def from_hex(values):
+    return np.array([float.fromhex(v) for v in values], dtype=np.float64)
+
+
+def load_fixture(name):
+    with open(os.path.join(GOLDEN, name)) as f:
+        return json.load(f)
+
+
+def fixture_inputs(fx):
+    shape = S.DecoderShape(**fx["shape"])
+    if fx["weights"]["kind"] == "reference-fixture":
+        decoder_file = S.synthetic_decoder_file(shape, fx["weights"]["storage"])
+        if fx.get("cross_rows"):
+            short = S.DecoderShape(*(shape.as_tuple()[:-1] + (fx["cross_rows"],)))
+            enc = np.full((shape.cross_positions, shape.width), -1234.0, dtype=np.float32)
+            enc[:fx["cross_rows"]] = S.synthetic_encoder_output(short)
+        else:
+            enc = S.synthetic_encoder_output(shape)
+            if fx["encoder"] == "second":
+                enc = (np.float32(-0.5) * enc + np.float32(0.25)).astype(np.float32)
+    elif fx["weights"]["dtype"] == "spread":
+        decoder_file = S.synthetic_decoder_file(shape, "Float")
+        enc = S.synthetic_encoder_output(shape)
+    else:
+        decoder_file = S.workload_decoder_file(shape, fx["weights"]["dtype"],
+                                               fx["weights"]["seed"])
+        enc = S.normal_encoder_output(shape.cross_positions, shape.width, fx["encoder_seed"])
+    return shape, decoder_file, enc
+
+
+def input_digest(decoder_file, encoder, layers):
+    import hashlib
+    h = hashlib.sha256()
+    for name in S.canonical_names(layers):
+        t = decoder_file[name]
+        h.update(name.encode())
+        h.update(t.dtype.encode())
+        h.update(np.ascontiguousarray(t.data).tobytes())
+    h.update(np.ascontiguousarray(encoder, dtype=np.float32).tobytes())
+    return h.hexdigest()
+
+
+PROMPT_FIXTURES = sorted(os.path.basename(p) for p in glob.glob(os.path.join(GOLDEN, "small_*.json")))
+GREEDY_FIXTURES = sorted(os.path.basename(p) for p in glob.glob(os.path.join(GOLDEN, "mid_*.json")))
+
+
+def test_fixture_sets_present():
+    assert len(PROMPT_FIXTURES) >= 5 and len(GREEDY_FIXTURES) >= 4
+
+
+@pytest.mark.parametrize("name", PROMPT_FIXTURES)
+def test_oracle_matches_golden_prompt(oracle, name):
+    fx = load_fixture(name)
+    shape, decoder_file, enc = fixture_inputs(fx)
+    assert input_digest(decoder_file, enc, shape.layers) == fx["input_sha256"]
+    tensors = tensors_in_order(decoder_file, S.canonical_names(shape.layers))
+    hidden, logits = oracle.decode_full(shape, tensors, enc, fx["tokens"], fx["cross_rows"])
+    assert worst_error(hidden.ravel(), from_hex(fx["hidden"])) < 1e-12
+    assert worst_error(logits.ravel(), from_hex(fx["logits"])) < 1e-12
+
+
+@pytest.mark.parametrize("name", GREEDY_FIXTURES)
+def test_oracle_greedy_matches_golden(oracle, name):
+    fx = load_fixture(name)
+    shape, decoder_file, enc = fixture_inputs(fx)
+    assert input_digest(decoder_file, enc, shape.layers) == fx["input_sha256"]
+    tensors = tensors_in_order(decoder_file, S.canonical_names(shape.layers))
+    session = oracle.session(shape, tensors)
+    session.begin(enc)
+    tokens, margins, last = session.greedy(fx["prompt"], fx["steps"])
+    assert list(tokens) == fx["tokens"]
+    assert np.allclose(margins, fx["margins"], rtol=0, atol=1e-12)
+    assert worst_error(last, from_hex(fx["last_logits"])) < 1e-12
+
+
+# --- ReferenceDecoderTests' four properties (Tests/Decoder/ReferenceDecoderTests.cpp) ---
+
+@pytest.fixture(scope="module")
+def small():
+    shape = S.small_decoder_shape()
+    decoder_file = S.synthetic_decoder_file(shape, "Float")
+    tensors = tensors_in_order(decoder_file, S.canonical_names(shape.layers))
+    return shape, decoder_file, tensors, S.synthetic_encoder_output(shape)
+
+
+def test_reference_is_finite(oracle, small):
+    shape, _, tensors, enc = small
+    hidden, logits = oracle.decode_full(shape, tensors, enc, [5, 17, 3, 11])
+    assert hidden.shape == (4, shape.width) and logits.shape == (4, shape.vocabulary_size)
+    assert np.isfinite(hidden).all() and np.isfinite(logits).all()
+
+
+def test_reference_is_causal(oracle, small):
+    shape, _, tensors, enc = small
+    tokens = [5, 17, 3, 11]
+    before_h, before_l = oracle.decode_full(shape, tensors, enc, tokens)
+    tokens[2] = (tokens[2] + 7) % shape.vocabulary_size
+    after_h, after_l = oracle.decode_full(shape, tensors, enc, tokens)
+    assert (before_h[:2] == after_h[:2]).all() and (before_l[:2] == after_l[:2]).all()
+    assert (before_h[2] != after_h[2]).any()
+
+
+def test_reference_logits_are_tied(oracle, small):
+    shape, decoder_file, tensors, enc = small
+    hidden, logits = oracle.decode_full(shape, tensors, enc, [5, 17, 3, 11])
+    table = decoder_file[S.MODEL_NAMES[0]].floats().astype(np.float64)
+    expected = hidden[1] @ table.T
+    assert np.all(np.abs(logits[1] - expected) <= 1e-12 * (1 + np.abs(expected)))
+
+
+def test_reference_reads_the_encoder(oracle, small):
+    shape, _, tensors, enc = small
+    before_h, _ = oracle.decode_full(shape, tensors, enc, [5, 17, 3, 11])
+    altered = enc.copy()
+    altered[0, 0] += 1.0
+    after_h, _ = oracle.decode_full(shape, tensors, altered, [5, 17, 3, 11])
+    assert before_h[0, 0] != after_h[0, 0]
+
+
+def test_cached_session_is_bitwise_the_full_recompute(oracle, small):
+    shape, _, tensors, enc = small
+    tokens = [5, 17, 3, 11, 2, 9, 23]
+    full_h, full_l = oracle.decode_full(shape, tensors, enc, tokens)
+    s = oracle.session(shape, tensors)
+    s.begin(enc)
+    h2, l2 = s.step(tokens[:2])
+    rows_h, rows_l = [h2], [l2]
+    for t in tokens[2:5]:
+        h, l = s.step([t])
+        rows_h.append(h)
+        rows_l.append(l)
+    h, l = s.step(tokens[5:])
+    rows_h.append(h)
+    rows_l.append(l)
+    assert (np.concatenate(rows_h) == full_h).all()
+    assert (np.concatenate(rows_l) == full_l).all()
+    assert s.position == len(tokens)
+
+
+def test_session_refuses_past_the_window(oracle, small):
+    shape, _, tensors, enc = small
+    s = oracle.session(shape, tensors)
+    s.begin(enc)
+    s.step([i % shape.vocabulary_size for i in range(shape.max_positions)])
+    with pytest.raises(ValueError):
+        s.step([1])
+    assert s.position == shape.max_positions
+    with pytest.raises(ValueError):
+        s.begin(enc, shape.cross_positions + 1)
+
+
+def test_thread_count_does_not_change_results(oracle, small):
+    shape, _, tensors, enc = small
+    oracle.set_threads(1)
+    h1, l1 = oracle.decode_full(shape, tensors, enc, [5, 17, 3, 11])
+    oracle.set_threads(4)
+    h4, l4 = oracle.decode_full(shape, tensors, enc, [5, 17, 3, 11])
+    assert (h1 == h4).all() and (l1 == l4).all()
+
+
+# --- primitives -------------------------------------------------------------
+
+def test_layernorm_constant_row_yields_bias(oracle):
+    # Tests/Kernels/LayerNormTests.cpp:101-140
+    w = S.spread_values(32, 33, 2.0)
+    b = S.spread_values(32, 44, 2.0)
+    out = oracle.layernorm(np.full((1, 32), 2.5), w, b)
+    assert np.array_equal(out[0], b.astype(np.float64))
+
+
+def test_layernorm_matches_torch(oracle):
+    rows = np.random.RandomState(3).randn(6, 37) * np.arange(1, 7)[:, None] + np.arange(6)[:, None]
+    w = S.spread_values(37, 11, 1.5)
+    b = S.spread_values(37, 22, 0.75)
+    expected = torch.nn.functional.layer_norm(torch.from_numpy(rows), (37,),
+                                              torch.from_numpy(w.astype(np.float64)),
+                                              torch.from_numpy(b.astype(np.float64)),
+                                              eps=float(np.float32(1e-5))).numpy()
+    assert worst_error(oracle.layernorm(rows, w, b), expected) < 1e-13
+
+
+def test_linear_matches_matmul_and_orders_bias_first(oracle):
+    x = np.random.RandomState(4).randn(3, 40)
+    w = S.spread_values(7 * 40, 5, 0.5).reshape(7, 40)
+    b = S.spread_values(7, 6, 0.2)
+    expected = x @ w.astype(np.float64).T + b
+    assert worst_error(oracle.linear(x, w, b), expected) < 1e-14
+    assert worst_error(oracle.linear(x, w, None), x @ w.astype(np.float64).T) < 1e-14
+
+
+def test_attention_single_key_returns_the_value_row(oracle):
+    q = np.random.RandomState(1).randn(1, 8)
+    k = np.random.RandomState(2).randn(1, 8)
+    v = np.random.RandomState(3).randn(1, 8)
+    assert np.array_equal(oracle.attention(q, k, v, heads=2, causal=False), v)
+
+
+def test_attention_equal_scores_average_the_values(oracle):
+    q = np.zeros((1, 8))
+    k = np.random.RandomState(2).randn(5, 8)
+    v = np.random.RandomState(3).randn(5, 8)
+    out = oracle.attention(q, k, v, heads=2, causal=False)
+    assert np.allclose(out[0], v.mean(axis=0), atol=1e-15)
+
+
+def test_attention_causal_weights_are_exact_zeros(oracle):
+    # A future key with a huge value would leak into the output if weighted.
+    q = np.random.RandomState(1).randn(3, 8)
+    k = np.random.RandomState(2).randn(3, 8)
+    v = np.random.RandomState(3).randn(3, 8)
+    base = oracle.attention(q, k, v, heads=2, causal=True)
+    v2 = v.copy()
+    v2[2] = 1e30
+    out = oracle.attention(q, k, v2, heads=2, causal=True)
+    assert np.array_equal(out[:2], base[:2])
+    # and a cached query block starting at absolute position 1 sees keys 0..1+i
+    blk = oracle.attention(q[1:], k, v, heads=2, causal=True, first_query=1)
+    assert np.array_equal(blk, base[1:])
+
+
+def test_attention_matches_torch_softmax(oracle):
+    rs = np.random.RandomState(9)
+    q, k, v = rs.randn(4, 12), rs.randn(7, 12), rs.randn(7, 12)
+    out = oracle.attention(q, k, v, heads=3, causal=True, first_query=3)
+    for h in range(3):
+        cols = slice(4 * h, 4 * h + 4)
+        s = torch.from_numpy(q[:, cols] @ k[:, cols].T / 2.0)
+        mask = torch.ones(4, 7, dtype=torch.bool).triu(1 + 3)
+        p = torch.softmax(s.masked_fill(mask, float("-inf")), dim=-1).numpy()
+        assert worst_error(out[:, cols], p @ v[:, cols]) < 1e-14
+
+
+def test_gelu_closed_form(oracle):
+    assert oracle.gelu(0.0) == 0.0
+    for x in np.linspace(-8, 8, 513):
+        exact = 0.5 * x * (1 + math.erf(x / math.sqrt(2)))
+        assert abs(oracle.gelu(x) - exact) <= 1e-15 * (1 + abs(exact))
+        # gelu(x) - gelu(-x) == x
+        assert abs(oracle.gelu(x) - oracle.gelu(-x) - x) < 1e-14
+
+
+def test_argmax_reference_rows(oracle):
+    # Tests/Kernels/ArgmaxTests.cpp:100-131 (hand-built rows)
+    n = 37
+    i = np.arange(n, dtype=np.float32)
+    assert oracle.argmax(-i) == 0
+    assert oracle.argmax(-np.abs(i - 18)) == 18
+    assert oracle.argmax(i) == n - 1
+    row = np.where((i == 5) | (i == 29), 4.0, i * 0.01).astype(np.float32)
+    assert oracle.argmax(row) == 5  # the tie goes to the lower index
+
+
+def test_argmax_suppression_cases(oracle):
+    # Tests/Kernels/ArgmaxTests.cpp:158-208
+    n = 37
+    logits = (np.arange(n) * 0.5).astype(np.float32)
+    logits[7], logits[23] = 100.0, 50.0
+    mask = np.zeros(n, np.float32)
+    assert oracle.argmax(logits, mask) == 7
+    mask[7] = 1
+    assert oracle.argmax(logits, mask) == 23
+    mask[23] = 1
+    assert oracle.argmax(logits, mask) == n - 1
+    only = np.where(np.arange(n) == 11, 0.0, 1.0).astype(np.float32)
+    desc = (1000.0 - np.arange(n)).astype(np.float32)
+    desc[11] = -1000.0
+    assert oracle.argmax(desc, only) == 11
+    assert oracle.argmax(desc, np.ones(n, np.float32)) == 0  # all suppressed
+
+
+def test_argmax_over_the_vocabulary(oracle):
+    # Tests/Kernels/ArgmaxTests.cpp:210-233
+    logits = S.spread_values(51864, 51864, 4.0)
+    logits[50361], logits[318] = 900.0, 800.0
+    assert oracle.argmax(logits) == 50361
+    mask = np.zeros(51864, np.float32)
+    mask[50361] = 1
+    assert oracle.argmax(logits, mask) == 318
+
+
+def test_embed_counted_tables(oracle):
+    # Tests/Kernels/EmbedTests.cpp:66-77, 137-205
+    width, vocab, first = 5, 13, 9
+    tokens = [12, 0, 5, 7]
+    counted = lambda rows, scale: (scale * np.arange(rows)[:, None] + 0.25 * np.arange(width)[None, :]).astype(np.float32)  # noqa: E731
+    tok, pos = counted(vocab, 8.0), counted(16, 64.0)
+    by_token = oracle.embed(tokens, tok, np.zeros_like(pos), first)
+    by_pos = oracle.embed(tokens, np.zeros_like(tok), pos, first)
+    for t, token in enumerate(tokens):
+        assert np.array_equal(by_token[t], 8.0 * token + 0.25 * np.arange(width))
+        assert np.array_equal(by_pos[t], 64.0 * (first + t) + 0.25 * np.arange(width))
+    big = counted(51864, 1.0)[:, :3] * 0 + np.arange(51864, dtype=np.float32)[:, None]
+    ids = [0, 1, 220, 50256, 50257, 51863]
+    out = oracle.embed(ids, big, np.zeros((4, 3), np.float32), 0)
+    assert np.array_equal(out[:, 0], np.array(ids, dtype=np.float64))
+
+
+def test_half_conversions_match_numpy(oracle):
+    rs = np.random.RandomState(0)
+    bits = rs.randint(0, 2 ** 32, size=20000, dtype=np.uint32)
+    values = bits.view(np.float32)
+    extra = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 2 ** -24, 2 ** -25, 2 ** -25 * 1.0000001,
+                      3 * 2 ** -26, 6.0e-8, 1e-9, np.inf, -np.inf, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11],
+                     dtype=np.float32)
+    for x in np.concatenate([values, extra, S.normal_values(5000, 3, 0.02)]):
+        with np.errstate(over="ignore"):
+            expected = np.array([x], dtype=np.float32).astype(np.float16).view(np.uint16)[0]
+        got = oracle.f32_to_f16_bits(float(x))
+        if np.isnan(x):
+            assert (got & 0x7C00) == 0x7C00 and (got & 0x3FF) != 0
+        else:
+            assert got == expected, (x, hex(got), hex(expected))
+    for h in range(0, 65536, 7):
+        expected = np.array([h], dtype=np.uint16).view(np.float16).astype(np.float32)[0]
+        got = oracle.f16_bits_to_f32(h)
+        assert (np.isnan(expected) and np.isnan(got)) or got == expected
+
+
+def test_bfloat16_conversions_match_torch(oracle):
+    rs = np.random.RandomState(1)
+    values = np.concatenate([rs.randint(0, 2 ** 32, size=20000, dtype=np.uint32).view(np.float32),
+                             S.normal_values(5000, 4, 0.02),
+                             np.array([0.0, -0.0, 3.4e38, np.inf, -np.inf, 1.0 + 2 ** -8], np.float32)])
+    finite = values[~np.isnan(values)]
+    expected = torch.from_numpy(finite).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = np.array([oracle.f32_to_bf16_bits(float(x)) for x in finite], dtype=np.uint16)
+    assert np.array_equal(got, expected)
+    assert np.array_equal(S.f32_to_bf16_bits(finite), expected)
+    for h in range(0, 65536, 5):
+        e = torch.tensor([h], dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float().item()
+        g = oracle.bf16_bits_to_f32(h)
+        assert (math.isnan(e) and math.isnan(g)) or g == e
+
+
+def test_mt19937_known_answer_and_numpy_agreement(oracle):
+    assert oracle.mt19937(5489, 10000)[-1] == 4123659995
+    assert np.array_equal(oracle.mt19937(2000, 5000), S.mt19937_raw(2000, 5000))
+    # spreadValues in float arithmetic from the same draws
+    raw = oracle.mt19937(7, 100)
+    manual = np.float32(0.5) * ((raw % 2001).astype(np.float32) / np.float32(1000) - np.float32(1))
+    assert np.array_equal(manual, S.spread_values(100, 7, 0.5))
+
+
+def test_normal_generator_statistics():
+    v = S.normal_values(200001, 12, 1.0).astype(np.float64)
+    assert abs(v.mean()) < 0.01 and abs(v.std() - 1.0) < 0.01
+    assert len(v) == 200001
+
+
+# --- planted mistakes: each must be caught by the golden comparison ---------
+
+@pytest.mark.parametrize("mistake", ["scaled_norm_gamma", "transposed_projection",
+                                     "dropped_bias", "sign_flip_residual"])
+def test_planted_mistakes_fail_the_golden(oracle, mistake):
+    fx = load_fixture("small_shape_prompt_float.json")
+    shape, decoder_file, enc = fixture_inputs(fx)
+    names = S.canonical_names(shape.layers)
+    tensors = tensors_in_order(decoder_file, names)
+    i = names.index(S.layer_name(0, "self_attn.q_proj.weight"))
+    if mistake == "transposed_projection":
+        tensors[i] = np.ascontiguousarray(tensors[i].T)
+    elif mistake == "dropped_bias":
+        tensors[names.index(S.layer_name(1, "fc2.bias"))] = np.zeros(shape.width, np.float32)
+    elif mistake == "sign_flip_residual":
+        j = names.index(S.layer_name(0, "encoder_attn.out_proj.weight"))
+        tensors[j] = -tensors[j]
+    elif mistake == "scaled_norm_gamma":
+        j = names.index(S.layer_name(0, "self_attn_layer_norm.weight"))
+        tensors[j] = tensors[j] * np.float32(3.0)
+    _, logits = oracle.decode_full(shape, tensors, enc, fx["tokens"])
+    assert worst_error(logits.ravel(), from_hex(fx["logits"])) > 1e-6

@@ -1,0 +1,330 @@
+"""Synthetic decoder weights and encoder states: the inputs the parity tests
+and the benchmark run on.
+
+Two families, both from generators whose sequences are fixed by a standard
+rather than by an implementation (std::mt19937 draws, which numpy's legacy
+``RandomState(seed)`` reproduces exactly):
+
+* the reference test-suite's own fixture weights — ``spread_values`` /
+  ``shifted_values`` / ``synthetic_decoder_file`` / ``synthetic_encoder_output``
+  restate Tests/Kernels/Common.h:75-88, Tests/Encoder/Common.h:148-157 and
+  Tests/Decoder/Common.h:66-169, 473-488 (same seeds, same float arithmetic);
+* the benchmark workloads — every projection, bias and both embeddings drawn
+  N(0, 0.02) by Box-Muller over ``u = (raw + 0.5) / 2**32``, LayerNorm gamma = 1
+  and beta = 0, encoder states N(0, 1), one seed per tensor counting up in the
+  file's tensor order.
+
+Stored dtypes are "F32", "F16" or "BF16"; an F16 array is numpy float16 and a
+BF16 array is the uint16 bit pattern (round to nearest even from float32).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import Dict, List, Tuple
+
+import numpy as np
+
+
+@dataclasses.dataclass(frozen=True)
+class DecoderShape:
+    """Decoder/DecoderShape.h:20-83. Every extent one decoder is built against."""
+
+    width: int
+    heads: int
+    layers: int
+    feed_forward_width: int
+    vocabulary_size: int
+    max_positions: int
+    cross_positions: int
+
+    @property
+    def head_width(self) -> int:
+        return self.width // self.heads
+
+    def attention_scale(self) -> float:
+        """Decoder/DecoderShape.cpp:23-26: 1/sqrt(head width), in float."""
+        return float(np.float32(1.0) / np.sqrt(np.float32(self.head_width)))
+
+    def as_tuple(self) -> Tuple[int, ...]:
+        return dataclasses.astuple(self)
+
+
+def small_decoder_shape() -> DecoderShape:
+    """Tests/Decoder/Common.h:41-54: deliberately lopsided extents."""
+    return DecoderShape(8, 2, 2, 16, 24, 16, 6)
+
+
+# The five workloads: the reference's CPU-runnable tiny.en shape and the four
+# MI355X decode configurations (d, heads, layers, vocab, weight dtype, streams,
+# single-token steps).
+WORKLOADS = {
+    "tiny.en": dict(width=384, heads=6, layers=4, vocab=51864, dtype="F32", streams=1, steps=25),
+    "base.en": dict(width=512, heads=8, layers=6, vocab=51864, dtype="F32", streams=1, steps=64),
+    "small": dict(width=768, heads=12, layers=12, vocab=51865, dtype="F16", streams=1, steps=224),
+    "medium": dict(width=1024, heads=16, layers=24, vocab=51865, dtype="F16", streams=16, steps=128),
+    "large-v3": dict(width=1280, heads=20, layers=32, vocab=51866, dtype="BF16", streams=32, steps=444),
+}
+
+# Fixed four-token start-of-transcript prefixes from the public Whisper
+# vocabularies (any in-vocabulary ids serve with random weights).
+SOT_PREFIX = {
+    51864: [50257, 50258, 50358, 50362],
+    51865: [50258, 50259, 50359, 50363],
+    51866: [50258, 50259, 50360, 50364],
+}
+
+
+def workload_shape(name: str, cross_positions: int = 1500) -> DecoderShape:
+    w = WORKLOADS[name]
+    return DecoderShape(w["width"], w["heads"], w["layers"], 4 * w["width"], w["vocab"], 448,
+                        cross_positions)
+
+
+# ---------------------------------------------------------------------------
+# tensor names (the HuggingFace names a Whisper safetensors file carries)
+# ---------------------------------------------------------------------------
+
+_ATTENTION_SUFFIXES = [
+    "{norm}.weight", "{norm}.bias",
+    "{attn}.q_proj.weight", "{attn}.q_proj.bias",
+    "{attn}.k_proj.weight",
+    "{attn}.v_proj.weight", "{attn}.v_proj.bias",
+    "{attn}.out_proj.weight", "{attn}.out_proj.bias",
+]
+
+LAYER_SUFFIXES: List[str] = (
+    [s.format(norm="self_attn_layer_norm", attn="self_attn") for s in _ATTENTION_SUFFIXES]
+    + [s.format(norm="encoder_attn_layer_norm", attn="encoder_attn") for s in _ATTENTION_SUFFIXES]
+    + ["final_layer_norm.weight", "final_layer_norm.bias", "fc1.weight", "fc1.bias", "fc2.weight",
+       "fc2.bias"]
+)
+
+MODEL_NAMES = [
+    "model.decoder.embed_tokens.weight",
+    "model.decoder.embed_positions.weight",
+    "model.decoder.layer_norm.weight",
+    "model.decoder.layer_norm.bias",
+]
+
+
+def layer_name(index: int, suffix: str) -> str:
+    return f"model.decoder.layers.{index}.{suffix}"
+
+
+def canonical_names(layers: int) -> List[str]:
+    """Model tensors, then the 24 per-layer tensors in order — the order the
+    oracle and the C-ABI weight tables index by."""
+    names = list(MODEL_NAMES)
+    for layer in range(layers):
+        names += [layer_name(layer, s) for s in LAYER_SUFFIXES]
+    return names
+
+
+def tensor_extents(shape: DecoderShape, name: str) -> Tuple[int, ...]:
+    d, f = shape.width, shape.feed_forward_width
+    if name.endswith("embed_tokens.weight"):
+        return (shape.vocabulary_size, d)
+    if name.endswith("embed_positions.weight"):
+        return (shape.max_positions, d)
+    if name.endswith("fc1.weight"):
+        return (f, d)
+    if name.endswith("fc1.bias"):
+        return (f,)
+    if name.endswith("fc2.weight"):
+        return (d, f)
+    if name.endswith("proj.weight"):
+        return (d, d)
+    return (d,)
+
+
+def is_projection(name: str) -> bool:
+    return name.endswith("proj.weight") or name.endswith("fc1.weight") or name.endswith(
+        "fc2.weight")
+
+
+def is_norm_weight(name: str) -> bool:
+    return "layer_norm.weight" in name
+
+
+def is_norm_bias(name: str) -> bool:
+    return "layer_norm.bias" in name
+
+
+# ---------------------------------------------------------------------------
+# generators
+# ---------------------------------------------------------------------------
+
+def mt19937_raw(seed: int, count: int) -> np.ndarray:
+    """``count`` raw std::mt19937 draws for ``seed`` (uint32)."""
+    rs = np.random.RandomState(seed & 0xFFFFFFFF)
+    return rs.randint(0, 2 ** 32, size=count, dtype=np.uint32)
+
+
+def spread_values(count: int, seed: int, value_range: float) -> np.ndarray:
+    """Tests/Kernels/Common.h:75-88, in float32 arithmetic:
+    range * ((float)(engine() % 2001) / 1000.f - 1.f)."""
+    raw = mt19937_raw(seed, count) % np.uint32(2001)
+    v = raw.astype(np.float32) / np.float32(1000.0) - np.float32(1.0)
+    return (np.float32(value_range) * v).astype(np.float32)
+
+
+def shifted_values(count: int, seed: int, value_range: float) -> np.ndarray:
+    """Tests/Encoder/Common.h:148-157: spread values plus one."""
+    return (spread_values(count, seed, value_range) + np.float32(1.0)).astype(np.float32)
+
+
+def normal_values(count: int, seed: int, std: float) -> np.ndarray:
+    """N(0, std) as float32 by Box-Muller over mt19937 pairs: each pair of raw
+    draws gives r*cos(2*pi*u2) then r*sin(2*pi*u2), r = sqrt(-2 ln u1)."""
+    pairs = (count + 1) // 2
+    raw = mt19937_raw(seed, 2 * pairs).astype(np.float64)
+    u1 = (raw[0::2] + 0.5) / 4294967296.0
+    u2 = (raw[1::2] + 0.5) / 4294967296.0
+    r = np.sqrt(-2.0 * np.log(u1))
+    theta = 2.0 * math.pi * u2
+    out = np.empty(2 * pairs, dtype=np.float64)
+    out[0::2] = r * np.cos(theta)
+    out[1::2] = r * np.sin(theta)
+    return (std * out[:count]).astype(np.float32)
+
+
+def f32_to_bf16_bits(values: np.ndarray) -> np.ndarray:
+    """Round to nearest even; NaN stays a quiet NaN."""
+    x = np.ascontiguousarray(values, dtype=np.float32).view(np.uint32)
+    rounded = ((x + np.uint32(0x7FFF) + ((x >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16))
+    nan = (x & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+    rounded = np.where(nan, (x >> np.uint32(16)) | np.uint32(0x40), rounded)
+    return rounded.astype(np.uint16)
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def store(values: np.ndarray, dtype: str) -> np.ndarray:
+    """The stored form of float32 ``values`` under ``dtype``."""
+    if dtype == "F32":
+        return np.ascontiguousarray(values, dtype=np.float32)
+    if dtype == "F16":
+        return np.ascontiguousarray(values, dtype=np.float32).astype(np.float16)
+    if dtype == "BF16":
+        return f32_to_bf16_bits(values)
+    raise ValueError(f"unknown dtype {dtype}")
+
+
+def widen(stored: np.ndarray, dtype: str) -> np.ndarray:
+    """Exact float32 widening of a stored tensor."""
+    if dtype == "F32":
+        return np.ascontiguousarray(stored, dtype=np.float32)
+    if dtype == "F16":
+        return stored.astype(np.float32)
+    if dtype == "BF16":
+        return bf16_bits_to_f32(stored)
+    raise ValueError(f"unknown dtype {dtype}")
+
+
+@dataclasses.dataclass
+class StoredTensor:
+    name: str
+    dtype: str  # "F32" | "F16" | "BF16"
+    extents: Tuple[int, ...]
+    data: np.ndarray  # float32, float16, or uint16 (bf16 bits)
+
+    def floats(self) -> np.ndarray:
+        return widen(self.data, self.dtype).reshape(self.extents)
+
+
+DecoderFile = Dict[str, StoredTensor]
+
+
+def synthetic_decoder_file(shape: DecoderShape, storage: str = "Float") -> DecoderFile:
+    """Tests/Decoder/Common.h:66-169: seeds count up from 2000 in file order;
+    projections in [-0.5, 0.5], embeddings +-0.3, biases +-0.2, LayerNorm gamma
+    1 +- 0.2. ``storage`` is "Float", "PackedHalf" (projection weights F16) or
+    "EveryTensorHalf" (every tensor F16)."""
+    seed = [2000]
+    out: DecoderFile = {}
+
+    def nxt(count, value_range):
+        v = spread_values(count, seed[0], value_range)
+        seed[0] += 1
+        return v
+
+    def shifted(count, value_range):
+        v = shifted_values(count, seed[0], value_range)
+        seed[0] += 1
+        return v
+
+    def add(name, values, projection=False):
+        extents = tensor_extents(shape, name)
+        half = storage == "EveryTensorHalf" or (projection and storage != "Float")
+        dtype = "F16" if half else "F32"
+        out[name] = StoredTensor(name, dtype, extents, store(values, dtype))
+
+    d, f = shape.width, shape.feed_forward_width
+    add(MODEL_NAMES[0], nxt(shape.vocabulary_size * d, 0.3))
+    add(MODEL_NAMES[1], nxt(shape.max_positions * d, 0.3))
+
+    for layer in range(shape.layers):
+        for norm, attn in (("self_attn_layer_norm", "self_attn"),
+                           ("encoder_attn_layer_norm", "encoder_attn")):
+            add(layer_name(layer, f"{norm}.weight"), shifted(d, 0.2))
+            add(layer_name(layer, f"{norm}.bias"), nxt(d, 0.2))
+            add(layer_name(layer, f"{attn}.q_proj.weight"), nxt(d * d, 0.5), True)
+            add(layer_name(layer, f"{attn}.q_proj.bias"), nxt(d, 0.2))
+            add(layer_name(layer, f"{attn}.k_proj.weight"), nxt(d * d, 0.5), True)
+            add(layer_name(layer, f"{attn}.v_proj.weight"), nxt(d * d, 0.5), True)
+            add(layer_name(layer, f"{attn}.v_proj.bias"), nxt(d, 0.2))
+            add(layer_name(layer, f"{attn}.out_proj.weight"), nxt(d * d, 0.5), True)
+            add(layer_name(layer, f"{attn}.out_proj.bias"), nxt(d, 0.2))
+        add(layer_name(layer, "final_layer_norm.weight"), shifted(d, 0.2))
+        add(layer_name(layer, "final_layer_norm.bias"), nxt(d, 0.2))
+        add(layer_name(layer, "fc1.weight"), nxt(f * d, 0.5), True)
+        add(layer_name(layer, "fc1.bias"), nxt(f, 0.2))
+        add(layer_name(layer, "fc2.weight"), nxt(d * f, 0.5), True)
+        add(layer_name(layer, "fc2.bias"), nxt(d, 0.2))
+
+    add(MODEL_NAMES[2], shifted(d, 0.2))
+    add(MODEL_NAMES[3], nxt(d, 0.2))
+    return out
+
+
+def file_order(layers: int) -> List[str]:
+    """The order a Whisper decoder file lists its tensors in (the seed order)."""
+    names = MODEL_NAMES[:2]
+    for layer in range(layers):
+        names = names + [layer_name(layer, s) for s in LAYER_SUFFIXES]
+    return names + MODEL_NAMES[2:]
+
+
+def workload_decoder_file(shape: DecoderShape, dtype: str, base_seed: int = 1000) -> DecoderFile:
+    """The benchmark weights: N(0, 0.02) for projections, biases and both
+    embeddings; LayerNorm gamma 1 and beta 0. Tensor i in file order gets seed
+    base_seed + i. Every tensor is stored in ``dtype``."""
+    out: DecoderFile = {}
+    for index, name in enumerate(file_order(shape.layers)):
+        extents = tensor_extents(shape, name)
+        count = int(np.prod(extents))
+        if is_norm_weight(name):
+            values = np.ones(count, dtype=np.float32)
+        elif is_norm_bias(name):
+            values = np.zeros(count, dtype=np.float32)
+        else:
+            values = normal_values(count, base_seed + index, 0.02)
+        out[name] = StoredTensor(name, dtype, extents, store(values, dtype))
+    return out
+
+
+def synthetic_encoder_output(shape: DecoderShape) -> np.ndarray:
+    """Tests/Decoder/Common.h:473-488: a sin/cos sweep of unit-ish spread."""
+    position = np.arange(shape.cross_positions, dtype=np.float64)[:, None]
+    column = np.arange(shape.width, dtype=np.float64)[None, :]
+    phase = 0.13 * position + 0.041 * column
+    return (np.sin(phase) + 0.5 * np.cos(2.7 * phase)).astype(np.float32)
+
+
+def normal_encoder_output(rows: int, width: int, seed: int) -> np.ndarray:
+    """[rows, width] float32 N(0, 1) encoder states."""
+    return normal_values(rows * width, seed, 1.0).reshape(rows, width)
