@@ -1,0 +1,94 @@
+/*
+ * wsp_decoder.h — a C binding of the C++ decoder surface (include/whispereacp):
+ * the stub a non-C++ caller (Python ctypes, cgo, N-API) binds to drive
+ * WSP::Decoder, WSP::Argmax and the greedy loop. Every function returns a
+ * wsp_hip.h status; the message is wsp_decoder_last_error(). Device pointers
+ * are plain pointers into memory the caller allocated on the same device.
+ *
+ * Each call names the reference C++ entry point it exposes.
+ */
+#ifndef WSP_DECODER_H
+#define WSP_DECODER_H
+
+#include "wsp_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The host-side error class behind a non-zero status, mirroring the
+ * reference's exceptions. */
+enum
+{
+    WSP_KIND_NONE = 0,
+    WSP_KIND_MODEL_ERROR = 1,      /* WSP::ModelError (Model/ModelError.h:16-20) */
+    WSP_KIND_LOGIC_ERROR = 2,      /* std::logic_error */
+    WSP_KIND_INVALID_ARGUMENT = 3, /* std::invalid_argument */
+    WSP_KIND_RUNTIME_ERROR = 4     /* std::runtime_error (HIP) */
+};
+
+/* One tensor of a decoder file: its HuggingFace name, storage ("F32", "F16",
+ * "BF16"), extents and host bytes (row-major, little-endian). */
+typedef struct wsp_tensor_entry
+{
+    const char* name;
+    const char* dtype;
+    int rank;
+    const long long* extents;
+    const void* data;
+} wsp_tensor_entry;
+
+typedef struct wsp_decoder wsp_decoder;
+
+/* DecoderWeights(file, shape, packing) + Decoder(shape).prepare(device)
+ * (Decoder/DecoderWeights.cpp:151-178, Decoder/Decoder.cpp:194-227) +
+ * Argmax::prepare(maxPositions, vocabularySize). packing: 0 Float, 1 ExactHalf.
+ * stream is the hipStream_t every call records into. */
+int wsp_decoder_create(const wsp_decoder_shape* shape, const wsp_tensor_entry* tensors, int count,
+                       int packing, int device, void* stream, wsp_decoder** out);
+void wsp_decoder_destroy(wsp_decoder* decoder);
+const char* wsp_decoder_last_error(const wsp_decoder* decoder);
+int wsp_decoder_last_error_kind(const wsp_decoder* decoder);
+
+/* Decoder::beginSequence (Decoder/Decoder.h:75-78). encoder_rows: device f32
+ * [cross_positions, width]. */
+int wsp_decoder_begin_sequence(wsp_decoder* decoder, const float* encoder_rows, int cross_position_count);
+
+/* Decoder::step (Decoder/Decoder.h:92-96). tokens: device uint32 [count];
+ * logits: device f32 [count, vocabulary]. */
+int wsp_decoder_step(wsp_decoder* decoder, const uint32_t* tokens, int count, float* logits);
+
+/* A single-token step and its argmax under mask (device f32 or null), the
+ * token written to argmax_slot (device uint32) — Decoder::step followed by
+ * Argmax::encode (Whisper/Whisper.cpp:1186-1213), fused when possible. */
+int wsp_decoder_step_and_sample(wsp_decoder* decoder, const uint32_t* token, float* logits,
+                                const float* mask, uint32_t* argmax_slot);
+
+int wsp_decoder_position(const wsp_decoder* decoder);
+int wsp_decoder_cross_positions(const wsp_decoder* decoder);
+/* Decoder::hiddenStates (Decoder/Decoder.h:111-115): device f32 rows. */
+const float* wsp_decoder_hidden_states(const wsp_decoder* decoder);
+
+/* Whether single-token steps take the fused launch (default 1 when the
+ * weights' projections share one storage). */
+int wsp_decoder_set_fused(wsp_decoder* decoder, int enabled);
+int wsp_decoder_uses_fused(const wsp_decoder* decoder);
+
+/* Argmax::encode (Kernels/Argmax.h:236-241) into out (device uint32 [rows]). */
+int wsp_decoder_argmax(wsp_decoder* decoder, const float* logits, int rows, int row_length,
+                       const float* mask, uint32_t* out);
+
+/* The greedy loop of Whisper::decodeTranscript (Whisper/Whisper.cpp:1361-1443)
+ * over encoder_rows (device), prompt (host ints), with masks on the device
+ * (or null). end_of_text < 0 never stops early. Writes up to `capacity`
+ * tokens to tokens_out (host) and their count to *count_out. */
+int wsp_decoder_greedy(wsp_decoder* decoder, const float* encoder_rows, int cross_position_count,
+                       const int* prompt, int prompt_count, int maximum_tokens, int end_of_text,
+                       const float* first_mask, const float* later_mask, int* tokens_out, int capacity,
+                       int* count_out, double* decode_seconds);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,191 @@
+/*
+ * wsp_hip.h — the C ABI of the MI355X (gfx950) decoder kernels.
+ *
+ * Plain C: device pointers, sizes and status codes; no exceptions cross it and
+ * no C++ or torch types appear in it. Every call is asynchronous and ordered
+ * on the stream the context was created with; a context is bound to one
+ * device and is not thread-safe. All workspaces are sized when the context is
+ * created, so no call below allocates device memory.
+ *
+ * Each entry point names the reference interface it stands in for; the
+ * C++ layer in include/whispereacp/ (Net, HipNet, Decoder, Argmax) calls these
+ * exactly where the reference's KernelNet dispatched eacp programs.
+ */
+#ifndef WSP_HIP_H
+#define WSP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. Negative values map back onto the reference's exceptions in
+ * the C++ layer: SHAPE/CAPACITY -> ModelError or std::invalid_argument,
+ * LOGIC -> std::logic_error, HIP -> std::runtime_error. */
+enum
+{
+    WSP_OK = 0,
+    WSP_ERR_ARGUMENT = -1, /* a null pointer or a non-positive extent */
+    WSP_ERR_SHAPE = -2,    /* extents that do not fit together */
+    WSP_ERR_CAPACITY = -3, /* beyond what the context was sized for */
+    WSP_ERR_HIP = -4,      /* the HIP runtime reported an error */
+    WSP_ERR_LOGIC = -5,    /* misuse (e.g. unsupported head width) */
+    WSP_ERR_DEVICE = -6    /* a device-side watchdog tripped */
+};
+
+/* Storage of a weight matrix. F32 is read as is; F16 and BF16 are widened to
+ * float on load (Kernels/Linear.h:229-246 reads fp16 the same way). */
+enum
+{
+    WSP_F32 = 0,
+    WSP_F16 = 1,
+    WSP_BF16 = 2
+};
+
+/* Projection epilogue flags (Kernels/Linear.h:213-227): GELU applies the exact
+ * activation to x·Wᵀ + b; RESIDUAL adds the result into what y holds. */
+enum
+{
+    WSP_LINEAR_GELU = 1,
+    WSP_LINEAR_RESIDUAL = 2
+};
+
+/* Decoder/DecoderShape.h:20-83 */
+typedef struct wsp_decoder_shape
+{
+    int width;
+    int heads;
+    int layers;
+    int feed_forward_width;
+    int vocabulary_size;
+    int max_positions;
+    int cross_positions;
+} wsp_decoder_shape;
+
+typedef struct wsp_hip_ctx wsp_hip_ctx;
+
+/* Binds a context to `device` and `stream` (a hipStream_t; null is the
+ * default stream) and sizes its workspaces for `shape` (attention partials,
+ * argmax candidates). Replaces KernelNet::prepare's scratch and the
+ * SingleQueryAttention/Argmax prepare() sizing (Net/KernelNet.cpp:133-207,
+ * Kernels/SingleQueryAttention.cpp:32-60, Kernels/Argmax.cpp:26-40). */
+int wsp_hip_ctx_create(const wsp_decoder_shape* shape, int device, void* stream,
+                       wsp_hip_ctx** out);
+void wsp_hip_ctx_destroy(wsp_hip_ctx* ctx);
+
+/* The message behind the last non-zero status on this context. */
+const char* wsp_hip_last_error(const wsp_hip_ctx* ctx);
+
+/* The stream the context launches on (a hipStream_t). */
+void* wsp_hip_stream(const wsp_hip_ctx* ctx);
+
+/* y[r, o] = act(Σ_k x[r,k]·W[o,k] + b[o]) (+ y[r,o] when RESIDUAL).
+ * x [rows, inner] f32, W [out, inner] row-major in `wdtype`, bias [out] f32 or
+ * null (zero, which replaces the zero-bias buffers at
+ * Net/KernelNet.cpp:440-458), y [rows, out] f32. Rows up to 16 take the split
+ * GEMV, more take the tiled product. Replaces KernelNet::dispatchProjection
+ * (Net/KernelNet.cpp:817-859) over SplitLinear / HalfWeightSplitLinear
+ * (Kernels/Linear.h:129-276) and LinearProduct (Kernels/SimdTiledMatMul.h:470-486). */
+int wsp_hip_linear(wsp_hip_ctx* ctx, const float* x, int rows, int inner, const void* weight,
+                   int wdtype, const float* bias, float* y, int out, int flags);
+
+/* y = (x - mean) * rsqrt(var + eps) * gamma + beta over rows of `width`
+ * (biased variance of the centred values). Replaces LayerNorm
+ * (Kernels/LayerNorm.h:19-90). */
+int wsp_hip_layernorm(wsp_hip_ctx* ctx, const float* x, const float* gamma, const float* beta,
+                      float* y, int rows, int width, float eps);
+
+/* y[t, c] = token_table[tokens[t], c] + position_table[first + t, c].
+ * Replaces Embed (Kernels/Embed.h:38-62). */
+int wsp_hip_embed(wsp_hip_ctx* ctx, const uint32_t* tokens, int count, const float* token_table,
+                  const float* position_table, int first_position, float* y, int width);
+
+/* Multi-head attention of q_count queries (the last q_count of k_count
+ * positions when causal) against k_count cached keys and values, heads of
+ * width / heads columns. scale multiplies the summed dot product. One query
+ * takes the split-key form (Kernels/SingleQueryAttention.h:505-556); several
+ * take the causal multi-query form with the mask semantics of
+ * Kernels/Attention.h:34-47. Replaces KernelNet::runCachedAttention
+ * (Net/KernelNet.cpp:951-1013). Head width must be a multiple of 4, at most 64
+ * (the reference's own limit, Kernels/SingleQueryAttention.cpp:32-45). */
+int wsp_hip_attention(wsp_hip_ctx* ctx, const float* q, int q_count, const float* keys,
+                      const float* values, int k_count, int width, int heads, int causal,
+                      float scale, float* out);
+
+/* out[r] = the first j maximising logits[r * row_length + j] over the j with
+ * mask[j] == 0 (mask may be null); all suppressed gives 0. Replaces Argmax
+ * (Kernels/Argmax.h:46-262, Kernels/Argmax.cpp:43-81). */
+int wsp_hip_argmax(wsp_hip_ctx* ctx, const float* logits, int rows, int row_length,
+                   const float* mask, uint32_t* out);
+
+/* K = X·Wkᵀ and V = X·Wvᵀ + bv for `rows` encoder rows of `width`, with fp32
+ * accumulation; Wk, Wv [width, width] in `wdtype`. Replaces the two
+ * appendLinear calls per layer of recordSequenceStart
+ * (Decoder/Decoder.cpp:121-146) that route to LinearProduct. */
+int wsp_hip_project_cross_kv(wsp_hip_ctx* ctx, const float* x, int rows, int width,
+                             const void* wk, const void* wv, const float* bv, int wdtype,
+                             float* k_out, float* v_out);
+
+/* ---- the fused single-token step ----------------------------------------- */
+
+/* Device pointers of one decoder layer's tensors (Decoder/DecoderWeights.h:25-63).
+ * Projection weights are in the table's wdtype; everything else is f32. The
+ * fused step reads q/k/v of each attention through one concatenated
+ * [3·width, width] block: qkv_weight points at q_proj, followed by k_proj and
+ * v_proj; qkv_bias is [q_bias | 0 | v_bias] (k_proj has no bias). */
+typedef struct wsp_layer_tensors
+{
+    const float* self_norm_w;
+    const float* self_norm_b;
+    const void* self_qkv_w;
+    const float* self_qkv_b;
+    const void* self_out_w;
+    const float* self_out_b;
+    const float* cross_norm_w;
+    const float* cross_norm_b;
+    const void* cross_q_w;
+    const float* cross_q_b;
+    const void* cross_out_w;
+    const float* cross_out_b;
+    const float* final_norm_w;
+    const float* final_norm_b;
+    const void* fc1_w;
+    const float* fc1_b;
+    const void* fc2_w;
+    const float* fc2_b;
+    float* self_keys;    /* [max_positions, width] f32 */
+    float* self_values;  /* [max_positions, width] f32 */
+    const float* cross_keys;   /* [cross_positions, width] f32 */
+    const float* cross_values; /* [cross_positions, width] f32 */
+} wsp_layer_tensors;
+
+typedef struct wsp_decoder_tensors
+{
+    int wdtype;                   /* storage of every projection weight */
+    const float* token_embedding; /* [vocab, width] f32 (the gather's table) */
+    const void* logits_weight;    /* [vocab, width] in logits_wdtype (tied) */
+    int logits_wdtype;
+    const float* position_embedding; /* [max_positions, width] f32 */
+    const float* final_norm_w;
+    const float* final_norm_b;
+    const wsp_layer_tensors* layers; /* device-independent host array, `layers` long */
+} wsp_decoder_tensors;
+
+/* One single-token decoder step fused into one persistent launch: embeds
+ * tokens[0] at `position`, runs every layer (appending the new key and value
+ * rows to the self caches at row `position`), writes the final hidden row, the
+ * logits row and — when argmax_out is non-null — the masked argmax into
+ * *argmax_out. cross_rows encoder rows are attended. Same contract as
+ * Decoder::step with one token (Decoder/Decoder.cpp:270-308) followed by
+ * Argmax::encode (Whisper/Whisper.cpp:1164-1184). */
+int wsp_hip_decoder_step(wsp_hip_ctx* ctx, const wsp_decoder_tensors* tensors,
+                         const uint32_t* tokens, int position, int cross_rows, float* hidden,
+                         float* logits, const float* mask, uint32_t* argmax_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,90 @@
+"""The C ABI on the CPU: the library loads, exports every entry point the
+headers declare, and refuses bad arguments before touching a device."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from helpers import ROOT, ensure_library
+
+HEADERS = [os.path.join(ROOT, "include", "wsp_hip.h"), os.path.join(ROOT, "include", "wsp_decoder.h")]
+
+
+def declared_functions():
+    names = []
+    for path in HEADERS:
+        text = open(path).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[a-z_]+\*?\s+\*?(wsp_[a-z_]+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_headers_declare_the_entry_points():
+    names = declared_functions()
+    for required in ("wsp_hip_ctx_create", "wsp_hip_linear", "wsp_hip_layernorm", "wsp_hip_embed",
+                     "wsp_hip_attention", "wsp_hip_argmax", "wsp_hip_project_cross_kv", "wsp_hip_decoder_step",
+                     "wsp_decoder_create", "wsp_decoder_step", "wsp_decoder_greedy"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ensure_library()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_signatures_cover_every_declared_symbol():
+    from whispereacp_amd import _native
+    assert set(declared_functions()) == set(_native.SIGNATURES)
+
+
+def test_context_refuses_bad_arguments_without_a_device():
+    from whispereacp_amd import _native as N
+    lib = ensure_library()
+    handle = ctypes.c_void_p()
+    assert lib.wsp_hip_ctx_create(None, 0, None, ctypes.byref(handle)) == N.WSP_ERR_ARGUMENT
+    bad = N.wsp_decoder_shape(10, 3, 1, 16, 24, 16, 6)  # width not divisible by heads
+    assert lib.wsp_hip_ctx_create(ctypes.byref(bad), 0, None, ctypes.byref(handle)) == N.WSP_ERR_SHAPE
+    zero = N.wsp_decoder_shape(8, 2, 0, 16, 24, 16, 6)
+    assert lib.wsp_hip_ctx_create(ctypes.byref(zero), 0, None, ctypes.byref(handle)) == N.WSP_ERR_SHAPE
+    assert lib.wsp_hip_linear(None, None, 1, 1, None, 0, None, None, 1, 0) == N.WSP_ERR_ARGUMENT
+    assert lib.wsp_hip_argmax(None, None, 1, 1, None, None) == N.WSP_ERR_ARGUMENT
+    assert lib.wsp_hip_decoder_step(None, None, None, 0, 1, None, None, None, None) == N.WSP_ERR_ARGUMENT
+    assert lib.wsp_hip_last_error(None) == b"no context"
+
+
+def test_decoder_refuses_a_bad_shape_as_a_model_error():
+    from whispereacp_amd import _native as N
+    from whispereacp_amd.decoder import Decoder, ModelError
+    from whispereacp_amd import synthetic as S
+    ensure_library()
+    with pytest.raises(ModelError):
+        Decoder(S.DecoderShape(10, 3, 1, 16, 24, 16, 6), {})
+    assert N.load().wsp_decoder_create(None, None, 0, 0, 0, None, None) == N.WSP_ERR_ARGUMENT
+
+
+def test_loader_names_a_missing_or_misshapen_table_before_any_upload():
+    # embed_tokens is checked before anything reaches the device, so these run
+    # on the CPU (Tests/Decoder/DecoderWeightsTests.cpp:149-254).
+    from whispereacp_amd.decoder import Decoder, ModelError
+    from whispereacp_amd import synthetic as S
+    ensure_library()
+    shape = S.small_decoder_shape()
+    good = S.synthetic_decoder_file(shape, "Float")
+    missing = dict(good)
+    del missing["model.decoder.embed_tokens.weight"]
+    with pytest.raises(ModelError, match="embed_tokens"):
+        Decoder(shape, missing)
+    short = dict(good)
+    t = good["model.decoder.embed_tokens.weight"]
+    short["model.decoder.embed_tokens.weight"] = S.StoredTensor(t.name, t.dtype, (shape.vocabulary_size - 1,
+                                                                                 shape.width),
+                                                                 t.data[: (shape.vocabulary_size - 1) * shape.width])
+    with pytest.raises(ModelError, match="embed_tokens"):
+        Decoder(shape, short)
+    odd = dict(good)
+    odd["model.decoder.embed_tokens.weight"] = S.StoredTensor(t.name, "I8", t.extents, t.data)
+    with pytest.raises(ModelError, match="I8"):
+        Decoder(shape, odd)

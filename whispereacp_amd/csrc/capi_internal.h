@@ -1,0 +1,43 @@
+// The context behind wsp_hip_ctx and the internal entry points the C ABI
+// shares between its translation units.
+#pragma once
+
+#include "../../include/wsp_hip.h"
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+struct wsp_hip_ctx
+{
+    wsp_decoder_shape shape {};
+    int device = 0;
+    hipStream_t stream = nullptr;
+
+    float* attention_workspace = nullptr;
+    size_t attention_floats = 0;
+
+    float* argmax_values = nullptr;
+    uint32_t* argmax_indices = nullptr;
+    size_t argmax_candidates = 0;
+
+    void* fused = nullptr; // fused-step state (fused_step.hip)
+
+    char error[512] = {0};
+};
+
+namespace wsp
+{
+using Context = wsp_hip_ctx;
+
+int context_fail(Context* ctx, int code, const char* message);
+int context_hip(Context* ctx, hipError_t e, const char* what);
+
+// fused_step.hip
+int fused_prepare(Context* ctx);
+void fused_release(Context* ctx);
+
+// cross_kv.hip: out = X·Wᵀ (+ bias) for `rows` rows of `width`.
+int cross_kv_projection(Context* ctx, const float* x, int rows, int width, const void* weight,
+                        const float* bias, int wdtype, float* out);
+} // namespace wsp

@@ -1,0 +1,125 @@
+// Device helpers shared by the gfx950 kernels: weight widening, wave64
+// reductions and the exact GELU. CDNA4 only: waves are 64 lanes wide.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wsp
+{
+constexpr int kWave = 64;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+enum WeightType : int
+{
+    kF32 = 0,
+    kF16 = 1,
+    kBF16 = 2
+};
+
+__device__ __forceinline__ float bf16_to_float(uint16_t bits)
+{
+    return __uint_as_float((uint32_t) bits << 16);
+}
+
+// Eight consecutive weights widened to float from one 16-byte load (F16,
+// BF16) or two (F32). `index` is an element index, a multiple of 8.
+template <int WT>
+__device__ __forceinline__ void load8(const void* base, size_t index, float (&w)[8])
+{
+    if constexpr (WT == kF32)
+    {
+        const float4v* p = reinterpret_cast<const float4v*>(static_cast<const float*>(base) + index);
+        const float4v a = p[0], b = p[1];
+        w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
+        w[4] = b[0]; w[5] = b[1]; w[6] = b[2]; w[7] = b[3];
+    }
+    else if constexpr (WT == kF16)
+    {
+        const half8 h = *reinterpret_cast<const half8*>(static_cast<const _Float16*>(base) + index);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            w[i] = (float) h[i];
+    }
+    else
+    {
+        const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + index);
+        const uint32_t v[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            w[2 * i] = __uint_as_float(v[i] << 16);
+            w[2 * i + 1] = __uint_as_float(v[i] & 0xFFFF0000u);
+        }
+    }
+}
+
+template <int WT>
+__device__ __forceinline__ float load1(const void* base, size_t index)
+{
+    if constexpr (WT == kF32)
+        return static_cast<const float*>(base)[index];
+    else if constexpr (WT == kF16)
+        return (float) static_cast<const _Float16*>(base)[index];
+    else
+        return bf16_to_float(static_cast<const uint16_t*>(base)[index]);
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1)
+        v += __shfl_xor(v, offset, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1)
+        v = fmaxf(v, __shfl_xor(v, offset, kWave));
+    return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (at most 1024). `scratch`
+// holds one float per wave. Every thread returns the total.
+__device__ __forceinline__ float block_sum(float v, float* scratch)
+{
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int waves = blockDim.x / kWave;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0)
+        scratch[wave] = v;
+    __syncthreads();
+    float total = 0.f;
+    for (int i = 0; i < waves; ++i)
+        total += scratch[i];
+    return total;
+}
+
+__device__ __forceinline__ float block_max(float v, float* scratch)
+{
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int waves = blockDim.x / kWave;
+    v = wave_max(v);
+    __syncthreads();
+    if (lane == 0)
+        scratch[wave] = v;
+    __syncthreads();
+    float best = scratch[0];
+    for (int i = 1; i < waves; ++i)
+        best = fmaxf(best, scratch[i]);
+    return best;
+}
+
+// x * 0.5 * (1 + erf(x / sqrt(2))), the exact form (Kernels/Gelu.h:16-21),
+// with the device library's erff.
+__device__ __forceinline__ float exact_gelu(float x)
+{
+    return 0.5f * x * (1.f + erff(x * 0.70710678118654752f));
+}
+} // namespace wsp

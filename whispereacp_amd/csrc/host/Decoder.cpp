@@ -1,0 +1,272 @@
+// The decoder body against Net and the Decoder class around it
+// (Decoder/Decoder.cpp:1-308), plus the fused single-token path.
+#include "../../../include/whispereacp/Decoder.h"
+#include "host_common.h"
+
+#include <functional>
+#include <string>
+#include <utility>
+
+namespace WSP
+{
+namespace
+{
+// One pre-norm attention sublayer: normalise, project the queries (and, for
+// self-attention, append this step's keys and values from the same
+// normalised rows), attend, and add the output projection into the stream.
+Tensor attentionSublayer(Net& net, const DecoderShape& shape, const TensorBuffer& normWeight,
+                         const TensorBuffer& normBias, const TensorBuffer& queryWeight,
+                         const TensorBuffer& queryBias, const TensorBuffer& outputWeight,
+                         const TensorBuffer& outputBias, const Tensor& stream, bool causal,
+                         const std::function<std::pair<Tensor, Tensor>(const Tensor&)>& keysAndValues)
+{
+    const Tensor normalised = net.layerNorm(stream, normWeight, normBias);
+    const Tensor queries = net.linear(normalised, queryWeight, &queryBias, Activation::none);
+    const auto [keys, values] = keysAndValues(normalised);
+    const Tensor attended = net.attention(queries, keys, values, shape.heads, causal);
+    return net.linearAdd(attended, outputWeight, &outputBias, stream);
+}
+
+Tensor layerBody(Net& net, const DecoderShape& shape, const DecoderLayerWeights& w, DecoderCaches& caches,
+                 int layer, const Tensor& hidden)
+{
+    // Self-attention: keys and values come from this step's normalised rows,
+    // appended to the cache; the causal mask keeps each row out of its future.
+    const Tensor afterSelf = attentionSublayer(
+        net, shape, w.selfAttentionNormWeight, w.selfAttentionNormBias, w.selfQueryWeight, w.selfQueryBias,
+        w.selfAttentionOutputWeight, w.selfAttentionOutputBias, hidden, true, [&](const Tensor& normalised) {
+            Tensor keys = net.appendLinear(caches.selfKeys[(std::size_t) layer], normalised, w.selfKeyWeight, nullptr);
+            Tensor values = net.appendLinear(caches.selfValues[(std::size_t) layer], normalised, w.selfValueWeight,
+                                             &w.selfValueBias);
+            return std::make_pair(keys, values);
+        });
+
+    // Cross-attention: the keys and values were projected when the sequence
+    // opened; nothing is masked.
+    const Tensor afterCross = attentionSublayer(
+        net, shape, w.crossAttentionNormWeight, w.crossAttentionNormBias, w.crossQueryWeight, w.crossQueryBias,
+        w.crossAttentionOutputWeight, w.crossAttentionOutputBias, afterSelf, false, [&](const Tensor&) {
+            return std::make_pair(net.cached(caches.crossKeys[(std::size_t) layer]),
+                                  net.cached(caches.crossValues[(std::size_t) layer]));
+        });
+
+    const Tensor inner = net.linear(net.layerNorm(afterCross, w.finalNormWeight, w.finalNormBias),
+                                    w.feedForwardWeight, &w.feedForwardBias, Activation::gelu);
+    return net.linearAdd(inner, w.feedForwardOutputWeight, &w.feedForwardOutputBias, afterCross);
+}
+
+void addCaches(std::vector<Cache>& caches, Net& net, int layers, int rows, int width)
+{
+    caches.clear();
+    for (int i = 0; i < layers; ++i)
+        caches.push_back(net.makeCache(rows, width));
+}
+} // namespace
+
+void recordSequenceStart(Net& net, const DecoderShape& shape, const DecoderWeights& weights, DecoderCaches& caches,
+                         const Binding& encoderRows, int rows)
+{
+    const Tensor encoded = net.input(encoderRows, {rows, shape.width}, DType::float32);
+    for (int layer = 0; layer < shape.layers; ++layer)
+    {
+        const auto& w = weights.layers[(std::size_t) layer];
+        const auto i = (std::size_t) layer;
+        caches.selfKeys[i].clear();
+        caches.selfValues[i].clear();
+        caches.crossKeys[i].clear();
+        caches.crossValues[i].clear();
+        net.appendLinear(caches.crossKeys[i], encoded, w.crossKeyWeight, nullptr);
+        net.appendLinear(caches.crossValues[i], encoded, w.crossValueWeight, &w.crossValueBias);
+    }
+}
+
+void recordDecoderStep(Net& net, const DecoderShape& shape, const DecoderWeights& weights, DecoderCaches& caches,
+                       const Binding& tokens, int tokenCount, int firstPosition, const Binding& hiddenStates,
+                       const Binding& logits)
+{
+    Tensor hidden = net.embed(net.input(tokens, {tokenCount}, DType::int32), weights.tokenEmbedding,
+                              weights.positionalEmbedding, firstPosition);
+    for (int layer = 0; layer < shape.layers; ++layer)
+        hidden = layerBody(net, shape, weights.layers[(std::size_t) layer], caches, layer, hidden);
+
+    const Tensor normalised = net.layerNorm(hidden, weights.finalNormWeight, weights.finalNormBias);
+    net.output(normalised, hiddenStates);
+    // Tied logits: embed_tokens itself, no bias (Decoder/DecoderWeights.h:66-79).
+    net.output(net.linear(normalised, weights.logitsWeight(), nullptr, Activation::none), logits);
+}
+
+Decoder::Decoder(const DecoderShape& shapeToUse) : decoderShape(shapeToUse) {}
+
+void Decoder::prepare(const Device& device, void* hipStream)
+{
+    HipNetLayout layout;
+    layout.shape = decoderShape;
+    layout.scratch = {{decoderShape.stepElementCount(), 4}, {decoderShape.stepFeedForwardElementCount(), 1}};
+    hipNet.prepare(device, layout, hipStream);
+
+    const int layers = decoderShape.layers, width = decoderShape.width;
+    addCaches(caches.selfKeys, hipNet, layers, decoderShape.maxPositions, width);
+    addCaches(caches.selfValues, hipNet, layers, decoderShape.maxPositions, width);
+    addCaches(caches.crossKeys, hipNet, layers, decoderShape.crossPositions, width);
+    addCaches(caches.crossValues, hipNet, layers, decoderShape.crossPositions, width);
+
+    normalisedRows.emplace(device, (std::size_t) decoderShape.stepElementCount() * sizeof(float));
+    decodedPositions = 0;
+    activeCrossPositions = decoderShape.crossPositions;
+}
+
+void Decoder::prepare()
+{
+    prepare(Device::shared());
+}
+
+void Decoder::requireMatchingWeights(const DecoderWeights& weights) const
+{
+    if (!(weights.shape == decoderShape))
+        throw ModelError("the weights were loaded against a different decoder shape than this decoder was built for");
+    if (!normalisedRows)
+        throw std::logic_error("a decoder records once it is prepared");
+}
+
+void Decoder::requireRoomFor(int tokenCount) const
+{
+    if (tokenCount <= 0)
+        throw ModelError("a decoder step needs at least one token");
+    if (decodedPositions + tokenCount > decoderShape.maxPositions)
+        throw ModelError("this step would carry the sequence to " + std::to_string(decodedPositions + tokenCount)
+                         + " tokens, past the " + std::to_string(decoderShape.maxPositions)
+                         + " this decoder was built for");
+}
+
+void Decoder::beginSequence(Pass& pass, const DeviceBuffer& encoderOutput, const DecoderWeights& weights,
+                            int crossPositionCount)
+{
+    beginSequence(pass, BufferRange::of(encoderOutput), weights, crossPositionCount);
+}
+
+void Decoder::beginSequence(Pass& pass, const BufferRange& encoderOutput, const DecoderWeights& weights,
+                            int crossPositionCount)
+{
+    requireMatchingWeights(weights);
+    if (crossPositionCount < 0 || crossPositionCount > decoderShape.crossPositions)
+        throw ModelError("a decoder built for " + std::to_string(decoderShape.crossPositions)
+                         + " encoder rows was asked to attend to " + std::to_string(crossPositionCount));
+    const int rows = crossPositionCount == 0 ? decoderShape.crossPositions : crossPositionCount;
+    const Binding encoderRows {encoderOutput, Shape {decoderShape.crossPositions, decoderShape.width}, "encoder_rows"};
+
+    hipNet.begin(pass);
+    recordSequenceStart(hipNet, decoderShape, weights, caches, encoderRows, rows);
+    hipNet.end();
+
+    decodedPositions = 0;
+    activeCrossPositions = rows;
+}
+
+bool Decoder::usesFusedStep(const DecoderWeights& weights, int tokenCount) const
+{
+    const int headWidth = decoderShape.headWidth();
+    return fusedSteps && tokenCount == 1 && weights.uniformProjectionStorage().has_value() && headWidth % 4 == 0
+           && headWidth <= 64;
+}
+
+void Decoder::step(Pass& pass, const BufferRange& tokens, int tokenCount, const DecoderWeights& weights,
+                   const BufferRange& logits)
+{
+    requireMatchingWeights(weights);
+    requireRoomFor(tokenCount);
+
+    if (usesFusedStep(weights, tokenCount))
+    {
+        fusedStep(pass, tokens, weights, logits, nullptr, nullptr);
+        return;
+    }
+
+    const Binding tokenSlots {tokens, Shape {decoderShape.maxPositions}, "tokens"};
+    hipNet.begin(pass);
+    recordDecoderStep(hipNet, decoderShape, weights, caches, tokenSlots, tokenCount, decodedPositions,
+                      Binding {BufferRange::of(*normalisedRows), {}, "hidden_states"},
+                      Binding {logits, {}, "logits"});
+    hipNet.end();
+    decodedPositions += tokenCount;
+}
+
+void Decoder::stepAndSample(Pass& pass, const BufferRange& tokens, const DecoderWeights& weights,
+                            const BufferRange& logits, const float* mask, const BufferRange& argmaxSlot)
+{
+    requireMatchingWeights(weights);
+    requireRoomFor(1);
+    if (usesFusedStep(weights, 1))
+    {
+        fusedStep(pass, tokens, weights, logits, mask, &argmaxSlot);
+        return;
+    }
+    step(pass, tokens, 1, weights, logits);
+    const int status = wsp_hip_argmax(hipNet.context(), static_cast<const float*>(logits.data()), 1,
+                                      decoderShape.vocabularySize, mask, static_cast<uint32_t*>(argmaxSlot.data()));
+    if (status != WSP_OK)
+        throwForStatus(status, wsp_hip_last_error(hipNet.context()));
+}
+
+void Decoder::fusedStep(Pass& pass, const BufferRange& tokens, const DecoderWeights& weights,
+                        const BufferRange& logits, const float* mask, const BufferRange* argmaxSlot)
+{
+    if (pass.hipStream() != wsp_hip_stream(hipNet.context()))
+        throw std::logic_error("a decoder records into the stream it was prepared with");
+
+    fusedLayers.resize((std::size_t) decoderShape.layers);
+    for (int l = 0; l < decoderShape.layers; ++l)
+    {
+        const auto& w = weights.layers[(std::size_t) l];
+        const auto i = (std::size_t) l;
+        auto f = [](const TensorBuffer& t) { return static_cast<const float*>(t.data()); };
+        wsp_layer_tensors& L = fusedLayers[i];
+        L.self_norm_w = f(w.selfAttentionNormWeight);
+        L.self_norm_b = f(w.selfAttentionNormBias);
+        L.self_qkv_w = w.selfQueryWeight.data();
+        L.self_qkv_b = f(w.selfQkvBias);
+        L.self_out_w = w.selfAttentionOutputWeight.data();
+        L.self_out_b = f(w.selfAttentionOutputBias);
+        L.cross_norm_w = f(w.crossAttentionNormWeight);
+        L.cross_norm_b = f(w.crossAttentionNormBias);
+        L.cross_q_w = w.crossQueryWeight.data();
+        L.cross_q_b = f(w.crossQueryBias);
+        L.cross_out_w = w.crossAttentionOutputWeight.data();
+        L.cross_out_b = f(w.crossAttentionOutputBias);
+        L.final_norm_w = f(w.finalNormWeight);
+        L.final_norm_b = f(w.finalNormBias);
+        L.fc1_w = w.feedForwardWeight.data();
+        L.fc1_b = f(w.feedForwardBias);
+        L.fc2_w = w.feedForwardOutputWeight.data();
+        L.fc2_b = f(w.feedForwardOutputBias);
+        L.self_keys = hipNet.cacheData(caches.selfKeys[i]);
+        L.self_values = hipNet.cacheData(caches.selfValues[i]);
+        L.cross_keys = hipNet.cacheData(caches.crossKeys[i]);
+        L.cross_values = hipNet.cacheData(caches.crossValues[i]);
+    }
+
+    wsp_decoder_tensors tensors {};
+    tensors.wdtype = wsp_dtype_of(*weights.uniformProjectionStorage());
+    tensors.token_embedding = static_cast<const float*>(weights.tokenEmbedding.data());
+    tensors.logits_weight = weights.logitsWeight().data();
+    tensors.logits_wdtype = wsp_dtype_of(weights.logitsWeight().type);
+    tensors.position_embedding = static_cast<const float*>(weights.positionalEmbedding.data());
+    tensors.final_norm_w = static_cast<const float*>(weights.finalNormWeight.data());
+    tensors.final_norm_b = static_cast<const float*>(weights.finalNormBias.data());
+    tensors.layers = fusedLayers.data();
+
+    const int status = wsp_hip_decoder_step(
+        hipNet.context(), &tensors, static_cast<const uint32_t*>(tokens.data()), decodedPositions,
+        activeCrossPositions, static_cast<float*>(normalisedRows->data()), static_cast<float*>(logits.data()), mask,
+        argmaxSlot != nullptr ? static_cast<uint32_t*>(argmaxSlot->data()) : nullptr);
+    if (status != WSP_OK)
+        throwForStatus(status, wsp_hip_last_error(hipNet.context()));
+
+    // The self caches now hold one more row; their Cache records follow.
+    for (int l = 0; l < decoderShape.layers; ++l)
+    {
+        caches.selfKeys[(std::size_t) l].rows = decodedPositions + 1;
+        caches.selfValues[(std::size_t) l].rows = decodedPositions + 1;
+    }
+    decodedPositions += 1;
+}
+} // namespace WSP

@@ -1,0 +1,112 @@
+// The greedy loop of Whisper::decodeTranscript (Whisper/Whisper.cpp:1186-1224,
+// 1361-1443): step 0 opens the sequence, decodes the prompt and samples its
+// last row under the first-step mask; step j decodes the slot step j-1
+// sampled into and samples under the later-step mask. The sampled token never
+// leaves the device on its way to the next step; the host reads each step's
+// slot through a pinned copy behind that step's event, stepsInFlight steps
+// ahead.
+#include "../../../include/whispereacp/GreedyDecoder.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <chrono>
+#include <stdexcept>
+
+namespace WSP
+{
+GreedyDecoder::GreedyDecoder(Decoder& decoderToUse, const DecoderWeights& weightsToUse, const Device& device)
+    : decoder(decoderToUse), weights(weightsToUse)
+{
+    const DecoderShape& shape = decoder.shape();
+    void* stream = wsp_hip_stream(decoder.net().context());
+    selection.prepare(device, shape.maxPositions, shape.vocabularySize, stream);
+    sequenceTokens = DeviceBuffer(device, (std::size_t) (shape.maxPositions + 1) * sizeof(std::uint32_t));
+    logitRows = DeviceBuffer(device, (std::size_t) shape.maxPositions * shape.vocabularySize * sizeof(float));
+    checkHip(hipHostMalloc(reinterpret_cast<void**>(&hostSlots), stepsInFlight * sizeof(unsigned), 0),
+             "hipHostMalloc");
+    for (int i = 0; i < stepsInFlight; ++i)
+    {
+        hipEvent_t e = nullptr;
+        checkHip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+        events.push_back(e);
+    }
+}
+
+GreedyDecoder::~GreedyDecoder()
+{
+    for (void* e : events)
+        (void) hipEventDestroy(static_cast<hipEvent_t>(e));
+    if (hostSlots != nullptr)
+        (void) hipHostFree(hostSlots);
+}
+
+GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int crossPositionCount,
+                                const std::vector<int>& prompt, int maximumTokens, int endOfText,
+                                const float* firstMask, const float* laterMask)
+{
+    const DecoderShape& shape = decoder.shape();
+    const int promptLength = (int) prompt.size();
+    if (promptLength <= 0 || promptLength > shape.maxPositions)
+        throw ModelError("a transcript needs a prompt of 1 to " + std::to_string(shape.maxPositions) + " tokens");
+    if (maximumTokens <= 0)
+        throw ModelError("a transcript has to be allowed at least one token");
+    for (int id : prompt)
+        if (id < 0 || id >= shape.vocabularySize)
+            throw ModelError("prompt token " + std::to_string(id) + " is outside the vocabulary");
+
+    const auto stream = static_cast<hipStream_t>(pass.hipStream());
+    const int stepLimit = std::min(maximumTokens, shape.maxPositions - promptLength + 1);
+    const std::size_t slotBytes = sizeof(std::uint32_t);
+    const std::size_t rowBytes = (std::size_t) shape.vocabularySize * sizeof(float);
+    auto slot = [&](int index) {
+        return BufferRange {sequenceTokens.data(), (std::size_t) index * slotBytes, slotBytes};
+    };
+
+    std::vector<std::uint32_t> ids(prompt.begin(), prompt.end());
+    checkHip(hipMemcpyAsync(sequenceTokens.data(), ids.data(), ids.size() * slotBytes, hipMemcpyHostToDevice, stream),
+             "upload prompt");
+    checkHip(hipStreamSynchronize(stream), "upload prompt");
+
+    auto startStep = [&](int step) {
+        const int target = promptLength + step;
+        if (step == 0)
+        {
+            decoder.beginSequence(pass, encoderRows, weights, crossPositionCount);
+            decoder.step(pass, BufferRange {sequenceTokens.data(), 0, (std::size_t) promptLength * slotBytes},
+                         promptLength, weights, BufferRange::of(logitRows));
+            selection.encode(pass, BufferRange {logitRows.data(), (std::size_t) (promptLength - 1) * rowBytes, rowBytes},
+                             firstMask, slot(target), 1, shape.vocabularySize);
+        }
+        else
+            decoder.stepAndSample(pass, slot(target - 1), weights, BufferRange::of(logitRows), laterMask, slot(target));
+        checkHip(hipMemcpyAsync(&hostSlots[step % stepsInFlight], slot(target).data(), slotBytes,
+                                hipMemcpyDeviceToHost, stream),
+                 "read token");
+        checkHip(hipEventRecord(static_cast<hipEvent_t>(events[(std::size_t) (step % stepsInFlight)]), stream),
+                 "hipEventRecord");
+    };
+
+    GreedyRun run;
+    const auto start = std::chrono::steady_clock::now();
+    int nextStep = 0;
+    while (nextStep < stepsInFlight && nextStep < stepLimit)
+        startStep(nextStep++);
+
+    for (int step = 0; step < nextStep; ++step)
+    {
+        checkHip(hipEventSynchronize(static_cast<hipEvent_t>(events[(std::size_t) (step % stepsInFlight)])),
+                 "hipEventSynchronize");
+        const int sampled = (int) hostSlots[step % stepsInFlight];
+        ++run.steps;
+        if (sampled == endOfText)
+            break;
+        run.tokens.push_back(sampled);
+        if (nextStep < stepLimit)
+            startStep(nextStep++);
+    }
+    run.decodeSeconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
+    checkHip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    return run;
+}
+} // namespace WSP
