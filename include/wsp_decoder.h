@@ -74,6 +74,13 @@ const float* wsp_decoder_hidden_states(const wsp_decoder* decoder);
 int wsp_decoder_set_fused(wsp_decoder* decoder, int enabled);
 int wsp_decoder_uses_fused(const wsp_decoder* decoder);
 
+/* Whether fused single-token steps run as the one persistent launch (1) or
+ * as the per-op sequence (0); see wsp_hip_step_persistent. */
+int wsp_decoder_step_persistent(const wsp_decoder* decoder);
+
+/* The persistent step's watchdog word (see wsp_hip_device_status). */
+int wsp_decoder_device_status(wsp_decoder* decoder, int* status, int clear);
+
 /* Argmax::encode (Kernels/Argmax.h:236-241) into out (device uint32 [rows]). */
 int wsp_decoder_argmax(wsp_decoder* decoder, const float* logits, int rows, int row_length,
                        const float* mask, uint32_t* out);

@@ -184,6 +184,19 @@ int wsp_hip_decoder_step(wsp_hip_ctx* ctx, const wsp_decoder_tensors* tensors,
                          const uint32_t* tokens, int position, int cross_rows, float* hidden,
                          float* logits, const float* mask, uint32_t* argmax_out);
 
+/* Whether wsp_hip_decoder_step runs as the one persistent launch on this
+ * context (1) or falls back to the per-op sequence (0) because the shape or
+ * device is outside the persistent kernel's capacities. No reference
+ * counterpart: it reports which of this build's two step forms is in use. */
+int wsp_hip_step_persistent(const wsp_hip_ctx* ctx);
+
+/* Waits for the context's stream, then reports the persistent step's
+ * watchdog word in *status: 0 when every hand-over completed, 1 when a wait
+ * timed out and the launch left early (its outputs are then undefined).
+ * clear != 0 resets the word. No reference counterpart: the reference's
+ * passes cannot time out. */
+int wsp_hip_device_status(wsp_hip_ctx* ctx, int* status, int clear);
+
 #ifdef __cplusplus
 }
 #endif

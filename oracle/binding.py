@@ -135,6 +135,10 @@ class Oracle:
         tt = np.ascontiguousarray(token_table, dtype=np.float32)
         pt = np.ascontiguousarray(position_table, dtype=np.float32)
         width = tt.shape[1]
+        if pt.shape[1] != width or first_position < 0 or first_position + t.shape[0] > pt.shape[0]:
+            raise ValueError("embed: the position table has no row for every position")
+        if t.size and int(t.max()) >= tt.shape[0]:
+            raise ValueError("embed: a token id past the token table")
         out = np.empty((t.shape[0], width), dtype=np.float64)
         self.lib.oracle_embed(_ptr(t, _up), t.shape[0], _ptr(tt, _fp), _ptr(pt, _fp),
                               first_position, width, _ptr(out, _dp))

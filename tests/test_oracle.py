@@ -328,7 +328,7 @@ def test_embed_counted_tables(oracle):
         assert np.array_equal(by_pos[t], 64.0 * (first + t) + 0.25 * np.arange(width))
     big = counted(51864, 1.0)[:, :3] * 0 + np.arange(51864, dtype=np.float32)[:, None]
     ids = [0, 1, 220, 50256, 50257, 51863]
-    out = oracle.embed(ids, big, np.zeros((4, 3), np.float32), 0)
+    out = oracle.embed(ids, big, np.zeros((len(ids), 3), np.float32), 0)
     assert np.array_equal(out[:, 0], np.array(ids, dtype=np.float64))
 
 

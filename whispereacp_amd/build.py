@@ -20,7 +20,7 @@ BUILD = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(BUILD, "libwhispereacp_hip.so")
 ARCH = "gfx950"
 
-DEVICE_SOURCES = ["ops.hip", "capi.hip", "cross_kv.hip", "fused_step.hip"]
+DEVICE_SOURCES = ["ops.hip", "capi.hip", "cross_kv.hip", "fused_step.hip", "step_kernel.hip"]
 HOST_SOURCES = ["host/Gpu.cpp", "host/Net.cpp", "host/Half.cpp", "host/HipNet.cpp", "host/DecoderWeights.cpp",
                 "host/Decoder.cpp", "host/Argmax.cpp", "host/GreedyDecoder.cpp", "host/decoder_capi.cpp"]
 

@@ -36,6 +36,8 @@ int context_hip(Context* ctx, hipError_t e, const char* what);
 // fused_step.hip
 int fused_prepare(Context* ctx);
 void fused_release(Context* ctx);
+bool fused_persistent(const Context* ctx);
+int fused_status(Context* ctx, int* status, int clear);
 
 // cross_kv.hip: out = X·Wᵀ (+ bias) for `rows` rows of `width`.
 int cross_kv_projection(Context* ctx, const float* x, int rows, int width, const void* weight,

@@ -1,11 +1,19 @@
 // wsp_hip_decoder_step: one single-token decoder step plus its greedy argmax
 // (Decoder/Decoder.cpp:151-177 followed by Whisper/Whisper.cpp:1164-1184).
-// This version records the step as the per-op kernel sequence on the
-// context's stream.
+//
+// The step runs as one persistent cooperative launch (step_kernel.hip) when
+// the shape fits its capacities; otherwise it is recorded as the per-op
+// kernel sequence on the context's stream. This file sizes the persistent
+// kernel's exchange area, chooses its work split per call and launches it.
 #include "capi_internal.h"
 #include "ops.h"
+#include "step_kernel.h"
 
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
 #include <new>
+#include <vector>
 
 namespace wsp
 {
@@ -13,11 +21,30 @@ namespace
 {
 struct FusedState
 {
+    // Per-op sequence scratch.
     float* hidden = nullptr;     // residual stream [width]
     float* normalised = nullptr; // [width]
     float* query = nullptr;      // [width]
     float* attended = nullptr;   // [width]
     float* inner = nullptr;      // [feed_forward_width]
+
+    // Persistent kernel.
+    bool persistent = false;
+    char why_not[160] = {0};
+    int workgroups = 0;
+    int row_groups = 0;
+    int self_split_max = 0;
+    int cross_split_max = 0;
+    int layer_words = 0;
+    int off_qkv = 0, off_self = 0, off_h2 = 0, off_xq = 0, off_xpart = 0, off_xattn = 0, off_h3 = 0, off_ff = 0,
+        off_h4 = 0, off_argmax = 0;
+    uint64_t* exchange = nullptr;
+    size_t exchange_words = 0;
+    int* status = nullptr;
+    wsp_layer_tensors* table = nullptr; // device copy
+    std::vector<wsp_layer_tensors> table_host;
+    bool table_valid = false;
+    uint32_t epoch = 0;
 };
 
 size_t element_bytes(int wdtype)
@@ -29,65 +56,91 @@ const void* offset(const void* base, size_t elements, int wdtype)
 {
     return static_cast<const char*>(base) + elements * element_bytes(wdtype);
 }
-} // namespace
 
-int fused_prepare(Context* ctx)
+int ceil_div(int a, int b)
 {
-    auto* state = new (std::nothrow) FusedState {};
-    if (state == nullptr)
-        return context_fail(ctx, WSP_ERR_CAPACITY, "fused step state");
-    ctx->fused = state;
-    const size_t d = ctx->shape.width, f = ctx->shape.feed_forward_width;
-    float** buffers[] = {&state->hidden, &state->normalised, &state->query, &state->attended};
-    for (float** b : buffers)
-    {
-        const int status = context_hip(ctx, hipMalloc(b, d * sizeof(float)), "fused step scratch");
-        if (status != WSP_OK)
-            return status;
-    }
-    return context_hip(ctx, hipMalloc(&state->inner, f * sizeof(float)), "fused step scratch");
+    return (a + b - 1) / b;
 }
 
-void fused_release(Context* ctx)
+// Whether the persistent kernel can run this shape on this device, and its
+// fixed layout. Leaves state->persistent false with the reason otherwise.
+void plan_persistent(Context* ctx, FusedState* st)
 {
-    auto* state = static_cast<FusedState*>(ctx->fused);
-    if (state == nullptr)
-        return;
-    hipFree(state->hidden);
-    hipFree(state->normalised);
-    hipFree(state->query);
-    hipFree(state->attended);
-    hipFree(state->inner);
-    delete state;
-    ctx->fused = nullptr;
-}
-} // namespace wsp
-
-extern "C" int wsp_hip_decoder_step(wsp_hip_ctx* ctx, const wsp_decoder_tensors* tensors,
-                                    const uint32_t* tokens, int position, int cross_rows,
-                                    float* hidden, float* logits, const float* mask,
-                                    uint32_t* argmax_out)
-{
-    using namespace wsp;
-    if (ctx == nullptr)
-        return WSP_ERR_ARGUMENT;
-    if (tensors == nullptr || tensors->layers == nullptr || tokens == nullptr || hidden == nullptr
-        || logits == nullptr)
-        return context_fail(ctx, WSP_ERR_ARGUMENT, "decoder step: null pointer");
     const wsp_decoder_shape& s = ctx->shape;
-    if (position < 0 || position + 1 > s.max_positions)
-        return context_fail(ctx, WSP_ERR_CAPACITY, "decoder step: position past the window");
-    if (cross_rows <= 0 || cross_rows > s.cross_positions)
-        return context_fail(ctx, WSP_ERR_CAPACITY, "decoder step: cross rows outside the encoder output");
-    const int head_width = s.width / s.heads;
-    if (head_width % 4 != 0 || head_width > ops::kMaxHeadWidth)
-        return context_fail(ctx, WSP_ERR_LOGIC, "decoder step: unsupported head width");
+    const int d = s.width, f = s.feed_forward_width, H = s.heads, hd = d / H;
+    auto refuse = [&](const char* why) {
+        std::snprintf(st->why_not, sizeof(st->why_not), "%s", why);
+        st->persistent = false;
+    };
+    if (d > step::kMaxWidth || f > step::kMaxFeedForward)
+        return refuse("width or feed-forward width past the persistent kernel's capacity");
+    if (d % 8 != 0 || f % 8 != 0)
+        return refuse("widths must be multiples of 8");
+    if (f / 4 > step::kMaxRowChunks)
+        return refuse("feed-forward rows past the persistent kernel's capacity");
+    if (hd % 4 != 0 || hd > step::kMaxHeadWidth)
+        return refuse("head width must be a multiple of 4, at most 64");
 
-    auto* st = static_cast<FusedState*>(ctx->fused);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, ctx->device) != hipSuccess)
+        return refuse("device properties unavailable");
+    int cooperative = 0;
+    hipDeviceGetAttribute(&cooperative, hipDeviceAttributeCooperativeLaunch, ctx->device);
+    if (!cooperative)
+        return refuse("device has no cooperative launch");
+    const int G = prop.multiProcessorCount;
+    const int self_split_max = ceil_div(s.max_positions, step::kSelfKeys);
+    const int head_groups = H * self_split_max;
+    const int row_groups = G - head_groups;
+    if (row_groups < H)
+        return refuse("too few CUs for the head groups");
+    if (self_split_max * H * (hd + 2) > step::kMaxCombine || 2 * G > step::kMaxCombine)
+        return refuse("attention partials past the combine capacity");
+    const int cross_needed = ceil_div(s.cross_positions, step::kCrossKeys);
+    const int cross_cap = step::kMaxCombine / (hd + 2);
+    if (cross_needed > cross_cap)
+        return refuse("cross positions past the persistent kernel's capacity");
+    const int cross_split_max = std::min(cross_cap, std::max(cross_needed, row_groups / H));
+
+    // Every kernel variant must fit one workgroup per CU.
+    for (int wt : {WSP_F32, WSP_F16, WSP_BF16})
+    {
+        int blocks = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, step::kernel_for(wt), step::kThreads, 0)
+                != hipSuccess
+            || blocks < 1)
+            return refuse("the persistent kernel does not fit a CU");
+    }
+
+    st->workgroups = G;
+    st->row_groups = row_groups;
+    st->self_split_max = self_split_max;
+    st->cross_split_max = cross_split_max;
+    int at = 0;
+    st->off_qkv = at, at += 3 * d;
+    st->off_self = at, at += self_split_max * H * (hd + 2);
+    st->off_h2 = at, at += d;
+    st->off_xq = at, at += d;
+    st->off_xpart = at, at += H * cross_split_max * (hd + 2);
+    st->off_xattn = at, at += d;
+    st->off_h3 = at, at += d;
+    st->off_ff = at, at += f;
+    st->off_h4 = at, at += d;
+    st->layer_words = at;
+    st->off_argmax = at * s.layers;
+    st->exchange_words = (size_t) at * s.layers + 2 * G;
+    st->persistent = true;
+}
+
+int per_op_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* tensors, const uint32_t* tokens,
+                int position, int cross_rows, float* hidden, float* logits, const float* mask,
+                uint32_t* argmax_out)
+{
+    const wsp_decoder_shape& s = ctx->shape;
     const hipStream_t stream = ctx->stream;
     const int d = s.width, f = s.feed_forward_width;
     const int wt = tensors->wdtype;
-    const float scale = 1.f / sqrtf((float) head_width);
+    const float scale = 1.f / sqrtf((float) (s.width / s.heads));
     const float eps = 1e-5f;
     hipError_t e = hipSuccess;
 #define WSP_TRY(call)                                                                              \
@@ -138,4 +191,216 @@ extern "C" int wsp_hip_decoder_step(wsp_hip_ctx* ctx, const wsp_decoder_tensors*
                             ctx->argmax_indices));
 #undef WSP_TRY
     return WSP_OK;
+}
+
+bool aligned16(const void* p)
+{
+    return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+}
+
+int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* tensors, const uint32_t* tokens,
+                    int position, int cross_rows, float* hidden, float* logits, const float* mask,
+                    uint32_t* argmax_out)
+{
+    const wsp_decoder_shape& s = ctx->shape;
+    const int d = s.width, H = s.heads, hd = d / H;
+
+    // Every row the kernel streams in 16-byte chunks must start 16-byte aligned.
+    if (!aligned16(tensors->logits_weight) || !aligned16(tensors->token_embedding))
+        return context_fail(ctx, WSP_ERR_ARGUMENT, "decoder step: weights must be 16-byte aligned");
+    for (int l = 0; l < s.layers; ++l)
+    {
+        const wsp_layer_tensors& L = tensors->layers[l];
+        const void* rows[] = {L.self_qkv_w, L.self_out_w, L.cross_q_w, L.cross_out_w, L.fc1_w, L.fc2_w,
+                              L.self_keys, L.self_values, L.cross_keys, L.cross_values};
+        for (const void* p : rows)
+            if (p == nullptr || !aligned16(p))
+                return context_fail(ctx, WSP_ERR_ARGUMENT, "decoder step: layer tensors must be 16-byte aligned");
+    }
+
+    // The per-layer table lives on the device; it is uploaded when it changes.
+    const size_t table_bytes = sizeof(wsp_layer_tensors) * (size_t) s.layers;
+    if (!st->table_valid || std::memcmp(st->table_host.data(), tensors->layers, table_bytes) != 0)
+    {
+        st->table_host.assign(tensors->layers, tensors->layers + s.layers);
+        const hipError_t e = hipMemcpyAsync(st->table, st->table_host.data(), table_bytes, hipMemcpyHostToDevice,
+                                            ctx->stream);
+        if (e != hipSuccess)
+            return context_hip(ctx, e, "decoder step: layer table upload");
+        const hipError_t w = hipStreamSynchronize(ctx->stream);
+        if (w != hipSuccess)
+            return context_hip(ctx, w, "decoder step: layer table upload");
+        st->table_valid = true;
+    }
+
+    // The work split of this call.
+    const int self_splits = ceil_div(position + 1, step::kSelfKeys);
+    int cross_splits = std::max(1, std::min(st->row_groups / H, cross_rows));
+    cross_splits = std::max(cross_splits, ceil_div(cross_rows, step::kCrossKeys));
+    cross_splits = std::min(cross_splits, st->cross_split_max);
+    const int cross_chunk = ceil_div(cross_rows, cross_splits);
+    cross_splits = ceil_div(cross_rows, cross_chunk);
+    if (cross_chunk > step::kCrossKeys || self_splits > st->self_split_max)
+        return context_fail(ctx, WSP_ERR_CAPACITY, "decoder step: attention split past the planned capacity");
+
+    step::StepArgs a {};
+    a.layers = st->table;
+    a.token_embedding = tensors->token_embedding;
+    a.logits_weight = tensors->logits_weight;
+    a.position_embedding = tensors->position_embedding;
+    a.final_norm_w = tensors->final_norm_w;
+    a.final_norm_b = tensors->final_norm_b;
+    a.tokens = tokens;
+    a.hidden = hidden;
+    a.logits = logits;
+    a.mask = mask;
+    a.argmax_out = argmax_out;
+    a.exchange = st->exchange;
+    a.status = st->status;
+    a.width = d;
+    a.heads = H;
+    a.layer_count = s.layers;
+    a.feed_forward = s.feed_forward_width;
+    a.vocabulary = s.vocabulary_size;
+    a.logits_wdtype = tensors->logits_wdtype;
+    a.position = position;
+    a.cross_rows = cross_rows;
+    a.row_groups = st->row_groups;
+    a.self_splits = self_splits;
+    a.cross_splits = cross_splits;
+    a.cross_chunk = cross_chunk;
+    a.epoch = ++st->epoch;
+    a.scale = 1.f / sqrtf((float) hd);
+    a.eps = 1e-5f;
+    a.off_qkv = st->off_qkv;
+    a.off_self = st->off_self;
+    a.off_h2 = st->off_h2;
+    a.off_xq = st->off_xq;
+    a.off_xpart = st->off_xpart;
+    a.off_xattn = st->off_xattn;
+    a.off_h3 = st->off_h3;
+    a.off_ff = st->off_ff;
+    a.off_h4 = st->off_h4;
+    a.layer_words = st->layer_words;
+    a.off_argmax = st->off_argmax;
+
+    void* args[] = {&a};
+    const hipError_t e = hipLaunchCooperativeKernel(step::kernel_for(tensors->wdtype),
+                                                    dim3(st->workgroups), dim3(step::kThreads), args, 0, ctx->stream);
+    return context_hip(ctx, e, "decoder step launch");
+}
+} // namespace
+
+int fused_prepare(Context* ctx)
+{
+    auto* state = new (std::nothrow) FusedState {};
+    if (state == nullptr)
+        return context_fail(ctx, WSP_ERR_CAPACITY, "fused step state");
+    ctx->fused = state;
+    const size_t d = ctx->shape.width, f = ctx->shape.feed_forward_width;
+    float** buffers[] = {&state->hidden, &state->normalised, &state->query, &state->attended};
+    for (float** b : buffers)
+    {
+        const int status = context_hip(ctx, hipMalloc(b, d * sizeof(float)), "fused step scratch");
+        if (status != WSP_OK)
+            return status;
+    }
+    int status = context_hip(ctx, hipMalloc(&state->inner, f * sizeof(float)), "fused step scratch");
+    if (status != WSP_OK)
+        return status;
+
+    plan_persistent(ctx, state);
+    if (!state->persistent)
+        return WSP_OK;
+    status = context_hip(ctx, hipMalloc(&state->exchange, state->exchange_words * sizeof(uint64_t)),
+                         "step exchange area");
+    if (status == WSP_OK)
+        status = context_hip(ctx, hipMalloc(&state->status, sizeof(int)), "step status word");
+    if (status == WSP_OK)
+        status = context_hip(ctx,
+                             hipMalloc(&state->table, sizeof(wsp_layer_tensors) * (size_t) ctx->shape.layers),
+                             "step layer table");
+    // Epoch 0 is never used, so zeroed words never pass for a step's output.
+    if (status == WSP_OK)
+        status = context_hip(ctx, hipMemset(state->exchange, 0, state->exchange_words * sizeof(uint64_t)),
+                             "step exchange area");
+    if (status == WSP_OK)
+        status = context_hip(ctx, hipMemset(state->status, 0, sizeof(int)), "step status word");
+    return status;
+}
+
+void fused_release(Context* ctx)
+{
+    auto* state = static_cast<FusedState*>(ctx->fused);
+    if (state == nullptr)
+        return;
+    hipFree(state->hidden);
+    hipFree(state->normalised);
+    hipFree(state->query);
+    hipFree(state->attended);
+    hipFree(state->inner);
+    hipFree(state->exchange);
+    hipFree(state->status);
+    hipFree(state->table);
+    delete state;
+    ctx->fused = nullptr;
+}
+
+bool fused_persistent(const Context* ctx)
+{
+    const auto* state = static_cast<const FusedState*>(ctx->fused);
+    return state != nullptr && state->persistent;
+}
+
+int fused_status(Context* ctx, int* status, int clear)
+{
+    auto* state = static_cast<FusedState*>(ctx->fused);
+    *status = 0;
+    if (state == nullptr || state->status == nullptr)
+        return WSP_OK;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpy(status, state->status, sizeof(int), hipMemcpyDeviceToHost);
+    if (e == hipSuccess && clear && *status != 0)
+        e = hipMemset(state->status, 0, sizeof(int));
+    return context_hip(ctx, e, "step status word");
+}
+} // namespace wsp
+
+extern "C" int wsp_hip_decoder_step(wsp_hip_ctx* ctx, const wsp_decoder_tensors* tensors,
+                                    const uint32_t* tokens, int position, int cross_rows,
+                                    float* hidden, float* logits, const float* mask,
+                                    uint32_t* argmax_out)
+{
+    using namespace wsp;
+    if (ctx == nullptr)
+        return WSP_ERR_ARGUMENT;
+    if (tensors == nullptr || tensors->layers == nullptr || tokens == nullptr || hidden == nullptr
+        || logits == nullptr)
+        return context_fail(ctx, WSP_ERR_ARGUMENT, "decoder step: null pointer");
+    const wsp_decoder_shape& s = ctx->shape;
+    if (position < 0 || position + 1 > s.max_positions)
+        return context_fail(ctx, WSP_ERR_CAPACITY, "decoder step: position past the window");
+    if (cross_rows <= 0 || cross_rows > s.cross_positions)
+        return context_fail(ctx, WSP_ERR_CAPACITY, "decoder step: cross rows outside the encoder output");
+    const int head_width = s.width / s.heads;
+    if (head_width % 4 != 0 || head_width > ops::kMaxHeadWidth)
+        return context_fail(ctx, WSP_ERR_LOGIC, "decoder step: unsupported head width");
+
+    auto* st = static_cast<FusedState*>(ctx->fused);
+    if (st->persistent)
+        return persistent_step(ctx, st, tensors, tokens, position, cross_rows, hidden, logits, mask, argmax_out);
+    return per_op_step(ctx, st, tensors, tokens, position, cross_rows, hidden, logits, mask, argmax_out);
+}
+
+extern "C" int wsp_hip_step_persistent(const wsp_hip_ctx* ctx)
+{
+    return ctx != nullptr && wsp::fused_persistent(ctx) ? 1 : 0;
+}
+
+extern "C" int wsp_hip_device_status(wsp_hip_ctx* ctx, int* status, int clear)
+{
+    if (ctx == nullptr || status == nullptr)
+        return WSP_ERR_ARGUMENT;
+    return wsp::fused_status(ctx, status, clear);
 }

@@ -200,6 +200,18 @@ int wsp_decoder_uses_fused(const wsp_decoder* d)
     return d != nullptr && d->decoder && d->decoder->usesFusedStep(*d->weights, 1) ? 1 : 0;
 }
 
+int wsp_decoder_step_persistent(const wsp_decoder* d)
+{
+    return d != nullptr && d->decoder ? wsp_hip_step_persistent(d->decoder->net().context()) : 0;
+}
+
+int wsp_decoder_device_status(wsp_decoder* d, int* status, int clear)
+{
+    if (d == nullptr || !d->decoder || status == nullptr)
+        return WSP_ERR_ARGUMENT;
+    return wsp_hip_device_status(d->decoder->net().context(), status, clear);
+}
+
 int wsp_decoder_argmax(wsp_decoder* d, const float* logits, int rows, int row_length, const float* mask,
                        uint32_t* out)
 {

@@ -1,0 +1,61 @@
+// The persistent single-token step kernel (step_kernel.hip): its capacities and
+// its argument block. The host side (fused_step.hip) sizes the exchange area,
+// picks the work split and launches it cooperatively.
+#pragma once
+
+#include "../../include/wsp_hip.h"
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace wsp::step
+{
+constexpr int kThreads = 512;          // one workgroup per CU, 8 waves
+constexpr int kMaxWidth = 1280;        // d_model
+constexpr int kMaxFeedForward = 5120;  // fc1 width
+constexpr int kMaxHeadWidth = 64;
+constexpr int kMaxCombine = 4096;      // attention partial floats one workgroup combines
+constexpr int kMaxPoll = 16;           // exchange words per thread per wait (8192 per workgroup)
+constexpr int kSelfKeys = 256;         // self-attention keys one head group holds
+constexpr int kCrossKeys = 160;        // cross-attention keys one row group holds
+
+// Exchange words per layer, in this order (offsets in StepArgs):
+//   qkv [3d] | self partials [self_split_max][heads][hd + 2] | h2 [d] | xq [d]
+//   | cross partials [heads][cross_split_max][hd + 2] | xattn [d] | h3 [d] | ff [f] | h4 [d]
+// followed by one argmax block [2 * workgroups] after the last layer.
+struct StepArgs
+{
+    const wsp_layer_tensors* layers; // device copy of the per-layer table
+    const float* token_embedding;
+    const void* logits_weight;
+    const float* position_embedding;
+    const float* final_norm_w;
+    const float* final_norm_b;
+    const uint32_t* tokens;
+    float* hidden;
+    float* logits;
+    const float* mask;
+    uint32_t* argmax_out;
+    uint64_t* exchange;
+    int* status;
+
+    int width, heads, layer_count, feed_forward, vocabulary, logits_wdtype;
+    int position, cross_rows;
+    int row_groups;     // workgroups [0, row_groups) run projections and cross chunks
+    int self_splits;    // key splits per head for this position (<= self_split_max)
+    int cross_splits;   // key chunks per head
+    int cross_chunk;    // keys per chunk (<= kCrossKeys)
+    uint32_t epoch;
+    float scale, eps;
+
+    int off_qkv, off_self, off_h2, off_xq, off_xpart, off_xattn, off_h3, off_ff, off_h4;
+    int layer_words, off_argmax;
+};
+
+// Longest projection row, in 16-byte chunks: 16 slices of 3 chunks per lane.
+constexpr int kMaxRowChunks = 16 * 32 * 3;
+
+// The kernel for this projection storage (the logits storage is an argument).
+const void* kernel_for(int wdtype);
+} // namespace wsp::step

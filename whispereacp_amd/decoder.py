@@ -191,6 +191,18 @@ class Decoder:
     def uses_fused(self) -> bool:
         return bool(self.lib.wsp_decoder_uses_fused(self.handle))
 
+    @property
+    def uses_persistent_step(self) -> bool:
+        """Whether fused single-token steps run as the one persistent launch."""
+        return bool(self.lib.wsp_decoder_step_persistent(self.handle))
+
+    def device_status(self, clear: bool = False) -> int:
+        """Waits for the stream; 0 when every persistent step completed its
+        hand-overs, 1 when its watchdog cut a step short."""
+        status = ctypes.c_int(0)
+        self._check(self.lib.wsp_decoder_device_status(self.handle, ctypes.byref(status), int(clear)))
+        return status.value
+
     def argmax(self, logits: torch.Tensor, rows: int, row_length: int, mask: Optional[torch.Tensor],
                out: torch.Tensor):
         self._check(self.lib.wsp_decoder_argmax(self.handle, ptr(logits), rows, row_length, ptr(mask), ptr(out)))
