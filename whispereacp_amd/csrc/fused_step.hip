@@ -80,6 +80,8 @@ void plan_persistent(Context* ctx, FusedState* st)
         return refuse("feed-forward rows past the persistent kernel's capacity");
     if (hd % 4 != 0 || hd > step::kMaxHeadWidth)
         return refuse("head width must be a multiple of 4, at most 64");
+    if (s.layers > step::kMaxLayers)
+        return refuse("more layers than the persistent kernel's table holds");
 
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, ctx->device) != hipSuccess)

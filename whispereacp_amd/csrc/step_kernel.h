@@ -16,9 +16,9 @@ constexpr int kMaxWidth = 1280;        // d_model
 constexpr int kMaxFeedForward = 5120;  // fc1 width
 constexpr int kMaxHeadWidth = 64;
 constexpr int kMaxCombine = 4096;      // attention partial floats one workgroup combines
-constexpr int kMaxPoll = 16;           // exchange words per thread per wait (8192 per workgroup)
 constexpr int kSelfKeys = 256;         // self-attention keys one head group holds
 constexpr int kCrossKeys = 160;        // cross-attention keys one row group holds
+constexpr int kMaxLayers = 32;         // layer table entries held in LDS
 
 // Exchange words per layer, in this order (offsets in StepArgs):
 //   qkv [3d] | self partials [self_split_max][heads][hd + 2] | h2 [d] | xq [d]

@@ -11,17 +11,20 @@
 // its validity in one load, so a hand-over costs one store-to-load trip
 // through the memory side, with no barrier and no flag round trip.
 //
-// Why it streams at bandwidth: each workgroup issues the loads of its slice of
-// the next phase's weights (and of its cross-attention key/value chunk)
-// BEFORE it waits for that phase's inputs, so HBM traffic overlaps the
-// hand-over chain instead of following it.
+// Why it streams at bandwidth: a workgroup issues the loads of its slice of
+// the NEXT phase's weights while it computes the current one (two register
+// sets alternate), so a phase's weights are in registers when its input
+// arrives and HBM traffic overlaps the hand-over chain. The layer table lives
+// in LDS, so no phase waits on a pointer load, and every cross-lane reduction
+// is a DPP/swizzle tree in a fixed order.
 //
 // Roles (G workgroups of 512 threads, one per CU):
-//   - the first Gg ("row" groups) run every projection, the cross-attention
-//     key chunks and half of the logits;
+//   - the first Gg ("row" groups) run every projection and the
+//     cross-attention key chunks;
 //   - the last Ga = heads * self_split_max ("head" groups) run self-attention,
-//     each holding its head's cached keys and values in registers (prefetched
-//     one layer ahead), and the cross-attention combine of one head.
+//     each holding its head's cached keys and values in registers (loaded one
+//     layer ahead), and the cross-attention combine of one head;
+//   - all of them run the tied logits.
 // Per layer the chain is: LN1+QKV -> self attention -> out-proj (+residual)
 // -> LN2+cross-q -> cross partials -> cross combine -> cross out (+residual)
 // -> LN3+fc1+GELU -> fc2 (+residual). Then final LN + tied logits with a
@@ -44,10 +47,14 @@ constexpr int kSelfPasses = kSelfKeys / kKeySlots; // self keys held per head gr
 constexpr int kCrossPasses = kCrossKeys / kKeySlots;
 constexpr int kRowLanes = 32;                      // lanes per projection row
 constexpr int kRowGroups = kThreads / kRowLanes;   // rows in flight per workgroup
+constexpr int kChunks = 3;                         // 16-byte chunks per lane per row slice
+constexpr int kRing = 4;                           // logits rows in flight per row group
+constexpr int kWaves = kThreads / kWave;
 constexpr int kSpinLimit = 1 << 21;                // poll rounds before the watchdog trips
 constexpr uint32_t kUnchosen = 0xFFFFFFFFu;
 
 static_assert(kSelfKeys % kKeySlots == 0 && kCrossKeys % kKeySlots == 0, "key capacities");
+static_assert(kKeySlots / kWaves == 4, "attend() folds four key slots per wave");
 
 // ---------------------------------------------------------------------------
 // Exchange words
@@ -63,19 +70,108 @@ __device__ __forceinline__ uint64_t peek(const uint64_t* p)
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------------------
+// Cross-lane sums and maxima in a fixed order. A DPP "row" is 16 lanes: swap
+// neighbours, swap pairs, mirror within 8 and mirror within 16 leave the row
+// total in every lane; a swizzle adds the other row of a 32-lane half and two
+// readlanes join the halves of the wave. Every lane of the span must be active.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int kSwapNeighbours = 0xB1; // quad_perm [1,0,3,2]
+constexpr int kSwapPairs = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kMirrorHalfRow = 0x141; // row_half_mirror
+constexpr int kMirrorRow = 0x140;     // row_mirror
+constexpr int kSwap16 = 0x401F;       // ds_swizzle bit mode: lane ^ 16 within 32 lanes
+
+__device__ __forceinline__ float swap16(float v)
+{
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), kSwap16));
+}
+
+__device__ __forceinline__ float halves_sum(float v)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0))
+           + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+}
+
+__device__ __forceinline__ float sum16(float v)
+{
+    v += dpp<kSwapNeighbours>(v);
+    v += dpp<kSwapPairs>(v);
+    v += dpp<kMirrorHalfRow>(v);
+    v += dpp<kMirrorRow>(v);
+    return v;
+}
+
+__device__ __forceinline__ float sum32(float v)
+{
+    v = sum16(v);
+    return v + swap16(v);
+}
+
+__device__ __forceinline__ float sum64(float v)
+{
+    return halves_sum(sum32(v));
+}
+
+__device__ __forceinline__ float max64(float v)
+{
+    v = fmaxf(v, dpp<kSwapNeighbours>(v));
+    v = fmaxf(v, dpp<kSwapPairs>(v));
+    v = fmaxf(v, dpp<kMirrorHalfRow>(v));
+    v = fmaxf(v, dpp<kMirrorRow>(v));
+    v = fmaxf(v, swap16(v));
+    return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
+}
+
 struct Shared
 {
-    float raw[kMaxWidth];       // the residual stream as gathered (un-normalised)
-    float x[kMaxFeedForward];   // the current phase's input vector
-    float comb[kMaxCombine];    // attention partials being combined
-    float red[kKeySlots][kMaxHeadWidth]; // per-key-slot value rows
-    float q[3 * kMaxHeadWidth]; // a head's query, then (self-attention) its new key and value
-    float scratch[kThreads / kWave];
-    float part[kRowGroups];     // per-row-group partial sums of a projection pass
+    wsp_layer_tensors table[kMaxLayers]; // the layer table, read once per launch
+    alignas(16) float raw[kMaxWidth];    // the residual stream as gathered (un-normalised)
+    float x[kMaxFeedForward];            // the current phase's input vector
+    float comb[kMaxCombine];             // attention partials being combined
+    float red[kWaves][kMaxHeadWidth];    // per-wave value rows of an attention chunk
+    float q[3 * kMaxHeadWidth];          // a head's query, then (self-attention) its new key and value
+    float scratch[2][kWaves];            // workgroup reductions, two alternating slots
+    float part[kRowGroups];              // per-row-group partial sums of a projection pass
     float best_v[kRowGroups];
     uint32_t best_i[kRowGroups];
     int abort;
 };
+
+// Workgroup-wide sum/max through one barrier; consecutive calls must use
+// different slots.
+__device__ __forceinline__ float group_sum(float v, Shared& sh, int slot)
+{
+    v = sum64(v);
+    if ((threadIdx.x & (kWave - 1)) == 0)
+        sh.scratch[slot][threadIdx.x / kWave] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i)
+        t += sh.scratch[slot][i];
+    return t;
+}
+
+__device__ __forceinline__ float group_max(float v, Shared& sh, int slot)
+{
+    v = max64(v);
+    if ((threadIdx.x & (kWave - 1)) == 0)
+        sh.scratch[slot][threadIdx.x / kWave] = v;
+    __syncthreads();
+    float t = sh.scratch[slot][0];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i)
+        t = fmaxf(t, sh.scratch[slot][i]);
+    return t;
+}
 
 // Waits until the n words (n <= P * 512) at src carry `epoch` and copies their
 // floats to dst (LDS). With SEG, word i sits at
@@ -142,49 +238,11 @@ constexpr int kPollFeedForward = (kMaxFeedForward + kThreads - 1) / kThreads;
 constexpr int kPollCombine = (kMaxCombine + kThreads - 1) / kThreads;
 
 // ---------------------------------------------------------------------------
-// Reductions over the 512-thread workgroup (fixed order: wave butterfly, then
-// the eight wave totals in wave order).
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ float group_sum(float v, Shared& sh)
-{
-    v = wave_sum(v);
-    __syncthreads();
-    if ((threadIdx.x & (kWave - 1)) == 0)
-        sh.scratch[threadIdx.x / kWave] = v;
-    __syncthreads();
-    float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < kThreads / kWave; ++i)
-        t += sh.scratch[i];
-    return t;
-}
-
-__device__ __forceinline__ float group_max(float v, Shared& sh)
-{
-    v = wave_max(v);
-    __syncthreads();
-    if ((threadIdx.x & (kWave - 1)) == 0)
-        sh.scratch[threadIdx.x / kWave] = v;
-    __syncthreads();
-    float t = sh.scratch[0];
-#pragma unroll
-    for (int i = 1; i < kThreads / kWave; ++i)
-        t = fmaxf(t, sh.scratch[i]);
-    return t;
-}
-
-__device__ __forceinline__ float row_sum(float v)
-{
-#pragma unroll
-    for (int offset = kRowLanes / 2; offset > 0; offset >>= 1)
-        v += __shfl_xor(v, offset, kRowLanes);
-    return v;
-}
-
-// ---------------------------------------------------------------------------
 // LayerNorm of sh.raw into sh.x: mean, centred biased variance, then
 // (x - mean) * rsqrt(var + eps) * gamma + beta (Kernels/LayerNorm.h:44-89).
-// gamma/beta arrive as registers loaded before the inputs were awaited.
+// Every wave sums the whole row itself (same lanes, same order, so every wave
+// gets the same statistics); the only barrier is the one completing sh.x.
+// gamma/beta arrive as registers loaded a phase earlier.
 // ---------------------------------------------------------------------------
 constexpr int kNormPer = (kMaxWidth + kThreads - 1) / kThreads;
 
@@ -199,35 +257,38 @@ __device__ __forceinline__ void load_norm(NormParams& p, const float* gamma, con
 #pragma unroll
     for (int k = 0; k < kNormPer; ++k)
     {
-        const int i = threadIdx.x + k * kThreads;
-        p.g[k] = i < n ? gamma[i] : 0.f;
-        p.b[k] = i < n ? beta[i] : 0.f;
+        const int i = min((int) threadIdx.x + k * kThreads, n - 1);
+        p.g[k] = gamma[i];
+        p.b[k] = beta[i];
     }
 }
 
 __device__ __forceinline__ void layer_norm(const NormParams& p, int n, float eps, Shared& sh)
 {
+    // Lane l of every wave holds elements 4 (l + 64 k) .. + 3 (n is a multiple of 4).
+    constexpr int kRuns = (kMaxWidth + 4 * kWave - 1) / (4 * kWave);
+    const int lane = threadIdx.x & (kWave - 1);
+    float4v v[kRuns];
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < kNormPer; ++k)
+    for (int k = 0; k < kRuns; ++k)
     {
-        const int i = threadIdx.x + k * kThreads;
-        if (i < n)
-            s += sh.raw[i];
+        const int i = 4 * (lane + kWave * k);
+        v[k] = i < n ? *reinterpret_cast<const float4v*>(&sh.raw[i]) : float4v {0.f, 0.f, 0.f, 0.f};
+        s += v[k][0] + v[k][1] + v[k][2] + v[k][3];
     }
-    const float mean = group_sum(s, sh) / (float) n;
+    const float mean = sum64(s) / (float) n;
     float q = 0.f;
 #pragma unroll
-    for (int k = 0; k < kNormPer; ++k)
+    for (int k = 0; k < kRuns; ++k)
     {
-        const int i = threadIdx.x + k * kThreads;
-        if (i < n)
+        if (4 * (lane + kWave * k) < n)
         {
-            const float c = sh.raw[i] - mean;
-            q += c * c;
+            const float c0 = v[k][0] - mean, c1 = v[k][1] - mean, c2 = v[k][2] - mean, c3 = v[k][3] - mean;
+            q += c0 * c0 + c1 * c1 + c2 * c2 + c3 * c3;
         }
     }
-    const float scale = rsqrtf(group_sum(q, sh) / (float) n + eps);
+    const float scale = rsqrtf(sum64(q) / (float) n + eps);
 #pragma unroll
     for (int k = 0; k < kNormPer; ++k)
     {
@@ -239,18 +300,17 @@ __device__ __forceinline__ void layer_norm(const NormParams& p, int n, float eps
 }
 
 // ---------------------------------------------------------------------------
-// Projection rows. A row is cut into `slices` equal runs of 16-byte chunks (8
-// fp16/bf16 or 4 fp32 weights); one slice is walked by a row group of 32
-// lanes, lane l taking chunks l, l+32, l+64 of the run in ascending order, and
-// the 32 partials are summed by a fixed butterfly. The slices of a row are then
-// added in slice order. Row r of a phase belongs to workgroup r % stride; a
-// workgroup's (row, slice) tasks go to its 16 row groups in order, so with the
-// slice count chosen per phase every row group has work and holds at most
-// kChunks chunks per lane — all of which are in flight before the phase's
-// input is awaited.
+// Projection rows. A row is cut into `slices` (a power of two) equal runs of
+// 16-byte chunks (8 fp16/bf16 or 4 fp32 weights); one slice is walked by a
+// row group of 32 lanes, lane l taking chunks l, l+32, l+64 of the run in
+// ascending order, and the 32 partials are summed in a fixed order. The slices
+// of a row are then added in slice order. Row r of a phase belongs to
+// workgroup r % stride; a workgroup's (row, slice) tasks go to its 16 row
+// groups in order, with the slice count chosen so every row group has work.
+// Loads are issued unconditionally (lanes without a chunk re-read their run's
+// first chunk; row groups without a task read chunk 0 of row 0) so the number
+// of loads in flight is fixed and the compiler's waits stay exact.
 // ---------------------------------------------------------------------------
-constexpr int kChunks = 3;
-
 template <int WT>
 struct Storage
 {
@@ -263,39 +323,69 @@ struct RowLoad
     uint4 w[kChunks];
 };
 
-struct Phase
+// The split of one projection phase for this workgroup (identical for every
+// layer, so computed once per launch).
+struct PhaseShape
 {
-    const void* weight;
-    const float* bias; // null: none
     int rows;
-    int inner;
-    int slices;        // a power of two dividing kRowGroups
+    int row_bytes;
+    int chunks;        // 16-byte chunks per row
+    int slice_log2;    // slices = 1 << slice_log2
     int slice_chunks;  // chunks per slice (<= kRowLanes * kChunks)
+    int local_rows;    // rows this workgroup owns
+    int rows_per_pass; // kRowGroups >> slice_log2
+    int passes;
 };
 
 template <int WT>
-__device__ __forceinline__ Phase make_phase(const void* weight, const float* bias, int rows, int inner, int stride)
+__device__ __forceinline__ PhaseShape phase_shape(int rows, int inner, int group, int stride)
 {
-    const int chunks = inner / Storage<WT>::kPerChunk;
-    const int local_rows = (rows + stride - 1) / stride;
-    int slices = 1;
-    while (slices < kRowGroups && (slices * kRowLanes * kChunks < chunks || 2 * slices * local_rows <= kRowGroups))
-        slices *= 2;
-    return Phase {weight, bias, rows, inner, slices, (chunks + slices - 1) / slices};
+    PhaseShape ps;
+    ps.rows = rows;
+    ps.row_bytes = inner * Storage<WT>::kBytes;
+    ps.chunks = inner / Storage<WT>::kPerChunk;
+    const int most_rows = (rows + stride - 1) / stride;
+    int log2 = 0;
+    while (log2 < 4 && ((kRowLanes * kChunks << log2) < ps.chunks || (2 << log2) * most_rows <= kRowGroups))
+        ++log2;
+    ps.slice_log2 = log2;
+    ps.slice_chunks = (ps.chunks + (1 << log2) - 1) >> log2;
+    ps.local_rows = group < rows ? (rows - group + stride - 1) / stride : 0;
+    ps.rows_per_pass = kRowGroups >> log2;
+    ps.passes = (ps.local_rows + ps.rows_per_pass - 1) / ps.rows_per_pass;
+    return ps;
 }
 
-// Loads chunks [first, last) of `row`, lane l taking first + l + 32 i.
-template <int WT>
-__device__ __forceinline__ void load_run(RowLoad& r, const void* weight, int row, int inner, int first, int last)
+// This row group's (row, first chunk, end chunk) in `pass`; false when it has
+// no task (then the dummy row 0, chunks [0, 0)).
+__device__ __forceinline__ bool phase_task(const PhaseShape& ps, int group, int stride, int pass, int& row,
+                                           int& first, int& last)
+{
+    const int task = pass * kRowGroups + (int) (threadIdx.x / kRowLanes);
+    if (task >= (ps.local_rows << ps.slice_log2))
+    {
+        row = 0;
+        first = 0;
+        last = 0;
+        return false;
+    }
+    row = group + stride * (task >> ps.slice_log2);
+    first = (task & ((1 << ps.slice_log2) - 1)) * ps.slice_chunks;
+    last = min(first + ps.slice_chunks, ps.chunks);
+    return true;
+}
+
+// Loads chunks [first, last) of `row` (lane l taking first + l + 32 i); lanes
+// past `last` load the run's first chunk again.
+__device__ __forceinline__ void load_run(RowLoad& r, const void* weight, int row, int row_bytes, int first, int last)
 {
     const int lane = threadIdx.x & (kRowLanes - 1);
-    const char* base = static_cast<const char*>(weight) + (size_t) row * inner * Storage<WT>::kBytes;
+    const char* base = static_cast<const char*>(weight) + (size_t) row * row_bytes;
 #pragma unroll
     for (int i = 0; i < kChunks; ++i)
     {
         const int c = first + lane + kRowLanes * i;
-        if (c < last)
-            r.w[i] = *reinterpret_cast<const uint4*>(base + (size_t) c * 16);
+        r.w[i] = *reinterpret_cast<const uint4*>(base + (size_t) (c < last ? c : first) * 16);
     }
 }
 
@@ -345,9 +435,8 @@ __device__ __forceinline__ float chunk_dot(const uint4& u, const float* x)
 }
 
 template <int WT>
-__device__ __forceinline__ float run_dot(const RowLoad& r, const float* x, int first, int last)
+__device__ __forceinline__ float run_dot(const RowLoad& r, const float* x, int first, int last, int lane)
 {
-    const int lane = threadIdx.x & (kRowLanes - 1);
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < kChunks; ++i)
@@ -359,80 +448,74 @@ __device__ __forceinline__ float run_dot(const RowLoad& r, const float* x, int f
     return acc;
 }
 
-// The (row, slice) task of this row group in `pass`, or false when it has none.
-__device__ __forceinline__ bool phase_task(const Phase& ph, int group, int stride, int pass, int& row, int& first,
-                                           int& last)
-{
-    const int local_rows = group < ph.rows ? (ph.rows - group + stride - 1) / stride : 0;
-    const int task = pass * kRowGroups + (int) (threadIdx.x / kRowLanes);
-    if (task >= local_rows * ph.slices)
-        return false;
-    row = group + stride * (task / ph.slices);
-    first = (task % ph.slices) * ph.slice_chunks;
-    last = first + ph.slice_chunks;
-    return true;
-}
-
-template <int WT>
 struct Prefetch
 {
     RowLoad r;
     float bias; // the bias of the row this thread finishes in pass 0
 };
 
-template <int WT>
-__device__ __forceinline__ void prefetch_phase(Prefetch<WT>& p, const Phase& ph, int group, int stride)
+// Issues this row group's pass-0 weights and, for the finishing threads, the
+// bias of their pass-0 row.
+__device__ __forceinline__ void prefetch(Prefetch& p, const void* weight, const float* bias, const PhaseShape& ps,
+                                         int group, int stride)
 {
     int row, first, last;
-    const int chunks = ph.inner / Storage<WT>::kPerChunk;
-    if (phase_task(ph, group, stride, 0, row, first, last))
-        load_run<WT>(p.r, ph.weight, row, ph.inner, first, min(last, chunks));
-    const int finisher_row = group + stride * (int) threadIdx.x;
-    p.bias = 0.f;
-    if (ph.bias != nullptr && (int) threadIdx.x < kRowGroups / ph.slices && finisher_row < ph.rows)
-        p.bias = ph.bias[finisher_row];
+    phase_task(ps, group, stride, 0, row, first, last);
+    load_run(p.r, weight, row, ps.row_bytes, first, last);
+    const int finisher_row = min(group + stride * (int) threadIdx.x, ps.rows - 1);
+    p.bias = bias != nullptr ? bias[finisher_row] : 0.f;
+}
+
+// Sums a pass's partials, then the finishing threads add the slices of their
+// row in order, the bias, and hand the value to epi; two barriers bracket the
+// shared partial slots.
+template <class Epilogue, class Bias>
+__device__ __forceinline__ void finish_pass(float acc, bool has_task, int pass, const PhaseShape& ps, int group,
+                                            int stride, Shared& sh, Epilogue& epi, Bias bias_of)
+{
+    acc = sum32(acc);
+    if (has_task && (threadIdx.x & (kRowLanes - 1)) == 0)
+        sh.part[threadIdx.x / kRowLanes] = acc;
+    __syncthreads();
+    const int local = pass * ps.rows_per_pass + (int) threadIdx.x;
+    if ((int) threadIdx.x < ps.rows_per_pass && local < ps.local_rows)
+    {
+        const int slices = 1 << ps.slice_log2;
+        float v = 0.f;
+        for (int s = 0; s < slices; ++s)
+            v += sh.part[threadIdx.x * slices + s];
+        const int r = group + stride * local;
+        epi(r, v + bias_of(r));
+    }
+    __syncthreads();
 }
 
 // Runs every task of the phase against sh.x. epi(row, value) receives the dot
-// product plus bias, on thread (local row) % (16 / slices).
-template <int WT, class Epilogue>
-__device__ __forceinline__ void run_phase(const Prefetch<WT>& p, const Phase& ph, int group, int stride, Shared& sh,
-                                          Epilogue epi)
+// product plus bias, on thread (local row) % rows_per_pass. `then` runs once
+// the pass-0 dot products have consumed their registers — the place to issue
+// the next phase's loads. Pass 0 is straight-line code (its weights and bias
+// were loaded a phase earlier), so none of its waits covers those new loads;
+// further passes, which only long rows or narrow grids need, load on the spot.
+template <int WT, class Epilogue, class Then>
+__device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight, const float* bias,
+                                          const PhaseShape& ps, int group, int stride, Shared& sh, Epilogue epi,
+                                          Then then)
 {
-    const int chunks = ph.inner / Storage<WT>::kPerChunk;
-    const int local_rows = group < ph.rows ? (ph.rows - group + stride - 1) / stride : 0;
-    const int rows_per_pass = kRowGroups / ph.slices;
-    const int passes = (local_rows + rows_per_pass - 1) / rows_per_pass;
-    for (int pass = 0; pass < passes; ++pass)
+    const int lane = threadIdx.x & (kRowLanes - 1);
+    int row, first, last;
+    const bool has_task = phase_task(ps, group, stride, 0, row, first, last);
+    const float acc = run_dot<WT>(p.r, sh.x, first, last, lane);
+    const float bias0 = p.bias;
+    then();
+    if (ps.passes > 0)
+        finish_pass(acc, has_task, 0, ps, group, stride, sh, epi, [&](int) { return bias0; });
+    for (int pass = 1; pass < ps.passes; ++pass)
     {
-        int row, first, last;
-        if (phase_task(ph, group, stride, pass, row, first, last))
-        {
-            float acc;
-            if (pass == 0)
-                acc = run_dot<WT>(p.r, sh.x, first, min(last, chunks));
-            else
-            {
-                RowLoad r;
-                load_run<WT>(r, ph.weight, row, ph.inner, first, min(last, chunks));
-                acc = run_dot<WT>(r, sh.x, first, min(last, chunks));
-            }
-            acc = row_sum(acc);
-            if ((threadIdx.x & (kRowLanes - 1)) == 0)
-                sh.part[threadIdx.x / kRowLanes] = acc;
-        }
-        __syncthreads();
-        const int local = pass * rows_per_pass + (int) threadIdx.x;
-        if ((int) threadIdx.x < rows_per_pass && local < local_rows)
-        {
-            float v = 0.f;
-            for (int s2 = 0; s2 < ph.slices; ++s2)
-                v += sh.part[threadIdx.x * ph.slices + s2];
-            const int r = group + stride * local;
-            const float b = pass == 0 ? p.bias : (ph.bias != nullptr ? ph.bias[r] : 0.f);
-            epi(r, v + b);
-        }
-        __syncthreads();
+        const bool task = phase_task(ps, group, stride, pass, row, first, last);
+        RowLoad r;
+        load_run(r, weight, row, ps.row_bytes, first, last);
+        finish_pass(run_dot<WT>(r, sh.x, first, last, lane), task, pass, ps, group, stride, sh, epi,
+                    [&](int rr) { return bias != nullptr ? bias[rr] : 0.f; });
     }
 }
 
@@ -449,49 +532,45 @@ struct KeyRows
     float4v v[NP];
 };
 
+// Keys [first, first + count) of one head; slots past count re-read key `first`.
 template <int NP>
 __device__ __forceinline__ void load_keys(KeyRows<NP>& kr, const float* keys, const float* values, int first,
                                           int count, int width, int column, int head_width)
 {
     const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
+    const int channel = 4 * kl < head_width ? 4 * kl : 0;
 #pragma unroll
     for (int p = 0; p < NP; ++p)
     {
         const int key = ks + kKeySlots * p;
-        if (key < count && 4 * kl < head_width)
-        {
-            const size_t at = (size_t) (first + key) * width + column + 4 * kl;
-            kr.k[p] = *reinterpret_cast<const float4v*>(keys + at);
-            kr.v[p] = *reinterpret_cast<const float4v*>(values + at);
-        }
+        const size_t at = (size_t) (first + (key < count ? key : 0)) * width + column + channel;
+        kr.k[p] = *reinterpret_cast<const float4v*>(keys + at);
+        kr.v[p] = *reinterpret_cast<const float4v*>(values + at);
     }
 }
 
 // Writes (max, sum, row[head_width]) of `count` keys into out (exchange words).
 template <int NP>
 __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int head_width, float scale, uint64_t* out,
-                       uint32_t epoch, Shared& sh)
+                                       uint32_t epoch, Shared& sh)
 {
     const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
+    const bool live = 4 * kl < head_width;
     float4v qv = {0.f, 0.f, 0.f, 0.f};
-    if (4 * kl < head_width)
+    if (live)
         qv = *reinterpret_cast<const float4v*>(sh.q + 4 * kl);
     float s[NP];
     float local_max = -INFINITY;
 #pragma unroll
     for (int p = 0; p < NP; ++p)
     {
-        float part = 0.f;
-        if (4 * kl < head_width)
-            part = qv[0] * kr.k[p][0] + qv[1] * kr.k[p][1] + qv[2] * kr.k[p][2] + qv[3] * kr.k[p][3];
-#pragma unroll
-        for (int offset = kKeyLanes / 2; offset > 0; offset >>= 1)
-            part += __shfl_xor(part, offset, kKeyLanes);
-        s[p] = scale * part;
+        const float part =
+            live ? qv[0] * kr.k[p][0] + qv[1] * kr.k[p][1] + qv[2] * kr.k[p][2] + qv[3] * kr.k[p][3] : 0.f;
+        s[p] = scale * sum16(part);
         if (ks + kKeySlots * p < count)
             local_max = fmaxf(local_max, s[p]);
     }
-    const float m = group_max(local_max, sh);
+    const float m = group_max(local_max, sh, 0);
     float local_sum = 0.f;
     float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -508,15 +587,23 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
             acc[3] += e * kr.v[p][3];
         }
     }
-    const float l = group_sum(local_sum, sh);
-    if (4 * kl < head_width)
-        *reinterpret_cast<float4v*>(&sh.red[ks][4 * kl]) = acc;
-    __syncthreads();
+    // Fold the wave's four key slots (lanes 16 apart): slot pairs by swizzle,
+    // then the two halves of the wave; lanes 0-15 then hold the wave's row.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        acc[i] += swap16(acc[i]);
+        acc[i] += __shfl_xor(acc[i], 32, kWave);
+    }
+    if ((threadIdx.x & (kWave - 1)) < kKeyLanes && live)
+        *reinterpret_cast<float4v*>(&sh.red[threadIdx.x / kWave][4 * kl]) = acc;
+    const float l = group_sum(local_sum, sh, 1); // its barrier also completes sh.red
     if ((int) threadIdx.x < head_width)
     {
         float row = 0.f;
-        for (int slot = 0; slot < kKeySlots; ++slot)
-            row += sh.red[slot][threadIdx.x];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+            row += sh.red[w][threadIdx.x];
         put(out + 2 + threadIdx.x, row, epoch);
     }
     if (threadIdx.x == 0)
@@ -527,8 +614,8 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
     __syncthreads();
 }
 
-// Combines `parts` partials (stride head_width + 2, as written by attend)
-// into the normalised row: rescale each by exp(m_i - max) and divide
+// Combines `parts` partials (stride apart, as written by attend) into the
+// normalised row: rescale each by exp(m_i - max) and divide
 // (Kernels/SingleQueryAttention.h:312-373). Empty partials (sum 0) are skipped.
 __device__ __forceinline__ float combine(const float* part, int parts, int stride, int c)
 {
@@ -558,19 +645,147 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
 }
 
 // ---------------------------------------------------------------------------
+// Tied logits. Rows of `lanes` lanes (32 when a row fits 96 chunks, else 64);
+// row group g of workgroup w owns rows w + G * (g + groups * j). A ring of
+// kRing rows per row group is in flight: finishing row j issues row j + kRing.
+// The mask value rides along with each row. Rows past the vocabulary load
+// chunk 0 of row 0.
+// ---------------------------------------------------------------------------
+struct Ring
+{
+    RowLoad r[kRing];
+    float mask[kRing];
+};
+
+struct LogitShape
+{
+    int lanes_log2;
+    int groups;    // row groups per workgroup
+    int chunks;    // chunks per row
+    int row_bytes;
+};
+
+__device__ __forceinline__ LogitShape logit_shape(const StepArgs& a)
+{
+    LogitShape s;
+    const int bytes = a.logits_wdtype == kF32 ? 4 : 2;
+    s.row_bytes = a.width * bytes;
+    s.chunks = s.row_bytes / 16;
+    s.lanes_log2 = s.chunks <= kRowLanes * kChunks ? 5 : 6;
+    s.groups = kThreads >> s.lanes_log2;
+    return s;
+}
+
+__device__ __forceinline__ int logit_row(const LogitShape& s, int j)
+{
+    return blockIdx.x + gridDim.x * ((int) (threadIdx.x >> s.lanes_log2) + s.groups * j);
+}
+
+__device__ __forceinline__ void load_logit_row(RowLoad& r, float& mask, const StepArgs& a, const LogitShape& s, int j)
+{
+    const int row = logit_row(s, j);
+    const bool valid = row < a.vocabulary;
+    const int lane = threadIdx.x & ((1 << s.lanes_log2) - 1);
+    const char* base = static_cast<const char*>(a.logits_weight) + (size_t) (valid ? row : 0) * s.row_bytes;
+    const int last = valid ? s.chunks : 1;
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i)
+    {
+        const int c = lane + (i << s.lanes_log2);
+        r.w[i] = *reinterpret_cast<const uint4*>(base + (size_t) (c < last ? c : 0) * 16);
+    }
+    mask = a.mask != nullptr ? a.mask[valid ? row : 0] : 0.f;
+}
+
+__device__ __forceinline__ void issue_ring(Ring& ring, const StepArgs& a, const LogitShape& s)
+{
+#pragma unroll
+    for (int k = 0; k < kRing; ++k)
+        load_logit_row(ring.r[k], ring.mask[k], a, s, k);
+}
+
+template <int LWT>
+__device__ __forceinline__ float logit_dot(const RowLoad& r, const StepArgs& a, const LogitShape& s, int row,
+                                           const float* x)
+{
+    const int lanes = 1 << s.lanes_log2;
+    const int lane = threadIdx.x & (lanes - 1);
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i)
+    {
+        const int c = lane + i * lanes;
+        if (c < s.chunks)
+            acc += chunk_dot<LWT>(r.w[i], x + c * Storage<LWT>::kPerChunk);
+    }
+    // Rows longer than the ring's share load the rest here.
+    for (int c = lane + kChunks * lanes; c < s.chunks; c += lanes)
+        acc += chunk_dot<LWT>(*reinterpret_cast<const uint4*>(static_cast<const char*>(a.logits_weight)
+                                                              + (size_t) row * s.row_bytes + (size_t) c * 16),
+                              x + c * Storage<LWT>::kPerChunk);
+    return s.lanes_log2 == 5 ? sum32(acc) : sum64(acc);
+}
+
+template <int LWT>
+__device__ __forceinline__ void logits_loop(Ring& ring, const StepArgs& a, const LogitShape& s, const Shared& sh,
+                                            float& best_v, uint32_t& best_i)
+{
+    const int lane = threadIdx.x & ((1 << s.lanes_log2) - 1);
+    for (int j = 0;; j += kRing)
+    {
+#pragma unroll
+        for (int k = 0; k < kRing; ++k)
+        {
+            const int row = logit_row(s, j + k);
+            if (row >= a.vocabulary)
+                return;
+            const float v = logit_dot<LWT>(ring.r[k], a, s, row, sh.x);
+            const float m = ring.mask[k];
+            load_logit_row(ring.r[k], ring.mask[k], a, s, j + k + kRing);
+            if (lane == 0)
+            {
+                a.logits[row] = v;
+                if (m == 0.f && (best_i == kUnchosen || v > best_v))
+                {
+                    best_v = v;
+                    best_i = (uint32_t) row;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // The persistent step.
 // ---------------------------------------------------------------------------
 template <int WT>
-__device__ __forceinline__ void row_group_layers(const StepArgs& a, Shared& sh)
+__device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
 {
     const int d = a.width, f = a.feed_forward, H = a.heads, hd = d / H;
     const int group = blockIdx.x, stride = a.row_groups;
     const int pos = a.position;
     const uint32_t epoch = a.epoch;
+    const PhaseShape qkv_shape = phase_shape<WT>(3 * d, d, group, stride);
+    const PhaseShape square_shape = phase_shape<WT>(d, d, group, stride);
+    const PhaseShape fc1_shape = phase_shape<WT>(f, d, group, stride);
+    const PhaseShape fc2_shape = phase_shape<WT>(d, f, group, stride);
+    // One cross-attention chunk per row group when the split allows it; more
+    // tasks than row groups wrap around (and are not prefetched).
+    const int tasks = a.cross_splits * H;
+    const int task = group;
+    const int task_first = (task / H) * a.cross_chunk;
+    const int task_count = task < tasks ? min(a.cross_chunk, a.cross_rows - task_first) : 0;
+
+    Prefetch pa, pb;
+    NormParams norm;
+    KeyRows<kCrossPasses> cross;
 
     // The layer-0 input: the token and position rows (Kernels/Embed.h:9-14);
     // an id past the vocabulary poisons the row with NaN.
     {
+        const wsp_layer_tensors& L0 = sh.table[0];
+        prefetch(pa, L0.self_qkv_w, L0.self_qkv_b, qkv_shape, group, stride);
+        load_norm(norm, L0.self_norm_w, L0.self_norm_b, d);
         const uint32_t token = a.tokens[0];
         for (int c = threadIdx.x; c < d; c += kThreads)
             sh.raw[c] = token < (uint32_t) a.vocabulary
@@ -579,143 +794,154 @@ __device__ __forceinline__ void row_group_layers(const StepArgs& a, Shared& sh)
         __syncthreads();
     }
 
-    // One cross-attention chunk per row group when the split allows it; more
-    // tasks than row groups wrap around (and are not prefetched).
-    const int tasks = a.cross_splits * H;
-    const int task = group;
-
     for (int l = 0; l < a.layer_count; ++l)
     {
-        const wsp_layer_tensors& L = a.layers[l];
+        const wsp_layer_tensors& L = sh.table[l];
         uint64_t* ex = a.exchange + (size_t) l * a.layer_words;
-        NormParams norm;
-        Prefetch<WT> pre;
 
-        // ---- LN1 + fused q/k/v ---------------------------------------------
+        // ---- LN1 + fused q/k/v (weights in pa) ---------------------------------
+        if (l > 0
+            && !gather<kPollWidth>(a.exchange + (size_t) (l - 1) * a.layer_words + a.off_h4, d, sh.raw, epoch,
+                                   a.status, sh))
+            return false;
+        layer_norm(norm, d, a.eps, sh);
         {
-            const Phase ph = make_phase<WT>(L.self_qkv_w, L.self_qkv_b, 3 * d, d, stride);
-            prefetch_phase<WT>(pre, ph, group, stride);
-            load_norm(norm, L.self_norm_w, L.self_norm_b, d);
-            if (l > 0
-                && !gather<kPollWidth>(a.exchange + (size_t) (l - 1) * a.layer_words + a.off_h4, d, sh.raw, epoch,
-                                       a.status, sh))
-                return;
-            layer_norm(norm, d, a.eps, sh);
             uint64_t* qkv = ex + a.off_qkv;
             float* krow = L.self_keys + (size_t) pos * d;
             float* vrow = L.self_values + (size_t) pos * d;
-            run_phase<WT>(pre, ph, group, stride, sh, [&](int r, float v) {
-                put(qkv + r, v, epoch);
-                if (r >= 2 * d)
-                    vrow[r - 2 * d] = v;
-                else if (r >= d)
-                    krow[r - d] = v;
-            });
+            run_phase<WT>(
+                pa, L.self_qkv_w, L.self_qkv_b, qkv_shape, group, stride, sh,
+                [&](int r, float v) {
+                    put(qkv + r, v, epoch);
+                    if (r >= 2 * d)
+                        vrow[r - 2 * d] = v;
+                    else if (r >= d)
+                        krow[r - d] = v;
+                },
+                [&] { prefetch(pb, L.self_out_w, L.self_out_b, square_shape, group, stride); });
         }
 
-        // ---- self-attention combine + out-proj + residual --------------------
+        // ---- self-attention combine + out-proj + residual (weights in pb) ------
+        if (!gather<kPollCombine>(ex + a.off_self, a.self_splits * H * (hd + 2), sh.comb, epoch, a.status, sh))
+            return false;
+        for (int c = threadIdx.x; c < d; c += kThreads)
+            sh.x[c] = combine(sh.comb + (c / hd) * (hd + 2), a.self_splits, H * (hd + 2), c % hd);
+        __syncthreads();
         {
-            const Phase ph = make_phase<WT>(L.self_out_w, L.self_out_b, d, d, stride);
-            prefetch_phase<WT>(pre, ph, group, stride);
-            const int parts = a.self_splits * H * (hd + 2);
-            if (!gather<kPollCombine>(ex + a.off_self, parts, sh.comb, epoch, a.status, sh))
-                return;
-            for (int c = threadIdx.x; c < d; c += kThreads)
-                sh.x[c] = combine(sh.comb + (c / hd) * (hd + 2), a.self_splits, H * (hd + 2), c % hd);
-            __syncthreads();
             uint64_t* out = ex + a.off_h2;
-            run_phase<WT>(pre, ph, group, stride, sh, [&](int r, float v) { put(out + r, sh.raw[r] + v, epoch); });
+            run_phase<WT>(
+                pb, L.self_out_w, L.self_out_b, square_shape, group, stride, sh,
+                [&](int r, float v) { put(out + r, sh.raw[r] + v, epoch); },
+                [&] {
+                    prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
+                    load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
+                });
         }
 
-        // ---- LN2 + cross q ---------------------------------------------------
-        KeyRows<kCrossPasses> cross;
+        // ---- LN2 + cross q (weights in pa) ----------------------------------------
+        if (!gather<kPollWidth>(ex + a.off_h2, d, sh.raw, epoch, a.status, sh))
+            return false;
+        layer_norm(norm, d, a.eps, sh);
         {
-            const Phase ph = make_phase<WT>(L.cross_q_w, L.cross_q_b, d, d, stride);
-            prefetch_phase<WT>(pre, ph, group, stride);
-            load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
-            if (!gather<kPollWidth>(ex + a.off_h2, d, sh.raw, epoch, a.status, sh))
-                return;
-            if (task < tasks)
-            {
-                // Issued now, awaited only when the query arrives.
-                const int first = (task / H) * a.cross_chunk;
-                load_keys<kCrossPasses>(cross, L.cross_keys, L.cross_values, first,
-                                        min(a.cross_chunk, a.cross_rows - first), d, (task % H) * hd, hd);
-            }
-            layer_norm(norm, d, a.eps, sh);
             uint64_t* out = ex + a.off_xq;
-            run_phase<WT>(pre, ph, group, stride, sh, [&](int r, float v) { put(out + r, v, epoch); });
+            run_phase<WT>(
+                pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride, sh,
+                [&](int r, float v) { put(out + r, v, epoch); },
+                [&] {
+                    prefetch(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride);
+                    if (task_count > 0) // awaited only when the query arrives
+                        load_keys<kCrossPasses>(cross, L.cross_keys, L.cross_values, task_first, task_count, d,
+                                                (task % H) * hd, hd);
+                });
         }
 
-        // ---- cross-attention partials, then out-proj + residual ---------------
+        // ---- cross-attention partials over this group's key chunk(s) ---------------
+        for (int t = task; t < tasks; t += stride)
         {
-            const Phase ph = make_phase<WT>(L.cross_out_w, L.cross_out_b, d, d, stride);
-            prefetch_phase<WT>(pre, ph, group, stride);
-            for (int t = task; t < tasks; t += stride)
-            {
-                const int h = t % H, s = t / H;
-                const int first = s * a.cross_chunk;
-                const int count = min(a.cross_chunk, a.cross_rows - first);
-                if (t != task)
-                    load_keys<kCrossPasses>(cross, L.cross_keys, L.cross_values, first, count, d, h * hd, hd);
-                if (!gather<1>(ex + a.off_xq + h * hd, hd, sh.q, epoch, a.status, sh))
-                    return;
-                attend<kCrossPasses>(cross, count, hd, a.scale,
-                                     ex + a.off_xpart + (size_t) (h * a.cross_splits + s) * (hd + 2), epoch, sh);
-            }
-            if (!gather<kPollWidth>(ex + a.off_xattn, d, sh.x, epoch, a.status, sh))
-                return;
+            const int h = t % H, s = t / H;
+            const int first = s * a.cross_chunk;
+            const int count = min(a.cross_chunk, a.cross_rows - first);
+            if (t != task)
+                load_keys<kCrossPasses>(cross, L.cross_keys, L.cross_values, first, count, d, h * hd, hd);
+            if (!gather<1>(ex + a.off_xq + h * hd, hd, sh.q, epoch, a.status, sh))
+                return false;
+            attend<kCrossPasses>(cross, count, hd, a.scale,
+                                 ex + a.off_xpart + (size_t) (h * a.cross_splits + s) * (hd + 2), epoch, sh);
+        }
+
+        // ---- cross out-proj + residual (weights in pb) --------------------------------
+        if (!gather<kPollWidth>(ex + a.off_xattn, d, sh.x, epoch, a.status, sh))
+            return false;
+        {
             uint64_t* out = ex + a.off_h3;
-            run_phase<WT>(pre, ph, group, stride, sh, [&](int r, float v) { put(out + r, sh.raw[r] + v, epoch); });
+            run_phase<WT>(
+                pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride, sh,
+                [&](int r, float v) { put(out + r, sh.raw[r] + v, epoch); },
+                [&] {
+                    prefetch(pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride);
+                    load_norm(norm, L.final_norm_w, L.final_norm_b, d);
+                });
         }
 
-        // ---- LN3 + fc1 + GELU ---------------------------------------------------
+        // ---- LN3 + fc1 + GELU (weights in pa) ------------------------------------------
+        if (!gather<kPollWidth>(ex + a.off_h3, d, sh.raw, epoch, a.status, sh))
+            return false;
+        layer_norm(norm, d, a.eps, sh);
         {
-            const Phase ph = make_phase<WT>(L.fc1_w, L.fc1_b, f, d, stride);
-            prefetch_phase<WT>(pre, ph, group, stride);
-            load_norm(norm, L.final_norm_w, L.final_norm_b, d);
-            if (!gather<kPollWidth>(ex + a.off_h3, d, sh.raw, epoch, a.status, sh))
-                return;
-            layer_norm(norm, d, a.eps, sh);
             uint64_t* out = ex + a.off_ff;
-            run_phase<WT>(pre, ph, group, stride, sh, [&](int r, float v) { put(out + r, exact_gelu(v), epoch); });
+            run_phase<WT>(
+                pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride, sh,
+                [&](int r, float v) { put(out + r, exact_gelu(v), epoch); },
+                [&] { prefetch(pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride); });
         }
 
-        // ---- fc2 + residual ---------------------------------------------------------
+        // ---- fc2 + residual (weights in pb) ------------------------------------------------
+        if (!gather<kPollFeedForward>(ex + a.off_ff, f, sh.x, epoch, a.status, sh))
+            return false;
         {
-            const Phase ph = make_phase<WT>(L.fc2_w, L.fc2_b, d, f, stride);
-            prefetch_phase<WT>(pre, ph, group, stride);
-            if (!gather<kPollFeedForward>(ex + a.off_ff, f, sh.x, epoch, a.status, sh))
-                return;
             uint64_t* out = ex + a.off_h4;
-            run_phase<WT>(pre, ph, group, stride, sh, [&](int r, float v) { put(out + r, sh.raw[r] + v, epoch); });
+            const bool more = l + 1 < a.layer_count;
+            const wsp_layer_tensors& next = sh.table[more ? l + 1 : l];
+            run_phase<WT>(
+                pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride, sh,
+                [&](int r, float v) { put(out + r, sh.raw[r] + v, epoch); },
+                [&] {
+                    if (more)
+                    {
+                        prefetch(pa, next.self_qkv_w, next.self_qkv_b, qkv_shape, group, stride);
+                        load_norm(norm, next.self_norm_w, next.self_norm_b, d);
+                    }
+                });
         }
     }
+    return true;
 }
 
-__device__ __forceinline__ void head_group_layers(const StepArgs& a, Shared& sh)
+__device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
 {
     const int d = a.width, H = a.heads, hd = d / H;
     const int index = blockIdx.x - a.row_groups;
     const int head = index % H, split = index / H;
     const int n = a.position + 1; // keys attended, the new one included
     const int first = split * kSelfKeys;
-    const int count = min(kSelfKeys, n - first); // <= 0 for an idle split
+    const int count = min(kSelfKeys, n - first);               // <= 0 for an idle split
     const int cached = max(0, min(count, a.position - first)); // keys read from the cache
+    const bool attends = split < a.self_splits;
     const uint32_t epoch = a.epoch;
 
     KeyRows<kSelfPasses> self;
-    if (split < a.self_splits && cached > 0)
-        load_keys<kSelfPasses>(self, a.layers[0].self_keys, a.layers[0].self_values, first, cached, d, head * hd, hd);
+    if (attends && cached > 0)
+        load_keys<kSelfPasses>(self, sh.table[0].self_keys, sh.table[0].self_values, first, cached, d, head * hd, hd);
 
     for (int l = 0; l < a.layer_count; ++l)
     {
         uint64_t* ex = a.exchange + (size_t) l * a.layer_words;
-        if (split < a.self_splits)
+        const bool last_layer = l + 1 == a.layer_count;
+        if (attends)
         {
             // q, and the new key/value rows, of this head, in one wait.
             if (!gather<1, true>(ex + a.off_qkv + head * hd, 3 * hd, sh.q, epoch, a.status, sh, hd, d))
-                return;
+                return false;
             if (count > cached)
             {
                 // The new key sits at local index `cached` (= position - first).
@@ -730,103 +956,33 @@ __device__ __forceinline__ void head_group_layers(const StepArgs& a, Shared& sh)
             }
             attend<kSelfPasses>(self, count, hd, a.scale, ex + a.off_self + (size_t) (split * H + head) * (hd + 2),
                                 epoch, sh);
-            if (l + 1 < a.layer_count && cached > 0)
-                load_keys<kSelfPasses>(self, a.layers[l + 1].self_keys, a.layers[l + 1].self_values, first, cached,
-                                       d, head * hd, hd);
         }
-        // Cross-attention combine of one head.
+        // Cross-attention combine of one head; the next layer's keys are
+        // loaded after it, so they never hold up its wait.
         if (index < H)
         {
             const int parts = a.cross_splits;
             if (!gather<kPollCombine>(ex + a.off_xpart + (size_t) head * parts * (hd + 2), parts * (hd + 2), sh.comb,
                                       epoch, a.status, sh))
-                return;
+                return false;
             if ((int) threadIdx.x < hd)
                 put(ex + a.off_xattn + head * hd + threadIdx.x, combine(sh.comb, parts, hd + 2, threadIdx.x), epoch);
-            __syncthreads();
         }
+        if (!last_layer && attends && cached > 0)
+            load_keys<kSelfPasses>(self, sh.table[l + 1].self_keys, sh.table[l + 1].self_values, first, cached, d,
+                                   head * hd, hd);
+        __syncthreads();
     }
-}
-
-// Logits rows: row group g of workgroup w owns rows w + G * (g + 16 j); each
-// batch keeps kLogitRows rows in flight per row group (two batches
-// alternate), the mask value riding along with each row.
-constexpr int kLogitRows = 2;
-
-struct LogitBatch
-{
-    RowLoad r[kLogitRows];
-    float mask[kLogitRows];
-};
-
-__device__ __forceinline__ int logit_row(int j)
-{
-    return blockIdx.x + gridDim.x * ((int) (threadIdx.x / kRowLanes) + kRowGroups * j);
-}
-
-template <int LWT>
-__device__ __forceinline__ void load_logits(LogitBatch& b, const StepArgs& a, int j0)
-{
-    const int chunks = a.width / Storage<LWT>::kPerChunk;
-#pragma unroll
-    for (int k = 0; k < kLogitRows; ++k)
-    {
-        const int row = logit_row(j0 + k);
-        if (row < a.vocabulary)
-        {
-            load_run<LWT>(b.r[k], a.logits_weight, row, a.width, 0, min(chunks, kRowLanes * kChunks));
-            b.mask[k] = a.mask != nullptr ? a.mask[row] : 0.f;
-        }
-    }
-}
-
-// Finishes one batch: dot products (chunks past the first run load on the
-// spot), logits stores and this row group's running top-1. A row group's rows
-// ascend, so a strict ">" keeps the lowest index of a tie.
-template <int LWT>
-__device__ __forceinline__ void finish_logits(const LogitBatch& b, const StepArgs& a, int j0, const Shared& sh,
-                                              float& best_v, uint32_t& best_i)
-{
-    const int d = a.width, V = a.vocabulary;
-    const int chunks = d / Storage<LWT>::kPerChunk;
-    const int run = kRowLanes * kChunks;
-#pragma unroll
-    for (int k = 0; k < kLogitRows; ++k)
-    {
-        const int row = logit_row(j0 + k);
-        if (row >= V)
-            break;
-        float acc = run_dot<LWT>(b.r[k], sh.x, 0, min(chunks, run));
-        for (int c0 = run; c0 < chunks; c0 += run)
-        {
-            RowLoad t;
-            load_run<LWT>(t, a.logits_weight, row, d, c0, min(chunks, c0 + run));
-            acc += run_dot<LWT>(t, sh.x, c0, min(chunks, c0 + run));
-        }
-        acc = row_sum(acc);
-        if ((threadIdx.x & (kRowLanes - 1)) == 0)
-        {
-            a.logits[row] = acc;
-            if (b.mask[k] == 0.f && (best_i == kUnchosen || acc > best_v))
-            {
-                best_v = acc;
-                best_i = (uint32_t) row;
-            }
-        }
-    }
+    return true;
 }
 
 // Final LN of the last layer's output, the tied logits (Decoder/Decoder.cpp
-// :174-176) and this workgroup's top-1 under the mask. The first batch of
-// logits rows is in flight before the last layer's output is awaited.
+// :174-176) and this workgroup's top-1 under the mask.
 template <int LWT>
-__device__ __forceinline__ bool final_phase(const StepArgs& a, Shared& sh, float& best_v, uint32_t& best_i)
+__device__ __forceinline__ bool final_phase(const StepArgs& a, Shared& sh, Ring& ring, const NormParams& norm,
+                                            float& best_v, uint32_t& best_i)
 {
     const int d = a.width;
-    NormParams norm;
-    load_norm(norm, a.final_norm_w, a.final_norm_b, d);
-    LogitBatch b0, b1;
-    load_logits<LWT>(b0, a, 0);
     if (!gather<kPollWidth>(a.exchange + (size_t) (a.layer_count - 1) * a.layer_words + a.off_h4, d, sh.raw, a.epoch,
                             a.status, sh))
         return false;
@@ -834,17 +990,7 @@ __device__ __forceinline__ bool final_phase(const StepArgs& a, Shared& sh, float
     if (blockIdx.x == 0)
         for (int c = threadIdx.x; c < d; c += kThreads)
             a.hidden[c] = sh.x[c];
-    for (int j0 = 0;; j0 += 2 * kLogitRows)
-    {
-        if (logit_row(j0) >= a.vocabulary)
-            break;
-        load_logits<LWT>(b1, a, j0 + kLogitRows);
-        finish_logits<LWT>(b0, a, j0, sh, best_v, best_i);
-        if (logit_row(j0 + kLogitRows) >= a.vocabulary)
-            break;
-        load_logits<LWT>(b0, a, j0 + 2 * kLogitRows);
-        finish_logits<LWT>(b1, a, j0 + kLogitRows, sh, best_v, best_i);
-    }
+    logits_loop<LWT>(ring, a, logit_shape(a), sh, best_v, best_i);
     return true;
 }
 
@@ -854,31 +1000,43 @@ __global__ void __launch_bounds__(kThreads) step_kernel(StepArgs a)
     __shared__ Shared sh;
     if (threadIdx.x == 0)
         sh.abort = 0;
+    {
+        // The layer table, once.
+        const int words = a.layer_count * (int) (sizeof(wsp_layer_tensors) / sizeof(uint64_t));
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.layers);
+        uint64_t* dst = reinterpret_cast<uint64_t*>(sh.table);
+        for (int i = threadIdx.x; i < words; i += kThreads)
+            dst[i] = src[i];
+    }
     __syncthreads();
 
-    if ((int) blockIdx.x < a.row_groups)
-        row_group_layers<WT>(a, sh);
-    else
-        head_group_layers(a, sh);
-    if (sh.abort != 0)
+    const bool ok = (int) blockIdx.x < a.row_groups ? row_group_layers<WT>(a, sh) : head_group_layers(a, sh);
+    if (!ok)
         return;
+    // The first logits rows and the final norm are in flight before the last
+    // layer's output is awaited.
+    Ring ring;
+    NormParams norm;
+    issue_ring(ring, a, logit_shape(a));
+    load_norm(norm, a.final_norm_w, a.final_norm_b, a.width);
 
     // ---- final LN + tied logits with a per-workgroup top-1 -----------------------
     const int G = gridDim.x;
     const uint32_t epoch = a.epoch;
     float best_v = 0.f;
     uint32_t best_i = kUnchosen;
-    bool ok;
+    bool done;
     switch (a.logits_wdtype)
     {
-        case kF32: ok = final_phase<kF32>(a, sh, best_v, best_i); break;
-        case kF16: ok = final_phase<kF16>(a, sh, best_v, best_i); break;
-        default: ok = final_phase<kBF16>(a, sh, best_v, best_i); break;
+        case kF32: done = final_phase<kF32>(a, sh, ring, norm, best_v, best_i); break;
+        case kF16: done = final_phase<kF16>(a, sh, ring, norm, best_v, best_i); break;
+        default: done = final_phase<kBF16>(a, sh, ring, norm, best_v, best_i); break;
     }
-    if (!ok)
+    if (!done)
         return;
-    const int rg = threadIdx.x / kRowLanes;
-    if ((threadIdx.x & (kRowLanes - 1)) == 0)
+    const LogitShape ls = logit_shape(a);
+    const int rg = threadIdx.x >> ls.lanes_log2;
+    if ((threadIdx.x & ((1 << ls.lanes_log2) - 1)) == 0)
     {
         sh.best_v[rg] = best_v;
         sh.best_i[rg] = best_i;
@@ -888,7 +1046,7 @@ __global__ void __launch_bounds__(kThreads) step_kernel(StepArgs a)
     {
         float bv = 0.f;
         uint32_t bi = kUnchosen;
-        for (int k = 0; k < kRowGroups; ++k)
+        for (int k = 0; k < ls.groups; ++k)
             if (better(sh.best_v[k], sh.best_i[k], bv, bi))
             {
                 bv = sh.best_v[k];
