@@ -38,6 +38,7 @@ struct FusedState
     int layer_words = 0;
     int off_qkv = 0, off_self = 0, off_h2 = 0, off_xq = 0, off_xpart = 0, off_xattn = 0, off_h3 = 0, off_ff = 0,
         off_h4 = 0, off_argmax = 0;
+    int log2_qkv = 0, log2_d = 0, log2_f = 0;
     uint64_t* exchange = nullptr;
     size_t exchange_words = 0;
     int* status = nullptr;
@@ -96,10 +97,10 @@ void plan_persistent(Context* ctx, FusedState* st)
     const int row_groups = G - head_groups;
     if (row_groups < H)
         return refuse("too few CUs for the head groups");
-    if (self_split_max * H * (hd + 2) > step::kMaxCombine || 2 * G > step::kMaxCombine)
+    if (self_split_max * H * (hd + 2) > step::kMaxCombine || 2 * G > step::kMaxCombine || G > 256)
         return refuse("attention partials past the combine capacity");
     const int cross_needed = ceil_div(s.cross_positions, step::kCrossKeys);
-    const int cross_cap = step::kMaxCombine / (hd + 2);
+    const int cross_cap = std::min(step::kMaxCombine / (hd + 2), 64); // one wave folds the partials
     if (cross_needed > cross_cap)
         return refuse("cross positions past the persistent kernel's capacity");
     const int cross_split_max = std::min(cross_cap, std::max(cross_needed, row_groups / H));
@@ -114,23 +115,35 @@ void plan_persistent(Context* ctx, FusedState* st)
             return refuse("the persistent kernel does not fit a CU");
     }
 
+    // Producer blocks: a row group's rows of a phase, rounded up to a power of two.
+    auto block_log2 = [&](int rows) {
+        const int per = ceil_div(rows, row_groups);
+        int log2 = 0;
+        while ((1 << log2) < per)
+            ++log2;
+        return log2;
+    };
+    st->log2_qkv = block_log2(3 * d);
+    st->log2_d = block_log2(d);
+    st->log2_f = block_log2(f);
     st->workgroups = G;
     st->row_groups = row_groups;
     st->self_split_max = self_split_max;
     st->cross_split_max = cross_split_max;
     int at = 0;
-    st->off_qkv = at, at += 3 * d;
+    const int block_d = row_groups << st->log2_d;
+    st->off_qkv = at, at += row_groups << st->log2_qkv;
     st->off_self = at, at += self_split_max * H * (hd + 2);
-    st->off_h2 = at, at += d;
-    st->off_xq = at, at += d;
+    st->off_h2 = at, at += block_d;
+    st->off_xq = at, at += block_d;
     st->off_xpart = at, at += H * cross_split_max * (hd + 2);
     st->off_xattn = at, at += d;
-    st->off_h3 = at, at += d;
-    st->off_ff = at, at += f;
-    st->off_h4 = at, at += d;
+    st->off_h3 = at, at += block_d;
+    st->off_ff = at, at += row_groups << st->log2_f;
+    st->off_h4 = at, at += block_d;
     st->layer_words = at;
     st->off_argmax = at * s.layers;
-    st->exchange_words = (size_t) at * s.layers + 2 * G;
+    st->exchange_words = (size_t) at * s.layers + 16 * G;
     st->persistent = true;
 }
 
@@ -285,6 +298,9 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     a.off_h4 = st->off_h4;
     a.layer_words = st->layer_words;
     a.off_argmax = st->off_argmax;
+    a.log2_qkv = st->log2_qkv;
+    a.log2_d = st->log2_d;
+    a.log2_f = st->log2_f;
 
     void* args[] = {&a};
     const hipError_t e = hipLaunchCooperativeKernel(step::kernel_for(tensors->wdtype),

@@ -17,13 +17,17 @@ constexpr int kMaxFeedForward = 5120;  // fc1 width
 constexpr int kMaxHeadWidth = 64;
 constexpr int kMaxCombine = 4096;      // attention partial floats one workgroup combines
 constexpr int kSelfKeys = 256;         // self-attention keys one head group holds
-constexpr int kCrossKeys = 160;        // cross-attention keys one row group holds
+constexpr int kCrossKeys = 128;        // cross-attention keys one row group holds
 constexpr int kMaxLayers = 32;         // layer table entries held in LDS
 
 // Exchange words per layer, in this order (offsets in StepArgs):
-//   qkv [3d] | self partials [self_split_max][heads][hd + 2] | h2 [d] | xq [d]
-//   | cross partials [heads][cross_split_max][hd + 2] | xattn [d] | h3 [d] | ff [f] | h4 [d]
-// followed by one argmax block [2 * workgroups] after the last layer.
+//   qkv [row_groups << log2_qkv] | self partials [self_split_max][heads][hd + 2]
+//   | h2 [row_groups << log2_d] | xq [row_groups << log2_d]
+//   | cross partials [heads][cross_split_max][hd + 2] | xattn [d]
+//   | h3 [row_groups << log2_d] | ff [row_groups << log2_f] | h4 [row_groups << log2_d]
+// followed by one argmax block [16 * workgroups] after the last layer. A
+// row-group vector keeps each producing workgroup's rows in a block of its own
+// (2^log2 words: the workgroup's rows-per-phase rounded up to a power of two).
 struct StepArgs
 {
     const wsp_layer_tensors* layers; // device copy of the per-layer table
@@ -51,6 +55,7 @@ struct StepArgs
 
     int off_qkv, off_self, off_h2, off_xq, off_xpart, off_xattn, off_h3, off_ff, off_h4;
     int layer_words, off_argmax;
+    int log2_qkv, log2_d, log2_f; // producer block sizes of the row-group vectors
 };
 
 // Longest projection row, in 16-byte chunks: 16 slices of 3 chunks per lane.

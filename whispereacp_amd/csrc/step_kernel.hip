@@ -173,56 +173,70 @@ __device__ __forceinline__ float group_max(float v, Shared& sh, int slot)
     return t;
 }
 
-// Waits until the n words (n <= P * 512) at src carry `epoch` and copies their
-// floats to dst (LDS). With SEG, word i sits at
-// src[(i / segment) * segment_stride + i % segment], so a few equal runs of a
-// buffer (a head's q, k and v) are awaited together. Every poll round issues
-// all of a thread's outstanding loads at once. Returns false, uniformly over
-// the workgroup, when the watchdog tripped here or anywhere else.
-template <int P, bool SEG = false>
-__device__ __forceinline__ bool gather(const uint64_t* src, int n, float* dst, uint32_t epoch, int* status,
-                                       Shared& sh, int segment = 1, int segment_stride = 0)
+// Waits until the n words map(i) (i < n <= P * 448) of base carry `epoch`
+// and copies their floats to dst (LDS). map(i, offset, index) names word i's
+// offset from base and its index in dst, or returns false for a slot that
+// holds nothing. Waves 1-7 poll; wave 0 — the wave that stores a phase's
+// outputs — only waits for its own stores meanwhile, because on this
+// architecture a load's completion count also covers earlier stores, so a
+// poll issued behind them would see nothing until they were acknowledged.
+// Every poll round issues all of a thread's outstanding loads at once. Returns
+// false, uniformly over the workgroup, when the watchdog tripped here or
+// anywhere else.
+constexpr int kPollThreads = kThreads - kWave;
+
+template <int P, class Map>
+__device__ __forceinline__ bool poll(const uint64_t* base, int n, Map map, float* dst, uint32_t epoch, int* status,
+                                     Shared& sh)
 {
-    const uint64_t* at[P];
-    uint32_t pending = 0;
-#pragma unroll
-    for (int k = 0; k < P; ++k)
-    {
-        const int i = threadIdx.x + k * kThreads;
-        if (i < n)
-        {
-            pending |= 1u << k;
-            at[k] = SEG ? src + (i / segment) * segment_stride + i % segment : src + i;
-        }
-    }
-    int spins = 0;
     bool failed = false;
-    while (pending != 0)
+    if (threadIdx.x < kWave)
+        __builtin_amdgcn_s_waitcnt(0); // every counter at zero: this wave's stores and loads are done
+    else
     {
-        uint64_t w[P];
+        const int t = threadIdx.x - kWave;
+        uint32_t pending = 0;
 #pragma unroll
         for (int k = 0; k < P; ++k)
-            if (pending & (1u << k))
-                w[k] = peek(at[k]);
-#pragma unroll
-        for (int k = 0; k < P; ++k)
-            if ((pending & (1u << k)) && (uint32_t) (w[k] >> 32) == epoch)
-            {
-                dst[threadIdx.x + k * kThreads] = __uint_as_float((uint32_t) w[k]);
-                pending &= ~(1u << k);
-            }
-        if (pending != 0 && (++spins & 63) == 0)
         {
-            if (spins > kSpinLimit)
+            int offset, index;
+            if (t + k * kPollThreads < n && map(t + k * kPollThreads, offset, index))
+                pending |= 1u << k;
+        }
+        int spins = 0;
+        while (pending != 0)
+        {
+            uint64_t w[P];
+#pragma unroll
+            for (int k = 0; k < P; ++k)
+                if (pending & (1u << k))
+                {
+                    int offset, index;
+                    map(t + k * kPollThreads, offset, index);
+                    w[k] = peek(base + offset);
+                }
+#pragma unroll
+            for (int k = 0; k < P; ++k)
+                if ((pending & (1u << k)) && (uint32_t) (w[k] >> 32) == epoch)
+                {
+                    int offset, index;
+                    map(t + k * kPollThreads, offset, index);
+                    dst[index] = __uint_as_float((uint32_t) w[k]);
+                    pending &= ~(1u << k);
+                }
+            if (pending != 0 && (++spins & 63) == 0)
             {
-                __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                failed = true;
-                break;
-            }
-            if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
-            {
-                failed = true;
-                break;
+                if (spins > kSpinLimit)
+                {
+                    __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    failed = true;
+                    break;
+                }
+                if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
+                {
+                    failed = true;
+                    break;
+                }
             }
         }
     }
@@ -232,10 +246,53 @@ __device__ __forceinline__ bool gather(const uint64_t* src, int n, float* dst, u
     return sh.abort == 0;
 }
 
-// Words per thread for the vectors a phase awaits.
-constexpr int kPollWidth = (kMaxWidth + kThreads - 1) / kThreads;
-constexpr int kPollFeedForward = (kMaxFeedForward + kThreads - 1) / kThreads;
-constexpr int kPollCombine = (kMaxCombine + kThreads - 1) / kThreads;
+// n contiguous words.
+template <int P>
+__device__ __forceinline__ bool gather(const uint64_t* src, int n, float* dst, uint32_t epoch, int* status,
+                                       Shared& sh)
+{
+    return poll<P>(src, n, [](int i, int& offset, int& index) { offset = index = i; return true; }, dst, epoch,
+                   status, sh);
+}
+
+// Row-group outputs live in producer blocks: the workgroup that computes row
+// r (r % stride) stores it at slot (r % stride) * 2^log2_block + r / stride,
+// so each workgroup's rows share its own cache lines (no line has two
+// writers) and a reader polls the slots in order.
+__device__ __forceinline__ int block_slot(int row, int stride, int log2_block)
+{
+    return ((row % stride) << log2_block) + row / stride;
+}
+
+// The whole `rows`-row vector, read slot by slot in chunks of P * 448 slots.
+template <int P>
+__device__ __forceinline__ bool gather_blocked(const uint64_t* base, int rows, int log2_block, int stride, float* dst,
+                                               uint32_t epoch, int* status, Shared& sh)
+{
+    const int slots = stride << log2_block;
+    const int mask = (1 << log2_block) - 1;
+    for (int first = 0; first < slots; first += P * kPollThreads)
+    {
+        const bool ok = poll<P>(
+            base + first, min(P * kPollThreads, slots - first),
+            [&](int i, int& offset, int& index) {
+                const int slot = first + i;
+                offset = i;
+                index = (slot & mask) * stride + (slot >> log2_block);
+                return index < rows;
+            },
+            dst, epoch, status, sh);
+        if (!ok)
+            return false;
+    }
+    return true;
+}
+
+// Words per polling thread for the vectors a phase awaits.
+constexpr int kPollBlocked = 3;    // slots per thread per chunk of a width-long blocked vector (1344)
+constexpr int kPollBlockedFF = 9;  // ... of the feed-forward vector (4032)
+constexpr int kPollCombine = (kMaxCombine + kPollThreads - 1) / kPollThreads;
+constexpr int kPollArgmax = (16 * 256 + kPollThreads - 1) / kPollThreads;
 
 // ---------------------------------------------------------------------------
 // LayerNorm of sh.raw into sh.x: mean, centred biased variance, then
@@ -265,26 +322,31 @@ __device__ __forceinline__ void load_norm(NormParams& p, const float* gamma, con
 
 __device__ __forceinline__ void layer_norm(const NormParams& p, int n, float eps, Shared& sh)
 {
-    // Lane l of every wave holds elements 4 (l + 64 k) .. + 3 (n is a multiple of 4).
+    // Lane l of every wave reads elements 4 (l + 64 k) .. + 3 (n is a multiple
+    // of 4) — once for the mean, again for the centred squares.
     constexpr int kRuns = (kMaxWidth + 4 * kWave - 1) / (4 * kWave);
     const int lane = threadIdx.x & (kWave - 1);
-    float4v v[kRuns];
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < kRuns; ++k)
     {
         const int i = 4 * (lane + kWave * k);
-        v[k] = i < n ? *reinterpret_cast<const float4v*>(&sh.raw[i]) : float4v {0.f, 0.f, 0.f, 0.f};
-        s += v[k][0] + v[k][1] + v[k][2] + v[k][3];
+        if (i < n)
+        {
+            const float4v v = *reinterpret_cast<const float4v*>(&sh.raw[i]);
+            s += v[0] + v[1] + v[2] + v[3];
+        }
     }
     const float mean = sum64(s) / (float) n;
     float q = 0.f;
 #pragma unroll
     for (int k = 0; k < kRuns; ++k)
     {
-        if (4 * (lane + kWave * k) < n)
+        const int i = 4 * (lane + kWave * k);
+        if (i < n)
         {
-            const float c0 = v[k][0] - mean, c1 = v[k][1] - mean, c2 = v[k][2] - mean, c3 = v[k][3] - mean;
+            const float4v v = *reinterpret_cast<const float4v*>(&sh.raw[i]);
+            const float c0 = v[0] - mean, c1 = v[1] - mean, c2 = v[2] - mean, c3 = v[3] - mean;
             q += c0 * c0 + c1 * c1 + c2 * c2 + c3 * c3;
         }
     }
@@ -485,28 +547,25 @@ __device__ __forceinline__ void finish_pass(float acc, bool has_task, int pass, 
         for (int s = 0; s < slices; ++s)
             v += sh.part[threadIdx.x * slices + s];
         const int r = group + stride * local;
-        epi(r, v + bias_of(r));
+        epi(r, local, v + bias_of(r));
     }
     __syncthreads();
 }
 
 // Runs every task of the phase against sh.x. epi(row, value) receives the dot
-// product plus bias, on thread (local row) % rows_per_pass. `then` runs once
-// the pass-0 dot products have consumed their registers — the place to issue
-// the next phase's loads. Pass 0 is straight-line code (its weights and bias
-// were loaded a phase earlier), so none of its waits covers those new loads;
+// product plus bias, on thread (local row) % rows_per_pass (all in wave 0).
+// Pass 0 is straight-line code whose weights and bias were loaded a phase
+// earlier, so it never waits on the next phase's loads issued just before it;
 // further passes, which only long rows or narrow grids need, load on the spot.
-template <int WT, class Epilogue, class Then>
+template <int WT, class Epilogue>
 __device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight, const float* bias,
-                                          const PhaseShape& ps, int group, int stride, Shared& sh, Epilogue epi,
-                                          Then then)
+                                          const PhaseShape& ps, int group, int stride, Shared& sh, Epilogue epi)
 {
     const int lane = threadIdx.x & (kRowLanes - 1);
     int row, first, last;
     const bool has_task = phase_task(ps, group, stride, 0, row, first, last);
     const float acc = run_dot<WT>(p.r, sh.x, first, last, lane);
     const float bias0 = p.bias;
-    then();
     if (ps.passes > 0)
         finish_pass(acc, has_task, 0, ps, group, stride, sh, epi, [&](int) { return bias0; });
     for (int pass = 1; pass < ps.passes; ++pass)
@@ -633,6 +692,46 @@ __device__ __forceinline__ float combine(const float* part, int parts, int strid
         denominator += factor * p[1];
     }
     return numerator / denominator;
+}
+
+// The same combine for up to 64 partials of one head with the whole
+// workgroup: wave 0 finds the largest maximum and each partial's factor
+// exp(m_i - max) (0 for an empty partial) and the denominator; wave w then
+// sums partials w, w + 8, ... of every channel and the eight wave sums are
+// added in wave order. The normalised row goes to out (exchange words).
+__device__ __forceinline__ void combine_parts(const float* part, int parts, int head_width, uint64_t* out,
+                                              uint32_t epoch, Shared& sh)
+{
+    const int stride = head_width + 2;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    if (wave == 0)
+    {
+        const float m = lane < parts ? part[lane * stride] : -INFINITY;
+        const float l = lane < parts ? part[lane * stride + 1] : 0.f;
+        const float largest = max64(m);
+        const float factor = l == 0.f ? 0.f : expf(m - largest);
+        const float denominator = sum64(factor * l);
+        sh.q[lane] = factor; // a head's query slot is free while combining
+        if (lane == 0)
+            sh.scratch[0][0] = denominator;
+    }
+    __syncthreads();
+    if (lane < head_width)
+    {
+        float acc = 0.f;
+        for (int i = wave; i < parts; i += kWaves)
+            acc += sh.q[i] * part[i * stride + 2 + lane];
+        sh.red[wave][lane] = acc;
+    }
+    __syncthreads();
+    if ((int) threadIdx.x < head_width)
+    {
+        float numerator = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+            numerator += sh.red[w][threadIdx.x];
+        put(out + threadIdx.x, numerator / sh.scratch[0][0], epoch);
+    }
 }
 
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi)
@@ -801,58 +900,50 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
 
         // ---- LN1 + fused q/k/v (weights in pa) ---------------------------------
         if (l > 0
-            && !gather<kPollWidth>(a.exchange + (size_t) (l - 1) * a.layer_words + a.off_h4, d, sh.raw, epoch,
-                                   a.status, sh))
+            && !gather_blocked<kPollBlocked>(a.exchange + (size_t) (l - 1) * a.layer_words + a.off_h4, d, a.log2_d,
+                                             stride, sh.raw, epoch, a.status, sh))
             return false;
+        prefetch(pb, L.self_out_w, L.self_out_b, square_shape, group, stride);
         layer_norm(norm, d, a.eps, sh);
         {
             uint64_t* qkv = ex + a.off_qkv;
             float* krow = L.self_keys + (size_t) pos * d;
             float* vrow = L.self_values + (size_t) pos * d;
-            run_phase<WT>(
-                pa, L.self_qkv_w, L.self_qkv_b, qkv_shape, group, stride, sh,
-                [&](int r, float v) {
-                    put(qkv + r, v, epoch);
-                    if (r >= 2 * d)
-                        vrow[r - 2 * d] = v;
-                    else if (r >= d)
-                        krow[r - d] = v;
-                },
-                [&] { prefetch(pb, L.self_out_w, L.self_out_b, square_shape, group, stride); });
+            run_phase<WT>(pa, L.self_qkv_w, L.self_qkv_b, qkv_shape, group, stride, sh, [&](int r, int j, float v) {
+                put(qkv + (group << a.log2_qkv) + j, v, epoch);
+                if (r >= 2 * d)
+                    vrow[r - 2 * d] = v;
+                else if (r >= d)
+                    krow[r - d] = v;
+            });
         }
 
         // ---- self-attention combine + out-proj + residual (weights in pb) ------
         if (!gather<kPollCombine>(ex + a.off_self, a.self_splits * H * (hd + 2), sh.comb, epoch, a.status, sh))
             return false;
+        prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
+        load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
         for (int c = threadIdx.x; c < d; c += kThreads)
             sh.x[c] = combine(sh.comb + (c / hd) * (hd + 2), a.self_splits, H * (hd + 2), c % hd);
         __syncthreads();
         {
             uint64_t* out = ex + a.off_h2;
-            run_phase<WT>(
-                pb, L.self_out_w, L.self_out_b, square_shape, group, stride, sh,
-                [&](int r, float v) { put(out + r, sh.raw[r] + v, epoch); },
-                [&] {
-                    prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
-                    load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
-                });
+            run_phase<WT>(pb, L.self_out_w, L.self_out_b, square_shape, group, stride, sh,
+                          [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); });
         }
 
         // ---- LN2 + cross q (weights in pa) ----------------------------------------
-        if (!gather<kPollWidth>(ex + a.off_h2, d, sh.raw, epoch, a.status, sh))
+        if (!gather_blocked<kPollBlocked>(ex + a.off_h2, d, a.log2_d, stride, sh.raw, epoch, a.status, sh))
             return false;
+        prefetch(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride);
+        if (task_count > 0) // awaited only when the query arrives
+            load_keys<kCrossPasses>(cross, L.cross_keys, L.cross_values, task_first, task_count, d, (task % H) * hd,
+                                    hd);
         layer_norm(norm, d, a.eps, sh);
         {
             uint64_t* out = ex + a.off_xq;
-            run_phase<WT>(
-                pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride, sh,
-                [&](int r, float v) { put(out + r, v, epoch); },
-                [&] {
-                    prefetch(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride);
-                    if (task_count > 0) // awaited only when the query arrives
-                        load_keys<kCrossPasses>(cross, L.cross_keys, L.cross_values, task_first, task_count, d,
-                                                (task % H) * hd, hd);
-                });
+            run_phase<WT>(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride, sh,
+                          [&](int, int j, float v) { put(out + (group << a.log2_d) + j, v, epoch); });
         }
 
         // ---- cross-attention partials over this group's key chunk(s) ---------------
@@ -863,55 +954,54 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             const int count = min(a.cross_chunk, a.cross_rows - first);
             if (t != task)
                 load_keys<kCrossPasses>(cross, L.cross_keys, L.cross_values, first, count, d, h * hd, hd);
-            if (!gather<1>(ex + a.off_xq + h * hd, hd, sh.q, epoch, a.status, sh))
+            if (!poll<1>(
+                    ex + a.off_xq, hd,
+                    [&](int i, int& offset, int& index) {
+                        offset = block_slot(h * hd + i, stride, a.log2_d);
+                        index = i;
+                        return true;
+                    },
+                    sh.q, epoch, a.status, sh))
                 return false;
             attend<kCrossPasses>(cross, count, hd, a.scale,
                                  ex + a.off_xpart + (size_t) (h * a.cross_splits + s) * (hd + 2), epoch, sh);
         }
 
         // ---- cross out-proj + residual (weights in pb) --------------------------------
-        if (!gather<kPollWidth>(ex + a.off_xattn, d, sh.x, epoch, a.status, sh))
+        if (!gather<kPollCombine>(ex + a.off_xattn, d, sh.x, epoch, a.status, sh))
             return false;
+        prefetch(pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride);
+        load_norm(norm, L.final_norm_w, L.final_norm_b, d);
         {
             uint64_t* out = ex + a.off_h3;
-            run_phase<WT>(
-                pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride, sh,
-                [&](int r, float v) { put(out + r, sh.raw[r] + v, epoch); },
-                [&] {
-                    prefetch(pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride);
-                    load_norm(norm, L.final_norm_w, L.final_norm_b, d);
-                });
+            run_phase<WT>(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride, sh,
+                          [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); });
         }
 
         // ---- LN3 + fc1 + GELU (weights in pa) ------------------------------------------
-        if (!gather<kPollWidth>(ex + a.off_h3, d, sh.raw, epoch, a.status, sh))
+        if (!gather_blocked<kPollBlocked>(ex + a.off_h3, d, a.log2_d, stride, sh.raw, epoch, a.status, sh))
             return false;
+        prefetch(pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride);
         layer_norm(norm, d, a.eps, sh);
         {
             uint64_t* out = ex + a.off_ff;
-            run_phase<WT>(
-                pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride, sh,
-                [&](int r, float v) { put(out + r, exact_gelu(v), epoch); },
-                [&] { prefetch(pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride); });
+            run_phase<WT>(pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride, sh,
+                          [&](int, int j, float v) { put(out + (group << a.log2_f) + j, exact_gelu(v), epoch); });
         }
 
         // ---- fc2 + residual (weights in pb) ------------------------------------------------
-        if (!gather<kPollFeedForward>(ex + a.off_ff, f, sh.x, epoch, a.status, sh))
+        if (!gather_blocked<kPollBlockedFF>(ex + a.off_ff, f, a.log2_f, stride, sh.x, epoch, a.status, sh))
             return false;
+        if (l + 1 < a.layer_count)
+        {
+            const wsp_layer_tensors& next = sh.table[l + 1];
+            prefetch(pa, next.self_qkv_w, next.self_qkv_b, qkv_shape, group, stride);
+            load_norm(norm, next.self_norm_w, next.self_norm_b, d);
+        }
         {
             uint64_t* out = ex + a.off_h4;
-            const bool more = l + 1 < a.layer_count;
-            const wsp_layer_tensors& next = sh.table[more ? l + 1 : l];
-            run_phase<WT>(
-                pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride, sh,
-                [&](int r, float v) { put(out + r, sh.raw[r] + v, epoch); },
-                [&] {
-                    if (more)
-                    {
-                        prefetch(pa, next.self_qkv_w, next.self_qkv_b, qkv_shape, group, stride);
-                        load_norm(norm, next.self_norm_w, next.self_norm_b, d);
-                    }
-                });
+            run_phase<WT>(pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride, sh,
+                          [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); });
         }
     }
     return true;
@@ -940,7 +1030,14 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
         if (attends)
         {
             // q, and the new key/value rows, of this head, in one wait.
-            if (!gather<1, true>(ex + a.off_qkv + head * hd, 3 * hd, sh.q, epoch, a.status, sh, hd, d))
+            if (!poll<1>(
+                    ex + a.off_qkv, 3 * hd,
+                    [&](int i, int& offset, int& index) {
+                        offset = block_slot((i / hd) * d + head * hd + i % hd, a.row_groups, a.log2_qkv);
+                        index = i;
+                        return true;
+                    },
+                    sh.q, epoch, a.status, sh))
                 return false;
             if (count > cached)
             {
@@ -965,8 +1062,7 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
             if (!gather<kPollCombine>(ex + a.off_xpart + (size_t) head * parts * (hd + 2), parts * (hd + 2), sh.comb,
                                       epoch, a.status, sh))
                 return false;
-            if ((int) threadIdx.x < hd)
-                put(ex + a.off_xattn + head * hd + threadIdx.x, combine(sh.comb, parts, hd + 2, threadIdx.x), epoch);
+            combine_parts(sh.comb, parts, hd, ex + a.off_xattn + head * hd, epoch, sh);
         }
         if (!last_layer && attends && cached > 0)
             load_keys<kSelfPasses>(self, sh.table[l + 1].self_keys, sh.table[l + 1].self_values, first, cached, d,
@@ -983,8 +1079,8 @@ __device__ __forceinline__ bool final_phase(const StepArgs& a, Shared& sh, Ring&
                                             float& best_v, uint32_t& best_i)
 {
     const int d = a.width;
-    if (!gather<kPollWidth>(a.exchange + (size_t) (a.layer_count - 1) * a.layer_words + a.off_h4, d, sh.raw, a.epoch,
-                            a.status, sh))
+    if (!gather_blocked<kPollBlocked>(a.exchange + (size_t) (a.layer_count - 1) * a.layer_words + a.off_h4, d, a.log2_d,
+                                      a.row_groups, sh.raw, a.epoch, a.status, sh))
         return false;
     layer_norm(norm, d, a.eps, sh);
     if (blockIdx.x == 0)
@@ -1052,14 +1148,22 @@ __global__ void __launch_bounds__(kThreads) step_kernel(StepArgs a)
                 bv = sh.best_v[k];
                 bi = sh.best_i[k];
             }
-        put(a.exchange + a.off_argmax + 2 * blockIdx.x, bv, epoch);
-        put(a.exchange + a.off_argmax + 2 * blockIdx.x + 1, __uint_as_float(bi), epoch);
+        // One cache line per workgroup's candidate.
+        put(a.exchange + a.off_argmax + 16 * blockIdx.x, bv, epoch);
+        put(a.exchange + a.off_argmax + 16 * blockIdx.x + 1, __uint_as_float(bi), epoch);
     }
 
     // ---- the argmax fold (Kernels/Argmax.h:145-201) ---------------------------------
     if (blockIdx.x != 0 || a.argmax_out == nullptr)
         return;
-    if (!gather<kPollCombine>(a.exchange + a.off_argmax, 2 * G, sh.comb, epoch, a.status, sh))
+    if (!poll<kPollArgmax>(
+            a.exchange + a.off_argmax, 16 * G,
+            [](int i, int& offset, int& index) {
+                offset = i;
+                index = 2 * (i >> 4) + (i & 15);
+                return (i & 15) < 2;
+            },
+            sh.comb, epoch, a.status, sh))
         return;
     if (threadIdx.x < kWave)
     {
