@@ -43,6 +43,20 @@ def step_bytes(shape, weight_bytes: int, position: int, streams: int = 1) -> int
     return weights + params + streams * per_stream
 
 
+def measured_traffic(workload: str, unfused: bool):
+    """HBM bytes per step-kernel launch as the FETCH_SIZE and WRITE_SIZE
+    counters measured them (each scaled by its reading for a plain copy of
+    known size), from the summary committed under profiles/; None when there
+    is no summary for this workload and path."""
+    if unfused:
+        return None
+    path = os.path.join(ROOT, "profiles", f"step_kernel_{workload}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
 def cpu_baseline(shape, decoder_file, encoder, prompt, gpu_tokens, budget_s: float):
     """The oracle (the C restatement of the reference's double-precision
     decoder) on the host cores over a bounded sample: the prompt step, then
@@ -90,7 +104,21 @@ def main():
     parser.add_argument("--workload", default="small", choices=["base.en", "small"])
     parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of oracle time (0: skip)")
     parser.add_argument("--unfused", action="store_true", help="time the per-op kernel sequence instead")
+    parser.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                        help="only run a plain device-to-device copy of BYTES (the reference reading for the "
+                             "FETCH_SIZE/WRITE_SIZE counters) and exit")
     args = parser.parse_args()
+
+    if args.copy_calibration > 0:
+        import torch
+        src = torch.ones(args.copy_calibration, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": args.copy_calibration, "copies": 4}))
+        return
 
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for {args.gpus})",
@@ -148,6 +176,7 @@ def main():
     start.record()
     run_steps(args.steps)
     stop.record()
+    enqueue_s = time.perf_counter() - host0
     torch.cuda.synchronize()
     host_s = time.perf_counter() - host0
     gpu_ms = start.elapsed_time(stop)
@@ -158,6 +187,8 @@ def main():
     bytes_total = sum(step_bytes(shape, weight_bytes, p) for p in positions)
     bytes_per_step = bytes_total / args.steps
     achieved = bytes_per_step / (ms_per_step * 1e-3) / 1e9
+
+    traffic = measured_traffic(args.workload, args.unfused)
 
     baseline, parity = None, None
     if args.cpu_budget > 0:
@@ -183,11 +214,14 @@ def main():
                    "path": "per-op kernel sequence" if args.unfused else "fused single-token step",
                    "global_batch": 1, "seq_len": len(prompt) + args.steps, "parallelism": "none (one GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decoder step", "bytes_per_step": round(bytes_per_step)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "step_kernel (one persistent launch per decode step)" if not args.unfused
+                     else "per-op kernel sequence",
+                     "bytes_per_step": round(bytes_per_step)},
         "cpu_baseline": baseline,
         "parity": parity,
         "host_seconds": round(host_s, 4),
+        "host_enqueue_seconds": round(enqueue_s, 4),
     }
     print(json.dumps(line))
 

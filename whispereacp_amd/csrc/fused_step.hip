@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -302,9 +303,20 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     a.log2_d = st->log2_d;
     a.log2_f = st->log2_f;
 
+    // A plain launch: the grid is one workgroup per CU, a CU holds only one of
+    // these workgroups (registers), and the stream runs kernels one after
+    // another, so every workgroup is resident at once on a GPU this process
+    // has to itself. A cooperative launch guarantees the same but adds about
+    // 20 us per step; WSP_STEP_LAUNCH=cooperative asks for it (a GPU shared
+    // with other work). Either way every wait in the kernel is bounded.
     void* args[] = {&a};
-    const hipError_t e = hipLaunchCooperativeKernel(step::kernel_for(tensors->wdtype),
-                                                    dim3(st->workgroups), dim3(step::kThreads), args, 0, ctx->stream);
+    static const bool cooperative =
+        getenv("WSP_STEP_LAUNCH") != nullptr && strcmp(getenv("WSP_STEP_LAUNCH"), "cooperative") == 0;
+    const hipError_t e = cooperative
+                             ? hipLaunchCooperativeKernel(step::kernel_for(tensors->wdtype), dim3(st->workgroups),
+                                                          dim3(step::kThreads), args, 0, ctx->stream)
+                             : hipLaunchKernel(step::kernel_for(tensors->wdtype), dim3(st->workgroups),
+                                               dim3(step::kThreads), args, 0, ctx->stream);
     return context_hip(ctx, e, "decoder step launch");
 }
 } // namespace
