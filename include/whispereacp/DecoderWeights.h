@@ -118,4 +118,10 @@ struct DecoderWeights
     // what the fused step needs. Empty for a mixed file.
     std::optional<WeightStorage> uniformProjectionStorage() const;
 };
+
+// The device pointers of one layer's weights in the C ABI's layout, cache
+// pointers left null, and the whole decoder's table over `layers` (which must
+// outlive it). Needs a uniform projection storage.
+wsp_layer_tensors layerTable(const DecoderLayerWeights& w);
+wsp_decoder_tensors decoderTable(const DecoderWeights& weights, const std::vector<wsp_layer_tensors>& layers);
 } // namespace WSP

@@ -94,6 +94,32 @@ int wsp_decoder_greedy(wsp_decoder* decoder, const float* encoder_rows, int cros
                        const float* first_mask, const float* later_mask, int* tokens_out, int capacity,
                        int* count_out, double* decode_seconds);
 
+/* ---- independent streams decoded together (WSP::BatchedDecoder) ----------
+ * No reference counterpart: `streams` sequences share one weight read per
+ * step, each with its own caches; see wsp_batch_create in wsp_hip.h. The
+ * file's projections and logits must share one 16-bit storage (F16/BF16). */
+typedef struct wsp_batch_decoder wsp_batch_decoder;
+
+int wsp_batch_decoder_create(const wsp_decoder_shape* shape, const wsp_tensor_entry* tensors, int count,
+                             int packing, int streams, int max_step_tokens, int device, void* stream,
+                             wsp_batch_decoder** out);
+void wsp_batch_decoder_destroy(wsp_batch_decoder* decoder);
+const char* wsp_batch_decoder_last_error(const wsp_batch_decoder* decoder);
+int wsp_batch_decoder_last_error_kind(const wsp_batch_decoder* decoder);
+
+/* Decoder::beginSequence for every stream; encoder_rows: device f32
+ * [streams][cross_position_count (0: all)][width]. */
+int wsp_batch_decoder_begin(wsp_batch_decoder* decoder, const float* encoder_rows, int cross_position_count);
+
+/* Decoder::step for every stream: tokens device uint32 [streams][count],
+ * logits device f32 [streams·count][vocabulary]. With argmax_slots non-null
+ * each stream's masked argmax of its last row lands in argmax_slots[s]. */
+int wsp_batch_decoder_step(wsp_batch_decoder* decoder, const uint32_t* tokens, int count, float* logits,
+                           const float* mask, uint32_t* argmax_slots);
+
+int wsp_batch_decoder_position(const wsp_batch_decoder* decoder);
+const float* wsp_batch_decoder_hidden_states(const wsp_batch_decoder* decoder);
+
 #ifdef __cplusplus
 }
 #endif

@@ -197,6 +197,58 @@ int wsp_hip_step_persistent(const wsp_hip_ctx* ctx);
  * passes cannot time out. */
 int wsp_hip_device_status(wsp_hip_ctx* ctx, int* status, int clear);
 
+/* ---- batched independent streams ------------------------------------------
+ * No reference counterpart: the reference decodes one sequence per Decoder.
+ * A batch holds `streams` independent sequences that share one weight read
+ * per step. Each has its own self and cross caches, all advance together,
+ * and every stream's rows equal what Decoder::step computes for that stream
+ * alone (Decoder/Decoder.cpp:270-308). Projections need 16-bit storage (F16
+ * or BF16): they run on the matrix cores with the fp32 activations split into
+ * exact 16-bit parts. */
+
+/* One layer's cross-attention key and value projections (Decoder/DecoderWeights.h:25-63). */
+typedef struct wsp_cross_tensors
+{
+    const void* key_w;    /* [width, width], no bias (k_proj) */
+    const void* value_w;  /* [width, width] */
+    const float* value_b; /* [width] */
+} wsp_cross_tensors;
+
+typedef struct wsp_batch wsp_batch;
+
+/* Allocates every stream's caches (self [layers][streams][max_positions][width],
+ * cross [layers][streams][cross_positions][width], f32) and the step buffers
+ * for up to max_step_tokens tokens per stream per step; streams ×
+ * max_step_tokens ≤ 128. wdtype is the projections' storage (WSP_F16 or
+ * WSP_BF16). Decoder::prepare's role (Decoder/Decoder.cpp:194-227), per stream. */
+int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_tokens, int wdtype, int device,
+                     void* stream, wsp_batch** out);
+void wsp_batch_destroy(wsp_batch* batch);
+const char* wsp_batch_last_error(const wsp_batch* batch);
+int wsp_batch_position(const wsp_batch* batch);
+int wsp_batch_cross_rows(const wsp_batch* batch);
+
+/* Decoder::beginSequence for every stream (Decoder/Decoder.cpp:241-268):
+ * projects the cross keys and values of each stream's first cross_rows
+ * encoder rows (0: all) and resets the position. encoder_rows: device f32
+ * [streams][cross_rows][width]; layers: host array of `layers` entries. */
+int wsp_batch_begin(wsp_batch* batch, const wsp_cross_tensors* layers, int wdtype, const float* encoder_rows,
+                    int cross_rows);
+
+/* Decoder::step for every stream: tokens is device uint32 [streams][count]
+ * (stream-major), logits device f32 [streams·count][vocabulary], hidden
+ * (device f32 [streams·count][width]) or null. With argmax_out non-null,
+ * argmax_out[s] receives the masked argmax of stream s's last row
+ * (Argmax::encode, Kernels/Argmax.h:236-241), so it can feed the next step.
+ * The layer table's cache pointers are not used: the batch owns its caches. */
+int wsp_batch_step(wsp_batch* batch, const wsp_decoder_tensors* tensors, const uint32_t* tokens, int count,
+                   float* hidden, float* logits, const float* mask, uint32_t* argmax_out);
+
+/* Layer `layer`'s caches of stream 0; stream s starts max_positions·width
+ * (self) or cross_positions·width (cross) floats later. */
+int wsp_batch_self_cache(const wsp_batch* batch, int layer, const float** keys, const float** values);
+int wsp_batch_cross_cache(const wsp_batch* batch, int layer, const float** keys, const float** values);
+
 #ifdef __cplusplus
 }
 #endif

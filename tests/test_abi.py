@@ -88,3 +88,23 @@ def test_loader_names_a_missing_or_misshapen_table_before_any_upload():
     odd["model.decoder.embed_tokens.weight"] = S.StoredTensor(t.name, "I8", t.extents, t.data)
     with pytest.raises(ModelError, match="I8"):
         Decoder(shape, odd)
+
+
+def test_batch_refuses_bad_arguments_without_a_device():
+    from whispereacp_amd import _native as N
+    lib = ensure_library()
+    handle = ctypes.c_void_p()
+    shape = N.wsp_decoder_shape(1024, 16, 24, 4096, 51865, 448, 1500)
+    assert lib.wsp_batch_create(None, 16, 1, N.WSP_F16, 0, None, ctypes.byref(handle)) == N.WSP_ERR_ARGUMENT
+    assert lib.wsp_batch_create(ctypes.byref(shape), 0, 1, N.WSP_F16, 0, None, ctypes.byref(handle)) == N.WSP_ERR_ARGUMENT
+    # fp32 projections have no matrix-core form here
+    assert lib.wsp_batch_create(ctypes.byref(shape), 16, 1, N.WSP_F32, 0, None, ctypes.byref(handle)) == N.WSP_ERR_LOGIC
+    # more than 128 rows per step
+    assert lib.wsp_batch_create(ctypes.byref(shape), 33, 4, N.WSP_F16, 0, None, ctypes.byref(handle)) == N.WSP_ERR_CAPACITY
+    wide = N.wsp_decoder_shape(1024, 8, 24, 4096, 51865, 448, 1500)  # heads 128 wide
+    assert lib.wsp_batch_create(ctypes.byref(wide), 16, 1, N.WSP_F16, 0, None, ctypes.byref(handle)) == N.WSP_ERR_SHAPE
+    assert not handle.value
+    assert lib.wsp_batch_step(None, None, None, 1, None, None, None, None) == N.WSP_ERR_ARGUMENT
+    assert lib.wsp_batch_begin(None, None, N.WSP_F16, None, 0) == N.WSP_ERR_ARGUMENT
+    assert lib.wsp_batch_last_error(None) == b"null batch"
+    assert lib.wsp_batch_position(None) == -1

@@ -1,0 +1,210 @@
+"""Independent streams decoded together (wsp_batch_decoder_*, WSP::BatchedDecoder).
+
+The batch has no reference counterpart; its contract is that every stream
+computes what Decoder::step computes for that stream alone. So each stream is
+checked three ways:
+
+- against the single-stream GPU decoder (the persistent step, itself pinned to
+  the oracle by test_gpu_step.py), for every stream of the medium (16 streams,
+  fp16) and large-v3 (32 streams, bf16) configurations at their full shapes;
+- against the oracle directly for some streams;
+- in the small cases, with a mask, reduced cross rows and a causal prompt step.
+
+Greedy tokens must be equal. Logits meet the configurations' bar (max relative
+error 2e-2 with 16-bit weights), and, tighter, the reference's worst-error
+measure within 1e-4. Projections run on the matrix cores with the
+activations split into exact 16-bit parts, so they differ from the fp32
+single-stream path only in summation order."""
+
+import numpy as np
+import pytest
+
+from helpers import (WORST, check_run, ensure_library, greedy_on_gpu, margin, max_relative_error, oracle_greedy,
+                     oracle_tensors,
+                     worst_error)
+from whispereacp_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def library():
+    ensure_library()
+
+
+def batched_greedy(decoder, shape, encoders, prompt, steps, mask=None, cross_rows=0):
+    """begin for every stream, the prompt as one causal step per stream, then
+    `steps` single-token steps whose argmax feeds the next step on the device.
+    Returns per stream: tokens (prompt argmax first), the single-token steps'
+    logits rows [steps, V] and the prompt step's logits [t, V]."""
+    import torch
+    from whispereacp_amd.decoder import to_device
+    streams, V, t = len(encoders), shape.vocabulary_size, len(prompt)
+    enc = to_device(np.ascontiguousarray(np.stack(encoders), dtype=np.float32))
+    decoder.begin(enc, cross_rows)
+    tokens = torch.tensor([list(prompt)] * streams, dtype=torch.int32, device="cuda")
+    slots = torch.zeros((steps + 1, streams), dtype=torch.int32, device="cuda")
+    prompt_logits = torch.empty((streams * t, V), dtype=torch.float32, device="cuda")
+    decoder.step(tokens, t, prompt_logits, None, slots[0])
+    rows = torch.empty((steps, streams, V), dtype=torch.float32, device="cuda")
+    for j in range(steps):
+        decoder.step(slots[j], 1, rows[j], mask, slots[j + 1])
+    torch.cuda.synchronize()
+    return (slots.cpu().numpy().T.tolist(), rows.cpu().numpy().transpose(1, 0, 2),
+            prompt_logits.cpu().numpy().reshape(streams, t, V))
+
+
+def compare_streams(tokens, rows, references, label):
+    """Each stream against its single-stream GPU run; returns the worst errors."""
+    rel_all, worst_all = 0.0, 0.0
+    for s, (ref_tokens, ref_rows) in enumerate(references):
+        for j, (a, b) in enumerate(zip(tokens[s], ref_tokens)):
+            assert a == b, (f"{label} stream {s} token {j}: batched {a}, single-stream {b}; single-stream "
+                            f"top-2 margin {margin(ref_rows[j - 1]) if j > 0 else float('nan'):.3g}")
+        rel_all = max(rel_all, max_relative_error(rows[s], ref_rows))
+        worst_all = max(worst_all, worst_error(rows[s], ref_rows))
+    assert rel_all <= 2e-2, rel_all
+    assert worst_all <= WORST, worst_all
+    return rel_all, worst_all
+
+
+def single_stream_runs(shape, decoder_file, encoders, prompt, steps, mask=None):
+    from whispereacp_amd.decoder import Decoder
+    decoder = Decoder(shape, decoder_file, packing="ExactHalf")
+    print(f"single-stream reference: persistent step {decoder.uses_persistent_step}")
+    runs = [greedy_on_gpu(decoder, shape, e, prompt, steps, mask) for e in encoders]
+    assert decoder.device_status() == 0
+    return runs
+
+
+# -- the medium configuration: d 1024, 16 heads, 24 layers, fp16, 16 streams --
+
+@pytest.fixture(scope="module")
+def medium():
+    shape = S.workload_shape("medium")
+    return (shape, S.workload_decoder_file(shape, "F16", 1000),
+            [S.normal_encoder_output(1500, shape.width, 100 + s) for s in range(16)])
+
+
+@pytest.fixture(scope="module")
+def medium_batched(medium):
+    from whispereacp_amd.decoder import BatchedDecoder
+    shape, f, encoders = medium
+    decoder = BatchedDecoder(shape, f, streams=16)
+    out = batched_greedy(decoder, shape, encoders, S.SOT_PREFIX[shape.vocabulary_size], 16)
+    assert decoder.position == 4 + 16
+    return out
+
+
+def test_medium_streams_match_single_stream_decoders(medium, medium_batched):
+    shape, f, encoders = medium
+    tokens, rows, _ = medium_batched
+    refs = single_stream_runs(shape, f, encoders, S.SOT_PREFIX[shape.vocabulary_size], 16)
+    rel, worst = compare_streams(tokens, rows, refs, "medium")
+    print(f"medium, 16 streams x 16 steps vs single-stream: max relative {rel:.2e}, worst {worst:.2e}")
+
+
+def test_medium_stream_matches_oracle(oracle, medium, medium_batched):
+    shape, f, encoders = medium
+    tokens, rows, _ = medium_batched
+    ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, encoders[5], S.SOT_PREFIX[shape.vocabulary_size], 16)
+    rel, worst = check_run(tokens[5], rows[5], ref_tokens, ref_rows, 2e-2)
+    print(f"medium stream 5 vs oracle: max relative {rel:.2e}, worst {worst:.2e}")
+
+
+# -- the large-v3 configuration: d 1280, 20 heads, 32 layers, bf16, 32 streams --
+
+@pytest.fixture(scope="module")
+def large():
+    shape = S.workload_shape("large-v3")
+    return (shape, S.workload_decoder_file(shape, "BF16", 2000),
+            [S.normal_encoder_output(1500, shape.width, 300 + s) for s in range(32)])
+
+
+@pytest.fixture(scope="module")
+def large_batched(large):
+    from whispereacp_amd.decoder import BatchedDecoder
+    shape, f, encoders = large
+    decoder = BatchedDecoder(shape, f, streams=32)
+    return batched_greedy(decoder, shape, encoders, S.SOT_PREFIX[shape.vocabulary_size], 8)
+
+
+def test_large_streams_match_single_stream_decoders(large, large_batched):
+    shape, f, encoders = large
+    tokens, rows, _ = large_batched
+    refs = single_stream_runs(shape, f, encoders, S.SOT_PREFIX[shape.vocabulary_size], 8)
+    rel, worst = compare_streams(tokens, rows, refs, "large-v3")
+    print(f"large-v3, 32 streams x 8 steps vs single-stream: max relative {rel:.2e}, worst {worst:.2e}")
+
+
+def test_large_stream_matches_oracle(oracle, large, large_batched):
+    shape, f, encoders = large
+    tokens, rows, _ = large_batched
+    ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, encoders[31], S.SOT_PREFIX[shape.vocabulary_size], 8)
+    rel, worst = check_run(tokens[31], rows[31], ref_tokens, ref_rows, 2e-2)
+    print(f"large-v3 stream 31 vs oracle: max relative {rel:.2e}, worst {worst:.2e}")
+
+
+# -- small shapes: every stream against the oracle -----------------------------
+
+@pytest.mark.parametrize("dtype", ["F16", "BF16"])
+def test_streams_with_mask_reduced_cross_rows_and_prompt_step(oracle, dtype):
+    from whispereacp_amd.decoder import BatchedDecoder, to_device
+    shape = S.DecoderShape(256, 4, 2, 1024, 4099, 448, 300)
+    f = S.workload_decoder_file(shape, dtype, 77)
+    cross_rows, steps = 77, 12
+    encoders = [S.normal_encoder_output(cross_rows, shape.width, 500 + s) for s in range(3)]
+    prompt = [11, 4000, 7, 1234]
+    mask = np.zeros(shape.vocabulary_size, np.float32)
+    mask[::3] = 1.0
+    decoder = BatchedDecoder(shape, f, streams=3)
+    tokens, rows, prompt_logits = batched_greedy(decoder, shape, encoders, prompt, steps, to_device(mask),
+                                                 cross_rows)
+    for s in range(3):
+        session = oracle.session(shape, oracle_tensors(f, shape))
+        session.begin(encoders[s], cross_rows)
+        _, logits = session.step(prompt)
+        # the causal prompt step: all four rows
+        assert worst_error(prompt_logits[s], logits) <= WORST
+        ref = [int(np.argmax(logits[-1]))]
+        ref_rows = []
+        for _ in range(steps):
+            _, logits = session.step([ref[-1]])
+            ref_rows.append(logits[0])
+            ref.append(int(np.argmax(np.where(mask != 0, -np.inf, logits[0]))))
+        check_run(tokens[s], rows[s], ref, np.array(ref_rows), 2e-2, mask=mask)
+        assert all(t % 3 != 0 for t in tokens[s][1:])
+
+
+def test_long_sequence_splits_self_keys(oracle):
+    # 300 single-token steps: the self keys pass 128 and 256, so the split
+    # attention runs several chunks and the combine.
+    from whispereacp_amd.decoder import BatchedDecoder
+    shape = S.DecoderShape(128, 2, 2, 512, 1000, 448, 64)
+    f = S.workload_decoder_file(shape, "F16", 91)
+    encoders = [S.normal_encoder_output(64, shape.width, 600 + s) for s in range(2)]
+    prompt = [1, 2, 3, 4]
+    decoder = BatchedDecoder(shape, f, streams=2)
+    tokens, rows, _ = batched_greedy(decoder, shape, encoders, prompt, 300)
+    for s in range(2):
+        ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, encoders[s], prompt, 300)
+        check_run(tokens[s], rows[s], ref_tokens, ref_rows, 2e-2)
+
+
+def test_batch_refuses_steps_past_the_context_and_before_begin():
+    import torch
+    from whispereacp_amd.decoder import BatchedDecoder, LogicError, ModelError, to_device
+    shape = S.DecoderShape(128, 2, 1, 512, 1000, 8, 16)
+    f = S.workload_decoder_file(shape, "F16", 5)
+    decoder = BatchedDecoder(shape, f, streams=2)
+    logits = torch.empty((8, shape.vocabulary_size), dtype=torch.float32, device="cuda")
+    tokens = torch.ones((2, 4), dtype=torch.int32, device="cuda")
+    with pytest.raises(LogicError):
+        decoder.step(tokens, 4, logits)
+    decoder.begin(to_device(np.stack([S.normal_encoder_output(16, 128, 1)] * 2)))
+    decoder.step(tokens, 4, logits)
+    decoder.step(tokens, 4, logits)
+    assert decoder.position == 8
+    with pytest.raises(ModelError):
+        decoder.step(tokens, 1, logits)
+    assert decoder.position == 8

@@ -44,9 +44,11 @@ def weights(out, inner, dtype, seed):
 @pytest.mark.parametrize("dtype", ["F32", "F16", "BF16"])
 @pytest.mark.parametrize("rows,inner,out", [(1, 768, 768), (1, 768, 3072), (1, 3072, 768), (3, 384, 1536),
                                             (16, 64, 100), (1, 100, 37), (5, 36, 52), (40, 64, 96),
-                                            (1500, 256, 64)])
+                                            (1500, 256, 64), (40, 256, 128), (130, 96, 384), (300, 512, 256)])
 @pytest.mark.parametrize("flags", [0, 1, 2])
 def test_linear_matches_oracle(ctx, oracle, dtype, rows, inner, out, flags):
+    # More than 16 rows of 16-bit weights with out % 128 == 0 and inner % 32 == 0
+    # take the matrix-core product with split activations.
     import torch
     from whispereacp_amd import _native as N
     from whispereacp_amd.decoder import stored_to_device
@@ -262,9 +264,12 @@ def test_argmax_refuses_beyond_its_capacity(ctx):
 
 
 @pytest.mark.parametrize("dtype", ["F32", "F16", "BF16"])
-def test_cross_kv_projection_matches_oracle(ctx, oracle, dtype):
+@pytest.mark.parametrize("width", [64, 768])
+def test_cross_kv_projection_matches_oracle(ctx, oracle, dtype, width):
+    # width 768 with 16-bit weights takes the matrix-core product (keys and
+    # values in one launch); the other cases the fp32 tiled product.
     from whispereacp_amd.decoder import stored_to_device
-    rows, width = 1500, 64
+    rows = 1500
     x = S.normal_values(rows * width, 21, 1.0).reshape(rows, width)
     sk, wk = weights(width, width, dtype, 22)
     sv, wv = weights(width, width, dtype, 23)

@@ -56,6 +56,10 @@ class wsp_decoder_tensors(ctypes.Structure):
                 ("final_norm_b", c_void_p), ("layers", ctypes.POINTER(wsp_layer_tensors))]
 
 
+class wsp_cross_tensors(ctypes.Structure):
+    _fields_ = [("key_w", c_void_p), ("value_w", c_void_p), ("value_b", c_void_p)]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "wsp_hip_ctx_create": (c_int, [ctypes.POINTER(wsp_decoder_shape), c_int, c_void_p, ctypes.POINTER(c_void_p)]),
@@ -93,6 +97,26 @@ SIGNATURES = {
     "wsp_decoder_greedy": (c_int, [c_void_p, c_void_p, c_int, ctypes.POINTER(c_int), c_int, c_int, c_int, c_void_p,
                                    c_void_p, ctypes.POINTER(c_int), c_int, ctypes.POINTER(c_int),
                                    ctypes.POINTER(c_double)]),
+    "wsp_batch_create": (c_int, [ctypes.POINTER(wsp_decoder_shape), c_int, c_int, c_int, c_int, c_void_p,
+                                 ctypes.POINTER(c_void_p)]),
+    "wsp_batch_destroy": (None, [c_void_p]),
+    "wsp_batch_last_error": (c_char_p, [c_void_p]),
+    "wsp_batch_position": (c_int, [c_void_p]),
+    "wsp_batch_cross_rows": (c_int, [c_void_p]),
+    "wsp_batch_begin": (c_int, [c_void_p, ctypes.POINTER(wsp_cross_tensors), c_int, c_void_p, c_int]),
+    "wsp_batch_step": (c_int, [c_void_p, ctypes.POINTER(wsp_decoder_tensors), c_void_p, c_int, c_void_p, c_void_p,
+                               c_void_p, c_void_p]),
+    "wsp_batch_self_cache": (c_int, [c_void_p, c_int, ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p)]),
+    "wsp_batch_cross_cache": (c_int, [c_void_p, c_int, ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p)]),
+    "wsp_batch_decoder_create": (c_int, [ctypes.POINTER(wsp_decoder_shape), ctypes.POINTER(wsp_tensor_entry), c_int,
+                                         c_int, c_int, c_int, c_int, c_void_p, ctypes.POINTER(c_void_p)]),
+    "wsp_batch_decoder_destroy": (None, [c_void_p]),
+    "wsp_batch_decoder_last_error": (c_char_p, [c_void_p]),
+    "wsp_batch_decoder_last_error_kind": (c_int, [c_void_p]),
+    "wsp_batch_decoder_begin": (c_int, [c_void_p, c_void_p, c_int]),
+    "wsp_batch_decoder_step": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "wsp_batch_decoder_position": (c_int, [c_void_p]),
+    "wsp_batch_decoder_hidden_states": (c_void_p, [c_void_p]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

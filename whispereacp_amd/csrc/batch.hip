@@ -1,0 +1,963 @@
+// Batched decode of independent streams on gfx950. B sequences, each with its
+// own self and cross caches and all at the same position, share one read of
+// every weight per step; the step of one token per stream is the
+// medium/large-configuration decode loop.
+//
+// Projections run on the matrix cores. An fp32 activation x is carried as a
+// sum of 16-bit parts: hi = fp16(x), lo = fp16(x - hi) for fp16 weights, or
+// three bf16 parts (each the rounded remainder of the last) for bf16 weights.
+// Every part times a 16-bit weight is exact in fp32, so W·hi + W·lo (+ W·lo2)
+// accumulated in fp32 reproduces the fp32 product the reference computes with
+// widened weights (Kernels/Linear.h:229-246) to fp32 rounding, not to 16-bit
+// rounding. The fp16 form needs |x| < 65504.
+//
+// Kernels per layer: LayerNorm + split, the q/k/v product (k and v rows land
+// in the self caches), split-key attention (+ combine), the output product
+// with its residual, and the same for cross attention and the feed-forward
+// pair. Every reduction runs in a fixed order.
+#include "../../include/wsp_hip.h"
+#include "device_common.h"
+#include "ops.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+namespace wsp::batch
+{
+namespace
+{
+typedef uint16_t u16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kProductThreads = 512; // 8 waves split the inner dimension of a 16-column tile
+constexpr int kProductWaves = kProductThreads / kWave;
+constexpr int kAttendThreads = 256;  // 16 key groups x 16 lanes of four channels
+constexpr int kTileKeys = 128;       // keys an attention block holds per pass
+constexpr int kNormThreads = 256;
+constexpr int kMaxRowTiles = 8;      // 16-row tiles per product: 128 rows
+
+template <int WT>
+constexpr int parts_of()
+{
+    return WT == kF16 ? 2 : 3;
+}
+
+// x as 16-bit parts at out[p * part_stride + index].
+template <int WT>
+__device__ __forceinline__ void store_split(u16* out, size_t part_stride, size_t index, float x)
+{
+    if constexpr (WT == kF16)
+    {
+        const _Float16 hi = (_Float16) x;
+        const _Float16 lo = (_Float16) (x - (float) hi);
+        out[index] = __builtin_bit_cast(u16, hi);
+        out[part_stride + index] = __builtin_bit_cast(u16, lo);
+    }
+    else
+    {
+        float rest = x;
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+        {
+            const __bf16 b = (__bf16) rest;
+            out[(size_t) p * part_stride + index] = __builtin_bit_cast(u16, b);
+            rest -= (float) b;
+        }
+    }
+}
+
+template <int WT>
+__device__ __forceinline__ float4v mfma16(u32x4 a, u32x4 b, float4v c)
+{
+    if constexpr (WT == kF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm of one row into its split parts (Kernels/LayerNorm.h:44-89:
+// mean, centred biased variance, rsqrt(var + eps)); with EMBED the row is
+// first built as token_table[token] + position_table[position]
+// (Kernels/Embed.h:38-62) and kept as the residual stream.
+// ---------------------------------------------------------------------------
+struct Norm
+{
+    float* h;             // [rows, width] residual stream
+    int width;
+    const float* gamma;
+    const float* beta;
+    float eps;
+    u16* xs;              // split output [parts][rows_padded][width]
+    size_t xs_part;
+    float* y;             // optional f32 copy of the normalised rows
+    const uint32_t* tokens;
+    const float* token_table;
+    const float* position_table;
+    int position, step_tokens, vocabulary;
+};
+
+template <int WT, bool EMBED>
+__global__ void __launch_bounds__(kNormThreads) norm_kernel(Norm a)
+{
+    __shared__ float scratch[kNormThreads / kWave];
+    const int row = blockIdx.x;
+    float* h = a.h + (size_t) row * a.width;
+    if constexpr (EMBED)
+    {
+        const uint32_t token = a.tokens[row];
+        const int position = a.position + row % a.step_tokens;
+        for (int c = threadIdx.x; c < a.width; c += kNormThreads)
+            h[c] = token < (uint32_t) a.vocabulary
+                       ? a.token_table[(size_t) token * a.width + c] + a.position_table[(size_t) position * a.width + c]
+                       : __builtin_nanf("");
+    }
+    float total = 0.f;
+    for (int c = threadIdx.x; c < a.width; c += kNormThreads)
+        total += h[c];
+    const float mean = block_sum(total, scratch) / (float) a.width;
+    float squares = 0.f;
+    for (int c = threadIdx.x; c < a.width; c += kNormThreads)
+    {
+        const float centred = h[c] - mean;
+        squares += centred * centred;
+    }
+    const float scale = rsqrtf(block_sum(squares, scratch) / (float) a.width + a.eps);
+    for (int c = threadIdx.x; c < a.width; c += kNormThreads)
+    {
+        const float v = (h[c] - mean) * scale * a.gamma[c] + a.beta[c];
+        store_split<WT>(a.xs, a.xs_part, (size_t) row * a.width + c, v);
+        if (a.y != nullptr)
+            a.y[(size_t) row * a.width + c] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny product y[m, n] = Σ_k x[m, k]·W[n, k] for up to 128 rows. A block
+// owns 16 output columns for every row tile; its 8 waves split the inner
+// dimension into contiguous runs of 32-wide k-blocks, each lane loading 16
+// bytes of one weight row and of each split activation row per k-block
+// (v_mfma_f32_16x16x32: A = activations, lane l row l % 16; B = weights,
+// lane l column l % 16; both with k = 8(l / 16) + j). KB k-blocks are loaded
+// before their products. The 8 wave partials are summed in wave order.
+// ---------------------------------------------------------------------------
+enum Epilogue : int
+{
+    kStore = 0,     // y = acc + bias
+    kResidual = 1,  // y += acc + bias
+    kGeluSplit = 2, // split parts of gelu(acc + bias) into xs_out [parts][rows_padded][out]
+    kQkv = 3        // q | self key row | self value row
+};
+
+struct Product
+{
+    const u16* x;     // [parts][rows_padded][inner]
+    size_t x_part;
+    int rows, inner, out;
+    const void* w;    // [out][inner]
+    const float* bias;
+    int epilogue;
+    float* y;
+    int ldy;
+    u16* xs_out;
+    size_t xs_out_part;
+    float* q;
+    float* keys;      // stream 0's cache of this layer
+    float* values;
+    size_t stream_stride;
+    int position, step_tokens, width;
+};
+
+template <int WT>
+__device__ __forceinline__ void finish(const Product& a, int m, int n, float acc)
+{
+    const float v = acc + (a.bias != nullptr ? a.bias[n] : 0.f);
+    switch (a.epilogue)
+    {
+        case kStore: a.y[(size_t) m * a.ldy + n] = v; break;
+        case kResidual: a.y[(size_t) m * a.ldy + n] += v; break;
+        case kGeluSplit: store_split<WT>(a.xs_out, a.xs_out_part, (size_t) m * a.out + n, exact_gelu(v)); break;
+        default:
+        {
+            const int d = a.width;
+            const int stream = m / a.step_tokens, i = m % a.step_tokens;
+            const size_t row = (size_t) stream * a.stream_stride + (size_t) (a.position + i) * d;
+            if (n < d)
+                a.q[(size_t) m * d + n] = v;
+            else if (n < 2 * d)
+                a.keys[row + (n - d)] = v;
+            else
+                a.values[row + (n - 2 * d)] = v;
+        }
+    }
+}
+
+template <int P, int MT>
+constexpr int kblocks_per_load()
+{
+    constexpr int kb = 128 / (4 + 4 * P * MT);
+    return kb < 1 ? 1 : (kb > 8 ? 8 : kb);
+}
+
+template <int WT, int MT>
+__global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
+{
+    constexpr int P = parts_of<WT>();
+    constexpr int KB = kblocks_per_load<P, MT>();
+    __shared__ float partial[kProductWaves][256];
+
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int li = lane % 16, g = lane / 16;
+    const int n0 = blockIdx.x * 16;
+    const int kblocks = a.inner / 32;
+    const int kb_begin = wave * kblocks / kProductWaves;
+    const int kb_end = (wave + 1) * kblocks / kProductWaves;
+    // Columns past `out` (the last tile of a vocabulary) re-read the last row;
+    // their sums are never stored.
+    const u16* wrow = static_cast<const u16*>(a.w) + (size_t) min(n0 + li, a.out - 1) * a.inner + 8 * g;
+    const u16* xrow = a.x + (size_t) li * a.inner + 8 * g;
+
+    float4v acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+        acc[t] = float4v {0.f, 0.f, 0.f, 0.f};
+
+    for (int kb = kb_begin; kb < kb_end; kb += KB)
+    {
+        u32x4 wv[KB];
+        u32x4 xv[KB][P][MT];
+#pragma unroll
+        for (int u = 0; u < KB; ++u)
+        {
+            const int k = min(kb + u, kb_end - 1) * 32;
+            wv[u] = *reinterpret_cast<const u32x4*>(wrow + k);
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+                    xv[u][p][t] = *reinterpret_cast<const u32x4*>(xrow + p * a.x_part + (size_t) t * 16 * a.inner + k);
+        }
+#pragma unroll
+        for (int u = 0; u < KB; ++u)
+            if (kb + u < kb_end)
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+#pragma unroll
+                    for (int p = 0; p < P; ++p)
+                        acc[t] = mfma16<WT>(xv[u][p][t], wv[u], acc[t]);
+    }
+
+    // acc[t][r] of lane (g, li) is C[4g + r][li] of row tile t.
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+    {
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            partial[wave][lane * 4 + r] = acc[t][r];
+        __syncthreads();
+        if (threadIdx.x < 256)
+        {
+            const int row = threadIdx.x / 16, col = threadIdx.x % 16;
+            const int src = ((row / 4) * 16 + col) * 4 + row % 4;
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < kProductWaves; ++w)
+                v += partial[w][src];
+            const int m = t * 16 + row, n = n0 + col;
+            if (m < a.rows && n < a.out)
+                finish<WT>(a, m, n, v);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Split-key attention for (row, head, chunk): the row's query against keys
+// [chunk·len, min((chunk + 1)·len, visible)) of its stream's cache, visible
+// being the causal limit k_count - step_tokens + i + 1 for self attention
+// (Kernels/Attention.h:34-47) and k_count for cross attention. Keys are taken
+// 128 at a time; lane (group, sub) holds channels 4·sub.. of keys group + 16u
+// and all its key and value loads are issued together. Tiles fold into a
+// running (max, sum, row) with exact exp(m_old - m_new) rescaling; one chunk
+// writes the normalised split row, several write (max, sum, row) for the
+// combine (Kernels/SingleQueryAttention.h:27-37).
+// ---------------------------------------------------------------------------
+struct Attend
+{
+    const float* q;       // [rows][width]
+    const float* keys;    // stream 0's cache of this layer, [capacity][width]
+    const float* values;
+    size_t stream_stride; // elements between streams' caches
+    int k_count, step_tokens, causal, heads, head_width, width;
+    float scale;
+    int chunks, chunk_len;
+    u16* xs;              // split output [parts][rows_padded][width] when chunks == 1
+    size_t xs_part;
+    float* partials;      // [rows][heads][chunks][head_width + 2]
+};
+
+template <int WT>
+__global__ void __launch_bounds__(kAttendThreads) attend_kernel(Attend a)
+{
+    __shared__ float wave_max[2][4];
+    __shared__ float wave_sum[4];
+    __shared__ float4v wave_row[4][16];
+
+    const int chunk = blockIdx.x % a.chunks;
+    const int head = (blockIdx.x / a.chunks) % a.heads;
+    const int row = blockIdx.x / (a.chunks * a.heads);
+    const int stream = row / a.step_tokens, i = row % a.step_tokens;
+    const int sub = threadIdx.x % 16, group = threadIdx.x / 16;
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int quads = a.head_width / 4;
+    const int column = head * a.head_width + 4 * min(sub, quads - 1);
+
+    float4v qv = {0.f, 0.f, 0.f, 0.f};
+    if (sub < quads)
+        qv = *reinterpret_cast<const float4v*>(a.q + (size_t) row * a.width + column);
+    const int visible = a.causal ? a.k_count - a.step_tokens + i + 1 : a.k_count;
+    const int first = chunk * a.chunk_len;
+    const int last = min(first + a.chunk_len, visible);
+    const float* kbase = a.keys + (size_t) stream * a.stream_stride + column;
+    const float* vbase = a.values + (size_t) stream * a.stream_stride + column;
+
+    float run_max = -INFINITY, run_sum = 0.f;
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+    int flip = 0;
+    for (int ts = first; ts < last; ts += kTileKeys)
+    {
+        float4v kv[8], vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+        {
+            const size_t key = (size_t) min(ts + group + 16 * u, last - 1);
+            kv[u] = *reinterpret_cast<const float4v*>(kbase + key * a.width);
+            vv[u] = *reinterpret_cast<const float4v*>(vbase + key * a.width);
+        }
+        float s[8];
+        float tile_max = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+        {
+            float part = qv[0] * kv[u][0] + qv[1] * kv[u][1] + qv[2] * kv[u][2] + qv[3] * kv[u][3];
+#pragma unroll
+            for (int offset = 1; offset < 16; offset <<= 1)
+                part += __shfl_xor(part, offset, 16);
+            s[u] = ts + group + 16 * u < last ? a.scale * part : -INFINITY;
+            tile_max = fmaxf(tile_max, s[u]);
+        }
+        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
+        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+        if (lane == 0)
+            wave_max[flip][wave] = tile_max;
+        __syncthreads();
+        tile_max = fmaxf(fmaxf(wave_max[flip][0], wave_max[flip][1]), fmaxf(wave_max[flip][2], wave_max[flip][3]));
+        flip ^= 1;
+
+        const float new_max = fmaxf(run_max, tile_max);
+        const float factor = expf(run_max - new_max);
+        float psum = 0.f;
+        float4v pv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+        {
+            const float p = expf(s[u] - new_max);
+            psum += p;
+            pv += p * vv[u];
+        }
+        run_sum = run_sum * factor + psum;
+        acc = acc * factor + pv;
+        run_max = new_max;
+    }
+
+    // Sum the 16 key groups: the four of a wave by lane exchange, then the
+    // four waves in order.
+    run_sum += __shfl_xor(run_sum, 16);
+    run_sum += __shfl_xor(run_sum, 32);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+    {
+        acc[r] += __shfl_xor(acc[r], 16);
+        acc[r] += __shfl_xor(acc[r], 32);
+    }
+    if (lane < 16)
+    {
+        wave_row[wave][lane] = acc;
+        if (lane == 0)
+            wave_sum[wave] = run_sum;
+    }
+    __syncthreads();
+    if (threadIdx.x < a.head_width)
+    {
+        const int c = threadIdx.x, q4 = c / 4, r = c % 4;
+        const float total = (wave_sum[0] + wave_sum[1]) + (wave_sum[2] + wave_sum[3]);
+        const float value = (wave_row[0][q4][r] + wave_row[1][q4][r]) + (wave_row[2][q4][r] + wave_row[3][q4][r]);
+        if (a.chunks == 1)
+            store_split<WT>(a.xs, a.xs_part, (size_t) row * a.width + head * a.head_width + c, value / total);
+        else
+        {
+            float* part = a.partials + (((size_t) row * a.heads + head) * a.chunks + chunk) * (a.head_width + 2);
+            part[2 + c] = value;
+            if (c == 0)
+            {
+                part[0] = last > first ? run_max : -INFINITY;
+                part[1] = total;
+            }
+        }
+    }
+}
+
+template <int WT>
+__global__ void __launch_bounds__(kWave) combine_kernel(const float* __restrict__ partials, int heads,
+                                                        int head_width, int chunks, int width, u16* xs,
+                                                        size_t xs_part)
+{
+    const int head = blockIdx.x % heads, row = blockIdx.x / heads;
+    const int c = threadIdx.x;
+    if (c >= head_width)
+        return;
+    const float* base = partials + ((size_t) row * heads + head) * chunks * (head_width + 2);
+    float largest = -INFINITY;
+    for (int k = 0; k < chunks; ++k)
+        largest = fmaxf(largest, base[(size_t) k * (head_width + 2)]);
+    float numerator = 0.f, denominator = 0.f;
+    for (int k = 0; k < chunks; ++k)
+    {
+        const float* part = base + (size_t) k * (head_width + 2);
+        if (part[1] == 0.f)
+            continue;
+        const float factor = expf(part[0] - largest);
+        numerator += factor * part[2 + c];
+        denominator += factor * part[1];
+    }
+    store_split<WT>(xs, xs_part, (size_t) row * width + head * head_width + c, numerator / denominator);
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+int row_tiles(int rows)
+{
+    const int tiles = (rows + 15) / 16;
+    int t = 1;
+    while (t < tiles)
+        t *= 2;
+    return t;
+}
+
+template <int WT>
+hipError_t launch_product(hipStream_t stream, const Product& a)
+{
+    const dim3 grid((a.out + 15) / 16);
+    switch (row_tiles(a.rows))
+    {
+        case 1: hipLaunchKernelGGL((product_kernel<WT, 1>), grid, dim3(kProductThreads), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((product_kernel<WT, 2>), grid, dim3(kProductThreads), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((product_kernel<WT, 4>), grid, dim3(kProductThreads), 0, stream, a); break;
+        default: hipLaunchKernelGGL((product_kernel<WT, 8>), grid, dim3(kProductThreads), 0, stream, a); break;
+    }
+    return hipGetLastError();
+}
+
+template <int WT>
+hipError_t launch_norm(hipStream_t stream, const Norm& a, int rows, bool embed)
+{
+    if (embed)
+        hipLaunchKernelGGL((norm_kernel<WT, true>), dim3(rows), dim3(kNormThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((norm_kernel<WT, false>), dim3(rows), dim3(kNormThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+// Key chunks for `units` (row, head) pairs over k_count keys: about 2048
+// blocks in all, no chunk shorter than one 128-key tile.
+int attend_chunks(int units, int k_count)
+{
+    const int most = std::max(1, (k_count + kTileKeys - 1) / kTileKeys);
+    return std::max(1, std::min(most, (2048 + units - 1) / units));
+}
+
+// Attention of `rows` query rows; a.chunks and a.chunk_len are filled here.
+template <int WT>
+hipError_t launch_attend(hipStream_t stream, Attend a, int rows)
+{
+    a.chunks = attend_chunks(rows * a.heads, a.k_count);
+    a.chunk_len = (a.k_count + a.chunks - 1) / a.chunks;
+    a.chunks = (a.k_count + a.chunk_len - 1) / a.chunk_len;
+    hipLaunchKernelGGL((attend_kernel<WT>), dim3(rows * a.heads * a.chunks), dim3(kAttendThreads), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.chunks == 1)
+        return e;
+    hipLaunchKernelGGL((combine_kernel<WT>), dim3(rows * a.heads), dim3(kWave), 0, stream, a.partials, a.heads,
+                       a.head_width, a.chunks, a.width, a.xs, a.xs_part);
+    return hipGetLastError();
+}
+} // namespace
+} // namespace wsp::batch
+
+// ---------------------------------------------------------------------------
+// The batch context and its C ABI
+// ---------------------------------------------------------------------------
+struct wsp_batch
+{
+    wsp_decoder_shape shape {};
+    int streams = 0, max_step_tokens = 0, wdtype = 0, device = 0;
+    hipStream_t stream = nullptr;
+    int rows_cap = 0, rows_padded = 0;
+    int position = 0, cross_rows = 0;
+
+    float* self_keys = nullptr;   // [layers][streams][max_positions][width]
+    float* self_values = nullptr;
+    float* cross_keys = nullptr;  // [layers][streams][cross_positions][width]
+    float* cross_values = nullptr;
+    float* h = nullptr;           // [rows_padded][width] residual stream
+    float* q = nullptr;           // [rows_padded][width] queries
+    uint16_t* xs = nullptr;       // [parts][rows_padded][width]
+    uint16_t* xs_ff = nullptr;    // [parts][rows_padded][feed_forward]
+    float* partials = nullptr;
+    float* argmax_values = nullptr;
+    uint32_t* argmax_indices = nullptr;
+    std::vector<void*> owned;
+
+    char error[512] = {0};
+};
+
+namespace
+{
+using wsp::batch::u16;
+
+int fail(wsp_batch* b, int code, const char* message)
+{
+    std::snprintf(b->error, sizeof b->error, "%s", message);
+    return code;
+}
+
+int hip_fail(wsp_batch* b, hipError_t e, const char* what)
+{
+    if (e == hipSuccess)
+        return WSP_OK;
+    std::snprintf(b->error, sizeof b->error, "%s: %s", what, hipGetErrorString(e));
+    return WSP_ERR_HIP;
+}
+
+int parts_for(int wdtype)
+{
+    return wdtype == WSP_F16 ? 2 : 3;
+}
+
+size_t self_layer_stride(const wsp_batch* b)
+{
+    return (size_t) b->streams * b->shape.max_positions * b->shape.width;
+}
+
+size_t cross_layer_stride(const wsp_batch* b)
+{
+    return (size_t) b->streams * b->shape.cross_positions * b->shape.width;
+}
+
+void release(wsp_batch* b)
+{
+    for (void* p : b->owned)
+        (void) hipFree(p);
+    b->owned.clear();
+}
+
+template <typename T>
+hipError_t allocate(wsp_batch* b, T** out, size_t elements)
+{
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, std::max<size_t>(elements, 1) * sizeof(T));
+    if (e == hipSuccess)
+    {
+        b->owned.push_back(p);
+        *out = static_cast<T*>(p);
+    }
+    return e;
+}
+
+template <int WT>
+int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const uint32_t* tokens, int count, float* hidden,
+             float* logits, const float* mask, uint32_t* argmax_out)
+{
+    using namespace wsp::batch;
+    const wsp_decoder_shape& s = b->shape;
+    const int d = s.width, f = s.feed_forward_width, H = s.heads, hd = d / H;
+    const int rows = b->streams * count;
+    const size_t xs_part = (size_t) b->rows_padded * d, ff_part = (size_t) b->rows_padded * f;
+    const float eps = 1e-5f;
+    const float scale = 1.f / std::sqrt((float) hd);
+    hipStream_t st = b->stream;
+    hipError_t e = hipSuccess;
+
+    Norm n {};
+    n.h = b->h;
+    n.width = d;
+    n.eps = eps;
+    n.xs = b->xs;
+    n.xs_part = xs_part;
+    n.tokens = tokens;
+    n.token_table = T->token_embedding;
+    n.position_table = T->position_embedding;
+    n.position = b->position;
+    n.step_tokens = count;
+    n.vocabulary = s.vocabulary_size;
+
+    Product p {};
+    p.x = b->xs;
+    p.x_part = xs_part;
+    p.rows = rows;
+    p.inner = d;
+
+    Attend at {};
+    at.q = b->q;
+    at.step_tokens = count;
+    at.heads = H;
+    at.head_width = hd;
+    at.width = d;
+    at.scale = scale;
+    at.xs = b->xs;
+    at.xs_part = xs_part;
+    at.partials = b->partials;
+
+    for (int l = 0; l < s.layers; ++l)
+    {
+        const wsp_layer_tensors& L = T->layers[l];
+        float* self_k = b->self_keys + (size_t) l * self_layer_stride(b);
+        float* self_v = b->self_values + (size_t) l * self_layer_stride(b);
+        const float* cross_k = b->cross_keys + (size_t) l * cross_layer_stride(b);
+        const float* cross_v = b->cross_values + (size_t) l * cross_layer_stride(b);
+
+        // self attention
+        n.gamma = L.self_norm_w;
+        n.beta = L.self_norm_b;
+        n.y = nullptr;
+        if ((e = launch_norm<WT>(st, n, rows, l == 0)) != hipSuccess)
+            return hip_fail(b, e, "self-attention norm");
+
+        p.x = b->xs;
+        p.x_part = xs_part;
+        p.inner = d;
+        p.out = 3 * d;
+        p.w = L.self_qkv_w;
+        p.bias = L.self_qkv_b;
+        p.epilogue = kQkv;
+        p.q = b->q;
+        p.keys = self_k;
+        p.values = self_v;
+        p.stream_stride = (size_t) s.max_positions * d;
+        p.position = b->position;
+        p.step_tokens = count;
+        p.width = d;
+        if ((e = launch_product<WT>(st, p)) != hipSuccess)
+            return hip_fail(b, e, "q/k/v product");
+
+        at.keys = self_k;
+        at.values = self_v;
+        at.stream_stride = (size_t) s.max_positions * d;
+        at.k_count = b->position + count;
+        at.causal = 1;
+        if ((e = launch_attend<WT>(st, at, rows)) != hipSuccess)
+            return hip_fail(b, e, "self attention");
+
+        p.out = d;
+        p.w = L.self_out_w;
+        p.bias = L.self_out_b;
+        p.epilogue = kResidual;
+        p.y = b->h;
+        p.ldy = d;
+        if ((e = launch_product<WT>(st, p)) != hipSuccess)
+            return hip_fail(b, e, "self-attention output product");
+
+        // cross attention
+        n.gamma = L.cross_norm_w;
+        n.beta = L.cross_norm_b;
+        if ((e = launch_norm<WT>(st, n, rows, false)) != hipSuccess)
+            return hip_fail(b, e, "cross-attention norm");
+        p.w = L.cross_q_w;
+        p.bias = L.cross_q_b;
+        p.epilogue = kStore;
+        p.y = b->q;
+        if ((e = launch_product<WT>(st, p)) != hipSuccess)
+            return hip_fail(b, e, "cross query product");
+
+        at.keys = cross_k;
+        at.values = cross_v;
+        at.stream_stride = (size_t) s.cross_positions * d;
+        at.k_count = b->cross_rows;
+        at.causal = 0;
+        if ((e = launch_attend<WT>(st, at, rows)) != hipSuccess)
+            return hip_fail(b, e, "cross attention");
+
+        p.w = L.cross_out_w;
+        p.bias = L.cross_out_b;
+        p.epilogue = kResidual;
+        p.y = b->h;
+        if ((e = launch_product<WT>(st, p)) != hipSuccess)
+            return hip_fail(b, e, "cross-attention output product");
+
+        // feed-forward
+        n.gamma = L.final_norm_w;
+        n.beta = L.final_norm_b;
+        if ((e = launch_norm<WT>(st, n, rows, false)) != hipSuccess)
+            return hip_fail(b, e, "feed-forward norm");
+        p.out = f;
+        p.w = L.fc1_w;
+        p.bias = L.fc1_b;
+        p.epilogue = kGeluSplit;
+        p.xs_out = b->xs_ff;
+        p.xs_out_part = ff_part;
+        if ((e = launch_product<WT>(st, p)) != hipSuccess)
+            return hip_fail(b, e, "fc1 product");
+
+        p.x = b->xs_ff;
+        p.x_part = ff_part;
+        p.inner = f;
+        p.out = d;
+        p.w = L.fc2_w;
+        p.bias = L.fc2_b;
+        p.epilogue = kResidual;
+        p.y = b->h;
+        if ((e = launch_product<WT>(st, p)) != hipSuccess)
+            return hip_fail(b, e, "fc2 product");
+    }
+
+    n.gamma = T->final_norm_w;
+    n.beta = T->final_norm_b;
+    n.y = hidden;
+    if ((e = launch_norm<WT>(st, n, rows, false)) != hipSuccess)
+        return hip_fail(b, e, "final norm");
+
+    p.x = b->xs;
+    p.x_part = xs_part;
+    p.inner = d;
+    p.out = s.vocabulary_size;
+    p.w = T->logits_weight;
+    p.bias = nullptr;
+    p.epilogue = kStore;
+    p.y = logits;
+    p.ldy = s.vocabulary_size;
+    if ((e = launch_product<WT>(st, p)) != hipSuccess)
+        return hip_fail(b, e, "logits product");
+
+    if (argmax_out != nullptr)
+    {
+        const size_t V = (size_t) s.vocabulary_size;
+        e = wsp::ops::argmax_rows(st, logits + (size_t) (count - 1) * V, b->streams, (size_t) count * V,
+                                  s.vocabulary_size, mask, argmax_out, b->argmax_values, b->argmax_indices);
+        if (e != hipSuccess)
+            return hip_fail(b, e, "argmax");
+    }
+    b->position += count;
+    return WSP_OK;
+}
+} // namespace
+
+extern "C" {
+
+int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_tokens, int wdtype, int device,
+                     void* stream, wsp_batch** out)
+{
+    if (shape == nullptr || out == nullptr)
+        return WSP_ERR_ARGUMENT;
+    *out = nullptr;
+    const wsp_decoder_shape& s = *shape;
+    if (s.width <= 0 || s.heads <= 0 || s.layers <= 0 || s.feed_forward_width <= 0 || s.vocabulary_size <= 0
+        || s.max_positions <= 0 || s.cross_positions <= 0 || streams <= 0 || max_step_tokens <= 0)
+        return WSP_ERR_ARGUMENT;
+    if (wdtype != WSP_F16 && wdtype != WSP_BF16)
+        return WSP_ERR_LOGIC;
+    if (s.width % s.heads != 0 || (s.width / s.heads) % 4 != 0 || s.width / s.heads > 64 || s.width % 32 != 0
+        || s.feed_forward_width % 32 != 0)
+        return WSP_ERR_SHAPE;
+    if ((long long) streams * max_step_tokens > 16 * wsp::batch::kMaxRowTiles)
+        return WSP_ERR_CAPACITY;
+
+    wsp_batch* b = new (std::nothrow) wsp_batch;
+    if (b == nullptr)
+        return WSP_ERR_HIP;
+    b->shape = s;
+    b->streams = streams;
+    b->max_step_tokens = max_step_tokens;
+    b->wdtype = wdtype;
+    b->device = device;
+    b->stream = static_cast<hipStream_t>(stream);
+    b->rows_cap = streams * max_step_tokens;
+    b->rows_padded = 16 * wsp::batch::row_tiles(b->rows_cap);
+
+    const int P = parts_for(wdtype);
+    const size_t d = (size_t) s.width, H = (size_t) s.heads, hd = d / H;
+    const int most_chunks = std::max((s.cross_positions + wsp::batch::kTileKeys - 1) / wsp::batch::kTileKeys,
+                                     (s.max_positions + wsp::batch::kTileKeys - 1) / wsp::batch::kTileKeys);
+    const int groups = wsp::ops::argmax_groups(s.vocabulary_size);
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess)
+        e = allocate(b, &b->self_keys, (size_t) s.layers * self_layer_stride(b));
+    if (e == hipSuccess)
+        e = allocate(b, &b->self_values, (size_t) s.layers * self_layer_stride(b));
+    if (e == hipSuccess)
+        e = allocate(b, &b->cross_keys, (size_t) s.layers * cross_layer_stride(b));
+    if (e == hipSuccess)
+        e = allocate(b, &b->cross_values, (size_t) s.layers * cross_layer_stride(b));
+    if (e == hipSuccess)
+        e = allocate(b, &b->h, (size_t) b->rows_padded * d);
+    if (e == hipSuccess)
+        e = allocate(b, &b->q, (size_t) b->rows_padded * d);
+    if (e == hipSuccess)
+        e = allocate(b, &b->xs, (size_t) P * b->rows_padded * d);
+    if (e == hipSuccess)
+        e = allocate(b, &b->xs_ff, (size_t) P * b->rows_padded * s.feed_forward_width);
+    if (e == hipSuccess)
+        e = allocate(b, &b->partials, (size_t) b->rows_cap * H * most_chunks * (hd + 2));
+    if (e == hipSuccess)
+        e = allocate(b, &b->argmax_values, (size_t) streams * groups);
+    if (e == hipSuccess)
+        e = allocate(b, &b->argmax_indices, (size_t) streams * groups);
+    // Padding rows of the split buffers are read by the products (their sums
+    // are discarded); zero them once so they hold finite values.
+    if (e == hipSuccess)
+        e = hipMemsetAsync(b->xs, 0, (size_t) P * b->rows_padded * d * sizeof(u16), b->stream);
+    if (e == hipSuccess)
+        e = hipMemsetAsync(b->xs_ff, 0, (size_t) P * b->rows_padded * s.feed_forward_width * sizeof(u16), b->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(b->stream);
+    if (e != hipSuccess)
+    {
+        release(b);
+        delete b;
+        return WSP_ERR_HIP;
+    }
+    *out = b;
+    return WSP_OK;
+}
+
+void wsp_batch_destroy(wsp_batch* b)
+{
+    if (b == nullptr)
+        return;
+    (void) hipSetDevice(b->device);
+    (void) hipStreamSynchronize(b->stream);
+    release(b);
+    delete b;
+}
+
+const char* wsp_batch_last_error(const wsp_batch* b)
+{
+    return b == nullptr ? "null batch" : b->error;
+}
+
+int wsp_batch_position(const wsp_batch* b)
+{
+    return b == nullptr ? -1 : b->position;
+}
+
+int wsp_batch_cross_rows(const wsp_batch* b)
+{
+    return b == nullptr ? -1 : b->cross_rows;
+}
+
+int wsp_batch_begin(wsp_batch* b, const wsp_cross_tensors* layers, int wdtype, const float* encoder_rows,
+                    int cross_rows)
+{
+    if (b == nullptr)
+        return WSP_ERR_ARGUMENT;
+    b->error[0] = 0;
+    if (layers == nullptr || encoder_rows == nullptr)
+        return fail(b, WSP_ERR_ARGUMENT, "wsp_batch_begin: null layer table or encoder rows");
+    if (cross_rows == 0)
+        cross_rows = b->shape.cross_positions;
+    if (cross_rows < 0 || cross_rows > b->shape.cross_positions)
+        return fail(b, WSP_ERR_SHAPE, "wsp_batch_begin: more cross rows than the batch was sized for");
+    const int d = b->shape.width;
+    for (int l = 0; l < b->shape.layers; ++l)
+    {
+        const wsp_cross_tensors& L = layers[l];
+        if (L.key_w == nullptr || L.value_w == nullptr)
+            return fail(b, WSP_ERR_ARGUMENT, "wsp_batch_begin: a layer without cross key/value weights");
+        float* keys = b->cross_keys + (size_t) l * cross_layer_stride(b);
+        float* values = b->cross_values + (size_t) l * cross_layer_stride(b);
+        hipError_t e = hipSuccess;
+        if (wsp::ops::tile_product_fits(wdtype, d, 2 * d, d, encoder_rows))
+        {
+            // Every stream's rows in one launch: row r of the encoder block is
+            // row r % cross_rows of stream r / cross_rows.
+            wsp::ops::TileProduct p {};
+            p.x = encoder_rows;
+            p.rows = b->streams * cross_rows;
+            p.inner = d;
+            p.w0 = L.key_w;
+            p.w1 = L.value_w;
+            p.split = d;
+            p.out = 2 * d;
+            p.bias1 = L.value_b;
+            p.y0 = keys;
+            p.y1 = values;
+            p.ldy = d;
+            p.rows_per_group = cross_rows;
+            p.group_stride = (size_t) b->shape.cross_positions * d;
+            p.wdtype = wdtype;
+            e = wsp::ops::tile_product(b->stream, p);
+        }
+        else
+            for (int c = 0; c < b->streams && e == hipSuccess; ++c)
+            {
+                const float* x = encoder_rows + (size_t) c * cross_rows * d;
+                const size_t at = (size_t) c * b->shape.cross_positions * d;
+                e = wsp::ops::linear(b->stream, x, cross_rows, d, L.key_w, wdtype, nullptr, keys + at, d, 0);
+                if (e == hipSuccess)
+                    e = wsp::ops::linear(b->stream, x, cross_rows, d, L.value_w, wdtype, L.value_b, values + at, d, 0);
+            }
+        if (e != hipSuccess)
+            return hip_fail(b, e, "cross key/value projection");
+    }
+    b->cross_rows = cross_rows;
+    b->position = 0;
+    return WSP_OK;
+}
+
+int wsp_batch_step(wsp_batch* b, const wsp_decoder_tensors* tensors, const uint32_t* tokens, int count,
+                   float* hidden, float* logits, const float* mask, uint32_t* argmax_out)
+{
+    if (b == nullptr)
+        return WSP_ERR_ARGUMENT;
+    b->error[0] = 0;
+    if (tensors == nullptr || tensors->layers == nullptr || tokens == nullptr || logits == nullptr)
+        return fail(b, WSP_ERR_ARGUMENT, "wsp_batch_step: null tensors, tokens or logits");
+    if (count <= 0 || count > b->max_step_tokens)
+        return fail(b, WSP_ERR_CAPACITY, "wsp_batch_step: more tokens per stream than the batch was sized for");
+    if (b->cross_rows <= 0)
+        return fail(b, WSP_ERR_LOGIC, "wsp_batch_step: no sequence begun");
+    if (b->position + count > b->shape.max_positions)
+        return fail(b, WSP_ERR_SHAPE, "wsp_batch_step: the step runs past max_positions");
+    if (tensors->wdtype != b->wdtype || tensors->logits_wdtype != b->wdtype)
+        return fail(b, WSP_ERR_LOGIC, "wsp_batch_step: projections and logits must share the batch's 16-bit storage");
+    (void) hipSetDevice(b->device);
+    return b->wdtype == WSP_F16 ? run_step<wsp::kF16>(b, tensors, tokens, count, hidden, logits, mask, argmax_out)
+                                : run_step<wsp::kBF16>(b, tensors, tokens, count, hidden, logits, mask, argmax_out);
+}
+
+int wsp_batch_self_cache(const wsp_batch* b, int layer, const float** keys, const float** values)
+{
+    if (b == nullptr || keys == nullptr || values == nullptr || layer < 0 || layer >= b->shape.layers)
+        return WSP_ERR_ARGUMENT;
+    *keys = b->self_keys + (size_t) layer * self_layer_stride(b);
+    *values = b->self_values + (size_t) layer * self_layer_stride(b);
+    return WSP_OK;
+}
+
+int wsp_batch_cross_cache(const wsp_batch* b, int layer, const float** keys, const float** values)
+{
+    if (b == nullptr || keys == nullptr || values == nullptr || layer < 0 || layer >= b->shape.layers)
+        return WSP_ERR_ARGUMENT;
+    *keys = b->cross_keys + (size_t) layer * cross_layer_stride(b);
+    *values = b->cross_values + (size_t) layer * cross_layer_stride(b);
+    return WSP_OK;
+}
+
+} // extern "C"

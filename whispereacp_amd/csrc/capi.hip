@@ -237,10 +237,7 @@ int wsp_hip_project_cross_kv(wsp_hip_ctx* ctx, const float* x, int rows, int wid
     if (rows > ctx->shape.cross_positions)
         return fail(ctx, WSP_ERR_CAPACITY, "cross K/V: %d rows past the %d cross positions", rows,
                     ctx->shape.cross_positions);
-    int status = wsp::cross_kv_projection(ctx, x, rows, width, wk, nullptr, wdtype, k_out);
-    if (status == WSP_OK)
-        status = wsp::cross_kv_projection(ctx, x, rows, width, wv, bv, wdtype, v_out);
-    return status;
+    return wsp::cross_kv_projection(ctx, x, rows, width, wk, wv, bv, wdtype, k_out, v_out);
 }
 
 } // extern "C"

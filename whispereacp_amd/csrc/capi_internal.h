@@ -39,7 +39,7 @@ void fused_release(Context* ctx);
 bool fused_persistent(const Context* ctx);
 int fused_status(Context* ctx, int* status, int clear);
 
-// cross_kv.hip: out = X·Wᵀ (+ bias) for `rows` rows of `width`.
-int cross_kv_projection(Context* ctx, const float* x, int rows, int width, const void* weight,
-                        const float* bias, int wdtype, float* out);
+// cross_kv.hip: K = X·Wkᵀ and V = X·Wvᵀ + bv for `rows` rows of `width`.
+int cross_kv_projection(Context* ctx, const float* x, int rows, int width, const void* wk, const void* wv,
+                        const float* bv, int wdtype, float* k_out, float* v_out);
 } // namespace wsp

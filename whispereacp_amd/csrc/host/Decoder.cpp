@@ -216,43 +216,15 @@ void Decoder::fusedStep(Pass& pass, const BufferRange& tokens, const DecoderWeig
     fusedLayers.resize((std::size_t) decoderShape.layers);
     for (int l = 0; l < decoderShape.layers; ++l)
     {
-        const auto& w = weights.layers[(std::size_t) l];
         const auto i = (std::size_t) l;
-        auto f = [](const TensorBuffer& t) { return static_cast<const float*>(t.data()); };
         wsp_layer_tensors& L = fusedLayers[i];
-        L.self_norm_w = f(w.selfAttentionNormWeight);
-        L.self_norm_b = f(w.selfAttentionNormBias);
-        L.self_qkv_w = w.selfQueryWeight.data();
-        L.self_qkv_b = f(w.selfQkvBias);
-        L.self_out_w = w.selfAttentionOutputWeight.data();
-        L.self_out_b = f(w.selfAttentionOutputBias);
-        L.cross_norm_w = f(w.crossAttentionNormWeight);
-        L.cross_norm_b = f(w.crossAttentionNormBias);
-        L.cross_q_w = w.crossQueryWeight.data();
-        L.cross_q_b = f(w.crossQueryBias);
-        L.cross_out_w = w.crossAttentionOutputWeight.data();
-        L.cross_out_b = f(w.crossAttentionOutputBias);
-        L.final_norm_w = f(w.finalNormWeight);
-        L.final_norm_b = f(w.finalNormBias);
-        L.fc1_w = w.feedForwardWeight.data();
-        L.fc1_b = f(w.feedForwardBias);
-        L.fc2_w = w.feedForwardOutputWeight.data();
-        L.fc2_b = f(w.feedForwardOutputBias);
+        L = layerTable(weights.layers[i]);
         L.self_keys = hipNet.cacheData(caches.selfKeys[i]);
         L.self_values = hipNet.cacheData(caches.selfValues[i]);
         L.cross_keys = hipNet.cacheData(caches.crossKeys[i]);
         L.cross_values = hipNet.cacheData(caches.crossValues[i]);
     }
-
-    wsp_decoder_tensors tensors {};
-    tensors.wdtype = wsp_dtype_of(*weights.uniformProjectionStorage());
-    tensors.token_embedding = static_cast<const float*>(weights.tokenEmbedding.data());
-    tensors.logits_weight = weights.logitsWeight().data();
-    tensors.logits_wdtype = wsp_dtype_of(weights.logitsWeight().type);
-    tensors.position_embedding = static_cast<const float*>(weights.positionalEmbedding.data());
-    tensors.final_norm_w = static_cast<const float*>(weights.finalNormWeight.data());
-    tensors.final_norm_b = static_cast<const float*>(weights.finalNormBias.data());
-    tensors.layers = fusedLayers.data();
+    const wsp_decoder_tensors tensors = decoderTable(weights, fusedLayers);
 
     const int status = wsp_hip_decoder_step(
         hipNet.context(), &tensors, static_cast<const uint32_t*>(tokens.data()), decodedPositions,

@@ -6,6 +6,7 @@
 #include "host_common.h"
 
 #include <cstring>
+#include <stdexcept>
 #include <sstream>
 
 namespace WSP
@@ -311,5 +312,47 @@ std::optional<WeightStorage> DecoderWeights::uniformProjectionStorage() const
                 return std::nullopt;
     }
     return first;
+}
+
+wsp_layer_tensors layerTable(const DecoderLayerWeights& w)
+{
+    auto f = [](const TensorBuffer& t) { return static_cast<const float*>(t.data()); };
+    wsp_layer_tensors L {};
+    L.self_norm_w = f(w.selfAttentionNormWeight);
+    L.self_norm_b = f(w.selfAttentionNormBias);
+    L.self_qkv_w = w.selfQueryWeight.data();
+    L.self_qkv_b = f(w.selfQkvBias);
+    L.self_out_w = w.selfAttentionOutputWeight.data();
+    L.self_out_b = f(w.selfAttentionOutputBias);
+    L.cross_norm_w = f(w.crossAttentionNormWeight);
+    L.cross_norm_b = f(w.crossAttentionNormBias);
+    L.cross_q_w = w.crossQueryWeight.data();
+    L.cross_q_b = f(w.crossQueryBias);
+    L.cross_out_w = w.crossAttentionOutputWeight.data();
+    L.cross_out_b = f(w.crossAttentionOutputBias);
+    L.final_norm_w = f(w.finalNormWeight);
+    L.final_norm_b = f(w.finalNormBias);
+    L.fc1_w = w.feedForwardWeight.data();
+    L.fc1_b = f(w.feedForwardBias);
+    L.fc2_w = w.feedForwardOutputWeight.data();
+    L.fc2_b = f(w.feedForwardOutputBias);
+    return L;
+}
+
+wsp_decoder_tensors decoderTable(const DecoderWeights& weights, const std::vector<wsp_layer_tensors>& layers)
+{
+    const auto storage = weights.uniformProjectionStorage();
+    if (!storage)
+        throw std::logic_error("the fused and batched steps need one storage for every projection weight");
+    wsp_decoder_tensors tensors {};
+    tensors.wdtype = wsp_dtype_of(*storage);
+    tensors.token_embedding = static_cast<const float*>(weights.tokenEmbedding.data());
+    tensors.logits_weight = weights.logitsWeight().data();
+    tensors.logits_wdtype = wsp_dtype_of(weights.logitsWeight().type);
+    tensors.position_embedding = static_cast<const float*>(weights.positionalEmbedding.data());
+    tensors.final_norm_w = static_cast<const float*>(weights.finalNormWeight.data());
+    tensors.final_norm_b = static_cast<const float*>(weights.finalNormBias.data());
+    tensors.layers = layers.data();
+    return tensors;
 }
 } // namespace WSP

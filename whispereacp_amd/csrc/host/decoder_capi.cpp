@@ -3,9 +3,11 @@
 // plus its kind and message.
 #include "../../../include/wsp_decoder.h"
 #include "../../../include/whispereacp/Argmax.h"
+#include "../../../include/whispereacp/BatchedDecoder.h"
 #include "../../../include/whispereacp/Decoder.h"
 #include "../../../include/whispereacp/GreedyDecoder.h"
 
+#include <algorithm>
 #include <memory>
 #include <new>
 #include <stdexcept>
@@ -24,10 +26,20 @@ struct wsp_decoder
     int errorKind = WSP_KIND_NONE;
 };
 
+struct wsp_batch_decoder
+{
+    WSP::DecoderShape shape;
+    WSP::Device device;
+    std::unique_ptr<WSP::DecoderWeights> weights;
+    std::unique_ptr<WSP::BatchedDecoder> decoder;
+    std::string error;
+    int errorKind = WSP_KIND_NONE;
+};
+
 namespace
 {
-template <typename Body>
-int guarded(wsp_decoder* d, Body body)
+template <typename Handle, typename Body>
+int guarded(Handle* d, Body body)
 {
     if (d == nullptr)
         return WSP_ERR_ARGUMENT;
@@ -68,6 +80,33 @@ WSP::BufferRange range(const void* p, std::size_t bytes)
 {
     return {const_cast<void*>(p), 0, bytes};
 }
+
+WSP::DecoderShape checkedShape(const wsp_decoder_shape* shape)
+{
+    WSP::DecoderShape s {shape->width,           shape->heads,         shape->layers,       shape->feed_forward_width,
+                         shape->vocabulary_size, shape->max_positions, shape->cross_positions};
+    if (s.width <= 0 || s.heads <= 0 || s.width % s.heads != 0 || s.layers <= 0 || s.feedForwardWidth <= 0
+        || s.vocabularySize <= 0 || s.maxPositions <= 0 || s.crossPositions <= 0)
+        throw WSP::ModelError("a decoder shape needs positive extents and a width divisible by its heads");
+    return s;
+}
+
+WSP::MapTensorSource sourceOf(const wsp_tensor_entry* tensors, int count)
+{
+    WSP::MapTensorSource source;
+    for (int i = 0; i < count; ++i)
+    {
+        const wsp_tensor_entry& e = tensors[i];
+        if (e.name == nullptr || e.dtype == nullptr || e.rank < 0 || (e.rank > 0 && e.extents == nullptr))
+            throw std::invalid_argument("tensor entry " + std::to_string(i) + " is incomplete");
+        WSP::HostTensor t;
+        t.dtype = e.dtype;
+        t.extents.assign(e.extents, e.extents + e.rank);
+        t.data = e.data;
+        source.add(e.name, std::move(t));
+    }
+    return source;
+}
 } // namespace
 
 extern "C" {
@@ -82,26 +121,10 @@ int wsp_decoder_create(const wsp_decoder_shape* shape, const wsp_tensor_entry* t
     if (d == nullptr)
         return WSP_ERR_CAPACITY;
     const int status = guarded(d, [&] {
-        d->shape = {shape->width,           shape->heads,         shape->layers,       shape->feed_forward_width,
-                    shape->vocabulary_size, shape->max_positions, shape->cross_positions};
-        if (d->shape.width <= 0 || d->shape.heads <= 0 || d->shape.width % d->shape.heads != 0 || d->shape.layers <= 0
-            || d->shape.feedForwardWidth <= 0 || d->shape.vocabularySize <= 0 || d->shape.maxPositions <= 0
-            || d->shape.crossPositions <= 0)
-            throw WSP::ModelError("a decoder shape needs positive extents and a width divisible by its heads");
+        d->shape = checkedShape(shape);
         d->device = WSP::Device {device};
         d->stream = stream;
-        WSP::MapTensorSource source;
-        for (int i = 0; i < count; ++i)
-        {
-            const wsp_tensor_entry& e = tensors[i];
-            if (e.name == nullptr || e.dtype == nullptr || e.rank < 0 || (e.rank > 0 && e.extents == nullptr))
-                throw std::invalid_argument("tensor entry " + std::to_string(i) + " is incomplete");
-            WSP::HostTensor t;
-            t.dtype = e.dtype;
-            t.extents.assign(e.extents, e.extents + e.rank);
-            t.data = e.data;
-            source.add(e.name, std::move(t));
-        }
+        const WSP::MapTensorSource source = sourceOf(tensors, count);
         d->weights = std::make_unique<WSP::DecoderWeights>(
             source, d->shape, packing == 1 ? WSP::WeightPacking::ExactHalf : WSP::WeightPacking::Float, d->device);
         d->decoder = std::make_unique<WSP::Decoder>(d->shape);
@@ -248,6 +271,90 @@ int wsp_decoder_greedy(wsp_decoder* d, const float* encoder_rows, int cross_posi
         if (decode_seconds != nullptr)
             *decode_seconds = run.decodeSeconds;
     });
+}
+
+int wsp_batch_decoder_create(const wsp_decoder_shape* shape, const wsp_tensor_entry* tensors, int count,
+                             int packing, int streams, int max_step_tokens, int device, void* stream,
+                             wsp_batch_decoder** out)
+{
+    if (shape == nullptr || out == nullptr || (count > 0 && tensors == nullptr))
+        return WSP_ERR_ARGUMENT;
+    *out = nullptr;
+    auto* d = new (std::nothrow) wsp_batch_decoder {};
+    if (d == nullptr)
+        return WSP_ERR_CAPACITY;
+    const int status = guarded(d, [&] {
+        d->shape = checkedShape(shape);
+        d->device = WSP::Device {device};
+        const WSP::MapTensorSource source = sourceOf(tensors, count);
+        d->weights = std::make_unique<WSP::DecoderWeights>(
+            source, d->shape, packing == 1 ? WSP::WeightPacking::ExactHalf : WSP::WeightPacking::Float, d->device);
+        d->decoder = std::make_unique<WSP::BatchedDecoder>(d->shape, streams, max_step_tokens);
+        d->decoder->prepare(*d->weights, d->device, stream);
+    });
+    if (status != WSP_OK)
+    {
+        d->decoder.reset();
+        d->weights.reset();
+    }
+    *out = d;
+    return status;
+}
+
+void wsp_batch_decoder_destroy(wsp_batch_decoder* d)
+{
+    delete d;
+}
+
+const char* wsp_batch_decoder_last_error(const wsp_batch_decoder* d)
+{
+    return d == nullptr ? "no decoder" : d->error.c_str();
+}
+
+int wsp_batch_decoder_last_error_kind(const wsp_batch_decoder* d)
+{
+    return d == nullptr ? WSP_KIND_INVALID_ARGUMENT : d->errorKind;
+}
+
+int wsp_batch_decoder_begin(wsp_batch_decoder* d, const float* encoder_rows, int cross_position_count)
+{
+    return guarded(d, [&] {
+        if (!d->decoder)
+            throw std::logic_error("this batched decoder failed to build");
+        const int rows = cross_position_count == 0 ? d->shape.crossPositions : cross_position_count;
+        const std::size_t bytes = sizeof(float) * (std::size_t) d->decoder->streams() * (std::size_t) std::max(rows, 0)
+                                  * d->shape.width;
+        WSP::Pass pass(d->decoder->hipStream());
+        d->decoder->beginSequences(pass, range(encoder_rows, bytes), *d->weights, cross_position_count);
+    });
+}
+
+int wsp_batch_decoder_step(wsp_batch_decoder* d, const uint32_t* tokens, int count, float* logits, const float* mask,
+                           uint32_t* argmax_slots)
+{
+    return guarded(d, [&] {
+        if (!d->decoder)
+            throw std::logic_error("this batched decoder failed to build");
+        const std::size_t rows = (std::size_t) d->decoder->streams() * (std::size_t) std::max(count, 0);
+        WSP::Pass pass(d->decoder->hipStream());
+        const auto t = range(tokens, rows * sizeof(uint32_t));
+        const auto l = range(logits, rows * d->shape.vocabularySize * sizeof(float));
+        if (argmax_slots == nullptr)
+            d->decoder->step(pass, t, count, *d->weights, l);
+        else
+            d->decoder->stepAndSample(pass, t, count, *d->weights, l, mask,
+                                      range(argmax_slots, (std::size_t) d->decoder->streams() * sizeof(uint32_t)));
+    });
+}
+
+int wsp_batch_decoder_position(const wsp_batch_decoder* d)
+{
+    return d == nullptr || !d->decoder ? -1 : d->decoder->position();
+}
+
+const float* wsp_batch_decoder_hidden_states(const wsp_batch_decoder* d)
+{
+    return d == nullptr || !d->decoder ? nullptr : static_cast<const float*>(d->decoder->hiddenStates().data());
 }
 
 } // extern "C"

@@ -16,6 +16,34 @@ constexpr int kAttentionChunkKeys = 1024; // longest key chunk one workgroup sco
 hipError_t linear(hipStream_t stream, const float* x, int rows, int inner, const void* weight,
                   int wdtype, const float* bias, float* y, int out, int flags);
 
+// The matrix-core tall product (mfma_product.hip): y = X·Wᵀ (+ bias, GELU,
+// residual as in `flags`) for fp32 X [rows, inner] and 16-bit W. Output
+// columns n < split read W rows from w0 and write y0 (bias0); the rest read
+// w1 row n - split and write y1 (bias1) — the key and value projections in one
+// launch. Output row r of column c lands at
+// (r / rows_per_group)·group_stride + (r % rows_per_group)·ldy + c.
+struct TileProduct
+{
+    const float* x;
+    int rows, inner;
+    const void* w0;
+    const void* w1;
+    int split, out;
+    const float* bias0;
+    const float* bias1;
+    float* y0;
+    float* y1;
+    int ldy;
+    int rows_per_group;
+    size_t group_stride;
+    int flags;
+    int wdtype;
+};
+
+// 16-bit weights, inner % 32 == 0, out and split multiples of 128, X 16-byte aligned.
+bool tile_product_fits(int wdtype, int inner, int out, int split, const void* x);
+hipError_t tile_product(hipStream_t stream, const TileProduct& product);
+
 hipError_t layernorm(hipStream_t stream, const float* x, const float* gamma, const float* beta,
                      float* y, int rows, int width, float eps);
 
@@ -37,4 +65,9 @@ int argmax_groups(int row_length);
 hipError_t argmax(hipStream_t stream, const float* logits, int rows, int row_length,
                   const float* mask, uint32_t* out, float* partial_values,
                   uint32_t* partial_indices);
+
+// The same over rows `row_stride` floats apart.
+hipError_t argmax_rows(hipStream_t stream, const float* logits, int rows, size_t row_stride,
+                       int row_length, const float* mask, uint32_t* out, float* partial_values,
+                       uint32_t* partial_indices);
 } // namespace wsp::ops

@@ -420,14 +420,14 @@ __device__ __forceinline__ void block_argmax(float& v, uint32_t& i)
 }
 
 __global__ void __launch_bounds__(kBlock) argmax_partial_kernel(const float* __restrict__ logits,
-                                                                int row_length,
+                                                                size_t row_stride, int row_length,
                                                                 const float* __restrict__ mask,
                                                                 int groups,
                                                                 float* __restrict__ pv,
                                                                 uint32_t* __restrict__ pi)
 {
     const int row = blockIdx.x / groups, part = blockIdx.x % groups;
-    const float* values = logits + (size_t) row * row_length;
+    const float* values = logits + (size_t) row * row_stride;
     float bv = 0.f;
     uint32_t bi = kUnchosen;
     for (int j = part * kBlock + threadIdx.x; j < row_length; j += groups * kBlock)
@@ -520,6 +520,23 @@ hipError_t linear(hipStream_t stream, const float* x, int rows, int inner, const
             default: return launch_gemv<kBF16>(stream, x, rows, inner, weight, bias, y, out, flags);
         }
     }
+    if (tile_product_fits(wdtype, inner, out, out, x))
+    {
+        TileProduct p {};
+        p.x = x;
+        p.rows = rows;
+        p.inner = inner;
+        p.w0 = p.w1 = weight;
+        p.split = p.out = out;
+        p.bias0 = p.bias1 = bias;
+        p.y0 = p.y1 = y;
+        p.ldy = out;
+        p.rows_per_group = rows;
+        p.group_stride = 0;
+        p.flags = flags;
+        p.wdtype = wdtype;
+        return tile_product(stream, p);
+    }
     switch (wdtype)
     {
         case kF32: return launch_gemm<kF32>(stream, x, rows, inner, weight, bias, y, out, flags);
@@ -589,9 +606,17 @@ hipError_t argmax(hipStream_t stream, const float* logits, int rows, int row_len
                   const float* mask, uint32_t* out, float* partial_values,
                   uint32_t* partial_indices)
 {
+    return argmax_rows(stream, logits, rows, (size_t) row_length, row_length, mask, out, partial_values,
+                       partial_indices);
+}
+
+hipError_t argmax_rows(hipStream_t stream, const float* logits, int rows, size_t row_stride,
+                       int row_length, const float* mask, uint32_t* out, float* partial_values,
+                       uint32_t* partial_indices)
+{
     const int groups = argmax_groups(row_length);
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(rows * groups), dim3(kBlock), 0, stream, logits,
-                       row_length, mask, groups, partial_values, partial_indices);
+                       row_stride, row_length, mask, groups, partial_values, partial_indices);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;

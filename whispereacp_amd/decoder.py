@@ -222,6 +222,64 @@ class Decoder:
         return list(out[:count.value]), seconds.value
 
 
+class BatchedDecoder:
+    """DecoderWeights + BatchedDecoder over the gfx950 library
+    (wsp_batch_decoder_* in include/wsp_decoder.h): `streams` independent
+    sequences that advance together and share one weight read per step."""
+
+    def __init__(self, shape: DecoderShape, decoder_file: DecoderFile, streams: int, max_step_tokens: int = 4,
+                 packing: str = "ExactHalf", device: int = 0):
+        self.lib = N.load()
+        self.shape = shape
+        self.streams = streams
+        entries, keep = tensor_entries(decoder_file)
+        self._cshape = c_shape(shape)
+        handle = ctypes.c_void_p()
+        status = self.lib.wsp_batch_decoder_create(ctypes.byref(self._cshape), entries, len(decoder_file),
+                                                   1 if packing == "ExactHalf" else 0, streams, max_step_tokens,
+                                                   device, current_stream(), ctypes.byref(handle))
+        del keep
+        self.handle = handle
+        if status != N.WSP_OK:
+            message = self.lib.wsp_batch_decoder_last_error(handle).decode() if handle else "create failed"
+            kind = self.lib.wsp_batch_decoder_last_error_kind(handle) if handle else N.WSP_KIND_NONE
+            self.close()
+            _raise(kind, message, status)
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.wsp_batch_decoder_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+    def _check(self, status: int):
+        if status != N.WSP_OK:
+            _raise(self.lib.wsp_batch_decoder_last_error_kind(self.handle),
+                   self.lib.wsp_batch_decoder_last_error(self.handle).decode(), status)
+
+    def begin(self, encoder_rows: torch.Tensor, cross_position_count: int = 0):
+        """encoder_rows: device f32 [streams, rows, width]."""
+        self._check(self.lib.wsp_batch_decoder_begin(self.handle, ptr(encoder_rows), cross_position_count))
+
+    def step(self, tokens: torch.Tensor, count: int, logits: torch.Tensor, mask: Optional[torch.Tensor] = None,
+             argmax_slots: Optional[torch.Tensor] = None):
+        """tokens: device int32 [streams, count]; logits [streams·count, vocabulary]."""
+        self._check(self.lib.wsp_batch_decoder_step(self.handle, ptr(tokens), count, ptr(logits), ptr(mask),
+                                                    ptr(argmax_slots)))
+
+    @property
+    def position(self) -> int:
+        return self.lib.wsp_batch_decoder_position(self.handle)
+
+    def read_hidden(self, rows: int) -> np.ndarray:
+        out = torch.empty((rows, self.shape.width), dtype=torch.float32, device="cuda")
+        copy_device(out, self.lib.wsp_batch_decoder_hidden_states(self.handle), rows * self.shape.width * 4)
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+
 _hip = None
 
 

@@ -20,9 +20,11 @@ BF16 array is the uint16 bit pattern (round to nearest even from float32).
 
 from __future__ import annotations
 
+import concurrent.futures
 import dataclasses
 import math
-from typing import Dict, List, Tuple
+import os
+from typing import Dict, List, Optional, Tuple
 
 import numpy as np
 
@@ -175,19 +177,42 @@ def shifted_values(count: int, seed: int, value_range: float) -> np.ndarray:
     return (spread_values(count, seed, value_range) + np.float32(1.0)).astype(np.float32)
 
 
+def _box_muller(raw: np.ndarray, out: np.ndarray, std: float) -> None:
+    u1 = (raw[0::2].astype(np.float64) + 0.5) / 4294967296.0
+    u2 = (raw[1::2].astype(np.float64) + 0.5) / 4294967296.0
+    np.log(u1, out=u1)
+    u1 *= -2.0
+    np.sqrt(u1, out=u1)
+    u2 *= 2.0 * math.pi
+    first = np.cos(u2)
+    first *= u1
+    first *= std
+    out[0::2] = first
+    np.sin(u2, out=u2)
+    u2 *= u1
+    u2 *= std
+    out[1::2] = u2
+
+
+_pool: Optional[concurrent.futures.ThreadPoolExecutor] = None
+
+
 def normal_values(count: int, seed: int, std: float) -> np.ndarray:
     """N(0, std) as float32 by Box-Muller over mt19937 pairs: each pair of raw
-    draws gives r*cos(2*pi*u2) then r*sin(2*pi*u2), r = sqrt(-2 ln u1)."""
+    draws gives r*cos(2*pi*u2) then r*sin(2*pi*u2), r = sqrt(-2 ln u1), all in
+    double. The transform runs in chunks on a thread pool (numpy releases the
+    GIL), which changes nothing in the values."""
+    global _pool
+    if _pool is None:
+        _pool = concurrent.futures.ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1))
     pairs = (count + 1) // 2
-    raw = mt19937_raw(seed, 2 * pairs).astype(np.float64)
-    u1 = (raw[0::2] + 0.5) / 4294967296.0
-    u2 = (raw[1::2] + 0.5) / 4294967296.0
-    r = np.sqrt(-2.0 * np.log(u1))
-    theta = 2.0 * math.pi * u2
+    raw = mt19937_raw(seed, 2 * pairs)
     out = np.empty(2 * pairs, dtype=np.float64)
-    out[0::2] = r * np.cos(theta)
-    out[1::2] = r * np.sin(theta)
-    return (std * out[:count]).astype(np.float32)
+    step = 1 << 20
+    jobs = [_pool.submit(_box_muller, raw[i:i + step], out[i:i + step], std) for i in range(0, 2 * pairs, step)]
+    for job in jobs:
+        job.result()
+    return out[:count].astype(np.float32)
 
 
 def f32_to_bf16_bits(values: np.ndarray) -> np.ndarray:
@@ -302,9 +327,10 @@ def file_order(layers: int) -> List[str]:
 def workload_decoder_file(shape: DecoderShape, dtype: str, base_seed: int = 1000) -> DecoderFile:
     """The benchmark weights: N(0, 0.02) for projections, biases and both
     embeddings; LayerNorm gamma 1 and beta 0. Tensor i in file order gets seed
-    base_seed + i. Every tensor is stored in ``dtype``."""
-    out: DecoderFile = {}
-    for index, name in enumerate(file_order(shape.layers)):
+    base_seed + i. Every tensor is stored in ``dtype``. Tensors are generated
+    on a few threads; each depends on its own seed only."""
+
+    def make(index: int, name: str) -> StoredTensor:
         extents = tensor_extents(shape, name)
         count = int(np.prod(extents))
         if is_norm_weight(name):
@@ -313,8 +339,12 @@ def workload_decoder_file(shape: DecoderShape, dtype: str, base_seed: int = 1000
             values = np.zeros(count, dtype=np.float32)
         else:
             values = normal_values(count, base_seed + index, 0.02)
-        out[name] = StoredTensor(name, dtype, extents, store(values, dtype))
-    return out
+        return StoredTensor(name, dtype, extents, store(values, dtype))
+
+    names = file_order(shape.layers)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=4) as pool:
+        tensors = list(pool.map(make, range(len(names)), names))
+    return {t.name: t for t in tensors}
 
 
 def synthetic_encoder_output(shape: DecoderShape) -> np.ndarray:
