@@ -99,9 +99,9 @@ def cpu_baseline(shape, decoder_file, encoder, prompt, gpu_tokens, budget_s: flo
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=224)
+    parser.add_argument("--steps", type=int, default=None, help="timed steps (default: the workload's own)")
     parser.add_argument("--warmup", type=int, default=16)
-    parser.add_argument("--workload", default="small", choices=["base.en", "small"])
+    parser.add_argument("--workload", default="small", choices=["base.en", "small", "medium", "large-v3"])
     parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of oracle time (0: skip)")
     parser.add_argument("--unfused", action="store_true", help="time the per-op kernel sequence instead")
     parser.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -131,6 +131,11 @@ def main():
     from whispereacp_amd.decoder import Decoder, to_device
 
     w = S.WORKLOADS[args.workload]
+    if args.steps is None:
+        args.steps = w["steps"]
+    if w["streams"] > 1:
+        bench_streams(args, w)
+        return
     shape = S.workload_shape(args.workload)
     prompt = S.SOT_PREFIX[shape.vocabulary_size]
     if len(prompt) + args.steps > shape.max_positions or len(prompt) + args.warmup > shape.max_positions:
@@ -218,6 +223,117 @@ def main():
                      "kernel": "step_kernel (one persistent launch per decode step)" if not args.unfused
                      else "per-op kernel sequence",
                      "bytes_per_step": round(bytes_per_step)},
+        "cpu_baseline": baseline,
+        "parity": parity,
+        "host_seconds": round(host_s, 4),
+        "host_enqueue_seconds": round(enqueue_s, 4),
+    }
+    print(json.dumps(line))
+
+
+def bench_streams(args, w):
+    """The batched configurations: w["streams"] independent sequences, each
+    with its own N(0,1) encoder states, decoded together (BatchedDecoder), one
+    token per stream per step. With large-v3 the cross K/V projection of every
+    stream runs inside the timed region, as that configuration is quoted."""
+    import numpy as np
+    import torch
+    from whispereacp_amd import synthetic as S
+    from whispereacp_amd.decoder import BatchedDecoder, to_device
+
+    shape = S.workload_shape(args.workload)
+    streams, dtype = w["streams"], w["dtype"]
+    prompt = S.SOT_PREFIX[shape.vocabulary_size]
+    if len(prompt) + args.steps > shape.max_positions or len(prompt) + args.warmup > shape.max_positions:
+        print(f"--steps and --warmup each fit {shape.max_positions - len(prompt)} steps in one sequence",
+              file=sys.stderr)
+        sys.exit(2)
+    begin_timed = args.workload == "large-v3"
+    print(f"[bench] generating {args.workload} weights ({dtype}) and {streams} encoder outputs", file=sys.stderr,
+          flush=True)
+    decoder_file = S.workload_decoder_file(shape, dtype, 1000)
+    encoders = [S.normal_encoder_output(shape.cross_positions, shape.width, 7 + s) for s in range(streams)]
+    torch.cuda.set_device(0)
+    decoder = BatchedDecoder(shape, decoder_file, streams=streams)
+    enc = to_device(np.ascontiguousarray(np.stack(encoders)))
+    V = shape.vocabulary_size
+    t = len(prompt)
+    prompt_tokens = torch.tensor([prompt] * streams, dtype=torch.int32, device="cuda")
+    # Token ring [position][stream]: the prompt step's argmax lands in row t,
+    # each replayed step reads row p and writes row p + 1.
+    ring = torch.zeros((shape.max_positions + 1, streams), dtype=torch.int32, device="cuda")
+    ring[:t] = torch.tensor(prompt, dtype=torch.int32, device="cuda")[:, None].expand(t, streams)
+    prompt_logits = torch.empty((streams * t, V), dtype=torch.float32, device="cuda")
+    step_logits = torch.empty((streams, V), dtype=torch.float32, device="cuda")
+
+    def open_sequence():
+        decoder.begin(enc)
+        decoder.step(prompt_tokens, t, prompt_logits, None, ring[t])
+
+    def run_steps(count):
+        for _ in range(count):
+            decoder.ring_step(ring, step_logits, None)
+
+    print("[bench] warm-up", file=sys.stderr, flush=True)
+    open_sequence()
+    run_steps(args.warmup)
+    torch.cuda.synchronize()
+
+    print("[bench] timed region", file=sys.stderr, flush=True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if begin_timed:
+        torch.cuda.synchronize()
+        host0 = time.perf_counter()
+        start.record()
+        open_sequence()
+    else:
+        open_sequence()
+        torch.cuda.synchronize()
+        host0 = time.perf_counter()
+        start.record()
+    run_steps(args.steps)
+    stop.record()
+    enqueue_s = time.perf_counter() - host0
+    torch.cuda.synchronize()
+    host_s = time.perf_counter() - host0
+    gpu_ms = start.elapsed_time(stop)
+    ms_per_step = gpu_ms / args.steps
+    tokens = ring[t:t + args.steps + 1].cpu().numpy().T
+
+    weight_bytes = 4 if dtype == "F32" else 2
+    positions = range(t, t + args.steps)
+    bytes_per_step = sum(step_bytes(shape, weight_bytes, p, streams) for p in positions) / args.steps
+    achieved = bytes_per_step / (ms_per_step * 1e-3) / 1e9
+
+    baseline, parity = None, None
+    if args.cpu_budget > 0:
+        print("[bench] cpu baseline (oracle, stream 0)", file=sys.stderr, flush=True)
+        baseline, parity = cpu_baseline(shape, decoder_file, encoders[0], prompt, tokens[0].tolist(),
+                                        args.cpu_budget)
+        baseline["sample"] = "one stream: " + baseline["sample"]
+
+    line = {
+        "metric": f"decode tokens/s and ms/step, {streams} independent streams",
+        "value": round(streams * args.steps / (gpu_ms * 1e-3), 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": ("f16" if dtype == "F16" else "bf16") + "-weights/f32",
+        "data": "synthetic: N(0,0.02) weights (LayerNorm gamma 1, beta 0), N(0,1) encoder states per stream",
+        "config": {"workload": f"{args.workload} decoder: d_model {shape.width}, {shape.heads} heads, "
+                               f"{shape.layers} layers, vocab {V}, {dtype} weights, 1500 cross positions, "
+                               f"{streams} streams, {args.steps} single-token greedy steps after a 4-token prefix"
+                               + (", cross K/V projection of every stream timed" if begin_timed else ""),
+                   "path": "batched per-op kernels (matrix-core products), one HIP graph replay per step",
+                   "global_batch": streams, "seq_len": t + args.steps, "parallelism": "none (one GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole step (batched per-op kernels)", "bytes_per_step": round(bytes_per_step)},
         "cpu_baseline": baseline,
         "parity": parity,
         "host_seconds": round(host_s, 4),

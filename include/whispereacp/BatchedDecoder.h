@@ -41,6 +41,14 @@ public:
     void stepAndSample(Pass& pass, const BufferRange& tokens, int tokenCount, const DecoderWeights& weights,
                        const BufferRange& logits, const float* mask, const BufferRange& argmaxSlots);
 
+    // One single-token step per stream driven by a token ring [maxPositions +
+    // 1][streams] (position-major): each stream's token at the current
+    // position p is read from ring[p] and its masked greedy successor written
+    // to ring[p + 1], logits [streams][vocabularySize] too. Replayed from a
+    // captured HIP graph (wsp_batch_ring_step); needs p >= 1.
+    void ringStep(Pass& pass, const BufferRange& ring, const DecoderWeights& weights, const BufferRange& logits,
+                  const float* mask);
+
     const DecoderShape& shape() const { return decoderShape; }
     int streams() const { return streamCount; }
     int position() const;

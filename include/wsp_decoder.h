@@ -117,6 +117,10 @@ int wsp_batch_decoder_begin(wsp_batch_decoder* decoder, const float* encoder_row
 int wsp_batch_decoder_step(wsp_batch_decoder* decoder, const uint32_t* tokens, int count, float* logits,
                            const float* mask, uint32_t* argmax_slots);
 
+/* One graph-replayed single-token step per stream over a token ring
+ * [max_positions + 1][streams] (see wsp_batch_ring_step in wsp_hip.h). */
+int wsp_batch_decoder_ring_step(wsp_batch_decoder* decoder, uint32_t* ring, float* logits, const float* mask);
+
 int wsp_batch_decoder_position(const wsp_batch_decoder* decoder);
 const float* wsp_batch_decoder_hidden_states(const wsp_batch_decoder* decoder);
 

@@ -244,6 +244,19 @@ int wsp_batch_begin(wsp_batch* batch, const wsp_cross_tensors* layers, int wdtyp
 int wsp_batch_step(wsp_batch* batch, const wsp_decoder_tensors* tensors, const uint32_t* tokens, int count,
                    float* hidden, float* logits, const float* mask, uint32_t* argmax_out);
 
+/* One single-token step for every stream driven by a token ring: ring is
+ * device uint32 [max_positions + 1][streams], position-major. The step reads
+ * each stream's token at the current position p from ring[p] and writes its
+ * masked greedy successor to ring[p + 1]; logits [streams][vocabulary] are
+ * written too. Nothing in it depends on p on the host, so it is captured once
+ * as a HIP graph and replayed (re-captured when ring, logits, mask, the cross
+ * rows or the weight table change). Needs p >= 1 (the prompt step runs
+ * through wsp_batch_step, its argmax_out pointing at ring[p]). No reference
+ * counterpart: Whisper::decodeTranscript's device-side token feedback
+ * (Whisper/Whisper.cpp:1361-1443) for a batch, without per-launch host cost. */
+int wsp_batch_ring_step(wsp_batch* batch, const wsp_decoder_tensors* tensors, uint32_t* ring, float* logits,
+                        const float* mask);
+
 /* Layer `layer`'s caches of stream 0; stream s starts max_positions·width
  * (self) or cross_positions·width (cross) floats later. */
 int wsp_batch_self_cache(const wsp_batch* batch, int layer, const float** keys, const float** values);

@@ -208,3 +208,82 @@ def test_batch_refuses_steps_past_the_context_and_before_begin():
     with pytest.raises(ModelError):
         decoder.step(tokens, 1, logits)
     assert decoder.position == 8
+
+
+# -- the graph-replayed ring step ----------------------------------------------
+
+def ring_greedy(decoder, shape, encoders, prompt, steps, masks, cross_rows=0, sync_every=3):
+    """The prompt step eagerly (its argmax into ring row t), then `steps` ring
+    steps replayed from the captured graph with a fixed logits buffer; between
+    replays the program's own eager work (a copy of the logits row) and, every
+    few steps, a synchronisation. masks[j] is step j's mask (a change forces a
+    re-capture). Returns tokens per stream and the logits rows [streams, steps, V]."""
+    import torch
+    from whispereacp_amd.decoder import to_device
+    streams, V, t = len(encoders), shape.vocabulary_size, len(prompt)
+    decoder.begin(to_device(np.ascontiguousarray(np.stack(encoders), dtype=np.float32)), cross_rows)
+    ring = torch.zeros((shape.max_positions + 1, streams), dtype=torch.int32, device="cuda")
+    ring[:t] = torch.tensor(prompt, dtype=torch.int32, device="cuda")[:, None].expand(t, streams)
+    tokens = torch.tensor([list(prompt)] * streams, dtype=torch.int32, device="cuda")
+    prompt_logits = torch.empty((streams * t, V), dtype=torch.float32, device="cuda")
+    decoder.step(tokens, t, prompt_logits, None, ring[t])
+    logits = torch.empty((streams, V), dtype=torch.float32, device="cuda")
+    rows = torch.empty((steps, streams, V), dtype=torch.float32, device="cuda")
+    for j in range(steps):
+        decoder.ring_step(ring, logits, masks[j])
+        rows[j].copy_(logits)
+        if j % sync_every == sync_every - 1:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    assert decoder.position == t + steps
+    return ring[t:t + steps + 1].cpu().numpy().T.tolist(), rows.cpu().numpy().transpose(1, 0, 2)
+
+
+def test_ring_steps_replay_the_eager_steps_exactly():
+    # Positions stay below the fixed self-key chunk, where the replayed step
+    # and the eager step run the same arithmetic: tokens and logits bit-equal
+    # at every replay, across a re-capture when the mask changes.
+    from whispereacp_amd.decoder import BatchedDecoder, to_device
+    shape = S.DecoderShape(256, 4, 2, 1024, 4099, 448, 300)
+    f = S.workload_decoder_file(shape, "F16", 78)
+    encoders = [S.normal_encoder_output(90, shape.width, 700 + s) for s in range(3)]
+    prompt = [5, 6, 7, 8]
+    mask = np.zeros(shape.vocabulary_size, np.float32)
+    mask[1::4] = 1.0
+    mask_d = to_device(mask)
+    steps = 24
+    masks = [None] * 12 + [mask_d] * 12
+    decoder = BatchedDecoder(shape, f, streams=3)
+    ring_tokens, ring_rows = ring_greedy(decoder, shape, encoders, prompt, steps, masks, cross_rows=90)
+
+    import torch
+    eager = BatchedDecoder(shape, f, streams=3)
+    eager.begin(to_device(np.ascontiguousarray(np.stack(encoders))), 90)
+    V, t = shape.vocabulary_size, len(prompt)
+    slots = torch.zeros((steps + 1, 3), dtype=torch.int32, device="cuda")
+    eager.step(torch.tensor([prompt] * 3, dtype=torch.int32, device="cuda"), t,
+               torch.empty((3 * t, V), dtype=torch.float32, device="cuda"), None, slots[0])
+    rows = torch.empty((steps, 3, V), dtype=torch.float32, device="cuda")
+    for j in range(steps):
+        eager.step(slots[j], 1, rows[j], masks[j], slots[j + 1])
+    torch.cuda.synchronize()
+    eager_tokens = slots.cpu().numpy().T.tolist()
+    eager_rows = rows.cpu().numpy().transpose(1, 0, 2)
+    assert ring_tokens == eager_tokens
+    for j in range(steps):
+        assert np.array_equal(ring_rows[:, j], eager_rows[:, j]), f"replay {j} differs from the eager step"
+    assert all(tok % 4 != 1 for s in range(3) for tok in ring_tokens[s][13:])
+
+
+def test_ring_long_sequence_matches_oracle(oracle):
+    # 300 replayed steps: the self keys pass the fixed chunk boundaries.
+    from whispereacp_amd.decoder import BatchedDecoder
+    shape = S.DecoderShape(128, 2, 2, 512, 1000, 448, 64)
+    f = S.workload_decoder_file(shape, "BF16", 92)
+    encoders = [S.normal_encoder_output(64, shape.width, 800 + s) for s in range(2)]
+    prompt = [1, 2, 3, 4]
+    decoder = BatchedDecoder(shape, f, streams=2)
+    tokens, rows = ring_greedy(decoder, shape, encoders, prompt, 300, [None] * 300, sync_every=50)
+    for s in range(2):
+        ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, encoders[s], prompt, 300)
+        check_run(tokens[s], rows[s], ref_tokens, ref_rows, 2e-2)

@@ -106,6 +106,7 @@ SIGNATURES = {
     "wsp_batch_begin": (c_int, [c_void_p, ctypes.POINTER(wsp_cross_tensors), c_int, c_void_p, c_int]),
     "wsp_batch_step": (c_int, [c_void_p, ctypes.POINTER(wsp_decoder_tensors), c_void_p, c_int, c_void_p, c_void_p,
                                c_void_p, c_void_p]),
+    "wsp_batch_ring_step": (c_int, [c_void_p, ctypes.POINTER(wsp_decoder_tensors), c_void_p, c_void_p, c_void_p]),
     "wsp_batch_self_cache": (c_int, [c_void_p, c_int, ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p)]),
     "wsp_batch_cross_cache": (c_int, [c_void_p, c_int, ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p)]),
     "wsp_batch_decoder_create": (c_int, [ctypes.POINTER(wsp_decoder_shape), ctypes.POINTER(wsp_tensor_entry), c_int,
@@ -115,6 +116,7 @@ SIGNATURES = {
     "wsp_batch_decoder_last_error_kind": (c_int, [c_void_p]),
     "wsp_batch_decoder_begin": (c_int, [c_void_p, c_void_p, c_int]),
     "wsp_batch_decoder_step": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "wsp_batch_decoder_ring_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
     "wsp_batch_decoder_position": (c_int, [c_void_p]),
     "wsp_batch_decoder_hidden_states": (c_void_p, [c_void_p]),
 }

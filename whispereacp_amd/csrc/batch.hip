@@ -98,10 +98,12 @@ struct Norm
     u16* xs;              // split output [parts][rows_padded][width]
     size_t xs_part;
     float* y;             // optional f32 copy of the normalised rows
-    const uint32_t* tokens;
+    const uint32_t* tokens; // [streams][step_tokens], or null with a ring
+    const uint32_t* ring;   // position-major [max_positions + 1][streams] (one token per stream)
+    const int* state;       // device word: the position of the step's first token
     const float* token_table;
     const float* position_table;
-    int position, step_tokens, vocabulary;
+    int streams, step_tokens, vocabulary;
 };
 
 template <int WT, bool EMBED>
@@ -112,8 +114,9 @@ __global__ void __launch_bounds__(kNormThreads) norm_kernel(Norm a)
     float* h = a.h + (size_t) row * a.width;
     if constexpr (EMBED)
     {
-        const uint32_t token = a.tokens[row];
-        const int position = a.position + row % a.step_tokens;
+        const int first = *a.state;
+        const uint32_t token = a.ring != nullptr ? a.ring[(size_t) first * a.streams + row] : a.tokens[row];
+        const int position = first + row % a.step_tokens;
         for (int c = threadIdx.x; c < a.width; c += kNormThreads)
             h[c] = token < (uint32_t) a.vocabulary
                        ? a.token_table[(size_t) token * a.width + c] + a.position_table[(size_t) position * a.width + c]
@@ -172,7 +175,8 @@ struct Product
     float* keys;      // stream 0's cache of this layer
     float* values;
     size_t stream_stride;
-    int position, step_tokens, width;
+    const int* state; // device word: the position of the step's first token
+    int step_tokens, width;
 };
 
 template <int WT>
@@ -188,7 +192,7 @@ __device__ __forceinline__ void finish(const Product& a, int m, int n, float acc
         {
             const int d = a.width;
             const int stream = m / a.step_tokens, i = m % a.step_tokens;
-            const size_t row = (size_t) stream * a.stream_stride + (size_t) (a.position + i) * d;
+            const size_t row = (size_t) stream * a.stream_stride + (size_t) (*a.state + i) * d;
             if (n < d)
                 a.q[(size_t) m * d + n] = v;
             else if (n < 2 * d)
@@ -281,8 +285,9 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
 // ---------------------------------------------------------------------------
 // Split-key attention for (row, head, chunk): the row's query against keys
 // [chunk·len, min((chunk + 1)·len, visible)) of its stream's cache, visible
-// being the causal limit k_count - step_tokens + i + 1 for self attention
-// (Kernels/Attention.h:34-47) and k_count for cross attention. Keys are taken
+// being the causal limit position + i + 1 for self attention (the query at
+// position + i sees every key up to itself, Kernels/Attention.h:34-47) and
+// k_count for cross attention. Keys are taken
 // 128 at a time; lane (group, sub) holds channels 4·sub.. of keys group + 16u
 // and all its key and value loads are issued together. Tiles fold into a
 // running (max, sum, row) with exact exp(m_old - m_new) rescaling; one chunk
@@ -295,7 +300,8 @@ struct Attend
     const float* keys;    // stream 0's cache of this layer, [capacity][width]
     const float* values;
     size_t stream_stride; // elements between streams' caches
-    int k_count, step_tokens, causal, heads, head_width, width;
+    const int* state;     // device word: the position of the step's first token
+    int k_count, step_tokens, causal, heads, head_width, width; // k_count: cross rows (causal: unused)
     float scale;
     int chunks, chunk_len;
     u16* xs;              // split output [parts][rows_padded][width] when chunks == 1
@@ -322,7 +328,7 @@ __global__ void __launch_bounds__(kAttendThreads) attend_kernel(Attend a)
     float4v qv = {0.f, 0.f, 0.f, 0.f};
     if (sub < quads)
         qv = *reinterpret_cast<const float4v*>(a.q + (size_t) row * a.width + column);
-    const int visible = a.causal ? a.k_count - a.step_tokens + i + 1 : a.k_count;
+    const int visible = a.causal ? *a.state + i + 1 : a.k_count;
     const int first = chunk * a.chunk_len;
     const int last = min(first + a.chunk_len, visible);
     const float* kbase = a.keys + (size_t) stream * a.stream_stride + column;
@@ -440,6 +446,21 @@ __global__ void __launch_bounds__(kWave) combine_kernel(const float* __restrict_
     store_split<WT>(xs, xs_part, (size_t) row * width + head * head_width + c, numerator / denominator);
 }
 
+// The step's last launch: with a ring, each stream's greedy token goes to the
+// ring row of the next position; then the position word advances. One block,
+// so every thread has read the position before thread 0 moves it.
+__global__ void __launch_bounds__(128) advance_kernel(int* state, uint32_t* ring, const uint32_t* next, int streams,
+                                                      int count)
+{
+    const int position = *state;
+    if (ring != nullptr)
+        for (int s = threadIdx.x; s < streams; s += blockDim.x)
+            ring[(size_t) (position + count) * streams + s] = next[s];
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *state = position + count;
+}
+
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
@@ -476,21 +497,25 @@ hipError_t launch_norm(hipStream_t stream, const Norm& a, int rows, bool embed)
     return hipGetLastError();
 }
 
-// Key chunks for `units` (row, head) pairs over k_count keys: about 2048
-// blocks in all, no chunk shorter than one 128-key tile.
-int attend_chunks(int units, int k_count)
+// Key chunks for `units` (row, head) pairs over k_count keys: about `target`
+// blocks in all, no chunk shorter than one 128-key tile. Cross attention
+// (1500 keys a stream) aims at 2048 blocks to keep HBM busy; self attention
+// at 256, so a large batch covers the chip without the combine launch.
+int attend_chunks(int units, int k_count, int target)
 {
     const int most = std::max(1, (k_count + kTileKeys - 1) / kTileKeys);
-    return std::max(1, std::min(most, (2048 + units - 1) / units));
+    return std::max(1, std::min(most, (target + units - 1) / units));
 }
 
-// Attention of `rows` query rows; a.chunks and a.chunk_len are filled here.
+// Attention of `rows` query rows whose keys number at most `span`; a.chunks
+// and a.chunk_len are planned here for that span (chunks past the visible keys
+// come out empty, which the combine skips).
 template <int WT>
-hipError_t launch_attend(hipStream_t stream, Attend a, int rows)
+hipError_t launch_attend(hipStream_t stream, Attend a, int rows, int span)
 {
-    a.chunks = attend_chunks(rows * a.heads, a.k_count);
-    a.chunk_len = (a.k_count + a.chunks - 1) / a.chunks;
-    a.chunks = (a.k_count + a.chunk_len - 1) / a.chunk_len;
+    a.chunks = attend_chunks(rows * a.heads, span, a.causal ? 256 : 2048);
+    a.chunk_len = (span + a.chunks - 1) / a.chunks;
+    a.chunks = (span + a.chunk_len - 1) / a.chunk_len;
     hipLaunchKernelGGL((attend_kernel<WT>), dim3(rows * a.heads * a.chunks), dim3(kAttendThreads), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.chunks == 1)
@@ -524,7 +549,20 @@ struct wsp_batch
     float* partials = nullptr;
     float* argmax_values = nullptr;
     uint32_t* argmax_indices = nullptr;
+    int* state = nullptr;         // device word: the position of the next step's first token
+    uint32_t* next = nullptr;     // [streams] greedy tokens of a ring step
     std::vector<void*> owned;
+
+    // The single-token ring step, captured once as a HIP graph on a private
+    // stream and replayed on `stream`; re-captured when anything it bakes in
+    // (ring, logits, mask, cross rows, the weight table) changes.
+    hipStream_t capture = nullptr;
+    hipGraphExec_t graph = nullptr;
+    const void* graph_ring = nullptr;
+    const void* graph_logits = nullptr;
+    const void* graph_mask = nullptr;
+    int graph_cross_rows = -1;
+    std::vector<char> graph_table;
 
     char error[512] = {0};
 };
@@ -582,10 +620,30 @@ hipError_t allocate(wsp_batch* b, T** out, size_t elements)
     return e;
 }
 
-template <int WT>
-int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const uint32_t* tokens, int count, float* hidden,
-             float* logits, const float* mask, uint32_t* argmax_out)
+// What one step reads and writes. Either `tokens` ([streams][count]) and an
+// optional `argmax_out` ([streams]), or — one token per stream — a `ring`
+// read at the device position and written at the next (fixed_grid then plans
+// the self attention for max_positions keys, so nothing in the launches
+// depends on the position and the step can be replayed from a graph).
+struct StepIo
 {
+    const uint32_t* tokens;
+    uint32_t* ring;
+    int count;
+    float* hidden;
+    float* logits;
+    const float* mask;
+    uint32_t* argmax_out;
+    bool fixed_grid;
+};
+
+template <int WT>
+int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipStream_t st)
+{
+    const int count = io.count;
+    float* const hidden = io.hidden;
+    float* const logits = io.logits;
+    const float* const mask = io.mask;
     using namespace wsp::batch;
     const wsp_decoder_shape& s = b->shape;
     const int d = s.width, f = s.feed_forward_width, H = s.heads, hd = d / H;
@@ -593,7 +651,6 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const uint32_t* tokens,
     const size_t xs_part = (size_t) b->rows_padded * d, ff_part = (size_t) b->rows_padded * f;
     const float eps = 1e-5f;
     const float scale = 1.f / std::sqrt((float) hd);
-    hipStream_t st = b->stream;
     hipError_t e = hipSuccess;
 
     Norm n {};
@@ -602,10 +659,12 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const uint32_t* tokens,
     n.eps = eps;
     n.xs = b->xs;
     n.xs_part = xs_part;
-    n.tokens = tokens;
+    n.tokens = io.tokens;
+    n.ring = io.ring;
+    n.state = b->state;
+    n.streams = b->streams;
     n.token_table = T->token_embedding;
     n.position_table = T->position_embedding;
-    n.position = b->position;
     n.step_tokens = count;
     n.vocabulary = s.vocabulary_size;
 
@@ -625,6 +684,8 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const uint32_t* tokens,
     at.xs = b->xs;
     at.xs_part = xs_part;
     at.partials = b->partials;
+    at.state = b->state;
+    const int self_span = io.fixed_grid ? s.max_positions : b->position + count;
 
     for (int l = 0; l < s.layers; ++l)
     {
@@ -652,7 +713,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const uint32_t* tokens,
         p.keys = self_k;
         p.values = self_v;
         p.stream_stride = (size_t) s.max_positions * d;
-        p.position = b->position;
+        p.state = b->state;
         p.step_tokens = count;
         p.width = d;
         if ((e = launch_product<WT>(st, p)) != hipSuccess)
@@ -661,9 +722,9 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const uint32_t* tokens,
         at.keys = self_k;
         at.values = self_v;
         at.stream_stride = (size_t) s.max_positions * d;
-        at.k_count = b->position + count;
+        at.k_count = 0;
         at.causal = 1;
-        if ((e = launch_attend<WT>(st, at, rows)) != hipSuccess)
+        if ((e = launch_attend<WT>(st, at, rows, self_span)) != hipSuccess)
             return hip_fail(b, e, "self attention");
 
         p.out = d;
@@ -692,7 +753,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const uint32_t* tokens,
         at.stream_stride = (size_t) s.cross_positions * d;
         at.k_count = b->cross_rows;
         at.causal = 0;
-        if ((e = launch_attend<WT>(st, at, rows)) != hipSuccess)
+        if ((e = launch_attend<WT>(st, at, rows, b->cross_rows)) != hipSuccess)
             return hip_fail(b, e, "cross attention");
 
         p.w = L.cross_out_w;
@@ -746,6 +807,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const uint32_t* tokens,
     if ((e = launch_product<WT>(st, p)) != hipSuccess)
         return hip_fail(b, e, "logits product");
 
+    uint32_t* const argmax_out = io.ring != nullptr ? b->next : io.argmax_out;
     if (argmax_out != nullptr)
     {
         const size_t V = (size_t) s.vocabulary_size;
@@ -754,7 +816,68 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const uint32_t* tokens,
         if (e != hipSuccess)
             return hip_fail(b, e, "argmax");
     }
-    b->position += count;
+    hipLaunchKernelGGL(wsp::batch::advance_kernel, dim3(1), dim3(128), 0, st, b->state, io.ring, b->next, b->streams,
+                       count);
+    if ((e = hipGetLastError()) != hipSuccess)
+        return hip_fail(b, e, "position advance");
+    return WSP_OK;
+}
+
+bool same_table(const wsp_batch* b, const std::vector<char>& table)
+{
+    return b->graph_table.size() == table.size() && std::memcmp(b->graph_table.data(), table.data(), table.size()) == 0;
+}
+
+// The bytes the captured step bakes in from the weight table.
+std::vector<char> table_bytes(const wsp_decoder_tensors* T, int layers)
+{
+    std::vector<char> bytes(sizeof(wsp_decoder_tensors) + sizeof(wsp_layer_tensors) * (size_t) layers);
+    wsp_decoder_tensors top = *T;
+    top.layers = nullptr;
+    std::memcpy(bytes.data(), &top, sizeof top);
+    std::memcpy(bytes.data() + sizeof top, T->layers, sizeof(wsp_layer_tensors) * (size_t) layers);
+    return bytes;
+}
+
+void drop_graph(wsp_batch* b)
+{
+    if (b->graph != nullptr)
+        (void) hipGraphExecDestroy(b->graph);
+    b->graph = nullptr;
+    b->graph_table.clear();
+}
+
+template <int WT>
+int capture_ring_step(wsp_batch* b, const wsp_decoder_tensors* T, uint32_t* ring, float* logits, const float* mask)
+{
+    drop_graph(b);
+    hipError_t e = hipStreamBeginCapture(b->capture, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess)
+        return hip_fail(b, e, "graph capture");
+    StepIo io {nullptr, ring, 1, nullptr, logits, mask, nullptr, true};
+    const int status = run_step<WT>(b, T, io, b->capture);
+    hipGraph_t graph = nullptr;
+    e = hipStreamEndCapture(b->capture, &graph);
+    if (status != WSP_OK)
+    {
+        if (graph != nullptr)
+            (void) hipGraphDestroy(graph);
+        return status;
+    }
+    if (e != hipSuccess)
+        return hip_fail(b, e, "graph capture");
+    e = hipGraphInstantiate(&b->graph, graph, nullptr, nullptr, 0);
+    (void) hipGraphDestroy(graph);
+    if (e != hipSuccess)
+    {
+        b->graph = nullptr;
+        return hip_fail(b, e, "graph instantiate");
+    }
+    b->graph_ring = ring;
+    b->graph_logits = logits;
+    b->graph_mask = mask;
+    b->graph_cross_rows = b->cross_rows;
+    b->graph_table = table_bytes(T, b->shape.layers);
     return WSP_OK;
 }
 } // namespace
@@ -819,6 +942,14 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
         e = allocate(b, &b->argmax_values, (size_t) streams * groups);
     if (e == hipSuccess)
         e = allocate(b, &b->argmax_indices, (size_t) streams * groups);
+    if (e == hipSuccess)
+        e = allocate(b, &b->state, 4);
+    if (e == hipSuccess)
+        e = allocate(b, &b->next, (size_t) streams);
+    if (e == hipSuccess)
+        e = hipMemsetAsync(b->state, 0, 4 * sizeof(int), b->stream);
+    if (e == hipSuccess)
+        e = hipStreamCreateWithFlags(&b->capture, hipStreamNonBlocking);
     // Padding rows of the split buffers are read by the products (their sums
     // are discarded); zero them once so they hold finite values.
     if (e == hipSuccess)
@@ -829,6 +960,8 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
         e = hipStreamSynchronize(b->stream);
     if (e != hipSuccess)
     {
+        if (b->capture != nullptr)
+            (void) hipStreamDestroy(b->capture);
         release(b);
         delete b;
         return WSP_ERR_HIP;
@@ -843,6 +976,9 @@ void wsp_batch_destroy(wsp_batch* b)
         return;
     (void) hipSetDevice(b->device);
     (void) hipStreamSynchronize(b->stream);
+    drop_graph(b);
+    if (b->capture != nullptr)
+        (void) hipStreamDestroy(b->capture);
     release(b);
     delete b;
 }
@@ -916,6 +1052,9 @@ int wsp_batch_begin(wsp_batch* b, const wsp_cross_tensors* layers, int wdtype, c
         if (e != hipSuccess)
             return hip_fail(b, e, "cross key/value projection");
     }
+    const hipError_t e = hipMemsetAsync(b->state, 0, sizeof(int), b->stream);
+    if (e != hipSuccess)
+        return hip_fail(b, e, "position reset");
     b->cross_rows = cross_rows;
     b->position = 0;
     return WSP_OK;
@@ -938,8 +1077,42 @@ int wsp_batch_step(wsp_batch* b, const wsp_decoder_tensors* tensors, const uint3
     if (tensors->wdtype != b->wdtype || tensors->logits_wdtype != b->wdtype)
         return fail(b, WSP_ERR_LOGIC, "wsp_batch_step: projections and logits must share the batch's 16-bit storage");
     (void) hipSetDevice(b->device);
-    return b->wdtype == WSP_F16 ? run_step<wsp::kF16>(b, tensors, tokens, count, hidden, logits, mask, argmax_out)
-                                : run_step<wsp::kBF16>(b, tensors, tokens, count, hidden, logits, mask, argmax_out);
+    const StepIo io {tokens, nullptr, count, hidden, logits, mask, argmax_out, false};
+    const int status = b->wdtype == WSP_F16 ? run_step<wsp::kF16>(b, tensors, io, b->stream)
+                                            : run_step<wsp::kBF16>(b, tensors, io, b->stream);
+    if (status == WSP_OK)
+        b->position += count;
+    return status;
+}
+
+int wsp_batch_ring_step(wsp_batch* b, const wsp_decoder_tensors* tensors, uint32_t* ring, float* logits,
+                        const float* mask)
+{
+    if (b == nullptr)
+        return WSP_ERR_ARGUMENT;
+    b->error[0] = 0;
+    if (tensors == nullptr || tensors->layers == nullptr || ring == nullptr || logits == nullptr)
+        return fail(b, WSP_ERR_ARGUMENT, "wsp_batch_ring_step: null tensors, ring or logits");
+    if (b->cross_rows <= 0)
+        return fail(b, WSP_ERR_LOGIC, "wsp_batch_ring_step: no sequence begun");
+    if (b->position < 1 || b->position + 1 > b->shape.max_positions)
+        return fail(b, WSP_ERR_SHAPE, "wsp_batch_ring_step: the ring step needs a position in [1, max_positions)");
+    if (tensors->wdtype != b->wdtype || tensors->logits_wdtype != b->wdtype)
+        return fail(b, WSP_ERR_LOGIC, "wsp_batch_ring_step: projections and logits must share the batch's 16-bit storage");
+    (void) hipSetDevice(b->device);
+    if (b->graph == nullptr || b->graph_ring != ring || b->graph_logits != logits || b->graph_mask != mask
+        || b->graph_cross_rows != b->cross_rows || !same_table(b, table_bytes(tensors, b->shape.layers)))
+    {
+        const int status = b->wdtype == WSP_F16 ? capture_ring_step<wsp::kF16>(b, tensors, ring, logits, mask)
+                                                : capture_ring_step<wsp::kBF16>(b, tensors, ring, logits, mask);
+        if (status != WSP_OK)
+            return status;
+    }
+    const hipError_t e = hipGraphLaunch(b->graph, b->stream);
+    if (e != hipSuccess)
+        return hip_fail(b, e, "graph launch");
+    b->position += 1;
+    return WSP_OK;
 }
 
 int wsp_batch_self_cache(const wsp_batch* b, int layer, const float** keys, const float** values)

@@ -112,6 +112,33 @@ void BatchedDecoder::record(Pass& pass, const BufferRange& tokens, int tokenCoun
         throwForStatus(status, wsp_batch_last_error(batch));
 }
 
+void BatchedDecoder::ringStep(Pass& pass, const BufferRange& ring, const DecoderWeights& weights,
+                              const BufferRange& logits, const float* mask)
+{
+    requireMatchingWeights(weights);
+    if (batch == nullptr)
+        throw std::logic_error("step before prepare");
+    if (pass.hipStream() != stream)
+        throw std::logic_error("a batched decoder records into the stream it was prepared with");
+    if (crossPositions() <= 0)
+        throw std::logic_error("step before beginSequences");
+    if (position() < 1)
+        throw std::logic_error("a ring step follows the prompt step");
+    if (position() + 1 > decoderShape.maxPositions)
+        throw ModelError("decoding one more token would pass the " + std::to_string(decoderShape.maxPositions)
+                         + "-position context");
+    const std::size_t slots = (std::size_t) (decoderShape.maxPositions + 1) * streamCount;
+    if (ring.size < slots * sizeof(uint32_t))
+        throw ModelError("the token ring holds fewer than (maxPositions + 1) x streams slots");
+    if (logits.size < (std::size_t) streamCount * decoderShape.vocabularySize * sizeof(float))
+        throw ModelError("the logits range is smaller than streams rows");
+    const wsp_decoder_tensors tensors = decoderTable(weights, layerTables);
+    const int status = wsp_batch_ring_step(batch, &tensors, static_cast<uint32_t*>(ring.data()),
+                                           static_cast<float*>(logits.data()), mask);
+    if (status != WSP_OK)
+        throwForStatus(status, wsp_batch_last_error(batch));
+}
+
 void BatchedDecoder::step(Pass& pass, const BufferRange& tokens, int tokenCount, const DecoderWeights& weights,
                           const BufferRange& logits)
 {

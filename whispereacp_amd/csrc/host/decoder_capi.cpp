@@ -347,6 +347,18 @@ int wsp_batch_decoder_step(wsp_batch_decoder* d, const uint32_t* tokens, int cou
     });
 }
 
+int wsp_batch_decoder_ring_step(wsp_batch_decoder* d, uint32_t* ring, float* logits, const float* mask)
+{
+    return guarded(d, [&] {
+        if (!d->decoder)
+            throw std::logic_error("this batched decoder failed to build");
+        const std::size_t streams = (std::size_t) d->decoder->streams();
+        WSP::Pass pass(d->decoder->hipStream());
+        d->decoder->ringStep(pass, range(ring, (std::size_t) (d->shape.maxPositions + 1) * streams * sizeof(uint32_t)),
+                             *d->weights, range(logits, streams * d->shape.vocabularySize * sizeof(float)), mask);
+    });
+}
+
 int wsp_batch_decoder_position(const wsp_batch_decoder* d)
 {
     return d == nullptr || !d->decoder ? -1 : d->decoder->position();

@@ -269,6 +269,11 @@ class BatchedDecoder:
         self._check(self.lib.wsp_batch_decoder_step(self.handle, ptr(tokens), count, ptr(logits), ptr(mask),
                                                     ptr(argmax_slots)))
 
+    def ring_step(self, ring: torch.Tensor, logits: torch.Tensor, mask: Optional[torch.Tensor] = None):
+        """ring: device int32 [max_positions + 1, streams]; reads row p (the
+        position), writes row p + 1; logits [streams, vocabulary]."""
+        self._check(self.lib.wsp_batch_decoder_ring_step(self.handle, ptr(ring), ptr(logits), ptr(mask)))
+
     @property
     def position(self) -> int:
         return self.lib.wsp_batch_decoder_position(self.handle)
