@@ -149,7 +149,8 @@ __global__ void __launch_bounds__(kNormThreads) norm_kernel(Norm a)
 // bytes of one weight row and of each split activation row per k-block
 // (v_mfma_f32_16x16x32: A = activations, lane l row l % 16; B = weights,
 // lane l column l % 16; both with k = 8(l / 16) + j). KB k-blocks are loaded
-// before their products. The 8 wave partials are summed in wave order.
+// before their products, the next batch's weights ahead of them. The 8 wave
+// partials are summed in wave order.
 // ---------------------------------------------------------------------------
 enum Epilogue : int
 {
@@ -203,14 +204,16 @@ __device__ __forceinline__ void finish(const Product& a, int m, int n, float acc
     }
 }
 
+// k-blocks a wave loads at once: as many as about 160 registers of weight
+// and activation fragments hold (4 + 4·P·MT per k-block), at most 8.
 template <int P, int MT>
 constexpr int kblocks_per_load()
 {
-    constexpr int kb = 128 / (4 + 4 * P * MT);
+    constexpr int kb = 160 / (4 + 4 * P * MT);
     return kb < 1 ? 1 : (kb > 8 ? 8 : kb);
 }
 
-template <int WT, int MT>
+template <int WT, int MT, bool PREFETCH>
 __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
 {
     constexpr int P = parts_of<WT>();
@@ -233,20 +236,32 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
     for (int t = 0; t < MT; ++t)
         acc[t] = float4v {0.f, 0.f, 0.f, 0.f};
 
+    // The weights of the next batch of k-blocks are requested before the
+    // products of the current one, so HBM latency overlaps the matrix work;
+    // activations (L2-resident) are loaded per batch.
+    u32x4 wv[KB];
+#pragma unroll
+    for (int u = 0; u < KB; ++u)
+        wv[u] = *reinterpret_cast<const u32x4*>(wrow + min(kb_begin + u, kb_end - 1) * 32);
     for (int kb = kb_begin; kb < kb_end; kb += KB)
     {
-        u32x4 wv[KB];
         u32x4 xv[KB][P][MT];
 #pragma unroll
         for (int u = 0; u < KB; ++u)
         {
             const int k = min(kb + u, kb_end - 1) * 32;
-            wv[u] = *reinterpret_cast<const u32x4*>(wrow + k);
 #pragma unroll
             for (int p = 0; p < P; ++p)
 #pragma unroll
                 for (int t = 0; t < MT; ++t)
                     xv[u][p][t] = *reinterpret_cast<const u32x4*>(xrow + p * a.x_part + (size_t) t * 16 * a.inner + k);
+        }
+        u32x4 wn[KB];
+        if constexpr (PREFETCH)
+        {
+#pragma unroll
+            for (int u = 0; u < KB; ++u)
+                wn[u] = *reinterpret_cast<const u32x4*>(wrow + min(kb + KB + u, kb_end - 1) * 32);
         }
 #pragma unroll
         for (int u = 0; u < KB; ++u)
@@ -256,6 +271,18 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
 #pragma unroll
                     for (int p = 0; p < P; ++p)
                         acc[t] = mfma16<WT>(xv[u][p][t], wv[u], acc[t]);
+        if constexpr (PREFETCH)
+        {
+#pragma unroll
+            for (int u = 0; u < KB; ++u)
+                wv[u] = wn[u];
+        }
+        else if (kb + KB < kb_end)
+        {
+#pragma unroll
+            for (int u = 0; u < KB; ++u)
+                wv[u] = *reinterpret_cast<const u32x4*>(wrow + min(kb + KB + u, kb_end - 1) * 32);
+        }
     }
 
     // acc[t][r] of lane (g, li) is C[4g + r][li] of row tile t.
@@ -473,16 +500,29 @@ int row_tiles(int rows)
     return t;
 }
 
+template <int WT, int MT>
+void launch_product_tiles(hipStream_t stream, const Product& a)
+{
+    // Prefetch the next batch's weights only when a wave has more than one
+    // batch (the inner dimension is split over the block's 8 waves).
+    constexpr int KB = kblocks_per_load<parts_of<WT>(), MT>();
+    const int per_wave = (a.inner / 32 + kProductWaves - 1) / kProductWaves;
+    const dim3 grid((a.out + 15) / 16);
+    if (per_wave > KB)
+        hipLaunchKernelGGL((product_kernel<WT, MT, true>), grid, dim3(kProductThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((product_kernel<WT, MT, false>), grid, dim3(kProductThreads), 0, stream, a);
+}
+
 template <int WT>
 hipError_t launch_product(hipStream_t stream, const Product& a)
 {
-    const dim3 grid((a.out + 15) / 16);
     switch (row_tiles(a.rows))
     {
-        case 1: hipLaunchKernelGGL((product_kernel<WT, 1>), grid, dim3(kProductThreads), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((product_kernel<WT, 2>), grid, dim3(kProductThreads), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((product_kernel<WT, 4>), grid, dim3(kProductThreads), 0, stream, a); break;
-        default: hipLaunchKernelGGL((product_kernel<WT, 8>), grid, dim3(kProductThreads), 0, stream, a); break;
+        case 1: launch_product_tiles<WT, 1>(stream, a); break;
+        case 2: launch_product_tiles<WT, 2>(stream, a); break;
+        case 4: launch_product_tiles<WT, 4>(stream, a); break;
+        default: launch_product_tiles<WT, 8>(stream, a); break;
     }
     return hipGetLastError();
 }
