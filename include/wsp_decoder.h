@@ -94,11 +94,49 @@ int wsp_decoder_greedy(wsp_decoder* decoder, const float* encoder_rows, int cros
                        const float* first_mask, const float* later_mask, int* tokens_out, int capacity,
                        int* count_out, double* decode_seconds);
 
+/* ---- safetensors files (WSP::SafeTensors, Model/SafeTensors.h) -----------
+ * A mapped safetensors file and the decoder built from one. A malformed file
+ * is refused when it is opened, with the reason in the last error. */
+typedef struct wsp_safetensors wsp_safetensors;
+typedef struct wsp_batch_decoder wsp_batch_decoder;
+
+/* SafeTensors::fromFile / fromBytes (the bytes are copied). On failure *out
+ * still receives a handle whose last error says why (close it). */
+int wsp_safetensors_open(const char* path, wsp_safetensors** out);
+int wsp_safetensors_open_bytes(const void* bytes, size_t size, wsp_safetensors** out);
+void wsp_safetensors_close(wsp_safetensors* file);
+const char* wsp_safetensors_last_error(const wsp_safetensors* file);
+int wsp_safetensors_count(const wsp_safetensors* file);
+
+/* Tensor `index` in name order: its name, dtype ("F32", "BF16", ...), rank,
+ * up to `capacity` extents and byte count. */
+int wsp_safetensors_tensor(const wsp_safetensors* file, int index, const char** name, const char** dtype, int* rank,
+                           long long* extents, int capacity, long long* byte_count);
+
+/* SafeTensors::readFloats: F32/F16/BF16/F64 tensors as floats into out
+ * (capacity floats). */
+int wsp_safetensors_read_floats(wsp_safetensors* file, const char* name, float* out, long long capacity);
+
+/* The value of __metadata__[key], or null. */
+const char* wsp_safetensors_metadata(const wsp_safetensors* file, const char* key);
+
+/* DecoderShape::fromConfig over a HuggingFace config.json
+ * (Decoder/DecoderShape.cpp:7-17); cross_positions 0 takes
+ * max_source_positions. The reason for a failure goes to error. */
+int wsp_shape_from_config(const char* config_path, int cross_positions, wsp_decoder_shape* out, char* error,
+                          int error_capacity);
+
+/* wsp_decoder_create / wsp_batch_decoder_create over the tensors of a
+ * safetensors file (mapped while the weights upload). */
+int wsp_decoder_create_from_file(const char* path, const wsp_decoder_shape* shape, int packing, int device,
+                                 void* stream, wsp_decoder** out);
+int wsp_batch_decoder_create_from_file(const char* path, const wsp_decoder_shape* shape, int packing, int streams,
+                                       int max_step_tokens, int device, void* stream, wsp_batch_decoder** out);
+
 /* ---- independent streams decoded together (WSP::BatchedDecoder) ----------
  * No reference counterpart: `streams` sequences share one weight read per
  * step, each with its own caches; see wsp_batch_create in wsp_hip.h. The
  * file's projections and logits must share one 16-bit storage (F16/BF16). */
-typedef struct wsp_batch_decoder wsp_batch_decoder;
 
 int wsp_batch_decoder_create(const wsp_decoder_shape* shape, const wsp_tensor_entry* tensors, int count,
                              int packing, int streams, int max_step_tokens, int device, void* stream,

@@ -118,6 +118,21 @@ SIGNATURES = {
     "wsp_batch_decoder_step": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "wsp_batch_decoder_ring_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
     "wsp_batch_decoder_position": (c_int, [c_void_p]),
+    "wsp_batch_decoder_create_from_file": (c_int, [c_char_p, ctypes.POINTER(wsp_decoder_shape), c_int, c_int, c_int,
+                                                   c_int, c_void_p, ctypes.POINTER(c_void_p)]),
+    "wsp_decoder_create_from_file": (c_int, [c_char_p, ctypes.POINTER(wsp_decoder_shape), c_int, c_int, c_void_p,
+                                             ctypes.POINTER(c_void_p)]),
+    "wsp_safetensors_open": (c_int, [c_char_p, ctypes.POINTER(c_void_p)]),
+    "wsp_safetensors_open_bytes": (c_int, [c_void_p, ctypes.c_size_t, ctypes.POINTER(c_void_p)]),
+    "wsp_safetensors_close": (None, [c_void_p]),
+    "wsp_safetensors_last_error": (c_char_p, [c_void_p]),
+    "wsp_safetensors_count": (c_int, [c_void_p]),
+    "wsp_safetensors_tensor": (c_int, [c_void_p, c_int, ctypes.POINTER(c_char_p), ctypes.POINTER(c_char_p),
+                                       ctypes.POINTER(c_int), ctypes.POINTER(ctypes.c_longlong), c_int,
+                                       ctypes.POINTER(ctypes.c_longlong)]),
+    "wsp_safetensors_read_floats": (c_int, [c_void_p, c_char_p, c_void_p, ctypes.c_longlong]),
+    "wsp_safetensors_metadata": (c_char_p, [c_void_p, c_char_p]),
+    "wsp_shape_from_config": (c_int, [c_char_p, c_int, ctypes.POINTER(wsp_decoder_shape), ctypes.c_char_p, c_int]),
     "wsp_batch_decoder_hidden_states": (c_void_p, [c_void_p]),
 }
 

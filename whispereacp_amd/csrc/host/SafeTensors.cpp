@@ -1,0 +1,680 @@
+// The safetensors reader and the config.json decoder shape. The JSON reader
+// below takes exactly what these two files use — objects, arrays, strings,
+// numbers, true/false/null — and remembers whether a number was written as an
+// integer, which the header's shapes and offsets must be.
+#include "../../../include/whispereacp/SafeTensors.h"
+#include "../../../include/whispereacp/ModelError.h"
+#include "host_common.h"
+
+#include <algorithm>
+#include <cerrno>
+#include <cmath>
+#include <cstring>
+#include <fcntl.h>
+#include <fstream>
+#include <limits>
+#include <sstream>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+#include <utility>
+
+namespace WSP
+{
+namespace
+{
+// ---------------------------------------------------------------------------
+// JSON
+// ---------------------------------------------------------------------------
+struct Json
+{
+    enum class Kind
+    {
+        Null,
+        Bool,
+        Number,
+        String,
+        Array,
+        Object
+    };
+    Kind kind = Kind::Null;
+    bool boolean = false;
+    double number = 0;
+    bool integral = false; // written without fraction or exponent
+    long long integer = 0; // its value, when integral and in range
+    std::string text;
+    std::vector<Json> items;
+    std::vector<std::pair<std::string, Json>> members;
+
+    const Json* member(const std::string& key) const
+    {
+        for (const auto& [k, v]: members)
+            if (k == key)
+                return &v;
+        return nullptr;
+    }
+};
+
+class JsonReader
+{
+public:
+    JsonReader(const char* begin, const char* end, std::string what) : at(begin), stop(end), name(std::move(what)) {}
+
+    Json document()
+    {
+        Json value = parseValue(0);
+        skipSpace();
+        if (at != stop)
+            fail("trailing characters after the JSON value");
+        return value;
+    }
+
+private:
+    [[noreturn]] void fail(const std::string& why) const { throw ModelError(name + " is not valid JSON: " + why); }
+
+    void skipSpace()
+    {
+        while (at != stop && (*at == ' ' || *at == '\t' || *at == '\n' || *at == '\r'))
+            ++at;
+    }
+
+    Json parseValue(int depth)
+    {
+        if (depth > 64)
+            fail("nesting is too deep");
+        skipSpace();
+        if (at == stop)
+            fail("unexpected end");
+        const char c = *at;
+        if (c == '{')
+            return parseObject(depth);
+        if (c == '[')
+            return parseArray(depth);
+        if (c == '"')
+        {
+            Json v;
+            v.kind = Json::Kind::String;
+            v.text = parseString();
+            return v;
+        }
+        if (c == '-' || (c >= '0' && c <= '9'))
+            return parseNumber();
+        if (literal("true"))
+        {
+            Json v;
+            v.kind = Json::Kind::Bool;
+            v.boolean = true;
+            return v;
+        }
+        if (literal("false"))
+        {
+            Json v;
+            v.kind = Json::Kind::Bool;
+            return v;
+        }
+        if (literal("null"))
+            return Json {};
+        fail(std::string("unexpected character '") + c + "'");
+    }
+
+    bool literal(const char* word)
+    {
+        const std::size_t n = std::strlen(word);
+        if ((std::size_t) (stop - at) >= n && std::memcmp(at, word, n) == 0)
+        {
+            at += n;
+            return true;
+        }
+        return false;
+    }
+
+    Json parseObject(int depth)
+    {
+        Json v;
+        v.kind = Json::Kind::Object;
+        ++at;
+        skipSpace();
+        if (at != stop && *at == '}')
+        {
+            ++at;
+            return v;
+        }
+        while (true)
+        {
+            skipSpace();
+            if (at == stop || *at != '"')
+                fail("an object key is not a string");
+            std::string key = parseString();
+            skipSpace();
+            if (at == stop || *at != ':')
+                fail("a key is not followed by ':'");
+            ++at;
+            v.members.emplace_back(std::move(key), parseValue(depth + 1));
+            skipSpace();
+            if (at != stop && *at == ',')
+            {
+                ++at;
+                continue;
+            }
+            if (at != stop && *at == '}')
+            {
+                ++at;
+                return v;
+            }
+            fail("an object is not closed");
+        }
+    }
+
+    Json parseArray(int depth)
+    {
+        Json v;
+        v.kind = Json::Kind::Array;
+        ++at;
+        skipSpace();
+        if (at != stop && *at == ']')
+        {
+            ++at;
+            return v;
+        }
+        while (true)
+        {
+            v.items.push_back(parseValue(depth + 1));
+            skipSpace();
+            if (at != stop && *at == ',')
+            {
+                ++at;
+                continue;
+            }
+            if (at != stop && *at == ']')
+            {
+                ++at;
+                return v;
+            }
+            fail("an array is not closed");
+        }
+    }
+
+    static void appendUtf8(std::string& out, unsigned code)
+    {
+        if (code < 0x80)
+            out += (char) code;
+        else if (code < 0x800)
+        {
+            out += (char) (0xC0 | (code >> 6));
+            out += (char) (0x80 | (code & 0x3F));
+        }
+        else if (code < 0x10000)
+        {
+            out += (char) (0xE0 | (code >> 12));
+            out += (char) (0x80 | ((code >> 6) & 0x3F));
+            out += (char) (0x80 | (code & 0x3F));
+        }
+        else
+        {
+            out += (char) (0xF0 | (code >> 18));
+            out += (char) (0x80 | ((code >> 12) & 0x3F));
+            out += (char) (0x80 | ((code >> 6) & 0x3F));
+            out += (char) (0x80 | (code & 0x3F));
+        }
+    }
+
+    unsigned hex4()
+    {
+        if (stop - at < 4)
+            fail("a \\u escape is cut short");
+        unsigned v = 0;
+        for (int i = 0; i < 4; ++i)
+        {
+            const char c = *at++;
+            v <<= 4;
+            if (c >= '0' && c <= '9')
+                v |= (unsigned) (c - '0');
+            else if (c >= 'a' && c <= 'f')
+                v |= (unsigned) (c - 'a' + 10);
+            else if (c >= 'A' && c <= 'F')
+                v |= (unsigned) (c - 'A' + 10);
+            else
+                fail("a \\u escape has a non-hex digit");
+        }
+        return v;
+    }
+
+    std::string parseString()
+    {
+        ++at; // opening quote
+        std::string out;
+        while (true)
+        {
+            if (at == stop)
+                fail("a string is not closed");
+            const char c = *at++;
+            if (c == '"')
+                return out;
+            if ((unsigned char) c < 0x20)
+                fail("a string holds a control character");
+            if (c != '\\')
+            {
+                out += c;
+                continue;
+            }
+            if (at == stop)
+                fail("a string ends in an escape");
+            const char e = *at++;
+            switch (e)
+            {
+                case '"': out += '"'; break;
+                case '\\': out += '\\'; break;
+                case '/': out += '/'; break;
+                case 'b': out += '\b'; break;
+                case 'f': out += '\f'; break;
+                case 'n': out += '\n'; break;
+                case 'r': out += '\r'; break;
+                case 't': out += '\t'; break;
+                case 'u':
+                {
+                    unsigned code = hex4();
+                    if (code >= 0xD800 && code < 0xDC00)
+                    {
+                        if (stop - at < 6 || at[0] != '\\' || at[1] != 'u')
+                            fail("a surrogate pair is incomplete");
+                        at += 2;
+                        const unsigned low = hex4();
+                        if (low < 0xDC00 || low > 0xDFFF)
+                            fail("a surrogate pair is malformed");
+                        code = 0x10000 + ((code - 0xD800) << 10) + (low - 0xDC00);
+                    }
+                    appendUtf8(out, code);
+                    break;
+                }
+                default: fail(std::string("unknown escape \\") + e);
+            }
+        }
+    }
+
+    Json parseNumber()
+    {
+        const char* start = at;
+        bool integral = true;
+        if (*at == '-')
+            ++at;
+        if (at == stop || !(*at >= '0' && *at <= '9'))
+            fail("a number has no digits");
+        if (*at == '0')
+            ++at;
+        else
+            while (at != stop && *at >= '0' && *at <= '9')
+                ++at;
+        if (at != stop && *at == '.')
+        {
+            integral = false;
+            ++at;
+            if (at == stop || !(*at >= '0' && *at <= '9'))
+                fail("a fraction has no digits");
+            while (at != stop && *at >= '0' && *at <= '9')
+                ++at;
+        }
+        if (at != stop && (*at == 'e' || *at == 'E'))
+        {
+            integral = false;
+            ++at;
+            if (at != stop && (*at == '+' || *at == '-'))
+                ++at;
+            if (at == stop || !(*at >= '0' && *at <= '9'))
+                fail("an exponent has no digits");
+            while (at != stop && *at >= '0' && *at <= '9')
+                ++at;
+        }
+        const std::string digits(start, at);
+        Json v;
+        v.kind = Json::Kind::Number;
+        v.number = std::strtod(digits.c_str(), nullptr);
+        if (integral)
+        {
+            errno = 0;
+            const long long i = std::strtoll(digits.c_str(), nullptr, 10);
+            v.integral = errno == 0;
+            v.integer = i;
+        }
+        return v;
+    }
+
+    const char* at;
+    const char* stop;
+    std::string name;
+};
+
+// ---------------------------------------------------------------------------
+// dtypes
+// ---------------------------------------------------------------------------
+struct TypeName
+{
+    const char* name;
+    TensorType type;
+    int bytes;
+};
+
+constexpr TypeName kTypes[] = {
+    {"BOOL", TensorType::Bool, 1}, {"U8", TensorType::U8, 1},   {"I8", TensorType::I8, 1},
+    {"U16", TensorType::U16, 2},   {"I16", TensorType::I16, 2}, {"F16", TensorType::F16, 2},
+    {"BF16", TensorType::BF16, 2}, {"U32", TensorType::U32, 4}, {"I32", TensorType::I32, 4},
+    {"F32", TensorType::F32, 4},   {"U64", TensorType::U64, 8}, {"I64", TensorType::I64, 8},
+    {"F64", TensorType::F64, 8},
+};
+
+std::string describeShape(const std::vector<long long>& shape)
+{
+    std::ostringstream s;
+    s << "[";
+    for (std::size_t i = 0; i < shape.size(); ++i)
+        s << (i ? "," : "") << shape[i];
+    s << "]";
+    return s.str();
+}
+
+std::uint64_t readLittleEndian64(const std::uint8_t* p)
+{
+    std::uint64_t v = 0;
+    for (int i = 7; i >= 0; --i)
+        v = (v << 8) | p[i];
+    return v;
+}
+} // namespace
+
+const char* tensorTypeName(TensorType type)
+{
+    for (const auto& t: kTypes)
+        if (t.type == type)
+            return t.name;
+    return "?";
+}
+
+int tensorTypeBytes(TensorType type)
+{
+    for (const auto& t: kTypes)
+        if (t.type == type)
+            return t.bytes;
+    return 0;
+}
+
+long long TensorInfo::elementCount() const
+{
+    long long n = 1;
+    for (long long d: shape)
+        n *= d;
+    return n;
+}
+
+// Either a private copy of the bytes or a read-only mapping of the file.
+struct SafeTensors::Storage
+{
+    std::vector<std::uint8_t> copy;
+    void* map = nullptr;
+    std::size_t mapBytes = 0;
+
+    ~Storage()
+    {
+        if (map != nullptr)
+            munmap(map, mapBytes);
+    }
+};
+
+SafeTensors::SafeTensors(SafeTensors&&) noexcept = default;
+SafeTensors& SafeTensors::operator=(SafeTensors&&) noexcept = default;
+SafeTensors::~SafeTensors() = default;
+
+SafeTensors SafeTensors::fromBytes(const void* bytes, std::size_t size)
+{
+    SafeTensors file;
+    file.storage = std::make_unique<Storage>();
+    file.storage->copy.assign(static_cast<const std::uint8_t*>(bytes), static_cast<const std::uint8_t*>(bytes) + size);
+    file.parse(file.storage->copy.data(), size);
+    return file;
+}
+
+SafeTensors SafeTensors::fromFile(const std::string& path)
+{
+    const int fd = ::open(path.c_str(), O_RDONLY);
+    if (fd < 0)
+        throw ModelError("cannot open '" + path + "': " + std::strerror(errno));
+    struct stat st {};
+    if (::fstat(fd, &st) != 0 || !S_ISREG(st.st_mode))
+    {
+        ::close(fd);
+        throw ModelError("'" + path + "' is not a regular file");
+    }
+    const std::size_t size = (std::size_t) st.st_size;
+    SafeTensors file;
+    file.storage = std::make_unique<Storage>();
+    if (size > 0)
+    {
+        void* map = ::mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
+        ::close(fd);
+        if (map == MAP_FAILED)
+            throw ModelError("cannot map '" + path + "': " + std::strerror(errno));
+        file.storage->map = map;
+        file.storage->mapBytes = size;
+        file.parse(static_cast<const std::uint8_t*>(map), size);
+    }
+    else
+    {
+        ::close(fd);
+        file.parse(nullptr, 0);
+    }
+    return file;
+}
+
+void SafeTensors::parse(const std::uint8_t* bytes, std::size_t size)
+{
+    if (size < 8)
+        throw ModelError("a safetensors file is shorter than its 8-byte header length");
+    const std::uint64_t headerBytes = readLittleEndian64(bytes);
+    if (headerBytes > size - 8)
+        throw ModelError("the safetensors header length " + std::to_string(headerBytes) + " runs past the "
+                         + std::to_string(size) + "-byte file");
+    const char* text = reinterpret_cast<const char*>(bytes + 8);
+    const Json header = JsonReader(text, text + headerBytes, "the safetensors header").document();
+    if (header.kind != Json::Kind::Object)
+        throw ModelError("the safetensors header is not a JSON object");
+    blob = bytes + 8 + headerBytes;
+    blobBytes = size - 8 - headerBytes;
+
+    for (const auto& [key, value]: header.members)
+    {
+        if (key == "__metadata__")
+        {
+            if (value.kind != Json::Kind::Object)
+                throw ModelError("__metadata__ is not an object");
+            for (const auto& [mk, mv]: value.members)
+            {
+                if (mv.kind != Json::Kind::String)
+                    throw ModelError("__metadata__ entry '" + mk + "' is not a string");
+                meta[mk] = mv.text;
+            }
+            continue;
+        }
+        if (value.kind != Json::Kind::Object)
+            throw ModelError("tensor '" + key + "' is not described by an object");
+        const Json* dtype = value.member("dtype");
+        const Json* shape = value.member("shape");
+        const Json* offsets = value.member("data_offsets");
+        if (dtype == nullptr || shape == nullptr || offsets == nullptr)
+            throw ModelError("tensor '" + key + "' lacks dtype, shape or data_offsets");
+        if (dtype->kind != Json::Kind::String)
+            throw ModelError("tensor '" + key + "' has a dtype that is not a string");
+
+        TensorInfo t;
+        t.name = key;
+        int elementBytes = 0;
+        for (const auto& ty: kTypes)
+            if (dtype->text == ty.name)
+            {
+                t.type = ty.type;
+                elementBytes = ty.bytes;
+            }
+        if (elementBytes == 0)
+            throw ModelError("tensor '" + key + "' has the unsupported dtype '" + dtype->text + "'");
+
+        if (shape->kind != Json::Kind::Array)
+            throw ModelError("tensor '" + key + "' has a shape that is not an array");
+        long double elements = 1;
+        for (const Json& d: shape->items)
+        {
+            if (d.kind != Json::Kind::Number || !d.integral || d.integer < 0)
+                throw ModelError("tensor '" + key + "' has a shape entry that is not a non-negative integer");
+            t.shape.push_back(d.integer);
+            elements *= (long double) d.integer;
+        }
+
+        if (offsets->kind != Json::Kind::Array || offsets->items.size() != 2)
+            throw ModelError("tensor '" + key + "' needs data_offsets [begin, end]");
+        for (const Json& o: offsets->items)
+            if (o.kind != Json::Kind::Number || !o.integral || o.integer < 0)
+                throw ModelError("tensor '" + key + "' has a data offset that is not a non-negative integer");
+        t.begin = (std::uint64_t) offsets->items[0].integer;
+        t.end = (std::uint64_t) offsets->items[1].integer;
+        if (t.end < t.begin)
+            throw ModelError("tensor '" + key + "' ends before it begins");
+        if (t.end > blobBytes)
+            throw ModelError("tensor '" + key + "' runs past the " + std::to_string(blobBytes) + "-byte data blob");
+        t.byteCount = t.end - t.begin;
+        if ((long double) t.byteCount != elements * (long double) elementBytes)
+            throw ModelError("tensor '" + key + "' has shape " + describeShape(t.shape) + " of " + dtype->text
+                             + ", which is not the " + std::to_string(t.byteCount) + " bytes its range holds");
+        entries.push_back(std::move(t));
+    }
+    std::sort(entries.begin(), entries.end(), [](const TensorInfo& a, const TensorInfo& b) { return a.name < b.name; });
+    for (std::size_t i = 1; i < entries.size(); ++i)
+        if (entries[i].name == entries[i - 1].name)
+            throw ModelError("tensor '" + entries[i].name + "' is listed twice");
+
+    for (const TensorInfo& t: entries)
+    {
+        HostTensor h;
+        h.dtype = tensorTypeName(t.type);
+        h.extents = t.shape;
+        h.data = blob + t.begin;
+        hostTensors.emplace(t.name, std::move(h));
+    }
+}
+
+std::vector<std::string> SafeTensors::names() const
+{
+    std::vector<std::string> out;
+    out.reserve(entries.size());
+    for (const TensorInfo& t: entries)
+        out.push_back(t.name);
+    return out;
+}
+
+const TensorInfo* SafeTensors::findInfo(const std::string& name) const
+{
+    const auto it = std::lower_bound(entries.begin(), entries.end(), name,
+                                     [](const TensorInfo& t, const std::string& n) { return t.name < n; });
+    return it != entries.end() && it->name == name ? &*it : nullptr;
+}
+
+const TensorInfo& SafeTensors::info(const std::string& name) const
+{
+    const TensorInfo* t = findInfo(name);
+    if (t == nullptr)
+        throw ModelError("the safetensors file has no tensor '" + name + "'");
+    return *t;
+}
+
+const HostTensor* SafeTensors::find(const std::string& name) const
+{
+    const auto it = hostTensors.find(name);
+    return it == hostTensors.end() ? nullptr : &it->second;
+}
+
+void SafeTensors::readFloats(const std::string& name, float* destination, std::size_t capacity) const
+{
+    const TensorInfo& t = info(name);
+    const std::size_t n = (std::size_t) t.elementCount();
+    if (capacity < n)
+        throw ModelError("tensor '" + name + "' holds " + std::to_string(n) + " values, more than the "
+                         + std::to_string(capacity) + " the destination takes");
+    const std::uint8_t* p = rawBytes(t);
+    switch (t.type)
+    {
+        case TensorType::F32: std::memcpy(destination, p, n * 4); break;
+        case TensorType::F16:
+        case TensorType::BF16:
+            for (std::size_t i = 0; i < n; ++i)
+            {
+                std::uint16_t bits;
+                std::memcpy(&bits, p + 2 * i, 2);
+                destination[i] = t.type == TensorType::F16 ? halfToFloat(bits) : bfloat16ToFloat(bits);
+            }
+            break;
+        case TensorType::F64:
+            for (std::size_t i = 0; i < n; ++i)
+            {
+                double v;
+                std::memcpy(&v, p + 8 * i, 8);
+                destination[i] = (float) v;
+            }
+            break;
+        default:
+            throw ModelError("tensor '" + name + "' is " + tensorTypeName(t.type) + ", not a floating-point type");
+    }
+}
+
+std::vector<float> SafeTensors::readFloats(const std::string& name) const
+{
+    std::vector<float> out((std::size_t) info(name).elementCount());
+    readFloats(name, out.data(), out.size());
+    return out;
+}
+
+// ---------------------------------------------------------------------------
+// config.json
+// ---------------------------------------------------------------------------
+namespace
+{
+int positiveField(const Json& config, const char* key)
+{
+    const Json* v = config.member(key);
+    if (v == nullptr)
+        throw ModelError(std::string("config.json has no '") + key + "'");
+    if (v->kind != Json::Kind::Number || !v->integral || v->integer <= 0 || v->integer > std::numeric_limits<int>::max())
+        throw ModelError(std::string("config.json '") + key + "' is not a positive integer");
+    return (int) v->integer;
+}
+} // namespace
+
+DecoderShape decoderShapeFromConfig(const std::string& json, int crossPositionCount)
+{
+    const Json config = JsonReader(json.data(), json.data() + json.size(), "config.json").document();
+    if (config.kind != Json::Kind::Object)
+        throw ModelError("config.json is not a JSON object");
+    if (const Json* type = config.member("model_type"))
+        if (type->kind != Json::Kind::String || type->text != "whisper")
+            throw ModelError("config.json describes a '" + (type->kind == Json::Kind::String ? type->text : "?")
+                             + "' model, not a whisper one");
+    DecoderShape s;
+    s.width = positiveField(config, "d_model");
+    s.heads = positiveField(config, "decoder_attention_heads");
+    s.layers = positiveField(config, "decoder_layers");
+    s.feedForwardWidth = positiveField(config, "decoder_ffn_dim");
+    s.vocabularySize = positiveField(config, "vocab_size");
+    s.maxPositions = positiveField(config, "max_target_positions");
+    const int source = positiveField(config, "max_source_positions");
+    if (s.width % s.heads != 0)
+        throw ModelError("config.json d_model does not divide into the decoder head count");
+    if (crossPositionCount < 0)
+        throw ModelError("a negative cross position count");
+    s.crossPositions = crossPositionCount == 0 ? source : crossPositionCount;
+    return s;
+}
+
+DecoderShape decoderShapeFromConfigFile(const std::string& path, int crossPositionCount)
+{
+    std::ifstream in(path, std::ios::binary);
+    if (!in)
+        throw ModelError("cannot open '" + path + "'");
+    std::ostringstream text;
+    text << in.rdbuf();
+    return decoderShapeFromConfig(text.str(), crossPositionCount);
+}
+} // namespace WSP

@@ -6,8 +6,10 @@
 #include "../../../include/whispereacp/BatchedDecoder.h"
 #include "../../../include/whispereacp/Decoder.h"
 #include "../../../include/whispereacp/GreedyDecoder.h"
+#include "../../../include/whispereacp/SafeTensors.h"
 
 #include <algorithm>
+#include <cstring>
 #include <memory>
 #include <new>
 #include <stdexcept>
@@ -22,6 +24,13 @@ struct wsp_decoder
     std::unique_ptr<WSP::Decoder> decoder;
     std::unique_ptr<WSP::Argmax> selection;
     std::unique_ptr<WSP::GreedyDecoder> greedy;
+    std::string error;
+    int errorKind = WSP_KIND_NONE;
+};
+
+struct wsp_safetensors
+{
+    std::unique_ptr<WSP::SafeTensors> file;
     std::string error;
     int errorKind = WSP_KIND_NONE;
 };
@@ -107,6 +116,29 @@ WSP::MapTensorSource sourceOf(const wsp_tensor_entry* tensors, int count)
     }
     return source;
 }
+
+WSP::WeightPacking packingOf(int packing)
+{
+    return packing == 1 ? WSP::WeightPacking::ExactHalf : WSP::WeightPacking::Float;
+}
+
+// DecoderWeights + Decoder + Argmax, every buffer sized once.
+void buildDecoder(wsp_decoder* d, const WSP::TensorSource& source, int packing, void* stream)
+{
+    d->weights = std::make_unique<WSP::DecoderWeights>(source, d->shape, packingOf(packing), d->device);
+    d->decoder = std::make_unique<WSP::Decoder>(d->shape);
+    d->decoder->prepare(d->device, stream);
+    d->selection = std::make_unique<WSP::Argmax>();
+    d->selection->prepare(d->device, d->shape.maxPositions, d->shape.vocabularySize, stream);
+}
+
+void buildBatch(wsp_batch_decoder* d, const WSP::TensorSource& source, int packing, int streams, int maxStepTokens,
+                void* stream)
+{
+    d->weights = std::make_unique<WSP::DecoderWeights>(source, d->shape, packingOf(packing), d->device);
+    d->decoder = std::make_unique<WSP::BatchedDecoder>(d->shape, streams, maxStepTokens);
+    d->decoder->prepare(*d->weights, d->device, stream);
+}
 } // namespace
 
 extern "C" {
@@ -125,12 +157,7 @@ int wsp_decoder_create(const wsp_decoder_shape* shape, const wsp_tensor_entry* t
         d->device = WSP::Device {device};
         d->stream = stream;
         const WSP::MapTensorSource source = sourceOf(tensors, count);
-        d->weights = std::make_unique<WSP::DecoderWeights>(
-            source, d->shape, packing == 1 ? WSP::WeightPacking::ExactHalf : WSP::WeightPacking::Float, d->device);
-        d->decoder = std::make_unique<WSP::Decoder>(d->shape);
-        d->decoder->prepare(d->device, stream);
-        d->selection = std::make_unique<WSP::Argmax>();
-        d->selection->prepare(d->device, d->shape.maxPositions, d->shape.vocabularySize, stream);
+        buildDecoder(d, source, packing, stream);
     });
     if (status != WSP_OK)
     {
@@ -142,6 +169,31 @@ int wsp_decoder_create(const wsp_decoder_shape* shape, const wsp_tensor_entry* t
     }
     *out = d;
     return WSP_OK;
+}
+
+int wsp_decoder_create_from_file(const char* path, const wsp_decoder_shape* shape, int packing, int device,
+                                 void* stream, wsp_decoder** out)
+{
+    if (path == nullptr || shape == nullptr || out == nullptr)
+        return WSP_ERR_ARGUMENT;
+    *out = nullptr;
+    auto* d = new (std::nothrow) wsp_decoder {};
+    if (d == nullptr)
+        return WSP_ERR_CAPACITY;
+    const int status = guarded(d, [&] {
+        d->shape = checkedShape(shape);
+        d->device = WSP::Device {device};
+        d->stream = stream;
+        const WSP::SafeTensors file = WSP::SafeTensors::fromFile(path);
+        buildDecoder(d, file, packing, stream);
+    });
+    if (status != WSP_OK)
+    {
+        d->decoder.reset();
+        d->weights.reset();
+    }
+    *out = d;
+    return status;
 }
 
 void wsp_decoder_destroy(wsp_decoder* d)
@@ -287,10 +339,7 @@ int wsp_batch_decoder_create(const wsp_decoder_shape* shape, const wsp_tensor_en
         d->shape = checkedShape(shape);
         d->device = WSP::Device {device};
         const WSP::MapTensorSource source = sourceOf(tensors, count);
-        d->weights = std::make_unique<WSP::DecoderWeights>(
-            source, d->shape, packing == 1 ? WSP::WeightPacking::ExactHalf : WSP::WeightPacking::Float, d->device);
-        d->decoder = std::make_unique<WSP::BatchedDecoder>(d->shape, streams, max_step_tokens);
-        d->decoder->prepare(*d->weights, d->device, stream);
+        buildBatch(d, source, packing, streams, max_step_tokens, stream);
     });
     if (status != WSP_OK)
     {
@@ -367,6 +416,127 @@ int wsp_batch_decoder_position(const wsp_batch_decoder* d)
 const float* wsp_batch_decoder_hidden_states(const wsp_batch_decoder* d)
 {
     return d == nullptr || !d->decoder ? nullptr : static_cast<const float*>(d->decoder->hiddenStates().data());
+}
+
+int wsp_batch_decoder_create_from_file(const char* path, const wsp_decoder_shape* shape, int packing, int streams,
+                                       int max_step_tokens, int device, void* stream, wsp_batch_decoder** out)
+{
+    if (path == nullptr || shape == nullptr || out == nullptr)
+        return WSP_ERR_ARGUMENT;
+    *out = nullptr;
+    auto* d = new (std::nothrow) wsp_batch_decoder {};
+    if (d == nullptr)
+        return WSP_ERR_CAPACITY;
+    const int status = guarded(d, [&] {
+        d->shape = checkedShape(shape);
+        d->device = WSP::Device {device};
+        const WSP::SafeTensors file = WSP::SafeTensors::fromFile(path);
+        buildBatch(d, file, packing, streams, max_step_tokens, stream);
+    });
+    if (status != WSP_OK)
+    {
+        d->decoder.reset();
+        d->weights.reset();
+    }
+    *out = d;
+    return status;
+}
+
+int wsp_safetensors_open(const char* path, wsp_safetensors** out)
+{
+    if (path == nullptr || out == nullptr)
+        return WSP_ERR_ARGUMENT;
+    auto* f = new (std::nothrow) wsp_safetensors {};
+    if (f == nullptr)
+        return WSP_ERR_CAPACITY;
+    *out = f;
+    return guarded(f, [&] { f->file = std::make_unique<WSP::SafeTensors>(WSP::SafeTensors::fromFile(path)); });
+}
+
+int wsp_safetensors_open_bytes(const void* bytes, size_t size, wsp_safetensors** out)
+{
+    if ((bytes == nullptr && size > 0) || out == nullptr)
+        return WSP_ERR_ARGUMENT;
+    auto* f = new (std::nothrow) wsp_safetensors {};
+    if (f == nullptr)
+        return WSP_ERR_CAPACITY;
+    *out = f;
+    return guarded(f, [&] { f->file = std::make_unique<WSP::SafeTensors>(WSP::SafeTensors::fromBytes(bytes, size)); });
+}
+
+void wsp_safetensors_close(wsp_safetensors* f)
+{
+    delete f;
+}
+
+const char* wsp_safetensors_last_error(const wsp_safetensors* f)
+{
+    return f == nullptr ? "no file" : f->error.c_str();
+}
+
+int wsp_safetensors_count(const wsp_safetensors* f)
+{
+    return f == nullptr || !f->file ? -1 : (int) f->file->tensors().size();
+}
+
+int wsp_safetensors_tensor(const wsp_safetensors* f, int index, const char** name, const char** dtype, int* rank,
+                           long long* extents, int capacity, long long* byte_count)
+{
+    if (f == nullptr || !f->file || index < 0 || index >= (int) f->file->tensors().size())
+        return WSP_ERR_ARGUMENT;
+    const WSP::TensorInfo& t = f->file->tensors()[(std::size_t) index];
+    if (name != nullptr)
+        *name = t.name.c_str();
+    if (dtype != nullptr)
+        *dtype = WSP::tensorTypeName(t.type);
+    if (rank != nullptr)
+        *rank = t.rank();
+    if (extents != nullptr)
+        for (int i = 0; i < t.rank() && i < capacity; ++i)
+            extents[i] = t.shape[(std::size_t) i];
+    if (byte_count != nullptr)
+        *byte_count = (long long) t.byteCount;
+    return WSP_OK;
+}
+
+int wsp_safetensors_read_floats(wsp_safetensors* f, const char* name, float* out, long long capacity)
+{
+    return guarded(f, [&] {
+        if (!f->file)
+            throw std::logic_error("this safetensors file failed to open");
+        if (name == nullptr || (out == nullptr && capacity > 0) || capacity < 0)
+            throw std::invalid_argument("wsp_safetensors_read_floats: null name or destination");
+        f->file->readFloats(name, out, (std::size_t) capacity);
+    });
+}
+
+const char* wsp_safetensors_metadata(const wsp_safetensors* f, const char* key)
+{
+    if (f == nullptr || !f->file || key == nullptr)
+        return nullptr;
+    const auto it = f->file->metadata().find(key);
+    return it == f->file->metadata().end() ? nullptr : it->second.c_str();
+}
+
+int wsp_shape_from_config(const char* config_path, int cross_positions, wsp_decoder_shape* out, char* error,
+                          int error_capacity)
+{
+    if (config_path == nullptr || out == nullptr)
+        return WSP_ERR_ARGUMENT;
+    try
+    {
+        *out = WSP::decoderShapeFromConfigFile(config_path, cross_positions).toC();
+        return WSP_OK;
+    }
+    catch (const std::exception& e)
+    {
+        if (error != nullptr && error_capacity > 0)
+        {
+            std::strncpy(error, e.what(), (std::size_t) error_capacity - 1);
+            error[error_capacity - 1] = 0;
+        }
+        return WSP_ERR_SHAPE;
+    }
 }
 
 } // extern "C"

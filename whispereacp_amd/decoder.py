@@ -124,17 +124,22 @@ class Decoder:
     """DecoderWeights + Decoder + Argmax over the gfx950 library
     (include/wsp_decoder.h)."""
 
-    def __init__(self, shape: DecoderShape, decoder_file: DecoderFile, packing: str = "Float",
-                 device: int = 0):
+    def __init__(self, shape: DecoderShape, decoder_file: Optional[DecoderFile] = None, packing: str = "Float",
+                 device: int = 0, path: Optional[str] = None):
+        """From the tensors of decoder_file, or of the safetensors file at path."""
         self.lib = N.load()
         self.shape = shape
-        entries, keep = tensor_entries(decoder_file)
         self._cshape = c_shape(shape)
         handle = ctypes.c_void_p()
-        status = self.lib.wsp_decoder_create(ctypes.byref(self._cshape), entries, len(decoder_file),
-                                             1 if packing == "ExactHalf" else 0, device, current_stream(),
-                                             ctypes.byref(handle))
-        del keep
+        pack = 1 if packing == "ExactHalf" else 0
+        if path is not None:
+            status = self.lib.wsp_decoder_create_from_file(path.encode(), ctypes.byref(self._cshape), pack, device,
+                                                           current_stream(), ctypes.byref(handle))
+        else:
+            entries, keep = tensor_entries(decoder_file)
+            status = self.lib.wsp_decoder_create(ctypes.byref(self._cshape), entries, len(decoder_file), pack,
+                                                 device, current_stream(), ctypes.byref(handle))
+            del keep
         self.handle = handle
         if status != N.WSP_OK:
             message = self.lib.wsp_decoder_last_error(handle).decode() if handle else "create failed"
@@ -227,18 +232,25 @@ class BatchedDecoder:
     (wsp_batch_decoder_* in include/wsp_decoder.h): `streams` independent
     sequences that advance together and share one weight read per step."""
 
-    def __init__(self, shape: DecoderShape, decoder_file: DecoderFile, streams: int, max_step_tokens: int = 4,
-                 packing: str = "ExactHalf", device: int = 0):
+    def __init__(self, shape: DecoderShape, decoder_file: Optional[DecoderFile], streams: int,
+                 max_step_tokens: int = 4, packing: str = "ExactHalf", device: int = 0, path: Optional[str] = None):
+        """From the tensors of decoder_file, or of the safetensors file at path."""
         self.lib = N.load()
         self.shape = shape
         self.streams = streams
-        entries, keep = tensor_entries(decoder_file)
         self._cshape = c_shape(shape)
         handle = ctypes.c_void_p()
-        status = self.lib.wsp_batch_decoder_create(ctypes.byref(self._cshape), entries, len(decoder_file),
-                                                   1 if packing == "ExactHalf" else 0, streams, max_step_tokens,
-                                                   device, current_stream(), ctypes.byref(handle))
-        del keep
+        pack = 1 if packing == "ExactHalf" else 0
+        if path is not None:
+            status = self.lib.wsp_batch_decoder_create_from_file(path.encode(), ctypes.byref(self._cshape), pack,
+                                                                 streams, max_step_tokens, device, current_stream(),
+                                                                 ctypes.byref(handle))
+        else:
+            entries, keep = tensor_entries(decoder_file)
+            status = self.lib.wsp_batch_decoder_create(ctypes.byref(self._cshape), entries, len(decoder_file), pack,
+                                                       streams, max_step_tokens, device, current_stream(),
+                                                       ctypes.byref(handle))
+            del keep
         self.handle = handle
         if status != N.WSP_OK:
             message = self.lib.wsp_batch_decoder_last_error(handle).decode() if handle else "create failed"
@@ -283,6 +295,68 @@ class BatchedDecoder:
         copy_device(out, self.lib.wsp_batch_decoder_hidden_states(self.handle), rows * self.shape.width * 4)
         torch.cuda.synchronize()
         return out.cpu().numpy()
+
+
+class SafeTensorsFile:
+    """A safetensors file opened by the library's reader (wsp_safetensors_*):
+    mapped, validated when opened (ModelError with the reason otherwise)."""
+
+    def __init__(self, path: Optional[str] = None, data: Optional[bytes] = None):
+        self.lib = N.load()
+        handle = ctypes.c_void_p()
+        if path is not None:
+            status = self.lib.wsp_safetensors_open(path.encode(), ctypes.byref(handle))
+        else:
+            self._data = bytes(data or b"")
+            status = self.lib.wsp_safetensors_open_bytes(self._data, len(self._data), ctypes.byref(handle))
+        self.handle = handle
+        if status != N.WSP_OK:
+            message = self.lib.wsp_safetensors_last_error(handle).decode() if handle else "open failed"
+            self.close()
+            raise ModelError(message)
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.wsp_safetensors_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+    def tensors(self) -> List[Tuple[str, str, Tuple[int, ...], int]]:
+        """(name, dtype, shape, byte count) in name order."""
+        out = []
+        for i in range(self.lib.wsp_safetensors_count(self.handle)):
+            name, dtype = ctypes.c_char_p(), ctypes.c_char_p()
+            rank, nbytes = ctypes.c_int(), ctypes.c_longlong()
+            extents = (ctypes.c_longlong * 16)()
+            self.lib.wsp_safetensors_tensor(self.handle, i, ctypes.byref(name), ctypes.byref(dtype),
+                                            ctypes.byref(rank), extents, 16, ctypes.byref(nbytes))
+            out.append((name.value.decode(), dtype.value.decode(), tuple(extents[:rank.value]), nbytes.value))
+        return out
+
+    def read_floats(self, name: str, count: int) -> np.ndarray:
+        out = np.empty(count, dtype=np.float32)
+        status = self.lib.wsp_safetensors_read_floats(self.handle, name.encode(), out.ctypes.data, count)
+        if status != N.WSP_OK:
+            _raise(N.WSP_KIND_MODEL_ERROR if status == N.WSP_ERR_SHAPE else N.WSP_KIND_NONE,
+                   self.lib.wsp_safetensors_last_error(self.handle).decode(), status)
+        return out
+
+    def metadata(self, key: str) -> Optional[str]:
+        v = self.lib.wsp_safetensors_metadata(self.handle, key.encode())
+        return None if v is None else v.decode()
+
+
+def shape_from_config(path: str, cross_positions: int = 0) -> DecoderShape:
+    """DecoderShape::fromConfig over a HuggingFace config.json."""
+    lib = N.load()
+    out = N.wsp_decoder_shape()
+    error = ctypes.create_string_buffer(512)
+    if lib.wsp_shape_from_config(path.encode(), cross_positions, ctypes.byref(out), error, 512) != N.WSP_OK:
+        raise ModelError(error.value.decode())
+    return DecoderShape(out.width, out.heads, out.layers, out.feed_forward_width, out.vocabulary_size,
+                        out.max_positions, out.cross_positions)
 
 
 _hip = None
