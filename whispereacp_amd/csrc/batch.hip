@@ -73,6 +73,30 @@ __device__ __forceinline__ void store_split(u16* out, size_t part_stride, size_t
     }
 }
 
+// The same parts as register values.
+template <int WT>
+__device__ __forceinline__ void split_value(float x, u16 (&out)[parts_of<WT>()])
+{
+    if constexpr (WT == kF16)
+    {
+        const _Float16 hi = (_Float16) x;
+        const _Float16 lo = (_Float16) (x - (float) hi);
+        out[0] = __builtin_bit_cast(u16, hi);
+        out[1] = __builtin_bit_cast(u16, lo);
+    }
+    else
+    {
+        float rest = x;
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+        {
+            const __bf16 b = (__bf16) rest;
+            out[p] = __builtin_bit_cast(u16, b);
+            rest -= (float) b;
+        }
+    }
+}
+
 template <int WT>
 __device__ __forceinline__ float4v mfma16(u32x4 a, u32x4 b, float4v c)
 {
@@ -121,6 +145,8 @@ __global__ void __launch_bounds__(kNormThreads) norm_kernel(Norm a)
             h[c] = token < (uint32_t) a.vocabulary
                        ? a.token_table[(size_t) token * a.width + c] + a.position_table[(size_t) position * a.width + c]
                        : __builtin_nanf("");
+        if (a.xs == nullptr) // the embedding only: the next product normalises
+            return;
     }
     float total = 0.f;
     for (int c = threadIdx.x; c < a.width; c += kNormThreads)
@@ -178,6 +204,11 @@ struct Product
     size_t stream_stride;
     const int* state; // device word: the position of the step's first token
     int step_tokens, width;
+    // normed_product_kernel: x = LayerNorm(h) computed in the product
+    const float* h;   // [rows_padded][inner] residual stream
+    const float* gamma;
+    const float* beta;
+    float eps;
 };
 
 template <int WT>
@@ -239,10 +270,13 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
     // The weights of the next batch of k-blocks are requested before the
     // products of the current one, so HBM latency overlaps the matrix work;
     // activations (L2-resident) are loaded per batch.
+    // A wave may own no k-block (inner < 256): its loads then re-read its
+    // first block index, which is always < inner / 32, and are never used.
+    const int kb_last = max(kb_end - 1, kb_begin);
     u32x4 wv[KB];
 #pragma unroll
     for (int u = 0; u < KB; ++u)
-        wv[u] = *reinterpret_cast<const u32x4*>(wrow + min(kb_begin + u, kb_end - 1) * 32);
+        wv[u] = *reinterpret_cast<const u32x4*>(wrow + min(kb_begin + u, kb_last) * 32);
     for (int kb = kb_begin; kb < kb_end; kb += KB)
     {
         u32x4 xv[KB][P][MT];
@@ -286,6 +320,156 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
     }
 
     // acc[t][r] of lane (g, li) is C[4g + r][li] of row tile t.
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+    {
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            partial[wave][lane * 4 + r] = acc[t][r];
+        __syncthreads();
+        if (threadIdx.x < 256)
+        {
+            const int row = threadIdx.x / 16, col = threadIdx.x % 16;
+            const int src = ((row / 4) * 16 + col) * 4 + row % 4;
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < kProductWaves; ++w)
+                v += partial[w][src];
+            const int m = t * 16 + row, n = n0 + col;
+            if (m < a.rows && n < a.out)
+                finish<WT>(a, m, n, v);
+        }
+    }
+}
+
+// The same product with a LayerNorm in front (Kernels/LayerNorm.h:44-89):
+// x = (h - mean)·rsqrt(var + eps)·gamma + beta of the fp32 residual rows, for
+// up to 32 rows and inner ≤ 2048. Every wave holds the h values of its whole
+// k-range in registers, so the row statistics are two fixed-order sums of
+// per-wave partials through LDS — mean first, then the centred squares — and
+// the normalised values are split into their 16-bit parts in registers. No
+// separate LayerNorm launch, and no split activations written or read.
+constexpr int kNormedBlocks = 5;   // k-blocks per wave: inner <= 8 waves * 5 * 32 = 1280
+constexpr int kNormedWidth = kProductWaves * kNormedBlocks * 32;
+
+template <int WT, int MT>
+__global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product a)
+{
+    constexpr int P = parts_of<WT>();
+    __shared__ float partial[kProductWaves][256];
+    __shared__ float stats[2][kProductWaves][MT * 16];
+    __shared__ float4v sh_gamma[kNormedWidth / 4], sh_beta[kNormedWidth / 4];
+
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int li = lane % 16, g = lane / 16;
+    const int n0 = blockIdx.x * 16;
+    const int kblocks = a.inner / 32;
+    const int kb_begin = wave * kblocks / kProductWaves;
+    const int kb_end = (wave + 1) * kblocks / kProductWaves;
+    const int nkb = kb_end - kb_begin;
+    const u16* wrow = static_cast<const u16*>(a.w) + (size_t) min(n0 + li, a.out - 1) * a.inner + 8 * g;
+    const float* hrow = a.h + (size_t) li * a.inner + 8 * g;
+
+    u32x4 wv[kNormedBlocks];
+    float4v hv[kNormedBlocks][MT][2];
+#pragma unroll
+    for (int u = 0; u < kNormedBlocks; ++u)
+        if (u < nkb)
+        {
+            const int k = (kb_begin + u) * 32;
+            wv[u] = *reinterpret_cast<const u32x4*>(wrow + k);
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+            {
+                hv[u][t][0] = *reinterpret_cast<const float4v*>(hrow + (size_t) t * 16 * a.inner + k);
+                hv[u][t][1] = *reinterpret_cast<const float4v*>(hrow + (size_t) t * 16 * a.inner + k + 4);
+            }
+        }
+    for (int i = threadIdx.x; i < a.inner / 4; i += kProductThreads)
+    {
+        sh_gamma[i] = reinterpret_cast<const float4v*>(a.gamma)[i];
+        sh_beta[i] = reinterpret_cast<const float4v*>(a.beta)[i];
+    }
+
+    // Row t*16 + li: this lane's 8·nkb values, summed over the four lanes of
+    // the row (l ^ 16, l ^ 32), then over the 8 waves in order.
+    float mean[MT], scale[MT];
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass)
+    {
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+        {
+            float s = 0.f;
+#pragma unroll
+            for (int u = 0; u < kNormedBlocks; ++u)
+                if (u < nkb)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                        {
+                            const float v = hv[u][t][j][e];
+                            s += pass == 0 ? v : (v - mean[t]) * (v - mean[t]);
+                        }
+            s += __shfl_xor(s, 16);
+            s += __shfl_xor(s, 32);
+            if (g == 0)
+                stats[pass][wave][t * 16 + li] = s;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+        {
+            float total = 0.f;
+#pragma unroll
+            for (int w = 0; w < kProductWaves; ++w)
+                total += stats[pass][w][t * 16 + li];
+            if (pass == 0)
+                mean[t] = total / (float) a.inner;
+            else
+                scale[t] = rsqrtf(total / (float) a.inner + a.eps);
+        }
+    }
+
+    float4v acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+        acc[t] = float4v {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kNormedBlocks; ++u)
+        if (u < nkb)
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+            {
+                uint32_t packed[P][4];
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2)
+                {
+                    uint32_t lo16[P], hi16[P];
+#pragma unroll
+                    for (int half = 0; half < 2; ++half)
+                    {
+                        const int e = 2 * e2 + half;
+                        const int q4 = ((kb_begin + u) * 32 + 8 * g) / 4 + e / 4;
+                        const float v = (hv[u][t][e / 4][e % 4] - mean[t]) * scale[t] * sh_gamma[q4][e % 4]
+                                        + sh_beta[q4][e % 4];
+                        u16 parts[P];
+                        split_value<WT>(v, parts);
+#pragma unroll
+                        for (int p = 0; p < P; ++p)
+                            (half == 0 ? lo16 : hi16)[p] = parts[p];
+                    }
+#pragma unroll
+                    for (int p = 0; p < P; ++p)
+                        packed[p][e2] = lo16[p] | (hi16[p] << 16);
+                }
+#pragma unroll
+                for (int p = 0; p < P; ++p)
+                    acc[t] = mfma16<WT>(u32x4 {packed[p][0], packed[p][1], packed[p][2], packed[p][3]}, wv[u], acc[t]);
+            }
+
 #pragma unroll
     for (int t = 0; t < MT; ++t)
     {
@@ -527,6 +711,24 @@ hipError_t launch_product(hipStream_t stream, const Product& a)
     return hipGetLastError();
 }
 
+// Decode steps (at most 32 rows, inner at most 2048) take the product with the
+// LayerNorm folded in.
+bool normed_fits(int rows, int inner)
+{
+    return row_tiles(rows) <= 2 && inner <= kNormedWidth && inner % 32 == 0;
+}
+
+template <int WT>
+hipError_t launch_normed_product(hipStream_t stream, const Product& a)
+{
+    const dim3 grid((a.out + 15) / 16);
+    if (row_tiles(a.rows) == 1)
+        hipLaunchKernelGGL((normed_product_kernel<WT, 1>), grid, dim3(kProductThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((normed_product_kernel<WT, 2>), grid, dim3(kProductThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
 template <int WT>
 hipError_t launch_norm(hipStream_t stream, const Norm& a, int rows, bool embed)
 {
@@ -727,6 +929,19 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
     at.state = b->state;
     const int self_span = io.fixed_grid ? s.max_positions : b->position + count;
 
+    // Decode steps fold each LayerNorm into the product that consumes it.
+    const bool normed = wsp::batch::normed_fits(rows, d);
+    p.h = b->h;
+    p.eps = eps;
+    auto product_after_norm = [&](const float* gamma, const float* beta) -> hipError_t {
+        if (!normed)
+            return launch_product<WT>(st, p);
+        Product q = p;
+        q.gamma = gamma;
+        q.beta = beta;
+        return wsp::batch::launch_normed_product<WT>(st, q);
+    };
+
     for (int l = 0; l < s.layers; ++l)
     {
         const wsp_layer_tensors& L = T->layers[l];
@@ -739,8 +954,10 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         n.gamma = L.self_norm_w;
         n.beta = L.self_norm_b;
         n.y = nullptr;
-        if ((e = launch_norm<WT>(st, n, rows, l == 0)) != hipSuccess)
+        n.xs = normed ? nullptr : b->xs;
+        if ((l == 0 || !normed) && (e = launch_norm<WT>(st, n, rows, l == 0)) != hipSuccess)
             return hip_fail(b, e, "self-attention norm");
+        n.xs = b->xs;
 
         p.x = b->xs;
         p.x_part = xs_part;
@@ -756,7 +973,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         p.state = b->state;
         p.step_tokens = count;
         p.width = d;
-        if ((e = launch_product<WT>(st, p)) != hipSuccess)
+        if ((e = product_after_norm(L.self_norm_w, L.self_norm_b)) != hipSuccess)
             return hip_fail(b, e, "q/k/v product");
 
         at.keys = self_k;
@@ -779,13 +996,13 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         // cross attention
         n.gamma = L.cross_norm_w;
         n.beta = L.cross_norm_b;
-        if ((e = launch_norm<WT>(st, n, rows, false)) != hipSuccess)
+        if (!normed && (e = launch_norm<WT>(st, n, rows, false)) != hipSuccess)
             return hip_fail(b, e, "cross-attention norm");
         p.w = L.cross_q_w;
         p.bias = L.cross_q_b;
         p.epilogue = kStore;
         p.y = b->q;
-        if ((e = launch_product<WT>(st, p)) != hipSuccess)
+        if ((e = product_after_norm(L.cross_norm_w, L.cross_norm_b)) != hipSuccess)
             return hip_fail(b, e, "cross query product");
 
         at.keys = cross_k;
@@ -806,7 +1023,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         // feed-forward
         n.gamma = L.final_norm_w;
         n.beta = L.final_norm_b;
-        if ((e = launch_norm<WT>(st, n, rows, false)) != hipSuccess)
+        if (!normed && (e = launch_norm<WT>(st, n, rows, false)) != hipSuccess)
             return hip_fail(b, e, "feed-forward norm");
         p.out = f;
         p.w = L.fc1_w;
@@ -814,7 +1031,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         p.epilogue = kGeluSplit;
         p.xs_out = b->xs_ff;
         p.xs_out_part = ff_part;
-        if ((e = launch_product<WT>(st, p)) != hipSuccess)
+        if ((e = product_after_norm(L.final_norm_w, L.final_norm_b)) != hipSuccess)
             return hip_fail(b, e, "fc1 product");
 
         p.x = b->xs_ff;
