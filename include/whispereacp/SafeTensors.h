@@ -104,4 +104,25 @@ private:
 // max_target_positions; crossPositionCount zero takes max_source_positions.
 DecoderShape decoderShapeFromConfig(const std::string& json, int crossPositionCount = 0);
 DecoderShape decoderShapeFromConfigFile(const std::string& path, int crossPositionCount = 0);
+
+// The greedy loop's inputs a config.json carries (Model/ModelConfig.cpp:85-101,
+// Whisper/Whisper.cpp:202-254): the tokens every step suppresses
+// (suppress_tokens), those only the first step also suppresses
+// (begin_suppress_tokens), and the start / end-of-text ids (-1 when absent).
+struct DecodingConfig
+{
+    std::vector<int> suppressedTokens;
+    std::vector<int> initiallySuppressedTokens;
+    int decoderStartToken = -1;
+    int endOfTextToken = -1;
+    int vocabularySize = 0;
+
+    // Whisper::buildSuppressionMasks: float masks over the vocabulary (1 =
+    // suppressed); the first step's adds begin_suppress_tokens. An id outside
+    // the vocabulary is a ModelError.
+    void suppressionMasks(std::vector<float>& firstStep, std::vector<float>& laterSteps) const;
+};
+
+DecodingConfig decodingConfigFromConfig(const std::string& json);
+DecodingConfig decodingConfigFromConfigFile(const std::string& path);
 } // namespace WSP

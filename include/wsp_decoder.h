@@ -126,6 +126,15 @@ const char* wsp_safetensors_metadata(const wsp_safetensors* file, const char* ke
 int wsp_shape_from_config(const char* config_path, int cross_positions, wsp_decoder_shape* out, char* error,
                           int error_capacity);
 
+/* Whisper::buildSuppressionMasks and the prompt's ids from a config.json
+ * (Whisper/Whisper.cpp:202-254): first_mask / later_mask receive
+ * vocabulary_size floats each (host memory; 1 = suppressed), the first step's
+ * adding begin_suppress_tokens; start_token / end_token receive
+ * decoder_start_token_id and eos_token_id (-1 when absent). Either pointer
+ * pair may be null. A token past the vocabulary is refused. */
+int wsp_decoding_from_config(const char* config_path, float* first_mask, float* later_mask, int capacity,
+                             int* start_token, int* end_token, char* error, int error_capacity);
+
 /* wsp_decoder_create / wsp_batch_decoder_create over the tensors of a
  * safetensors file (mapped while the weights upload). */
 int wsp_decoder_create_from_file(const char* path, const wsp_decoder_shape* shape, int packing, int device,

@@ -102,3 +102,51 @@ def test_a_file_missing_a_tensor_is_a_model_error_naming_it(tmp_path):
     save(f, tmp_path / "model.safetensors")
     with pytest.raises(ModelError, match="fc2.bias"):
         Decoder(shape, packing="ExactHalf", path=str(tmp_path / "model.safetensors"))
+
+
+def test_greedy_from_a_checkpoint_directory_follows_the_config(tmp_path, oracle):
+    # The product loop end to end from files: shape, suppression masks, start
+    # and end-of-text ids from config.json, weights from model.safetensors, the
+    # prompt [decoder_start_token_id, 2, 3, 4] — against the oracle's greedy
+    # loop under the same masks (first step: suppress_tokens and
+    # begin_suppress_tokens; later: suppress_tokens) and the same stop.
+    from helpers import oracle_tensors
+    from whispereacp_amd.decoder import Decoder, decoding_from_config, shape_from_config, to_device
+    shape = S.DecoderShape(256, 4, 2, 1024, 4099, 64, 120)
+    f = S.workload_decoder_file(shape, "F16", 47)
+    enc = S.normal_encoder_output(120, shape.width, 13)
+    save(f, tmp_path / "model.safetensors")
+    prompt = [4000, 2, 3, 4]
+
+    def oracle_run(first_ids, later_ids, end=None, limit=30):
+        session = oracle.session(shape, oracle_tensors(f, shape))
+        session.begin(enc)
+        _, logits = session.step(prompt)
+        first, later = np.zeros(shape.vocabulary_size), np.zeros(shape.vocabulary_size)
+        first[first_ids + later_ids] = 1
+        later[later_ids] = 1
+        out = [int(np.argmax(np.where(first != 0, -np.inf, logits[-1])))]
+        while len(out) < limit and out[-1] != end:
+            _, logits = session.step([out[-1]])
+            out.append(int(np.argmax(np.where(later != 0, -np.inf, logits[0]))))
+        return out
+
+    free = oracle_run([], [], limit=4)
+    suppress, begin_suppress = [free[2]], [free[0]]
+    masked = oracle_run(begin_suppress, suppress)
+    end = masked[5]                               # an id the masked run meets
+    expected = masked[:masked.index(end)]
+    config = {"model_type": "whisper", "d_model": 256, "decoder_attention_heads": 4, "decoder_layers": 2,
+              "decoder_ffn_dim": 1024, "vocab_size": 4099, "max_target_positions": 64, "max_source_positions": 120,
+              "suppress_tokens": suppress, "begin_suppress_tokens": begin_suppress, "decoder_start_token_id": 4000,
+              "eos_token_id": end}
+    (tmp_path / "config.json").write_text(json.dumps(config))
+
+    loaded = shape_from_config(str(tmp_path / "config.json"))
+    first, later, start, eot = decoding_from_config(str(tmp_path / "config.json"), loaded.vocabulary_size)
+    assert (start, eot) == (4000, end)
+    decoder = Decoder(loaded, packing="ExactHalf", path=str(tmp_path / "model.safetensors"))
+    tokens, _ = decoder.greedy(to_device(enc), [start, 2, 3, 4], 30, end_of_text=eot,
+                               first_mask=to_device(first), later_mask=to_device(later))
+    assert tokens == expected
+    assert tokens[0] != free[0] and free[2] not in tokens

@@ -229,3 +229,36 @@ def test_config_errors_are_model_errors(tmp_path, change):
         shape_from_config(str(path))
     with pytest.raises(ModelError):
         shape_from_config(os.path.join(str(tmp_path), "absent.json"))
+
+
+def test_suppression_masks_and_prompt_ids_from_config(tmp_path):
+    # Whisper::buildSuppressionMasks: later steps suppress suppress_tokens, the
+    # first step those and begin_suppress_tokens (Whisper/Whisper.cpp:227-254).
+    from whispereacp_amd.decoder import decoding_from_config
+    config = dict(SMALL_CONFIG, suppress_tokens=[1, 2, 50256], begin_suppress_tokens=[220, 50256],
+                  decoder_start_token_id=50258, eos_token_id=50257)
+    path = tmp_path / "config.json"
+    path.write_text(json.dumps(config))
+    first, later, start, end = decoding_from_config(str(path), 51865)
+    assert np.flatnonzero(later).tolist() == [1, 2, 50256]
+    assert np.flatnonzero(first).tolist() == [1, 2, 220, 50256]
+    assert set(np.unique(first)) <= {0.0, 1.0}
+    assert (start, end) == (50258, 50257)
+
+
+def test_config_without_decoding_fields_suppresses_nothing(tmp_path):
+    from whispereacp_amd.decoder import decoding_from_config
+    path = tmp_path / "config.json"
+    path.write_text(json.dumps(SMALL_CONFIG))
+    first, later, start, end = decoding_from_config(str(path), 51865)
+    assert not first.any() and not later.any() and (start, end) == (-1, -1)
+
+
+@pytest.mark.parametrize("change", [{"suppress_tokens": [51865]}, {"begin_suppress_tokens": [-1]},
+                                    {"suppress_tokens": "1"}, {"eos_token_id": 1.5}])
+def test_config_tokens_outside_the_vocabulary_are_refused(tmp_path, change):
+    from whispereacp_amd.decoder import ModelError, decoding_from_config
+    path = tmp_path / "config.json"
+    path.write_text(json.dumps(dict(SMALL_CONFIG, **change)))
+    with pytest.raises(ModelError):
+        decoding_from_config(str(path), 51865)

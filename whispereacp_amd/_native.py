@@ -132,6 +132,8 @@ SIGNATURES = {
                                        ctypes.POINTER(ctypes.c_longlong)]),
     "wsp_safetensors_read_floats": (c_int, [c_void_p, c_char_p, c_void_p, ctypes.c_longlong]),
     "wsp_safetensors_metadata": (c_char_p, [c_void_p, c_char_p]),
+    "wsp_decoding_from_config": (c_int, [c_char_p, c_void_p, c_void_p, c_int, ctypes.POINTER(c_int),
+                                         ctypes.POINTER(c_int), ctypes.c_char_p, c_int]),
     "wsp_shape_from_config": (c_int, [c_char_p, c_int, ctypes.POINTER(wsp_decoder_shape), ctypes.c_char_p, c_int]),
     "wsp_batch_decoder_hidden_states": (c_void_p, [c_void_p]),
 }

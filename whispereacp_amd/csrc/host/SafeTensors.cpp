@@ -668,13 +668,85 @@ DecoderShape decoderShapeFromConfig(const std::string& json, int crossPositionCo
     return s;
 }
 
-DecoderShape decoderShapeFromConfigFile(const std::string& path, int crossPositionCount)
+namespace
+{
+std::string readText(const std::string& path)
 {
     std::ifstream in(path, std::ios::binary);
     if (!in)
         throw ModelError("cannot open '" + path + "'");
     std::ostringstream text;
     text << in.rdbuf();
-    return decoderShapeFromConfig(text.str(), crossPositionCount);
+    return text.str();
+}
+
+int optionalToken(const Json& config, const char* key)
+{
+    const Json* v = config.member(key);
+    if (v == nullptr || v->kind == Json::Kind::Null)
+        return -1;
+    if (v->kind != Json::Kind::Number || !v->integral || v->integer < 0 || v->integer > std::numeric_limits<int>::max())
+        throw ModelError(std::string("config.json '") + key + "' is not a token id");
+    return (int) v->integer;
+}
+
+std::vector<int> tokenList(const Json& config, const char* key)
+{
+    std::vector<int> ids;
+    const Json* v = config.member(key);
+    if (v == nullptr || v->kind == Json::Kind::Null)
+        return ids;
+    if (v->kind != Json::Kind::Array)
+        throw ModelError(std::string("config.json '") + key + "' is not a list of token ids");
+    for (const Json& item: v->items)
+    {
+        if (item.kind != Json::Kind::Number || !item.integral || item.integer > std::numeric_limits<int>::max()
+            || item.integer < std::numeric_limits<int>::min())
+            throw ModelError(std::string("config.json '") + key + "' holds an entry that is not a token id");
+        ids.push_back((int) item.integer);
+    }
+    return ids;
+}
+} // namespace
+
+DecoderShape decoderShapeFromConfigFile(const std::string& path, int crossPositionCount)
+{
+    return decoderShapeFromConfig(readText(path), crossPositionCount);
+}
+
+DecodingConfig decodingConfigFromConfig(const std::string& json)
+{
+    const Json config = JsonReader(json.data(), json.data() + json.size(), "config.json").document();
+    if (config.kind != Json::Kind::Object)
+        throw ModelError("config.json is not a JSON object");
+    DecodingConfig c;
+    c.vocabularySize = positiveField(config, "vocab_size");
+    c.suppressedTokens = tokenList(config, "suppress_tokens");
+    c.initiallySuppressedTokens = tokenList(config, "begin_suppress_tokens");
+    c.decoderStartToken = optionalToken(config, "decoder_start_token_id");
+    c.endOfTextToken = optionalToken(config, "eos_token_id");
+    return c;
+}
+
+DecodingConfig decodingConfigFromConfigFile(const std::string& path)
+{
+    return decodingConfigFromConfig(readText(path));
+}
+
+void DecodingConfig::suppressionMasks(std::vector<float>& firstStep, std::vector<float>& laterSteps) const
+{
+    auto mark = [this](std::vector<float>& mask, const std::vector<int>& ids) {
+        for (int id: ids)
+        {
+            if (id < 0 || id >= vocabularySize)
+                throw ModelError("config.json suppresses token " + std::to_string(id)
+                                 + ", which is outside the vocabulary");
+            mask[(std::size_t) id] = 1.0f;
+        }
+    };
+    laterSteps.assign((std::size_t) vocabularySize, 0.0f);
+    mark(laterSteps, suppressedTokens);
+    firstStep = laterSteps;
+    mark(firstStep, initiallySuppressedTokens);
 }
 } // namespace WSP

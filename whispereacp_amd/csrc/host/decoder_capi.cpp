@@ -518,6 +518,42 @@ const char* wsp_safetensors_metadata(const wsp_safetensors* f, const char* key)
     return it == f->file->metadata().end() ? nullptr : it->second.c_str();
 }
 
+int wsp_decoding_from_config(const char* config_path, float* first_mask, float* later_mask, int capacity,
+                             int* start_token, int* end_token, char* error, int error_capacity)
+{
+    if (config_path == nullptr)
+        return WSP_ERR_ARGUMENT;
+    try
+    {
+        const WSP::DecodingConfig config = WSP::decodingConfigFromConfigFile(config_path);
+        if (first_mask != nullptr || later_mask != nullptr)
+        {
+            if (capacity < config.vocabularySize)
+                throw WSP::ModelError("the masks hold fewer floats than config.json's vocab_size");
+            std::vector<float> first, later;
+            config.suppressionMasks(first, later);
+            if (first_mask != nullptr)
+                std::memcpy(first_mask, first.data(), first.size() * sizeof(float));
+            if (later_mask != nullptr)
+                std::memcpy(later_mask, later.data(), later.size() * sizeof(float));
+        }
+        if (start_token != nullptr)
+            *start_token = config.decoderStartToken;
+        if (end_token != nullptr)
+            *end_token = config.endOfTextToken;
+        return WSP_OK;
+    }
+    catch (const std::exception& e)
+    {
+        if (error != nullptr && error_capacity > 0)
+        {
+            std::strncpy(error, e.what(), (std::size_t) error_capacity - 1);
+            error[error_capacity - 1] = 0;
+        }
+        return WSP_ERR_SHAPE;
+    }
+}
+
 int wsp_shape_from_config(const char* config_path, int cross_positions, wsp_decoder_shape* out, char* error,
                           int error_capacity)
 {

@@ -359,6 +359,21 @@ def shape_from_config(path: str, cross_positions: int = 0) -> DecoderShape:
                         out.max_positions, out.cross_positions)
 
 
+def decoding_from_config(path: str, vocabulary_size: int):
+    """Whisper::buildSuppressionMasks from a config.json: (first-step mask,
+    later-step mask, decoder_start_token_id, eos_token_id), masks as float32
+    numpy arrays (1 = suppressed), ids -1 when absent."""
+    lib = N.load()
+    first = np.zeros(vocabulary_size, dtype=np.float32)
+    later = np.zeros(vocabulary_size, dtype=np.float32)
+    start, end = ctypes.c_int(-1), ctypes.c_int(-1)
+    error = ctypes.create_string_buffer(512)
+    if lib.wsp_decoding_from_config(path.encode(), first.ctypes.data, later.ctypes.data, vocabulary_size,
+                                    ctypes.byref(start), ctypes.byref(end), error, 512) != N.WSP_OK:
+        raise ModelError(error.value.decode())
+    return first, later, start.value, end.value
+
+
 _hip = None
 
 
