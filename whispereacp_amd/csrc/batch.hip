@@ -741,8 +741,10 @@ hipError_t launch_norm(hipStream_t stream, const Norm& a, int rows, bool embed)
 
 // Key chunks for `units` (row, head) pairs over k_count keys: about `target`
 // blocks in all, no chunk shorter than one 128-key tile. Cross attention
-// (1500 keys a stream) aims at 2048 blocks to keep HBM busy; self attention
-// at 256, so a large batch covers the chip without the combine launch.
+// (1500 keys a stream) aims at one full round of resident blocks (blocks per
+// CU x CUs: 1536 on MI355X, which measured faster than 1024, 2048, 3072 or
+// 4096); self attention at 256, so a large batch covers the chip without the
+// combine launch.
 int attend_chunks(int units, int k_count, int target)
 {
     const int most = std::max(1, (k_count + kTileKeys - 1) / kTileKeys);
@@ -753,9 +755,9 @@ int attend_chunks(int units, int k_count, int target)
 // and a.chunk_len are planned here for that span (chunks past the visible keys
 // come out empty, which the combine skips).
 template <int WT>
-hipError_t launch_attend(hipStream_t stream, Attend a, int rows, int span)
+hipError_t launch_attend(hipStream_t stream, Attend a, int rows, int span, int cross_target)
 {
-    a.chunks = attend_chunks(rows * a.heads, span, a.causal ? 256 : 2048);
+    a.chunks = attend_chunks(rows * a.heads, span, a.causal ? 256 : cross_target);
     a.chunk_len = (span + a.chunks - 1) / a.chunks;
     a.chunks = (span + a.chunk_len - 1) / a.chunk_len;
     hipLaunchKernelGGL((attend_kernel<WT>), dim3(rows * a.heads * a.chunks), dim3(kAttendThreads), 0, stream, a);
@@ -779,6 +781,7 @@ struct wsp_batch
     hipStream_t stream = nullptr;
     int rows_cap = 0, rows_padded = 0;
     int position = 0, cross_rows = 0;
+    int cross_target = 1536; // cross-attention blocks per launch: one round of resident blocks
 
     float* self_keys = nullptr;   // [layers][streams][max_positions][width]
     float* self_values = nullptr;
@@ -981,7 +984,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         at.stream_stride = (size_t) s.max_positions * d;
         at.k_count = 0;
         at.causal = 1;
-        if ((e = launch_attend<WT>(st, at, rows, self_span)) != hipSuccess)
+        if ((e = launch_attend<WT>(st, at, rows, self_span, b->cross_target)) != hipSuccess)
             return hip_fail(b, e, "self attention");
 
         p.out = d;
@@ -1010,7 +1013,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         at.stream_stride = (size_t) s.cross_positions * d;
         at.k_count = b->cross_rows;
         at.causal = 0;
-        if ((e = launch_attend<WT>(st, at, rows, b->cross_rows)) != hipSuccess)
+        if ((e = launch_attend<WT>(st, at, rows, b->cross_rows, b->cross_target)) != hipSuccess)
             return hip_fail(b, e, "cross attention");
 
         p.w = L.cross_out_w;
@@ -1207,6 +1210,18 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
         e = hipMemsetAsync(b->state, 0, 4 * sizeof(int), b->stream);
     if (e == hipSuccess)
         e = hipStreamCreateWithFlags(&b->capture, hipStreamNonBlocking);
+    if (e == hipSuccess)
+    {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess
+            && hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu,
+                                                            wdtype == WSP_F16
+                                                                ? (const void*) wsp::batch::attend_kernel<wsp::kF16>
+                                                                : (const void*) wsp::batch::attend_kernel<wsp::kBF16>,
+                                                            wsp::batch::kAttendThreads, 0) == hipSuccess
+            && cus > 0 && per_cu > 0)
+            b->cross_target = cus * per_cu;
+    }
     // Padding rows of the split buffers are read by the products (their sums
     // are discarded); zero them once so they hold finite values.
     if (e == hipSuccess)
