@@ -20,6 +20,34 @@ enum WeightType : int
     kBF16 = 2
 };
 
+// Global-memory views of pointers the compiler cannot place itself (pointers
+// read from LDS or from memory). Accesses through them are global_load /
+// global_store, which count only in vmcnt; the same access through a generic
+// pointer is a flat access, which also counts in lgkmcnt, so every later LDS
+// wait would also wait for it.
+template <class T>
+using global_ptr = __attribute__((address_space(1))) T*;
+
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* global(const T* p)
+{
+    return (const __attribute__((address_space(1))) T*) p;
+}
+
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* global_mut(T* p)
+{
+    return (__attribute__((address_space(1))) T*) p;
+}
+
+// 16 bytes from global memory.
+__device__ __forceinline__ uint4 load_global16(const void* p)
+{
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = *global(static_cast<const u32x4*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ __forceinline__ float bf16_to_float(uint16_t bits)
 {
     return __uint_as_float((uint32_t) bits << 16);

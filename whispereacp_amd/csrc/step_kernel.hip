@@ -73,8 +73,12 @@ __device__ __forceinline__ uint64_t peek(const uint64_t* p)
 // ---------------------------------------------------------------------------
 // Cross-lane sums and maxima in a fixed order. A DPP "row" is 16 lanes: swap
 // neighbours, swap pairs, mirror within 8 and mirror within 16 leave the row
-// total in every lane; a swizzle adds the other row of a 32-lane half and two
-// readlanes join the halves of the wave. Every lane of the span must be active.
+// total in every lane; a permlane16 swap then adds the neighbouring row (lane
+// l and lane l ^ 16) and a permlane32 swap the other half of the wave (lane l
+// and lane l ^ 32). Both swaps are VALU operations of gfx950: no LDS round
+// trip and no scalar register. Every pair is added in an order-independent
+// way (a + b == b + a), so every lane of the span holds the same bits. Every
+// lane of the span must be active.
 // ---------------------------------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v)
@@ -86,17 +90,40 @@ constexpr int kSwapNeighbours = 0xB1; // quad_perm [1,0,3,2]
 constexpr int kSwapPairs = 0x4E;      // quad_perm [2,3,0,1]
 constexpr int kMirrorHalfRow = 0x141; // row_half_mirror
 constexpr int kMirrorRow = 0x140;     // row_mirror
-constexpr int kSwap16 = 0x401F;       // ds_swizzle bit mode: lane ^ 16 within 32 lanes
 
-__device__ __forceinline__ float swap16(float v)
+// Lane l's value and lane (l ^ 16)'s, in some order.
+__device__ __forceinline__ void rows_pair(float v, float& a, float& b)
 {
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), kSwap16));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
+// Lane l's value and lane (l ^ 32)'s, in some order.
+__device__ __forceinline__ void halves_pair(float v, float& a, float& b)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float add16(float v)
+{
+    float a, b;
+    rows_pair(v, a, b);
+    return a + b;
+}
+
+__device__ __forceinline__ float add32(float v)
+{
+    float a, b;
+    halves_pair(v, a, b);
+    return a + b;
 }
 
 __device__ __forceinline__ float halves_sum(float v)
 {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0))
-           + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    return add32(v);
 }
 
 __device__ __forceinline__ float sum16(float v)
@@ -110,8 +137,7 @@ __device__ __forceinline__ float sum16(float v)
 
 __device__ __forceinline__ float sum32(float v)
 {
-    v = sum16(v);
-    return v + swap16(v);
+    return add16(sum16(v));
 }
 
 __device__ __forceinline__ float sum64(float v)
@@ -125,16 +151,18 @@ __device__ __forceinline__ float max64(float v)
     v = fmaxf(v, dpp<kSwapPairs>(v));
     v = fmaxf(v, dpp<kMirrorHalfRow>(v));
     v = fmaxf(v, dpp<kMirrorRow>(v));
-    v = fmaxf(v, swap16(v));
-    return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
-                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
+    float a, b;
+    rows_pair(v, a, b);
+    v = fmaxf(a, b);
+    halves_pair(v, a, b);
+    return fmaxf(a, b);
 }
 
 struct Shared
 {
     wsp_layer_tensors table[kMaxLayers]; // the layer table, read once per launch
     alignas(16) float raw[kMaxWidth];    // the residual stream as gathered (un-normalised)
-    float x[kMaxFeedForward];            // the current phase's input vector
+    alignas(16) float x[kMaxFeedForward]; // the current phase's input vector
     float comb[kMaxCombine];             // attention partials being combined
     float red[kWaves][kMaxHeadWidth];    // per-wave value rows of an attention chunk
     float q[3 * kMaxHeadWidth];          // a head's query, then (self-attention) its new key and value
@@ -297,66 +325,68 @@ constexpr int kPollArgmax = (16 * 256 + kPollThreads - 1) / kPollThreads;
 // ---------------------------------------------------------------------------
 // LayerNorm of sh.raw into sh.x: mean, centred biased variance, then
 // (x - mean) * rsqrt(var + eps) * gamma + beta (Kernels/LayerNorm.h:44-89).
-// Every wave sums the whole row itself (same lanes, same order, so every wave
-// gets the same statistics); the only barrier is the one completing sh.x.
-// gamma/beta arrive as registers loaded a phase earlier.
+// Lane l of every wave holds the runs 4 (l + 64 k) .. + 3 of the row (n is a
+// multiple of 4), read from LDS in one batch, and every wave sums them in the
+// same order, so every wave gets the same statistics without a barrier. Wave
+// w then writes run w (kNormRuns runs cover the widest row), with gamma/beta
+// of that run held in registers since the previous phase. The only barrier is
+// the one completing sh.x.
 // ---------------------------------------------------------------------------
-constexpr int kNormPer = (kMaxWidth + kThreads - 1) / kThreads;
+constexpr int kNormRuns = (kMaxWidth + 4 * kWave - 1) / (4 * kWave);
+static_assert(kNormRuns <= kThreads / kWave, "one wave writes each run");
 
 struct NormParams
 {
-    float g[kNormPer];
-    float b[kNormPer];
+    float4v g;
+    float4v b;
 };
+
+// The run this thread's wave writes, clamped into the row (a wave past the
+// row loads the last run and writes nothing).
+__device__ __forceinline__ int norm_run(int n)
+{
+    const int i = 4 * ((int) (threadIdx.x & (kWave - 1)) + kWave * (int) (threadIdx.x / kWave));
+    return min(i, n - 4);
+}
 
 __device__ __forceinline__ void load_norm(NormParams& p, const float* gamma, const float* beta, int n)
 {
-#pragma unroll
-    for (int k = 0; k < kNormPer; ++k)
-    {
-        const int i = min((int) threadIdx.x + k * kThreads, n - 1);
-        p.g[k] = gamma[i];
-        p.b[k] = beta[i];
-    }
+    const int i = norm_run(n);
+    p.g = *global(reinterpret_cast<const float4v*>(gamma + i));
+    p.b = *global(reinterpret_cast<const float4v*>(beta + i));
 }
 
 __device__ __forceinline__ void layer_norm(const NormParams& p, int n, float eps, Shared& sh)
 {
-    // Lane l of every wave reads elements 4 (l + 64 k) .. + 3 (n is a multiple
-    // of 4) — once for the mean, again for the centred squares.
-    constexpr int kRuns = (kMaxWidth + 4 * kWave - 1) / (4 * kWave);
     const int lane = threadIdx.x & (kWave - 1);
+    float4v v[kNormRuns];
+#pragma unroll
+    for (int k = 0; k < kNormRuns; ++k)
+        v[k] = *reinterpret_cast<const float4v*>(&sh.raw[min(4 * (lane + kWave * k), n - 4)]);
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < kRuns; ++k)
-    {
-        const int i = 4 * (lane + kWave * k);
-        if (i < n)
-        {
-            const float4v v = *reinterpret_cast<const float4v*>(&sh.raw[i]);
-            s += v[0] + v[1] + v[2] + v[3];
-        }
-    }
+    for (int k = 0; k < kNormRuns; ++k)
+        if (4 * (lane + kWave * k) < n)
+            s += v[k][0] + v[k][1] + v[k][2] + v[k][3];
     const float mean = sum64(s) / (float) n;
     float q = 0.f;
 #pragma unroll
-    for (int k = 0; k < kRuns; ++k)
-    {
-        const int i = 4 * (lane + kWave * k);
-        if (i < n)
+    for (int k = 0; k < kNormRuns; ++k)
+        if (4 * (lane + kWave * k) < n)
         {
-            const float4v v = *reinterpret_cast<const float4v*>(&sh.raw[i]);
-            const float c0 = v[0] - mean, c1 = v[1] - mean, c2 = v[2] - mean, c3 = v[3] - mean;
+            const float c0 = v[k][0] - mean, c1 = v[k][1] - mean, c2 = v[k][2] - mean, c3 = v[k][3] - mean;
             q += c0 * c0 + c1 * c1 + c2 * c2 + c3 * c3;
         }
-    }
     const float scale = rsqrtf(sum64(q) / (float) n + eps);
-#pragma unroll
-    for (int k = 0; k < kNormPer; ++k)
+    const int i = 4 * (lane + kWave * (int) (threadIdx.x / kWave));
+    if (i < n)
     {
-        const int i = threadIdx.x + k * kThreads;
-        if (i < n)
-            sh.x[i] = (sh.raw[i] - mean) * scale * p.g[k] + p.b[k];
+        const float4v x = *reinterpret_cast<const float4v*>(&sh.raw[i]);
+        float4v y;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            y[c] = (x[c] - mean) * scale * p.g[c] + p.b[c];
+        *reinterpret_cast<float4v*>(&sh.x[i]) = y;
     }
     __syncthreads();
 }
@@ -447,7 +477,7 @@ __device__ __forceinline__ void load_run(RowLoad& r, const void* weight, int row
     for (int i = 0; i < kChunks; ++i)
     {
         const int c = first + lane + kRowLanes * i;
-        r.w[i] = *reinterpret_cast<const uint4*>(base + (size_t) (c < last ? c : first) * 16);
+        r.w[i] = load_global16(base + (size_t) (c < last ? c : first) * 16);
     }
 }
 
@@ -525,7 +555,7 @@ __device__ __forceinline__ void prefetch(Prefetch& p, const void* weight, const 
     phase_task(ps, group, stride, 0, row, first, last);
     load_run(p.r, weight, row, ps.row_bytes, first, last);
     const int finisher_row = min(group + stride * (int) threadIdx.x, ps.rows - 1);
-    p.bias = bias != nullptr ? bias[finisher_row] : 0.f;
+    p.bias = bias != nullptr ? global(bias)[finisher_row] : 0.f;
 }
 
 // Sums a pass's partials, then the finishing threads add the slices of their
@@ -574,7 +604,7 @@ __device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight,
         RowLoad r;
         load_run(r, weight, row, ps.row_bytes, first, last);
         finish_pass(run_dot<WT>(r, sh.x, first, last, lane), task, pass, ps, group, stride, sh, epi,
-                    [&](int rr) { return bias != nullptr ? bias[rr] : 0.f; });
+                    [&](int rr) { return bias != nullptr ? global(bias)[rr] : 0.f; });
     }
 }
 
@@ -603,8 +633,8 @@ __device__ __forceinline__ void load_keys(KeyRows<NP>& kr, const float* keys, co
     {
         const int key = ks + kKeySlots * p;
         const size_t at = (size_t) (first + (key < count ? key : 0)) * width + column + channel;
-        kr.k[p] = *reinterpret_cast<const float4v*>(keys + at);
-        kr.v[p] = *reinterpret_cast<const float4v*>(values + at);
+        kr.k[p] = *global(reinterpret_cast<const float4v*>(keys + at));
+        kr.v[p] = *global(reinterpret_cast<const float4v*>(values + at));
     }
 }
 
@@ -623,11 +653,15 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
 #pragma unroll
     for (int p = 0; p < NP; ++p)
     {
-        const float part =
-            live ? qv[0] * kr.k[p][0] + qv[1] * kr.k[p][1] + qv[2] * kr.k[p][2] + qv[3] * kr.k[p][3] : 0.f;
-        s[p] = scale * sum16(part);
-        if (ks + kKeySlots * p < count)
-            local_max = fmaxf(local_max, s[p]);
+        s[p] = -INFINITY;
+        if (kKeySlots * p < count) // uniform: passes past the keys are skipped
+        {
+            const float part =
+                live ? qv[0] * kr.k[p][0] + qv[1] * kr.k[p][1] + qv[2] * kr.k[p][2] + qv[3] * kr.k[p][3] : 0.f;
+            s[p] = scale * sum16(part);
+            if (ks + kKeySlots * p < count)
+                local_max = fmaxf(local_max, s[p]);
+        }
     }
     const float m = group_max(local_max, sh, 0);
     float local_sum = 0.f;
@@ -635,7 +669,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
 #pragma unroll
     for (int p = 0; p < NP; ++p)
     {
-        if (ks + kKeySlots * p < count)
+        if (kKeySlots * p < count && ks + kKeySlots * p < count)
         {
             const float e = expf(s[p] - m);
             if (kl == 0)
@@ -650,10 +684,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
     // then the two halves of the wave; lanes 0-15 then hold the wave's row.
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-    {
-        acc[i] += swap16(acc[i]);
-        acc[i] += __shfl_xor(acc[i], 32, kWave);
-    }
+        acc[i] = add32(add16(acc[i]));
     if ((threadIdx.x & (kWave - 1)) < kKeyLanes && live)
         *reinterpret_cast<float4v*>(&sh.red[threadIdx.x / kWave][4 * kl]) = acc;
     const float l = group_sum(local_sum, sh, 1); // its barrier also completes sh.red
@@ -791,7 +822,7 @@ __device__ __forceinline__ void load_logit_row(RowLoad& r, float& mask, const St
     for (int i = 0; i < kChunks; ++i)
     {
         const int c = lane + (i << s.lanes_log2);
-        r.w[i] = *reinterpret_cast<const uint4*>(base + (size_t) (c < last ? c : 0) * 16);
+        r.w[i] = load_global16(base + (size_t) (c < last ? c : 0) * 16);
     }
     mask = a.mask != nullptr ? a.mask[valid ? row : 0] : 0.f;
 }
@@ -912,9 +943,9 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             run_phase<WT>(pa, L.self_qkv_w, L.self_qkv_b, qkv_shape, group, stride, sh, [&](int r, int j, float v) {
                 put(qkv + (group << a.log2_qkv) + j, v, epoch);
                 if (r >= 2 * d)
-                    vrow[r - 2 * d] = v;
+                    global_mut(vrow)[r - 2 * d] = v;
                 else if (r >= d)
-                    krow[r - d] = v;
+                    global_mut(krow)[r - d] = v;
             });
         }
 
