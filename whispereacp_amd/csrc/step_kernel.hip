@@ -283,6 +283,12 @@ __device__ __forceinline__ bool gather(const uint64_t* src, int n, float* dst, u
                    status, sh);
 }
 
+// n <= kMaxCombine contiguous words, polled with as few slots per thread as
+// the count needs (a poll round costs every unrolled slot's test, so the usual
+// vector of a few hundred words takes the two-slot form).
+__device__ __forceinline__ bool gather_any(const uint64_t* src, int n, float* dst, uint32_t epoch, int* status,
+                                           Shared& sh);
+
 // Row-group outputs live in producer blocks: the workgroup that computes row
 // r (r % stride) stores it at slot (r % stride) * 2^log2_block + r / stride,
 // so each workgroup's rows share its own cache lines (no line has two
@@ -319,8 +325,17 @@ __device__ __forceinline__ bool gather_blocked(const uint64_t* base, int rows, i
 // Words per polling thread for the vectors a phase awaits.
 constexpr int kPollBlocked = 3;    // slots per thread per chunk of a width-long blocked vector (1344)
 constexpr int kPollBlockedFF = 9;  // ... of the feed-forward vector (4032)
+
 constexpr int kPollCombine = (kMaxCombine + kPollThreads - 1) / kPollThreads;
 constexpr int kPollArgmax = (16 * 256 + kPollThreads - 1) / kPollThreads;
+
+__device__ __forceinline__ bool gather_any(const uint64_t* src, int n, float* dst, uint32_t epoch, int* status,
+                                           Shared& sh)
+{
+    if (n <= 2 * kPollThreads)
+        return gather<2>(src, n, dst, epoch, status, sh);
+    return gather<kPollCombine>(src, n, dst, epoch, status, sh);
+}
 
 // ---------------------------------------------------------------------------
 // LayerNorm of sh.raw into sh.x: mean, centred biased variance, then
@@ -555,7 +570,14 @@ __device__ __forceinline__ void prefetch(Prefetch& p, const void* weight, const 
     phase_task(ps, group, stride, 0, row, first, last);
     load_run(p.r, weight, row, ps.row_bytes, first, last);
     const int finisher_row = min(group + stride * (int) threadIdx.x, ps.rows - 1);
-    p.bias = bias != nullptr ? global(bias)[finisher_row] : 0.f;
+    // The load is issued whether or not the phase has a bias (a phase without
+    // one reads a weight word and drops it): the compiler counts outstanding
+    // loads per program point, and a load skipped on some path makes every
+    // later wait for an older load count one load too few, so it would also
+    // wait for the newest one — the next phase's weights.
+    const float* source = bias != nullptr ? bias : static_cast<const float*>(weight);
+    const float b = global(source)[finisher_row];
+    p.bias = bias != nullptr ? b : 0.f;
 }
 
 // Sums a pass's partials, then the finishing threads add the slices of their
@@ -949,8 +971,16 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             });
         }
 
+        // This group's cross-attention keys, issued while the self-attention
+        // hand-overs are in flight (the workgroup has nothing else to do then)
+        // and awaited only when the cross query arrives. Every workgroup issues
+        // them (one without a task reads key 0), so the number of loads in
+        // flight is the same on every path.
+        load_keys<kCrossPasses>(cross, L.cross_keys, L.cross_values, task_count > 0 ? task_first : 0,
+                                max(task_count, 1), d, (task % H) * hd, hd);
+
         // ---- self-attention combine + out-proj + residual (weights in pb) ------
-        if (!gather<kPollCombine>(ex + a.off_self, a.self_splits * H * (hd + 2), sh.comb, epoch, a.status, sh))
+        if (!gather_any(ex + a.off_self, a.self_splits * H * (hd + 2), sh.comb, epoch, a.status, sh))
             return false;
         prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
         load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
@@ -967,9 +997,6 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
         if (!gather_blocked<kPollBlocked>(ex + a.off_h2, d, a.log2_d, stride, sh.raw, epoch, a.status, sh))
             return false;
         prefetch(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride);
-        if (task_count > 0) // awaited only when the query arrives
-            load_keys<kCrossPasses>(cross, L.cross_keys, L.cross_values, task_first, task_count, d, (task % H) * hd,
-                                    hd);
         layer_norm(norm, d, a.eps, sh);
         {
             uint64_t* out = ex + a.off_xq;
@@ -999,7 +1026,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
         }
 
         // ---- cross out-proj + residual (weights in pb) --------------------------------
-        if (!gather<kPollCombine>(ex + a.off_xattn, d, sh.x, epoch, a.status, sh))
+        if (!gather_any(ex + a.off_xattn, d, sh.x, epoch, a.status, sh))
             return false;
         prefetch(pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride);
         load_norm(norm, L.final_norm_w, L.final_norm_b, d);
@@ -1023,9 +1050,11 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
         // ---- fc2 + residual (weights in pb) ------------------------------------------------
         if (!gather_blocked<kPollBlockedFF>(ex + a.off_ff, f, a.log2_f, stride, sh.x, epoch, a.status, sh))
             return false;
-        if (l + 1 < a.layer_count)
         {
-            const wsp_layer_tensors& next = sh.table[l + 1];
+            // The next layer's q/k/v slice and LN1 parameters (the last layer
+            // loads its own again, unused, so these loads are issued on every
+            // path).
+            const wsp_layer_tensors& next = sh.table[min(l + 1, a.layer_count - 1)];
             prefetch(pa, next.self_qkv_w, next.self_qkv_b, qkv_shape, group, stride);
             load_norm(norm, next.self_norm_w, next.self_norm_b, d);
         }
@@ -1090,7 +1119,7 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
         if (index < H)
         {
             const int parts = a.cross_splits;
-            if (!gather<kPollCombine>(ex + a.off_xpart + (size_t) head * parts * (hd + 2), parts * (hd + 2), sh.comb,
+            if (!gather_any(ex + a.off_xpart + (size_t) head * parts * (hd + 2), parts * (hd + 2), sh.comb,
                                       epoch, a.status, sh))
                 return false;
             combine_parts(sh.comb, parts, hd, ex + a.off_xattn + head * hd, epoch, sh);
