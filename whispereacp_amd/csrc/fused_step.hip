@@ -95,7 +95,23 @@ void plan_persistent(Context* ctx, FusedState* st)
     const int G = prop.multiProcessorCount;
     const int self_split_max = ceil_div(s.max_positions, step::kSelfKeys);
     const int head_groups = H * self_split_max;
-    const int row_groups = G - head_groups;
+    // Row groups: every CU not holding a head group, or a few less when that
+    // lets a width-long vector's producer blocks fit two words per polling
+    // thread (each poll round tests every slot a thread holds, so rounds of
+    // two slots are the shortest). Spare workgroups run as idle head groups
+    // and join the tied logits.
+    int row_groups = G - head_groups;
+    for (int rg = row_groups; rg >= row_groups - row_groups / 8 && rg > 0; --rg)
+    {
+        int block = 1;
+        while (block < ceil_div(d, rg))
+            block <<= 1;
+        if (rg * block <= step::kPollBlocked * step::kPollThreads)
+        {
+            row_groups = rg;
+            break;
+        }
+    }
     if (row_groups < H)
         return refuse("too few CUs for the head groups");
     if (self_split_max * H * (hd + 2) > step::kMaxCombine || 2 * G > step::kMaxCombine || G > 256)

@@ -19,6 +19,9 @@ constexpr int kMaxCombine = 4096;      // attention partial floats one workgroup
 constexpr int kSelfKeys = 256;         // self-attention keys one head group holds
 constexpr int kCrossKeys = 128;        // cross-attention keys one row group holds
 constexpr int kMaxLayers = 32;         // layer table entries held in LDS
+constexpr int kPollThreads = kThreads - 64; // threads that poll exchange words (waves 1-7)
+constexpr int kPollBlocked = 2;        // slots per polling thread for a width-long vector, per chunk
+constexpr int kPollBlockedFF = 8;      // ... for the feed-forward vector
 
 // Exchange words per layer, in this order (offsets in StepArgs):
 //   qkv [row_groups << log2_qkv] | self partials [self_split_max][heads][hd + 2]

@@ -211,7 +211,7 @@ __device__ __forceinline__ float group_max(float v, Shared& sh, int slot)
 // Every poll round issues all of a thread's outstanding loads at once. Returns
 // false, uniformly over the workgroup, when the watchdog tripped here or
 // anywhere else.
-constexpr int kPollThreads = kThreads - kWave;
+static_assert(kPollThreads == kThreads - kWave, "wave 0 does not poll");
 
 template <int P, class Map>
 __device__ __forceinline__ bool poll(const uint64_t* base, int n, Map map, float* dst, uint32_t epoch, int* status,
@@ -322,9 +322,9 @@ __device__ __forceinline__ bool gather_blocked(const uint64_t* base, int rows, i
     return true;
 }
 
-// Words per polling thread for the vectors a phase awaits.
-constexpr int kPollBlocked = 3;    // slots per thread per chunk of a width-long blocked vector (1344)
-constexpr int kPollBlockedFF = 9;  // ... of the feed-forward vector (4032)
+// Words per polling thread for the vectors a phase awaits: kPollBlocked and
+// kPollBlockedFF (step_kernel.h) per chunk of a blocked vector; a larger
+// vector is polled chunk after chunk.
 
 constexpr int kPollCombine = (kMaxCombine + kPollThreads - 1) / kPollThreads;
 constexpr int kPollArgmax = (16 * 256 + kPollThreads - 1) / kPollThreads;
@@ -334,6 +334,8 @@ __device__ __forceinline__ bool gather_any(const uint64_t* src, int n, float* ds
 {
     if (n <= 2 * kPollThreads)
         return gather<2>(src, n, dst, epoch, status, sh);
+    if (n <= 3 * kPollThreads)
+        return gather<3>(src, n, dst, epoch, status, sh);
     return gather<kPollCombine>(src, n, dst, epoch, status, sh);
 }
 
