@@ -662,10 +662,13 @@ __device__ __forceinline__ void load_keys(KeyRows<NP>& kr, const float* keys, co
     }
 }
 
-// Writes (max, sum, row[head_width]) of `count` keys into out (exchange words).
+// Writes (max, sum, row[head_width]) of `count` keys into out (exchange
+// words). With `normalized` the row is written already divided by the sum —
+// the combine of a single partial, so a consumer of the only partial of a
+// head can take the row as it is.
 template <int NP>
 __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int head_width, float scale, uint64_t* out,
-                                       uint32_t epoch, Shared& sh)
+                                       uint32_t epoch, Shared& sh, bool normalized = false)
 {
     const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
     const bool live = 4 * kl < head_width;
@@ -718,7 +721,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
             row += sh.red[w][threadIdx.x];
-        put(out + 2 + threadIdx.x, row, epoch);
+        put(out + 2 + threadIdx.x, normalized ? row / l : row, epoch);
     }
     if (threadIdx.x == 0)
     {
@@ -982,13 +985,34 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
                                 max(task_count, 1), d, (task % H) * hd, hd);
 
         // ---- self-attention combine + out-proj + residual (weights in pb) ------
-        if (!gather_any(ex + a.off_self, a.self_splits * H * (hd + 2), sh.comb, epoch, a.status, sh))
-            return false;
-        prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
-        load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
-        for (int c = threadIdx.x; c < d; c += kThreads)
-            sh.x[c] = combine(sh.comb + (c / hd) * (hd + 2), a.self_splits, H * (hd + 2), c % hd);
-        __syncthreads();
+        if (a.self_splits == 1 && (hd & (hd - 1)) == 0)
+        {
+            // One partial per head, written normalized: its rows are the
+            // attention output, gathered straight into sh.x (two poll slots
+            // per thread cover 896 words, three the widest row).
+            const int shift = 31 - __builtin_clz(hd);
+            auto map = [&](int i, int& offset, int& index) {
+                offset = (i >> shift) * (hd + 2) + 2 + (i & (hd - 1));
+                index = i;
+                return true;
+            };
+            static_assert(3 * kPollThreads >= kMaxWidth, "three slots cover the widest row");
+            if (!(d <= 2 * kPollThreads ? poll<2>(ex + a.off_self, d, map, sh.x, epoch, a.status, sh)
+                                        : poll<3>(ex + a.off_self, d, map, sh.x, epoch, a.status, sh)))
+                return false;
+            prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
+            load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
+        }
+        else
+        {
+            if (!gather_any(ex + a.off_self, a.self_splits * H * (hd + 2), sh.comb, epoch, a.status, sh))
+                return false;
+            prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
+            load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
+            for (int c = threadIdx.x; c < d; c += kThreads)
+                sh.x[c] = combine(sh.comb + (c / hd) * (hd + 2), a.self_splits, H * (hd + 2), c % hd);
+            __syncthreads();
+        }
         {
             uint64_t* out = ex + a.off_h2;
             run_phase<WT>(pb, L.self_out_w, L.self_out_b, square_shape, group, stride, sh,
@@ -1114,7 +1138,7 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
                     }
             }
             attend<kSelfPasses>(self, count, hd, a.scale, ex + a.off_self + (size_t) (split * H + head) * (hd + 2),
-                                epoch, sh);
+                                epoch, sh, a.self_splits == 1);
         }
         // Cross-attention combine of one head; the next layer's keys are
         // loaded after it, so they never hold up its wait.
