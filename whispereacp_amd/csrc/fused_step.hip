@@ -20,6 +20,23 @@ namespace wsp
 {
 namespace
 {
+// Where a WSP_STEP_TIMELINE build writes each launch's timestamps (set with
+// wsp_step_timeline; null otherwise).
+uint64_t* step_timeline = nullptr;
+} // namespace
+} // namespace wsp
+
+#ifdef WSP_STEP_TIMELINE
+extern "C" void wsp_step_timeline(uint64_t* buffer)
+{
+    wsp::step_timeline = buffer;
+}
+#endif
+
+namespace wsp
+{
+namespace
+{
 struct FusedState
 {
     // Per-op sequence scratch.
@@ -318,6 +335,7 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     a.log2_qkv = st->log2_qkv;
     a.log2_d = st->log2_d;
     a.log2_f = st->log2_f;
+    a.timeline = step_timeline;
 
     // A plain launch: the grid is one workgroup per CU, a CU holds only one of
     // these workgroups (registers), and the stream runs kernels one after

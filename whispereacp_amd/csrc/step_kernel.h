@@ -59,6 +59,7 @@ struct StepArgs
     int off_qkv, off_self, off_h2, off_xq, off_xpart, off_xattn, off_h3, off_ff, off_h4;
     int layer_words, off_argmax;
     int log2_qkv, log2_d, log2_f; // producer block sizes of the row-group vectors
+    uint64_t* timeline; // per-workgroup timestamps of a WSP_STEP_TIMELINE build (else unused)
 };
 
 // Longest projection row, in 16-byte chunks: 16 slices of 3 chunks per lane.

@@ -56,6 +56,26 @@ constexpr uint32_t kUnchosen = 0xFFFFFFFFu;
 static_assert(kSelfKeys % kKeySlots == 0 && kCrossKeys % kKeySlots == 0, "key capacities");
 static_assert(kKeySlots / kWaves == 4, "attend() folds four key slots per wave");
 
+// Optional timeline: built with WSP_STEP_TIMELINE, thread 0 of every
+// workgroup records the real-time clock (100 MHz) at the points marked
+// STEP_STAMP(event, layer) into LDS, and the kernel writes them to
+// StepArgs::timeline ([workgroup][kTimelineEvents][kTimelineLayers]) at its
+// end. Without it the marks compile to nothing.
+constexpr int kTimelineEvents = 24, kTimelineLayers = 33;
+#ifdef WSP_STEP_TIMELINE
+#define STEP_STAMP(e, l)                                      \
+    do                                                        \
+    {                                                         \
+        if (threadIdx.x == 0)                                 \
+            sh.timeline[(e)][(l)] = wall_clock64();           \
+    } while (0)
+#else
+#define STEP_STAMP(e, l) \
+    do                   \
+    {                    \
+    } while (0)
+#endif
+
 // ---------------------------------------------------------------------------
 // Exchange words
 // ---------------------------------------------------------------------------
@@ -171,6 +191,9 @@ struct Shared
     float best_v[kRowGroups];
     uint32_t best_i[kRowGroups];
     int abort;
+#ifdef WSP_STEP_TIMELINE
+    uint64_t timeline[kTimelineEvents][kTimelineLayers];
+#endif
 };
 
 // Workgroup-wide sum/max through one barrier; consecutive calls must use
@@ -327,7 +350,7 @@ __device__ __forceinline__ bool gather_blocked(const uint64_t* base, int rows, i
 // vector is polled chunk after chunk.
 
 constexpr int kPollCombine = (kMaxCombine + kPollThreads - 1) / kPollThreads;
-constexpr int kPollArgmax = (16 * 256 + kPollThreads - 1) / kPollThreads;
+constexpr int kPollArgmax = (2 * 256 + kPollThreads - 1) / kPollThreads; // the two used words of each candidate line
 
 __device__ __forceinline__ bool gather_any(const uint64_t* src, int n, float* dst, uint32_t epoch, int* status,
                                            Shared& sh)
@@ -851,7 +874,10 @@ __device__ __forceinline__ void load_logit_row(RowLoad& r, float& mask, const St
         const int c = lane + (i << s.lanes_log2);
         r.w[i] = load_global16(base + (size_t) (c < last ? c : 0) * 16);
     }
-    mask = a.mask != nullptr ? a.mask[valid ? row : 0] : 0.f;
+    // Issued with or without a mask (then a weight word, dropped), so every
+    // path has the same number of loads in flight.
+    const float m = *global(a.mask != nullptr ? a.mask + (valid ? row : 0) : static_cast<const float*>(a.logits_weight));
+    mask = a.mask != nullptr ? m : 0.f;
 }
 
 __device__ __forceinline__ void issue_ring(Ring& ring, const StepArgs& a, const LogitShape& s)
@@ -950,6 +976,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
                             : __builtin_nanf("");
         __syncthreads();
     }
+    STEP_STAMP(0, 0);
 
     for (int l = 0; l < a.layer_count; ++l)
     {
@@ -961,6 +988,8 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             && !gather_blocked<kPollBlocked>(a.exchange + (size_t) (l - 1) * a.layer_words + a.off_h4, d, a.log2_d,
                                              stride, sh.raw, epoch, a.status, sh))
             return false;
+        if (l > 0)
+            STEP_STAMP(0, l);
         prefetch(pb, L.self_out_w, L.self_out_b, square_shape, group, stride);
         layer_norm(norm, d, a.eps, sh);
         {
@@ -975,6 +1004,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
                     global_mut(krow)[r - d] = v;
             });
         }
+        STEP_STAMP(1, l);
 
         // This group's cross-attention keys, issued while the self-attention
         // hand-overs are in flight (the workgroup has nothing else to do then)
@@ -1000,6 +1030,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             if (!(d <= 2 * kPollThreads ? poll<2>(ex + a.off_self, d, map, sh.x, epoch, a.status, sh)
                                         : poll<3>(ex + a.off_self, d, map, sh.x, epoch, a.status, sh)))
                 return false;
+            STEP_STAMP(2, l);
             prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
             load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
         }
@@ -1007,6 +1038,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
         {
             if (!gather_any(ex + a.off_self, a.self_splits * H * (hd + 2), sh.comb, epoch, a.status, sh))
                 return false;
+            STEP_STAMP(2, l);
             prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
             load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
             for (int c = threadIdx.x; c < d; c += kThreads)
@@ -1018,10 +1050,12 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             run_phase<WT>(pb, L.self_out_w, L.self_out_b, square_shape, group, stride, sh,
                           [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); });
         }
+        STEP_STAMP(3, l);
 
         // ---- LN2 + cross q (weights in pa) ----------------------------------------
         if (!gather_blocked<kPollBlocked>(ex + a.off_h2, d, a.log2_d, stride, sh.raw, epoch, a.status, sh))
             return false;
+        STEP_STAMP(4, l);
         prefetch(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride);
         layer_norm(norm, d, a.eps, sh);
         {
@@ -1029,6 +1063,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             run_phase<WT>(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride, sh,
                           [&](int, int j, float v) { put(out + (group << a.log2_d) + j, v, epoch); });
         }
+        STEP_STAMP(5, l);
 
         // ---- cross-attention partials over this group's key chunk(s) ---------------
         for (int t = task; t < tasks; t += stride)
@@ -1047,13 +1082,17 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
                     },
                     sh.q, epoch, a.status, sh))
                 return false;
+            if (t == task)
+                STEP_STAMP(6, l);
             attend<kCrossPasses>(cross, count, hd, a.scale,
                                  ex + a.off_xpart + (size_t) (h * a.cross_splits + s) * (hd + 2), epoch, sh);
         }
+        STEP_STAMP(7, l);
 
         // ---- cross out-proj + residual (weights in pb) --------------------------------
         if (!gather_any(ex + a.off_xattn, d, sh.x, epoch, a.status, sh))
             return false;
+        STEP_STAMP(8, l);
         prefetch(pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride);
         load_norm(norm, L.final_norm_w, L.final_norm_b, d);
         {
@@ -1061,10 +1100,12 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             run_phase<WT>(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride, sh,
                           [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); });
         }
+        STEP_STAMP(9, l);
 
         // ---- LN3 + fc1 + GELU (weights in pa) ------------------------------------------
         if (!gather_blocked<kPollBlocked>(ex + a.off_h3, d, a.log2_d, stride, sh.raw, epoch, a.status, sh))
             return false;
+        STEP_STAMP(10, l);
         prefetch(pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride);
         layer_norm(norm, d, a.eps, sh);
         {
@@ -1072,10 +1113,12 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             run_phase<WT>(pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride, sh,
                           [&](int, int j, float v) { put(out + (group << a.log2_f) + j, exact_gelu(v), epoch); });
         }
+        STEP_STAMP(11, l);
 
         // ---- fc2 + residual (weights in pb) ------------------------------------------------
         if (!gather_blocked<kPollBlockedFF>(ex + a.off_ff, f, a.log2_f, stride, sh.x, epoch, a.status, sh))
             return false;
+        STEP_STAMP(12, l);
         {
             // The next layer's q/k/v slice and LN1 parameters (the last layer
             // loads its own again, unused, so these loads are issued on every
@@ -1089,6 +1132,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             run_phase<WT>(pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride, sh,
                           [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); });
         }
+        STEP_STAMP(13, l);
     }
     return true;
 }
@@ -1125,6 +1169,7 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
                     },
                     sh.q, epoch, a.status, sh))
                 return false;
+            STEP_STAMP(14, l);
             if (count > cached)
             {
                 // The new key sits at local index `cached` (= position - first).
@@ -1139,6 +1184,7 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
             }
             attend<kSelfPasses>(self, count, hd, a.scale, ex + a.off_self + (size_t) (split * H + head) * (hd + 2),
                                 epoch, sh, a.self_splits == 1);
+            STEP_STAMP(15, l);
         }
         // Cross-attention combine of one head; the next layer's keys are
         // loaded after it, so they never hold up its wait.
@@ -1148,7 +1194,9 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
             if (!gather_any(ex + a.off_xpart + (size_t) head * parts * (hd + 2), parts * (hd + 2), sh.comb,
                                       epoch, a.status, sh))
                 return false;
+            STEP_STAMP(16, l);
             combine_parts(sh.comb, parts, hd, ex + a.off_xattn + head * hd, epoch, sh);
+            STEP_STAMP(17, l);
         }
         if (!last_layer && attends && cached > 0)
             load_keys<kSelfPasses>(self, sh.table[l + 1].self_keys, sh.table[l + 1].self_values, first, cached, d,
@@ -1168,18 +1216,22 @@ __device__ __forceinline__ bool final_phase(const StepArgs& a, Shared& sh, Ring&
     if (!gather_blocked<kPollBlocked>(a.exchange + (size_t) (a.layer_count - 1) * a.layer_words + a.off_h4, d, a.log2_d,
                                       a.row_groups, sh.raw, a.epoch, a.status, sh))
         return false;
+    STEP_STAMP(18, 0);
+    // The first logits rows are issued once the last layer's output is in:
+    // issued before, they would share the memory pipeline with its polls.
+    issue_ring(ring, a, logit_shape(a));
     layer_norm(norm, d, a.eps, sh);
     if (blockIdx.x == 0)
         for (int c = threadIdx.x; c < d; c += kThreads)
             a.hidden[c] = sh.x[c];
     logits_loop<LWT>(ring, a, logit_shape(a), sh, best_v, best_i);
+    STEP_STAMP(19, 0);
     return true;
 }
 
 template <int WT>
-__global__ void __launch_bounds__(kThreads) step_kernel(StepArgs a)
+__device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
 {
-    __shared__ Shared sh;
     if (threadIdx.x == 0)
         sh.abort = 0;
     {
@@ -1191,15 +1243,15 @@ __global__ void __launch_bounds__(kThreads) step_kernel(StepArgs a)
             dst[i] = src[i];
     }
     __syncthreads();
+    STEP_STAMP(21, 0);
 
     const bool ok = (int) blockIdx.x < a.row_groups ? row_group_layers<WT>(a, sh) : head_group_layers(a, sh);
     if (!ok)
         return;
-    // The first logits rows and the final norm are in flight before the last
-    // layer's output is awaited.
+    // The final norm's parameters are in flight before the last layer's output
+    // is awaited.
     Ring ring;
     NormParams norm;
-    issue_ring(ring, a, logit_shape(a));
     load_norm(norm, a.final_norm_w, a.final_norm_b, a.width);
 
     // ---- final LN + tied logits with a per-workgroup top-1 -----------------------
@@ -1243,11 +1295,11 @@ __global__ void __launch_bounds__(kThreads) step_kernel(StepArgs a)
     if (blockIdx.x != 0 || a.argmax_out == nullptr)
         return;
     if (!poll<kPollArgmax>(
-            a.exchange + a.off_argmax, 16 * G,
+            a.exchange + a.off_argmax, 2 * G,
             [](int i, int& offset, int& index) {
-                offset = i;
-                index = 2 * (i >> 4) + (i & 15);
-                return (i & 15) < 2;
+                offset = 16 * (i >> 1) + (i & 1);
+                index = i;
+                return true;
             },
             sh.comb, epoch, a.status, sh))
         return;
@@ -1278,7 +1330,26 @@ __global__ void __launch_bounds__(kThreads) step_kernel(StepArgs a)
         }
         if (threadIdx.x == 0)
             a.argmax_out[0] = bi == kUnchosen ? 0u : bi;
+        STEP_STAMP(20, 0);
     }
+}
+
+template <int WT>
+__global__ void __launch_bounds__(kThreads) step_kernel(StepArgs a)
+{
+    __shared__ Shared sh;
+#ifdef WSP_STEP_TIMELINE
+    for (int i = threadIdx.x; i < kTimelineEvents * kTimelineLayers; i += kThreads)
+        (&sh.timeline[0][0])[i] = 0;
+    __syncthreads();
+#endif
+    step_body<WT>(a, sh);
+#ifdef WSP_STEP_TIMELINE
+    __syncthreads();
+    if (a.timeline != nullptr)
+        for (int i = threadIdx.x; i < kTimelineEvents * kTimelineLayers; i += kThreads)
+            a.timeline[(size_t) blockIdx.x * kTimelineEvents * kTimelineLayers + i] = (&sh.timeline[0][0])[i];
+#endif
 }
 } // namespace
 
