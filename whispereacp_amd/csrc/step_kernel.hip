@@ -399,34 +399,42 @@ __device__ __forceinline__ void load_norm(NormParams& p, const float* gamma, con
 __device__ __forceinline__ void layer_norm(const NormParams& p, int n, float eps, Shared& sh)
 {
     const int lane = threadIdx.x & (kWave - 1);
+    const int own = 4 * (lane + kWave * (int) (threadIdx.x / kWave)); // the run this wave writes
+    // Every LDS read is issued before the first is used: the row's runs and
+    // this thread's own run.
     float4v v[kNormRuns];
 #pragma unroll
     for (int k = 0; k < kNormRuns; ++k)
         v[k] = *reinterpret_cast<const float4v*>(&sh.raw[min(4 * (lane + kWave * k), n - 4)]);
+    const float4v x = *reinterpret_cast<const float4v*>(&sh.raw[min(own, n - 4)]);
+    // Pairwise sums (a fixed order, shallow dependency chains).
+    float t[kNormRuns];
+#pragma unroll
+    for (int k = 0; k < kNormRuns; ++k)
+        t[k] = 4 * (lane + kWave * k) < n ? (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]) : 0.f;
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < kNormRuns; ++k)
-        if (4 * (lane + kWave * k) < n)
-            s += v[k][0] + v[k][1] + v[k][2] + v[k][3];
+    for (int k = 0; k < kNormRuns; k += 2)
+        s += k + 1 < kNormRuns ? t[k] + t[k + 1] : t[k];
     const float mean = sum64(s) / (float) n;
-    float q = 0.f;
 #pragma unroll
     for (int k = 0; k < kNormRuns; ++k)
-        if (4 * (lane + kWave * k) < n)
-        {
-            const float c0 = v[k][0] - mean, c1 = v[k][1] - mean, c2 = v[k][2] - mean, c3 = v[k][3] - mean;
-            q += c0 * c0 + c1 * c1 + c2 * c2 + c3 * c3;
-        }
-    const float scale = rsqrtf(sum64(q) / (float) n + eps);
-    const int i = 4 * (lane + kWave * (int) (threadIdx.x / kWave));
-    if (i < n)
     {
-        const float4v x = *reinterpret_cast<const float4v*>(&sh.raw[i]);
+        const float c0 = v[k][0] - mean, c1 = v[k][1] - mean, c2 = v[k][2] - mean, c3 = v[k][3] - mean;
+        t[k] = 4 * (lane + kWave * k) < n ? (c0 * c0 + c1 * c1) + (c2 * c2 + c3 * c3) : 0.f;
+    }
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < kNormRuns; k += 2)
+        q += k + 1 < kNormRuns ? t[k] + t[k + 1] : t[k];
+    const float scale = rsqrtf(sum64(q) / (float) n + eps);
+    if (own < n)
+    {
         float4v y;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
             y[c] = (x[c] - mean) * scale * p.g[c] + p.b[c];
-        *reinterpret_cast<float4v*>(&sh.x[i]) = y;
+        *reinterpret_cast<float4v*>(&sh.x[own]) = y;
     }
     __syncthreads();
 }
