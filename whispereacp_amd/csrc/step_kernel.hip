@@ -187,7 +187,7 @@ struct Shared
     float red[kWaves][kMaxHeadWidth];    // per-wave value rows of an attention chunk
     float q[3 * kMaxHeadWidth];          // a head's query, then (self-attention) its new key and value
     float scratch[2][kWaves];            // workgroup reductions, two alternating slots
-    float part[kRowGroups];              // per-row-group partial sums of a projection pass
+    alignas(16) float part[kRowGroups];  // per-row-group partial sums of a projection pass
     float best_v[kRowGroups];
     uint32_t best_i[kRowGroups];
     int abort;
@@ -613,9 +613,42 @@ __device__ __forceinline__ void prefetch(Prefetch& p, const void* weight, const 
     p.bias = bias != nullptr ? b : 0.f;
 }
 
+// The slices of finisher t's row (slots [t << log2, (t + 1) << log2) of
+// sh.part), read in one or a few vector reads and added pairwise.
+__device__ __forceinline__ float slice_total(const Shared& sh, int t, int log2)
+{
+    const float4v* run = reinterpret_cast<const float4v*>(sh.part);
+    switch (log2)
+    {
+        case 0: return sh.part[t];
+        case 1:
+        {
+            const float2 v = reinterpret_cast<const float2*>(sh.part)[t];
+            return v.x + v.y;
+        }
+        case 2:
+        {
+            const float4v v = run[t];
+            return (v[0] + v[1]) + (v[2] + v[3]);
+        }
+        case 3:
+        {
+            const float4v u = run[2 * t], v = run[2 * t + 1];
+            return ((u[0] + u[1]) + (u[2] + u[3])) + ((v[0] + v[1]) + (v[2] + v[3]));
+        }
+        default:
+        {
+            const float4v u = run[0], v = run[1], w = run[2], x = run[3];
+            return (((u[0] + u[1]) + (u[2] + u[3])) + ((v[0] + v[1]) + (v[2] + v[3])))
+                   + (((w[0] + w[1]) + (w[2] + w[3])) + ((x[0] + x[1]) + (x[2] + x[3])));
+        }
+    }
+}
+static_assert(kRowGroups == 16, "slice_total covers up to 16 slices");
+
 // Sums a pass's partials, then the finishing threads add the slices of their
-// row in order, the bias, and hand the value to epi; two barriers bracket the
-// shared partial slots.
+// row, the bias, and hand the value to epi; two barriers bracket the shared
+// partial slots.
 template <class Epilogue, class Bias>
 __device__ __forceinline__ void finish_pass(float acc, bool has_task, int pass, const PhaseShape& ps, int group,
                                             int stride, Shared& sh, Epilogue& epi, Bias bias_of)
@@ -627,24 +660,26 @@ __device__ __forceinline__ void finish_pass(float acc, bool has_task, int pass, 
     const int local = pass * ps.rows_per_pass + (int) threadIdx.x;
     if ((int) threadIdx.x < ps.rows_per_pass && local < ps.local_rows)
     {
-        const int slices = 1 << ps.slice_log2;
-        float v = 0.f;
-        for (int s = 0; s < slices; ++s)
-            v += sh.part[threadIdx.x * slices + s];
+        const float v = slice_total(sh, (int) threadIdx.x, ps.slice_log2);
         const int r = group + stride * local;
         epi(r, local, v + bias_of(r));
     }
+    // Also keeps the other waves from issuing loads (polls, prefetches)
+    // ahead of the finishers' stores.
     __syncthreads();
 }
 
 // Runs every task of the phase against sh.x. epi(row, value) receives the dot
 // product plus bias, on thread (local row) % rows_per_pass (all in wave 0).
 // Pass 0 is straight-line code whose weights and bias were loaded a phase
-// earlier, so it never waits on the next phase's loads issued just before it;
-// further passes, which only long rows or narrow grids need, load on the spot.
-template <int WT, class Epilogue>
+// earlier; further passes, which only long rows or narrow grids need, load on
+// the spot. after() issues the loads of a later phase (its prefetch): every
+// thread calls it once, after pass 0's stores, so they are not held up behind
+// the issue.
+template <int WT, class Epilogue, class After>
 __device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight, const float* bias,
-                                          const PhaseShape& ps, int group, int stride, Shared& sh, Epilogue epi)
+                                          const PhaseShape& ps, int group, int stride, Shared& sh, Epilogue epi,
+                                          After after)
 {
     const int lane = threadIdx.x & (kRowLanes - 1);
     int row, first, last;
@@ -653,6 +688,7 @@ __device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight,
     const float bias0 = p.bias;
     if (ps.passes > 0)
         finish_pass(acc, has_task, 0, ps, group, stride, sh, epi, [&](int) { return bias0; });
+    after();
     for (int pass = 1; pass < ps.passes; ++pass)
     {
         const bool task = phase_task(ps, group, stride, pass, row, first, last);
@@ -998,7 +1034,6 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             return false;
         if (l > 0)
             STEP_STAMP(0, l);
-        prefetch(pb, L.self_out_w, L.self_out_b, square_shape, group, stride);
         layer_norm(norm, d, a.eps, sh);
         {
             uint64_t* qkv = ex + a.off_qkv;
@@ -1010,7 +1045,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
                     global_mut(vrow)[r - 2 * d] = v;
                 else if (r >= d)
                     global_mut(krow)[r - d] = v;
-            });
+            }, [&] { prefetch(pb, L.self_out_w, L.self_out_b, square_shape, group, stride); });
         }
         STEP_STAMP(1, l);
 
@@ -1039,24 +1074,25 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
                                         : poll<3>(ex + a.off_self, d, map, sh.x, epoch, a.status, sh)))
                 return false;
             STEP_STAMP(2, l);
-            prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
-            load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
         }
         else
         {
             if (!gather_any(ex + a.off_self, a.self_splits * H * (hd + 2), sh.comb, epoch, a.status, sh))
                 return false;
             STEP_STAMP(2, l);
-            prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
-            load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
             for (int c = threadIdx.x; c < d; c += kThreads)
                 sh.x[c] = combine(sh.comb + (c / hd) * (hd + 2), a.self_splits, H * (hd + 2), c % hd);
             __syncthreads();
         }
         {
             uint64_t* out = ex + a.off_h2;
-            run_phase<WT>(pb, L.self_out_w, L.self_out_b, square_shape, group, stride, sh,
-                          [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); });
+            run_phase<WT>(
+                pb, L.self_out_w, L.self_out_b, square_shape, group, stride, sh,
+                [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); },
+                [&] {
+                    prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
+                    load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
+                });
         }
         STEP_STAMP(3, l);
 
@@ -1064,12 +1100,13 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
         if (!gather_blocked<kPollBlocked>(ex + a.off_h2, d, a.log2_d, stride, sh.raw, epoch, a.status, sh))
             return false;
         STEP_STAMP(4, l);
-        prefetch(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride);
         layer_norm(norm, d, a.eps, sh);
         {
             uint64_t* out = ex + a.off_xq;
-            run_phase<WT>(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride, sh,
-                          [&](int, int j, float v) { put(out + (group << a.log2_d) + j, v, epoch); });
+            run_phase<WT>(
+                pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride, sh,
+                [&](int, int j, float v) { put(out + (group << a.log2_d) + j, v, epoch); },
+                [&] { prefetch(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride); });
         }
         STEP_STAMP(5, l);
 
@@ -1101,12 +1138,15 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
         if (!gather_any(ex + a.off_xattn, d, sh.x, epoch, a.status, sh))
             return false;
         STEP_STAMP(8, l);
-        prefetch(pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride);
-        load_norm(norm, L.final_norm_w, L.final_norm_b, d);
         {
             uint64_t* out = ex + a.off_h3;
-            run_phase<WT>(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride, sh,
-                          [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); });
+            run_phase<WT>(
+                pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride, sh,
+                [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); },
+                [&] {
+                    prefetch(pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride);
+                    load_norm(norm, L.final_norm_w, L.final_norm_b, d);
+                });
         }
         STEP_STAMP(9, l);
 
@@ -1114,12 +1154,13 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
         if (!gather_blocked<kPollBlocked>(ex + a.off_h3, d, a.log2_d, stride, sh.raw, epoch, a.status, sh))
             return false;
         STEP_STAMP(10, l);
-        prefetch(pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride);
         layer_norm(norm, d, a.eps, sh);
         {
             uint64_t* out = ex + a.off_ff;
-            run_phase<WT>(pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride, sh,
-                          [&](int, int j, float v) { put(out + (group << a.log2_f) + j, exact_gelu(v), epoch); });
+            run_phase<WT>(
+                pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride, sh,
+                [&](int, int j, float v) { put(out + (group << a.log2_f) + j, exact_gelu(v), epoch); },
+                [&] { prefetch(pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride); });
         }
         STEP_STAMP(11, l);
 
@@ -1128,17 +1169,18 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
             return false;
         STEP_STAMP(12, l);
         {
-            // The next layer's q/k/v slice and LN1 parameters (the last layer
-            // loads its own again, unused, so these loads are issued on every
-            // path).
+            // After the dot products: the next layer's q/k/v slice and LN1
+            // parameters (the last layer loads its own again, unused, so these
+            // loads are issued on every path).
             const wsp_layer_tensors& next = sh.table[min(l + 1, a.layer_count - 1)];
-            prefetch(pa, next.self_qkv_w, next.self_qkv_b, qkv_shape, group, stride);
-            load_norm(norm, next.self_norm_w, next.self_norm_b, d);
-        }
-        {
             uint64_t* out = ex + a.off_h4;
-            run_phase<WT>(pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride, sh,
-                          [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); });
+            run_phase<WT>(
+                pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride, sh,
+                [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); },
+                [&] {
+                    prefetch(pa, next.self_qkv_w, next.self_qkv_b, qkv_shape, group, stride);
+                    load_norm(norm, next.self_norm_w, next.self_norm_b, d);
+                });
         }
         STEP_STAMP(13, l);
     }
