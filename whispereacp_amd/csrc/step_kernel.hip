@@ -365,12 +365,12 @@ __device__ __forceinline__ bool gather_any(const uint64_t* src, int n, float* ds
 // ---------------------------------------------------------------------------
 // LayerNorm of sh.raw into sh.x: mean, centred biased variance, then
 // (x - mean) * rsqrt(var + eps) * gamma + beta (Kernels/LayerNorm.h:44-89).
-// Lane l of every wave holds the runs 4 (l + 64 k) .. + 3 of the row (n is a
-// multiple of 4), read from LDS in one batch, and every wave sums them in the
-// same order, so every wave gets the same statistics without a barrier. Wave
-// w then writes run w (kNormRuns runs cover the widest row), with gamma/beta
-// of that run held in registers since the previous phase. The only barrier is
-// the one completing sh.x.
+// Lane l of a wave holds the runs 4 (l + 64 k) .. + 3 of the row (n is a
+// multiple of 4), read from LDS in one batch, and each wave that writes a run
+// sums them in the same order, so those waves get the same statistics without
+// a barrier. Wave w then writes run w (kNormRuns runs cover the widest row),
+// with gamma/beta of that run held in registers since the previous phase. The
+// only barrier is the one completing sh.x.
 // ---------------------------------------------------------------------------
 constexpr int kNormRuns = (kMaxWidth + 4 * kWave - 1) / (4 * kWave);
 static_assert(kNormRuns <= kThreads / kWave, "one wave writes each run");
@@ -396,37 +396,38 @@ __device__ __forceinline__ void load_norm(NormParams& p, const float* gamma, con
     p.b = *global(reinterpret_cast<const float4v*>(beta + i));
 }
 
-__device__ __forceinline__ void layer_norm(const NormParams& p, int n, float eps, Shared& sh)
+// The statistics and this wave's run, with R runs per lane (R * 256 >= n).
+template <int R>
+__device__ __forceinline__ void norm_row(const NormParams& p, int n, float eps, Shared& sh, int lane, int own)
 {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int own = 4 * (lane + kWave * (int) (threadIdx.x / kWave)); // the run this wave writes
     // Every LDS read is issued before the first is used: the row's runs and
     // this thread's own run.
-    float4v v[kNormRuns];
+    float4v v[R];
 #pragma unroll
-    for (int k = 0; k < kNormRuns; ++k)
+    for (int k = 0; k < R; ++k)
         v[k] = *reinterpret_cast<const float4v*>(&sh.raw[min(4 * (lane + kWave * k), n - 4)]);
     const float4v x = *reinterpret_cast<const float4v*>(&sh.raw[min(own, n - 4)]);
-    // Pairwise sums (a fixed order, shallow dependency chains).
-    float t[kNormRuns];
+    // Pairwise sums (a fixed order, shallow dependency chains; runs past the
+    // row add zeros, so the order does not depend on R).
+    float t[R];
 #pragma unroll
-    for (int k = 0; k < kNormRuns; ++k)
+    for (int k = 0; k < R; ++k)
         t[k] = 4 * (lane + kWave * k) < n ? (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]) : 0.f;
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < kNormRuns; k += 2)
-        s += k + 1 < kNormRuns ? t[k] + t[k + 1] : t[k];
+    for (int k = 0; k < R; k += 2)
+        s += k + 1 < R ? t[k] + t[k + 1] : t[k];
     const float mean = sum64(s) / (float) n;
 #pragma unroll
-    for (int k = 0; k < kNormRuns; ++k)
+    for (int k = 0; k < R; ++k)
     {
         const float c0 = v[k][0] - mean, c1 = v[k][1] - mean, c2 = v[k][2] - mean, c3 = v[k][3] - mean;
         t[k] = 4 * (lane + kWave * k) < n ? (c0 * c0 + c1 * c1) + (c2 * c2 + c3 * c3) : 0.f;
     }
     float q = 0.f;
 #pragma unroll
-    for (int k = 0; k < kNormRuns; k += 2)
-        q += k + 1 < kNormRuns ? t[k] + t[k + 1] : t[k];
+    for (int k = 0; k < R; k += 2)
+        q += k + 1 < R ? t[k] + t[k + 1] : t[k];
     const float scale = rsqrtf(sum64(q) / (float) n + eps);
     if (own < n)
     {
@@ -435,6 +436,25 @@ __device__ __forceinline__ void layer_norm(const NormParams& p, int n, float eps
         for (int c = 0; c < 4; ++c)
             y[c] = (x[c] - mean) * scale * p.g[c] + p.b[c];
         *reinterpret_cast<float4v*>(&sh.x[own]) = y;
+    }
+}
+
+__device__ __forceinline__ void layer_norm(const NormParams& p, int n, float eps, Shared& sh)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    const int own = 4 * (lane + kWave * (int) (threadIdx.x / kWave)); // the run this wave writes
+    // Only the waves that write a run compute the statistics; the others go
+    // straight to the barrier and leave their SIMDs' issue slots to them.
+    if (own - 4 * lane < n)
+    {
+        switch ((n + 4 * kWave - 1) / (4 * kWave))
+        {
+            case 1:
+            case 2: norm_row<2>(p, n, eps, sh, lane, own); break;
+            case 3: norm_row<3>(p, n, eps, sh, lane, own); break;
+            case 4: norm_row<4>(p, n, eps, sh, lane, own); break;
+            default: norm_row<kNormRuns>(p, n, eps, sh, lane, own); break;
+        }
     }
     __syncthreads();
 }
