@@ -196,21 +196,8 @@ struct Shared
 #endif
 };
 
-// Workgroup-wide sum/max through one barrier; consecutive calls must use
+// Workgroup-wide maximum through one barrier; consecutive calls must use
 // different slots.
-__device__ __forceinline__ float group_sum(float v, Shared& sh, int slot)
-{
-    v = sum64(v);
-    if ((threadIdx.x & (kWave - 1)) == 0)
-        sh.scratch[slot][threadIdx.x / kWave] = v;
-    __syncthreads();
-    float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i)
-        t += sh.scratch[slot][i];
-    return t;
-}
-
 __device__ __forceinline__ float group_max(float v, Shared& sh, int slot)
 {
     v = max64(v);
@@ -723,8 +710,12 @@ __device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight,
 // Single-query attention over keys held in registers: thread t holds channels
 // 4*(t%16).. of key slot t/16 for keys slot + 32*p. Scores (scale * q.k),
 // their maximum, exp(s - max), the sum and the unnormalised value row — the
-// chunk form of Kernels/SingleQueryAttention.h:27-37.
+// chunk form of Kernels/SingleQueryAttention.h:27-37. Scores are kept in
+// base-2 units (scale * log2(e) * q.k), so exp(s - max) is one exp2; the
+// maxima written to the exchange, and the combines, use the same units.
 // ---------------------------------------------------------------------------
+constexpr float kLog2e = 1.44269504088896340736f;
+
 template <int NP>
 struct KeyRows
 {
@@ -754,7 +745,7 @@ __device__ __forceinline__ void load_keys(KeyRows<NP>& kr, const float* keys, co
 // the combine of a single partial, so a consumer of the only partial of a
 // head can take the row as it is.
 template <int NP>
-__device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int head_width, float scale, uint64_t* out,
+__device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int head_width, float scale2, uint64_t* out,
                                        uint32_t epoch, Shared& sh, bool normalized = false)
 {
     const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
@@ -772,7 +763,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
         {
             const float part =
                 live ? qv[0] * kr.k[p][0] + qv[1] * kr.k[p][1] + qv[2] * kr.k[p][2] + qv[3] * kr.k[p][3] : 0.f;
-            s[p] = scale * sum16(part);
+            s[p] = scale2 * sum16(part);
             if (ks + kKeySlots * p < count)
                 local_max = fmaxf(local_max, s[p]);
         }
@@ -785,7 +776,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
     {
         if (kKeySlots * p < count && ks + kKeySlots * p < count)
         {
-            const float e = expf(s[p] - m);
+            const float e = exp2f(s[p] - m);
             if (kl == 0)
                 local_sum += e;
             acc[0] += e * kr.v[p][0];
@@ -794,26 +785,34 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
             acc[3] += e * kr.v[p][3];
         }
     }
-    // Fold the wave's four key slots (lanes 16 apart): slot pairs by swizzle,
-    // then the two halves of the wave; lanes 0-15 then hold the wave's row.
+    // Fold the wave's four key slots (lanes 16 apart) with the neighbouring
+    // row, then the other half of the wave: lanes 0-15 then hold the wave's
+    // row, and lane 0 its sum (kept by the kl == 0 lanes).
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         acc[i] = add32(add16(acc[i]));
-    if ((threadIdx.x & (kWave - 1)) < kKeyLanes && live)
-        *reinterpret_cast<float4v*>(&sh.red[threadIdx.x / kWave][4 * kl]) = acc;
-    const float l = group_sum(local_sum, sh, 1); // its barrier also completes sh.red
+    local_sum = add32(add16(local_sum));
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    if (lane < kKeyLanes && live)
+        *reinterpret_cast<float4v*>(&sh.red[wave][4 * kl]) = acc;
+    if (lane == 0)
+        sh.scratch[1][wave] = local_sum;
+    __syncthreads();
     if ((int) threadIdx.x < head_width)
     {
-        float row = 0.f;
+        float row = 0.f, l = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
+        {
             row += sh.red[w][threadIdx.x];
+            l += sh.scratch[1][w];
+        }
         put(out + 2 + threadIdx.x, normalized ? row / l : row, epoch);
-    }
-    if (threadIdx.x == 0)
-    {
-        put(out, count > 0 ? m : -INFINITY, epoch);
-        put(out + 1, l, epoch);
+        if (threadIdx.x == 0)
+        {
+            put(out, count > 0 ? m : -INFINITY, epoch);
+            put(out + 1, l, epoch);
+        }
     }
     __syncthreads();
 }
@@ -832,7 +831,7 @@ __device__ __forceinline__ float combine(const float* part, int parts, int strid
         const float* p = part + i * stride;
         if (p[1] == 0.f)
             continue;
-        const float factor = expf(p[0] - largest);
+        const float factor = exp2f(p[0] - largest);
         numerator += factor * p[2 + c];
         denominator += factor * p[1];
     }
@@ -854,7 +853,7 @@ __device__ __forceinline__ void combine_parts(const float* part, int parts, int 
         const float m = lane < parts ? part[lane * stride] : -INFINITY;
         const float l = lane < parts ? part[lane * stride + 1] : 0.f;
         const float largest = max64(m);
-        const float factor = l == 0.f ? 0.f : expf(m - largest);
+        const float factor = l == 0.f ? 0.f : exp2f(m - largest);
         const float denominator = sum64(factor * l);
         sh.q[lane] = factor; // a head's query slot is free while combining
         if (lane == 0)
@@ -1149,7 +1148,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
                 return false;
             if (t == task)
                 STEP_STAMP(6, l);
-            attend<kCrossPasses>(cross, count, hd, a.scale,
+            attend<kCrossPasses>(cross, count, hd, a.scale * kLog2e,
                                  ex + a.off_xpart + (size_t) (h * a.cross_splits + s) * (hd + 2), epoch, sh);
         }
         STEP_STAMP(7, l);
@@ -1244,15 +1243,18 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
             {
                 // The new key sits at local index `cached` (= position - first).
                 const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
+                const int c = 4 * min(kl, hd / 4 - 1);
+                const float4v nk = *reinterpret_cast<const float4v*>(&sh.q[hd + c]);
+                const float4v nv = *reinterpret_cast<const float4v*>(&sh.q[2 * hd + c]);
 #pragma unroll
                 for (int p = 0; p < kSelfPasses; ++p)
                     if (ks + kKeySlots * p == cached && 4 * kl < hd)
                     {
-                        self.k[p] = *reinterpret_cast<const float4v*>(&sh.q[hd + 4 * kl]);
-                        self.v[p] = *reinterpret_cast<const float4v*>(&sh.q[2 * hd + 4 * kl]);
+                        self.k[p] = nk;
+                        self.v[p] = nv;
                     }
             }
-            attend<kSelfPasses>(self, count, hd, a.scale, ex + a.off_self + (size_t) (split * H + head) * (hd + 2),
+            attend<kSelfPasses>(self, count, hd, a.scale * kLog2e, ex + a.off_self + (size_t) (split * H + head) * (hd + 2),
                                 epoch, sh, a.self_splits == 1);
             STEP_STAMP(15, l);
         }
