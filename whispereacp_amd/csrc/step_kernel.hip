@@ -100,10 +100,13 @@ __device__ __forceinline__ uint64_t peek(const uint64_t* p)
 // way (a + b == b + a), so every lane of the span holds the same bits. Every
 // lane of the span must be active.
 // ---------------------------------------------------------------------------
+// (bound_ctrl set: every pattern used reads a lane of the same row, so no lane
+// reads out of range, and the move folds into the consuming add as one
+// v_add_f32_dpp.)
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v)
 {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
 constexpr int kSwapNeighbours = 0xB1; // quad_perm [1,0,3,2]
