@@ -114,20 +114,36 @@ constexpr int kSwapPairs = 0x4E;      // quad_perm [2,3,0,1]
 constexpr int kMirrorHalfRow = 0x141; // row_half_mirror
 constexpr int kMirrorRow = 0x140;     // row_mirror
 
-// Lane l's value and lane (l ^ 16)'s, in some order.
-__device__ __forceinline__ void rows_pair(float v, float& a, float& b)
+// Lane l's value and lane (l ^ 16)'s, in an order that depends only on l.
+__device__ __forceinline__ void rows_pair_bits(uint32_t v, uint32_t& a, uint32_t& b)
 {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    a = __uint_as_float(r[0]);
-    b = __uint_as_float(r[1]);
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
 }
 
-// Lane l's value and lane (l ^ 32)'s, in some order.
+// Lane l's value and lane (l ^ 32)'s, in an order that depends only on l.
+__device__ __forceinline__ void halves_pair_bits(uint32_t v, uint32_t& a, uint32_t& b)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+}
+
+__device__ __forceinline__ void rows_pair(float v, float& a, float& b)
+{
+    uint32_t x, y;
+    rows_pair_bits(__float_as_uint(v), x, y);
+    a = __uint_as_float(x);
+    b = __uint_as_float(y);
+}
+
 __device__ __forceinline__ void halves_pair(float v, float& a, float& b)
 {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    a = __uint_as_float(r[0]);
-    b = __uint_as_float(r[1]);
+    uint32_t x, y;
+    halves_pair_bits(__float_as_uint(v), x, y);
+    a = __uint_as_float(x);
+    b = __uint_as_float(y);
 }
 
 __device__ __forceinline__ float add16(float v)
@@ -890,6 +906,53 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
     return v > bv || (v == bv && i < bi);
 }
 
+// Candidate folds across lanes. better() orders candidates totally (larger
+// value, then lower index, an unchosen one last), so which lane of a pair
+// holds which candidate does not change the result.
+__device__ __forceinline__ void keep_better(float& v, uint32_t& i, float ov, uint32_t oi)
+{
+    if (better(ov, oi, v, i))
+    {
+        v = ov;
+        i = oi;
+    }
+}
+
+template <int CTRL>
+__device__ __forceinline__ void fold_dpp(float& v, uint32_t& i)
+{
+    const float ov = dpp<CTRL>(v);
+    const uint32_t oi = (uint32_t) __builtin_amdgcn_mov_dpp((int) i, CTRL, 0xF, 0xF, true);
+    keep_better(v, i, ov, oi);
+}
+
+// Every lane of each 16-lane row ends with the row's best candidate.
+__device__ __forceinline__ void fold16(float& v, uint32_t& i)
+{
+    fold_dpp<kSwapNeighbours>(v, i);
+    fold_dpp<kSwapPairs>(v, i);
+    fold_dpp<kMirrorHalfRow>(v, i);
+    fold_dpp<kMirrorRow>(v, i);
+}
+
+// Every lane of the wave ends with the wave's best candidate.
+__device__ __forceinline__ void fold64(float& v, uint32_t& i)
+{
+    fold16(v, i);
+    float a, b;
+    uint32_t ia, ib;
+    rows_pair(v, a, b); // the value and the index pair up the same lanes in the same order
+    rows_pair_bits(i, ia, ib);
+    v = a;
+    i = ia;
+    keep_better(v, i, b, ib);
+    halves_pair(v, a, b);
+    halves_pair_bits(i, ia, ib);
+    v = a;
+    i = ia;
+    keep_better(v, i, b, ib);
+}
+
 // ---------------------------------------------------------------------------
 // Tied logits. Rows of `lanes` lanes (32 when a row fits 96 chunks, else 64);
 // row group g of workgroup w owns rows w + G * (g + groups * j). A ring of
@@ -1007,8 +1070,36 @@ __device__ __forceinline__ void logits_loop(Ring& ring, const StepArgs& a, const
 // ---------------------------------------------------------------------------
 // The persistent step.
 // ---------------------------------------------------------------------------
+// The layer-0 input: the token and position rows (Kernels/Embed.h:9-14); an
+// id past the vocabulary poisons the row with NaN (it reads row 0, unused).
+// The loads are issued at launch, ahead of the layer table's copy, and the
+// two parts are added where the row is written.
+constexpr int kEmbedSlots = (kMaxWidth + kThreads - 1) / kThreads;
+
+struct Embedding
+{
+    float token[kEmbedSlots];
+    float position[kEmbedSlots];
+    bool known;
+};
+
+__device__ __forceinline__ void issue_embedding(Embedding& e, const StepArgs& a)
+{
+    const int d = a.width;
+    const uint32_t token = a.tokens[0];
+    e.known = token < (uint32_t) a.vocabulary;
+    const size_t row = e.known ? (size_t) token * d : 0;
+#pragma unroll
+    for (int k = 0; k < kEmbedSlots; ++k)
+    {
+        const int c = min((int) threadIdx.x + kThreads * k, d - 1);
+        e.position[k] = global(a.position_embedding)[(size_t) a.position * d + c];
+        e.token[k] = global(a.token_embedding)[row + c];
+    }
+}
+
 template <int WT>
-__device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
+__device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, const Embedding& embed)
 {
     const int d = a.width, f = a.feed_forward, H = a.heads, hd = d / H;
     const int group = blockIdx.x, stride = a.row_groups;
@@ -1029,17 +1120,17 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh)
     NormParams norm;
     KeyRows<kCrossPasses> cross;
 
-    // The layer-0 input: the token and position rows (Kernels/Embed.h:9-14);
-    // an id past the vocabulary poisons the row with NaN.
     {
         const wsp_layer_tensors& L0 = sh.table[0];
         prefetch(pa, L0.self_qkv_w, L0.self_qkv_b, qkv_shape, group, stride);
         load_norm(norm, L0.self_norm_w, L0.self_norm_b, d);
-        const uint32_t token = a.tokens[0];
-        for (int c = threadIdx.x; c < d; c += kThreads)
-            sh.raw[c] = token < (uint32_t) a.vocabulary
-                            ? a.token_embedding[(size_t) token * d + c] + a.position_embedding[(size_t) pos * d + c]
-                            : __builtin_nanf("");
+#pragma unroll
+        for (int k = 0; k < kEmbedSlots; ++k)
+        {
+            const int c = (int) threadIdx.x + kThreads * k;
+            if (c < d)
+                sh.raw[c] = embed.known ? embed.token[k] + embed.position[k] : __builtin_nanf("");
+        }
         __syncthreads();
     }
     STEP_STAMP(0, 0);
@@ -1309,6 +1400,10 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
 {
     if (threadIdx.x == 0)
         sh.abort = 0;
+    const bool row_group = (int) blockIdx.x < a.row_groups;
+    Embedding embed;
+    if (row_group)
+        issue_embedding(embed, a);
     {
         // The layer table, once.
         const int words = a.layer_count * (int) (sizeof(wsp_layer_tensors) / sizeof(uint64_t));
@@ -1320,7 +1415,7 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
     __syncthreads();
     STEP_STAMP(21, 0);
 
-    const bool ok = (int) blockIdx.x < a.row_groups ? row_group_layers<WT>(a, sh) : head_group_layers(a, sh);
+    const bool ok = row_group ? row_group_layers<WT>(a, sh, embed) : head_group_layers(a, sh);
     if (!ok)
         return;
     // The final norm's parameters are in flight before the last layer's output
@@ -1351,19 +1446,20 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
         sh.best_i[rg] = best_i;
     }
     __syncthreads();
-    if (threadIdx.x == 0)
+    if (threadIdx.x < kKeyLanes)
     {
-        float bv = 0.f;
-        uint32_t bi = kUnchosen;
-        for (int k = 0; k < ls.groups; ++k)
-            if (better(sh.best_v[k], sh.best_i[k], bv, bi))
-            {
-                bv = sh.best_v[k];
-                bi = sh.best_i[k];
-            }
+        // The row groups' candidates (at most 16: rows of 32 or 64 lanes) in
+        // the first row of wave 0.
+        const bool held = (int) threadIdx.x < ls.groups;
+        float bv = held ? sh.best_v[threadIdx.x] : 0.f;
+        uint32_t bi = held ? sh.best_i[threadIdx.x] : kUnchosen;
+        fold16(bv, bi);
         // One cache line per workgroup's candidate.
-        put(a.exchange + a.off_argmax + 16 * blockIdx.x, bv, epoch);
-        put(a.exchange + a.off_argmax + 16 * blockIdx.x + 1, __uint_as_float(bi), epoch);
+        if (threadIdx.x == 0)
+        {
+            put(a.exchange + a.off_argmax + 16 * blockIdx.x, bv, epoch);
+            put(a.exchange + a.off_argmax + 16 * blockIdx.x + 1, __uint_as_float(bi), epoch);
+        }
     }
 
     // ---- the argmax fold (Kernels/Argmax.h:145-201) ---------------------------------
@@ -1392,17 +1488,7 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
                 bi = i;
             }
         }
-#pragma unroll
-        for (int offset = kWave / 2; offset > 0; offset >>= 1)
-        {
-            const float ov = __shfl_xor(bv, offset, kWave);
-            const uint32_t oi = __shfl_xor(bi, offset, kWave);
-            if (better(ov, oi, bv, bi))
-            {
-                bv = ov;
-                bi = oi;
-            }
-        }
+        fold64(bv, bi);
         if (threadIdx.x == 0)
             a.argmax_out[0] = bi == kUnchosen ? 0u : bi;
         STEP_STAMP(20, 0);
