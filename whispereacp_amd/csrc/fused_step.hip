@@ -321,6 +321,7 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     a.epoch = ++st->epoch;
     a.scale = 1.f / sqrtf((float) hd);
     a.eps = 1e-5f;
+    a.inv_width = 1.f / (float) s.width;
     a.off_qkv = st->off_qkv;
     a.off_self = st->off_self;
     a.off_h2 = st->off_h2;

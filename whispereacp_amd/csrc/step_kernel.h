@@ -55,6 +55,7 @@ struct StepArgs
     int cross_chunk;    // keys per chunk (<= kCrossKeys)
     uint32_t epoch;
     float scale, eps;
+    float inv_width; // 1 / width, the LayerNorm mean factor
 
     int off_qkv, off_self, off_h2, off_xq, off_xpart, off_xattn, off_h3, off_ff, off_h4;
     int layer_words, off_argmax;

@@ -205,7 +205,7 @@ struct Shared
     float comb[kMaxCombine];             // attention partials being combined
     float red[kWaves][kMaxHeadWidth];    // per-wave value rows of an attention chunk
     float q[3 * kMaxHeadWidth];          // a head's query, then (self-attention) its new key and value
-    float scratch[2][kWaves];            // workgroup reductions, two alternating slots
+    float scratch[2][kWaves];            // per-wave maxima and sums of an attention chunk
     alignas(16) float part[kRowGroups];  // per-row-group partial sums of a projection pass
     float best_v[kRowGroups];
     uint32_t best_i[kRowGroups];
@@ -214,21 +214,6 @@ struct Shared
     uint64_t timeline[kTimelineEvents][kTimelineLayers];
 #endif
 };
-
-// Workgroup-wide maximum through one barrier; consecutive calls must use
-// different slots.
-__device__ __forceinline__ float group_max(float v, Shared& sh, int slot)
-{
-    v = max64(v);
-    if ((threadIdx.x & (kWave - 1)) == 0)
-        sh.scratch[slot][threadIdx.x / kWave] = v;
-    __syncthreads();
-    float t = sh.scratch[slot][0];
-#pragma unroll
-    for (int i = 1; i < kWaves; ++i)
-        t = fmaxf(t, sh.scratch[slot][i]);
-    return t;
-}
 
 // Waits until the n words map(i) (i < n <= P * 448) of base carry `epoch`
 // and copies their floats to dst (LDS). map(i, offset, index) names word i's
@@ -404,7 +389,8 @@ __device__ __forceinline__ void load_norm(NormParams& p, const float* gamma, con
 
 // The statistics and this wave's run, with R runs per lane (R * 256 >= n).
 template <int R>
-__device__ __forceinline__ void norm_row(const NormParams& p, int n, float eps, Shared& sh, int lane, int own)
+__device__ __forceinline__ void norm_row(const NormParams& p, int n, float inv_n, float eps, Shared& sh, int lane,
+                                         int own)
 {
     // Every LDS read is issued before the first is used: the row's runs and
     // this thread's own run.
@@ -423,7 +409,7 @@ __device__ __forceinline__ void norm_row(const NormParams& p, int n, float eps, 
 #pragma unroll
     for (int k = 0; k < R; k += 2)
         s += k + 1 < R ? t[k] + t[k + 1] : t[k];
-    const float mean = sum64(s) / (float) n;
+    const float mean = sum64(s) * inv_n;
 #pragma unroll
     for (int k = 0; k < R; ++k)
     {
@@ -434,7 +420,7 @@ __device__ __forceinline__ void norm_row(const NormParams& p, int n, float eps, 
 #pragma unroll
     for (int k = 0; k < R; k += 2)
         q += k + 1 < R ? t[k] + t[k + 1] : t[k];
-    const float scale = rsqrtf(sum64(q) / (float) n + eps);
+    const float scale = rsqrtf(sum64(q) * inv_n + eps);
     if (own < n)
     {
         float4v y;
@@ -445,7 +431,8 @@ __device__ __forceinline__ void norm_row(const NormParams& p, int n, float eps, 
     }
 }
 
-__device__ __forceinline__ void layer_norm(const NormParams& p, int n, float eps, Shared& sh)
+// inv_n = 1 / n (the row means are the sums times inv_n).
+__device__ __forceinline__ void layer_norm(const NormParams& p, int n, float inv_n, float eps, Shared& sh)
 {
     const int lane = threadIdx.x & (kWave - 1);
     const int own = 4 * (lane + kWave * (int) (threadIdx.x / kWave)); // the run this wave writes
@@ -456,10 +443,10 @@ __device__ __forceinline__ void layer_norm(const NormParams& p, int n, float eps
         switch ((n + 4 * kWave - 1) / (4 * kWave))
         {
             case 1:
-            case 2: norm_row<2>(p, n, eps, sh, lane, own); break;
-            case 3: norm_row<3>(p, n, eps, sh, lane, own); break;
-            case 4: norm_row<4>(p, n, eps, sh, lane, own); break;
-            default: norm_row<kNormRuns>(p, n, eps, sh, lane, own); break;
+            case 2: norm_row<2>(p, n, inv_n, eps, sh, lane, own); break;
+            case 3: norm_row<3>(p, n, inv_n, eps, sh, lane, own); break;
+            case 4: norm_row<4>(p, n, inv_n, eps, sh, lane, own); break;
+            default: norm_row<kNormRuns>(p, n, inv_n, eps, sh, lane, own); break;
         }
     }
     __syncthreads();
@@ -588,14 +575,17 @@ __device__ __forceinline__ float chunk_dot(const uint4& u, const float* x)
                 w[2 * i + 1] = __uint_as_float(v[i] & 0xFFFF0000u);
             }
         }
+        // Two chains of four (even and odd weights), added at the end.
+        float odd = 0.f;
         acc += xa[0] * w[0];
-        acc += xa[1] * w[1];
+        odd += xa[1] * w[1];
         acc += xa[2] * w[2];
-        acc += xa[3] * w[3];
+        odd += xa[3] * w[3];
         acc += xb[0] * w[4];
-        acc += xb[1] * w[5];
+        odd += xb[1] * w[5];
         acc += xb[2] * w[6];
-        acc += xb[3] * w[7];
+        odd += xb[3] * w[7];
+        acc += odd;
     }
     return acc;
 }
@@ -762,12 +752,17 @@ __device__ __forceinline__ void load_keys(KeyRows<NP>& kr, const float* keys, co
 // Writes (max, sum, row[head_width]) of `count` keys into out (exchange
 // words). With `normalized` the row is written already divided by the sum —
 // the combine of a single partial, so a consumer of the only partial of a
-// head can take the row as it is.
+// head can take the row as it is. Each wave takes the softmax of its own key
+// slots against its own maximum; after one barrier the waves' rows are
+// rescaled to the largest maximum and added in wave order (the combine of
+// Kernels/SingleQueryAttention.h:312-373 over the eight waves). The caller
+// writes sh.red and sh.scratch again only after a barrier of its own.
 template <int NP>
 __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int head_width, float scale2, uint64_t* out,
                                        uint32_t epoch, Shared& sh, bool normalized = false)
 {
     const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const bool live = 4 * kl < head_width;
     float4v qv = {0.f, 0.f, 0.f, 0.f};
     if (live)
@@ -781,13 +776,13 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
         if (kKeySlots * p < count) // uniform: passes past the keys are skipped
         {
             const float part =
-                live ? qv[0] * kr.k[p][0] + qv[1] * kr.k[p][1] + qv[2] * kr.k[p][2] + qv[3] * kr.k[p][3] : 0.f;
+                live ? (qv[0] * kr.k[p][0] + qv[1] * kr.k[p][1]) + (qv[2] * kr.k[p][2] + qv[3] * kr.k[p][3]) : 0.f;
             s[p] = scale2 * sum16(part);
             if (ks + kKeySlots * p < count)
                 local_max = fmaxf(local_max, s[p]);
         }
     }
-    const float m = group_max(local_max, sh, 0);
+    const float m = max64(local_max); // this wave's keys; -inf when it holds none
     float local_sum = 0.f;
     float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -811,29 +806,43 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
     for (int i = 0; i < 4; ++i)
         acc[i] = add32(add16(acc[i]));
     local_sum = add32(add16(local_sum));
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     if (lane < kKeyLanes && live)
         *reinterpret_cast<float4v*>(&sh.red[wave][4 * kl]) = acc;
     if (lane == 0)
+    {
+        sh.scratch[0][wave] = m;
         sh.scratch[1][wave] = local_sum;
+    }
     __syncthreads();
     if ((int) threadIdx.x < head_width)
     {
-        float row = 0.f, l = 0.f;
+        float mw[kWaves], lw[kWaves], rw[kWaves];
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
         {
-            row += sh.red[w][threadIdx.x];
-            l += sh.scratch[1][w];
+            mw[w] = sh.scratch[0][w];
+            lw[w] = sh.scratch[1][w];
+            rw[w] = sh.red[w][threadIdx.x];
         }
-        put(out + 2 + threadIdx.x, normalized ? row / l : row, epoch);
+        static_assert(kWaves == 8, "three-level trees over the waves");
+        const float top = fmaxf(fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3])),
+                                fmaxf(fmaxf(mw[4], mw[5]), fmaxf(mw[6], mw[7])));
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+        {
+            const float f = lw[w] == 0.f ? 0.f : exp2f(mw[w] - top); // a wave without keys adds nothing
+            lw[w] *= f;
+            rw[w] *= f;
+        }
+        const float l = ((lw[0] + lw[1]) + (lw[2] + lw[3])) + ((lw[4] + lw[5]) + (lw[6] + lw[7]));
+        const float row = ((rw[0] + rw[1]) + (rw[2] + rw[3])) + ((rw[4] + rw[5]) + (rw[6] + rw[7]));
+        put(out + 2 + threadIdx.x, normalized ? row * __builtin_amdgcn_rcpf(l) : row, epoch);
         if (threadIdx.x == 0)
         {
-            put(out, count > 0 ? m : -INFINITY, epoch);
+            put(out, count > 0 ? top : -INFINITY, epoch);
             put(out + 1, l, epoch);
         }
     }
-    __syncthreads();
 }
 
 // Combines `parts` partials (stride apart, as written by attend) into the
@@ -858,42 +867,37 @@ __device__ __forceinline__ float combine(const float* part, int parts, int strid
 }
 
 // The same combine for up to 64 partials of one head with the whole
-// workgroup: wave 0 finds the largest maximum and each partial's factor
-// exp(m_i - max) (0 for an empty partial) and the denominator; wave w then
-// sums partials w, w + 8, ... of every channel and the eight wave sums are
-// added in wave order. The normalised row goes to out (exchange words).
+// workgroup: every wave finds the largest maximum, each partial's factor
+// exp(m_i - max) (0 for an empty partial) and the denominator itself (no
+// barrier); wave w then sums partials w, w + 8, ... of every channel, and the
+// eight wave sums are added pairwise. The normalised row goes to out
+// (exchange words).
 __device__ __forceinline__ void combine_parts(const float* part, int parts, int head_width, uint64_t* out,
                                               uint32_t epoch, Shared& sh)
 {
     const int stride = head_width + 2;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    if (wave == 0)
-    {
-        const float m = lane < parts ? part[lane * stride] : -INFINITY;
-        const float l = lane < parts ? part[lane * stride + 1] : 0.f;
-        const float largest = max64(m);
-        const float factor = l == 0.f ? 0.f : exp2f(m - largest);
-        const float denominator = sum64(factor * l);
-        sh.q[lane] = factor; // a head's query slot is free while combining
-        if (lane == 0)
-            sh.scratch[0][0] = denominator;
-    }
-    __syncthreads();
+    const float m = lane < parts ? part[lane * stride] : -INFINITY;
+    const float l = lane < parts ? part[lane * stride + 1] : 0.f;
+    const float largest = max64(m);
+    const float factor = l == 0.f ? 0.f : exp2f(m - largest);
+    const float denominator = sum64(factor * l);
     if (lane < head_width)
     {
         float acc = 0.f;
-        for (int i = wave; i < parts; i += kWaves)
-            acc += sh.q[i] * part[i * stride + 2 + lane];
+        for (int i = wave; i < parts; i += kWaves) // i is uniform over the wave
+            acc += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(factor), i)) * part[i * stride + 2 + lane];
         sh.red[wave][lane] = acc;
     }
     __syncthreads();
     if ((int) threadIdx.x < head_width)
     {
-        float numerator = 0.f;
+        float r[kWaves];
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
-            numerator += sh.red[w][threadIdx.x];
-        put(out + threadIdx.x, numerator / sh.scratch[0][0], epoch);
+            r[w] = sh.red[w][threadIdx.x];
+        const float numerator = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        put(out + threadIdx.x, numerator * __builtin_amdgcn_rcpf(denominator), epoch);
     }
 }
 
@@ -1147,7 +1151,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
             return false;
         if (l > 0)
             STEP_STAMP(0, l);
-        layer_norm(norm, d, a.eps, sh);
+        layer_norm(norm, d, a.inv_width, a.eps, sh);
         {
             uint64_t* qkv = ex + a.off_qkv;
             float* krow = L.self_keys + (size_t) pos * d;
@@ -1213,7 +1217,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         if (!gather_blocked<kPollBlocked>(ex + a.off_h2, d, a.log2_d, stride, sh.raw, epoch, a.status, sh))
             return false;
         STEP_STAMP(4, l);
-        layer_norm(norm, d, a.eps, sh);
+        layer_norm(norm, d, a.inv_width, a.eps, sh);
         {
             uint64_t* out = ex + a.off_xq;
             run_phase<WT>(
@@ -1267,7 +1271,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         if (!gather_blocked<kPollBlocked>(ex + a.off_h3, d, a.log2_d, stride, sh.raw, epoch, a.status, sh))
             return false;
         STEP_STAMP(10, l);
-        layer_norm(norm, d, a.eps, sh);
+        layer_norm(norm, d, a.inv_width, a.eps, sh);
         {
             uint64_t* out = ex + a.off_ff;
             run_phase<WT>(
@@ -1386,7 +1390,7 @@ __device__ __forceinline__ bool final_phase(const StepArgs& a, Shared& sh, Ring&
     // The first logits rows are issued once the last layer's output is in:
     // issued before, they would share the memory pipeline with its polls.
     issue_ring(ring, a, logit_shape(a));
-    layer_norm(norm, d, a.eps, sh);
+    layer_norm(norm, d, a.inv_width, a.eps, sh);
     if (blockIdx.x == 0)
         for (int c = threadIdx.x; c < d; c += kThreads)
             a.hidden[c] = sh.x[c];
