@@ -725,6 +725,15 @@ __device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight,
 // ---------------------------------------------------------------------------
 constexpr float kLog2e = 1.44269504088896340736f;
 
+// 2^x for x <= 0 (a softmax weight): the hardware exp2 alone. Results below
+// 2^-126, which the library's exp2f would keep as denormals, come out as 0 —
+// weights no sum can notice — and the library's range fix-up (a compare, a
+// scalar select and an ldexp per call) stays off the dependency chain.
+__device__ __forceinline__ float exp2_weight(float x)
+{
+    return __builtin_amdgcn_exp2f(x);
+}
+
 template <int NP>
 struct KeyRows
 {
@@ -790,7 +799,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
     {
         if (kKeySlots * p < count && ks + kKeySlots * p < count)
         {
-            const float e = exp2f(s[p] - m);
+            const float e = exp2_weight(s[p] - m);
             if (kl == 0)
                 local_sum += e;
             acc[0] += e * kr.v[p][0];
@@ -830,7 +839,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
         {
-            const float f = lw[w] == 0.f ? 0.f : exp2f(mw[w] - top); // a wave without keys adds nothing
+            const float f = lw[w] == 0.f ? 0.f : exp2_weight(mw[w] - top); // a wave without keys adds nothing
             lw[w] *= f;
             rw[w] *= f;
         }
@@ -859,7 +868,7 @@ __device__ __forceinline__ float combine(const float* part, int parts, int strid
         const float* p = part + i * stride;
         if (p[1] == 0.f)
             continue;
-        const float factor = exp2f(p[0] - largest);
+        const float factor = exp2_weight(p[0] - largest);
         numerator += factor * p[2 + c];
         denominator += factor * p[1];
     }
@@ -880,7 +889,7 @@ __device__ __forceinline__ void combine_parts(const float* part, int parts, int 
     const float m = lane < parts ? part[lane * stride] : -INFINITY;
     const float l = lane < parts ? part[lane * stride + 1] : 0.f;
     const float largest = max64(m);
-    const float factor = l == 0.f ? 0.f : exp2f(m - largest);
+    const float factor = l == 0.f ? 0.f : exp2_weight(m - largest);
     const float denominator = sum64(factor * l);
     if (lane < head_width)
     {
