@@ -28,7 +28,7 @@
 // Per layer the chain is: LN1+QKV -> self attention -> out-proj (+residual)
 // -> LN2+cross-q -> cross partials -> cross combine -> cross out (+residual)
 // -> LN3+fc1+GELU -> fc2 (+residual). Then final LN + tied logits with a
-// per-workgroup top-1, and the argmax fold in workgroup 0.
+// per-workgroup top-1, and the argmax fold in the last workgroup.
 //
 // Every wait is bounded: a watchdog flags the context's status word and all
 // workgroups leave, so a broken hand-over ends the launch instead of hanging.
@@ -1476,7 +1476,9 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
     }
 
     // ---- the argmax fold (Kernels/Argmax.h:145-201) ---------------------------------
-    if (blockIdx.x != 0 || a.argmax_out == nullptr)
+    // The last workgroup folds: workgroup 0 also stores the hidden row, and
+    // its polls would wait for those stores' acknowledgements.
+    if (blockIdx.x != gridDim.x - 1 || a.argmax_out == nullptr)
         return;
     if (!poll<kPollArgmax>(
             a.exchange + a.off_argmax, 2 * G,
