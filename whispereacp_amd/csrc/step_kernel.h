@@ -28,7 +28,8 @@ constexpr int kPollBlockedFF = 8;      // ... for the feed-forward vector
 //   | h2 [row_groups << log2_d] | xq [row_groups << log2_d]
 //   | cross partials [heads][cross_split_max][hd + 2] | xattn [d]
 //   | h3 [row_groups << log2_d] | ff [row_groups << log2_f] | h4 [row_groups << log2_d]
-// followed by one argmax block [16 * workgroups] after the last layer. A
+// followed by one argmax block [16 * workgroups] after the last layer (its
+// first 2 * workgroups words: a (value, index) candidate per workgroup). A
 // row-group vector keeps each producing workgroup's rows in a block of its own
 // (2^log2 words: the workgroup's rows-per-phase rounded up to a power of two).
 struct StepArgs

@@ -341,7 +341,7 @@ __device__ __forceinline__ bool gather_blocked(const uint64_t* base, int rows, i
 // vector is polled chunk after chunk.
 
 constexpr int kPollCombine = (kMaxCombine + kPollThreads - 1) / kPollThreads;
-constexpr int kPollArgmax = (2 * 256 + kPollThreads - 1) / kPollThreads; // the two used words of each candidate line
+constexpr int kPollArgmax = (2 * 256 + kPollThreads - 1) / kPollThreads; // two words per workgroup candidate
 
 __device__ __forceinline__ bool gather_any(const uint64_t* src, int n, float* dst, uint32_t epoch, int* status,
                                            Shared& sh)
@@ -1467,11 +1467,11 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
         float bv = held ? sh.best_v[threadIdx.x] : 0.f;
         uint32_t bi = held ? sh.best_i[threadIdx.x] : kUnchosen;
         fold16(bv, bi);
-        // One cache line per workgroup's candidate.
+        // The candidates packed two words each, so the fold polls few lines.
         if (threadIdx.x == 0)
         {
-            put(a.exchange + a.off_argmax + 16 * blockIdx.x, bv, epoch);
-            put(a.exchange + a.off_argmax + 16 * blockIdx.x + 1, __uint_as_float(bi), epoch);
+            put(a.exchange + a.off_argmax + 2 * blockIdx.x, bv, epoch);
+            put(a.exchange + a.off_argmax + 2 * blockIdx.x + 1, __uint_as_float(bi), epoch);
         }
     }
 
@@ -1483,7 +1483,7 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
     if (!poll<kPollArgmax>(
             a.exchange + a.off_argmax, 2 * G,
             [](int i, int& offset, int& index) {
-                offset = 16 * (i >> 1) + (i & 1);
+                offset = i;
                 index = i;
                 return true;
             },
