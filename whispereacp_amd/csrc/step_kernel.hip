@@ -312,6 +312,12 @@ __device__ __forceinline__ int block_slot(int row, int stride, int log2_block)
     return ((row % stride) << log2_block) + row / stride;
 }
 
+// The same for a vector of blocked ownership (`block` rows per workgroup).
+__device__ __forceinline__ int blocked_slot(int row, int block, int log2_block)
+{
+    return ((row / block) << log2_block) + row % block;
+}
+
 // The whole `rows`-row vector, read slot by slot in chunks of P * 448 slots.
 template <int P>
 __device__ __forceinline__ bool gather_blocked(const uint64_t* base, int rows, int log2_block, int stride, float* dst,
@@ -488,10 +494,15 @@ struct PhaseShape
     int local_rows;    // rows this workgroup owns
     int rows_per_pass; // kRowGroups >> slice_log2
     int passes;
+    int block;         // blocked ownership: workgroup w owns rows [w * block, w * block + block); 0: strided
 };
 
+// Strided ownership (row r belongs to workgroup r % stride) spreads the rows a
+// consumer of the whole vector needs evenly; blocked ownership gives a head's
+// rows to a few consecutive workgroups, so a consumer of one head's rows
+// polls a few producer blocks instead of one line per row.
 template <int WT>
-__device__ __forceinline__ PhaseShape phase_shape(int rows, int inner, int group, int stride)
+__device__ __forceinline__ PhaseShape phase_shape(int rows, int inner, int group, int stride, bool blocked = false)
 {
     PhaseShape ps;
     ps.rows = rows;
@@ -503,10 +514,18 @@ __device__ __forceinline__ PhaseShape phase_shape(int rows, int inner, int group
         ++log2;
     ps.slice_log2 = log2;
     ps.slice_chunks = (ps.chunks + (1 << log2) - 1) >> log2;
-    ps.local_rows = group < rows ? (rows - group + stride - 1) / stride : 0;
+    ps.block = blocked ? most_rows : 0;
+    ps.local_rows = blocked ? max(0, min(most_rows, rows - group * most_rows))
+                            : (group < rows ? (rows - group + stride - 1) / stride : 0);
     ps.rows_per_pass = kRowGroups >> log2;
     ps.passes = (ps.local_rows + ps.rows_per_pass - 1) / ps.rows_per_pass;
     return ps;
+}
+
+// The row of this workgroup's local row `local`.
+__device__ __forceinline__ int phase_row(const PhaseShape& ps, int group, int stride, int local)
+{
+    return ps.block ? group * ps.block + local : group + stride * local;
 }
 
 // This row group's (row, first chunk, end chunk) in `pass`; false when it has
@@ -522,7 +541,7 @@ __device__ __forceinline__ bool phase_task(const PhaseShape& ps, int group, int 
         last = 0;
         return false;
     }
-    row = group + stride * (task >> ps.slice_log2);
+    row = phase_row(ps, group, stride, task >> ps.slice_log2);
     first = (task & ((1 << ps.slice_log2) - 1)) * ps.slice_chunks;
     last = min(first + ps.slice_chunks, ps.chunks);
     return true;
@@ -618,7 +637,7 @@ __device__ __forceinline__ void prefetch(Prefetch& p, const void* weight, const 
     int row, first, last;
     phase_task(ps, group, stride, 0, row, first, last);
     load_run(p.r, weight, row, ps.row_bytes, first, last);
-    const int finisher_row = min(group + stride * (int) threadIdx.x, ps.rows - 1);
+    const int finisher_row = min(phase_row(ps, group, stride, (int) threadIdx.x), ps.rows - 1);
     // The load is issued whether or not the phase has a bias (a phase without
     // one reads a weight word and drops it): the compiler counts outstanding
     // loads per program point, and a load skipped on some path makes every
@@ -677,7 +696,7 @@ __device__ __forceinline__ void finish_pass(float acc, bool has_task, int pass, 
     if ((int) threadIdx.x < ps.rows_per_pass && local < ps.local_rows)
     {
         const float v = slice_total(sh, (int) threadIdx.x, ps.slice_log2);
-        const int r = group + stride * local;
+        const int r = phase_row(ps, group, stride, local);
         epi(r, local, v + bias_of(r));
     }
     // Also keeps the other waves from issuing loads (polls, prefetches)
@@ -1118,8 +1137,9 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
     const int group = blockIdx.x, stride = a.row_groups;
     const int pos = a.position;
     const uint32_t epoch = a.epoch;
-    const PhaseShape qkv_shape = phase_shape<WT>(3 * d, d, group, stride);
+    const PhaseShape qkv_shape = phase_shape<WT>(3 * d, d, group, stride, true); // read per head
     const PhaseShape square_shape = phase_shape<WT>(d, d, group, stride);
+    const PhaseShape xq_shape = phase_shape<WT>(d, d, group, stride, true); // read per head
     const PhaseShape fc1_shape = phase_shape<WT>(f, d, group, stride);
     const PhaseShape fc2_shape = phase_shape<WT>(d, f, group, stride);
     // One cross-attention chunk per row group when the split allows it; more
@@ -1216,7 +1236,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
                 pb, L.self_out_w, L.self_out_b, square_shape, group, stride, sh,
                 [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); },
                 [&] {
-                    prefetch(pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride);
+                    prefetch(pa, L.cross_q_w, L.cross_q_b, xq_shape, group, stride);
                     load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
                 });
         }
@@ -1230,7 +1250,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         {
             uint64_t* out = ex + a.off_xq;
             run_phase<WT>(
-                pa, L.cross_q_w, L.cross_q_b, square_shape, group, stride, sh,
+                pa, L.cross_q_w, L.cross_q_b, xq_shape, group, stride, sh,
                 [&](int, int j, float v) { put(out + (group << a.log2_d) + j, v, epoch); },
                 [&] { prefetch(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride); });
         }
@@ -1247,7 +1267,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
             if (!poll<1>(
                     ex + a.off_xq, hd,
                     [&](int i, int& offset, int& index) {
-                        offset = block_slot(h * hd + i, stride, a.log2_d);
+                        offset = blocked_slot(h * hd + i, xq_shape.block, a.log2_d);
                         index = i;
                         return true;
                     },
@@ -1317,6 +1337,7 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
 {
     const int d = a.width, H = a.heads, hd = d / H;
     const int index = blockIdx.x - a.row_groups;
+    const int qkv_block = (3 * d + a.row_groups - 1) / a.row_groups; // the q/k/v phase's rows per workgroup
     const int head = index % H, split = index / H;
     const int n = a.position + 1; // keys attended, the new one included
     const int first = split * kSelfKeys;
@@ -1339,7 +1360,7 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
             if (!poll<1>(
                     ex + a.off_qkv, 3 * hd,
                     [&](int i, int& offset, int& index) {
-                        offset = block_slot((i / hd) * d + head * hd + i % hd, a.row_groups, a.log2_qkv);
+                        offset = blocked_slot((i / hd) * d + head * hd + i % hd, qkv_block, a.log2_qkv);
                         index = i;
                         return true;
                     },
