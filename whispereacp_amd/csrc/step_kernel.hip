@@ -1,6 +1,6 @@
 // The single-token decoder step (Decoder/Decoder.cpp:151-177 with one token,
 // then Argmax over the logits row, Whisper/Whisper.cpp:1164-1184) as ONE
-// persistent cooperative launch on gfx950.
+// persistent launch on gfx950 (every workgroup resident at once).
 //
 // Why one launch: at batch 1 every phase of the step is a dependent GEMV or
 // attention of a few MB, so a launch per op (170+ per step) is bound by launch
@@ -12,9 +12,9 @@
 // through the memory side, with no barrier and no flag round trip.
 //
 // Why it streams at bandwidth: a workgroup issues the loads of its slice of
-// the NEXT phase's weights while it computes the current one (two register
-// sets alternate), so a phase's weights are in registers when its input
-// arrives and HBM traffic overlaps the hand-over chain. The layer table lives
+// the NEXT phase's weights right after it stores the current phase's outputs
+// (two register sets alternate), so a phase's weights are in registers when
+// its input arrives and HBM traffic overlaps the hand-over chain. The layer table lives
 // in LDS, so no phase waits on a pointer load, and every cross-lane reduction
 // is a DPP/swizzle tree in a fixed order.
 //
