@@ -62,6 +62,26 @@ def test_cached_steps_match_reference(oracle, fused):
     print("one token at a time: worst error", worst)
 
 
+def test_a_destroyed_contexts_exchange_area_is_reused_cleanly(oracle):
+    """The persistent step's exchange area outlives its context (uncached
+    device memory goes to a process-wide pool instead of being freed), and the
+    next context of the shape takes it still holding the first one's words,
+    tagged with the same step numbers its own steps will use. They must not
+    pass for its outputs: every step of the second context matches the oracle."""
+    shape, f, enc = small_setup()
+    h, l = oracle.decode_full(shape, oracle_tensors(f, shape), enc, PROMPT)
+    first = DecoderRun(shape, f)
+    assert first.decoder.uses_fused
+    first.begin(enc)
+    for t in PROMPT:
+        first.step([t])
+    first.decoder.close()
+    second = DecoderRun(shape, f)
+    second.begin(enc)
+    for i, t in enumerate(PROMPT):
+        check_rows(second.step([t]), h, l, i, 1)
+
+
 def test_mixed_steps_and_a_second_sequence(oracle):
     shape, f, enc = small_setup()
     tensors = oracle_tensors(f, shape)
