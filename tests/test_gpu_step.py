@@ -1,4 +1,4 @@
-"""The persistent single-token step (one cooperative launch per step) against
+"""The persistent single-token step (one launch per step) against
 the oracle at the decode configurations' own shapes, through the C binding.
 
 Greedy tokens must equal the oracle's; every step's token must also be the
@@ -74,6 +74,24 @@ def test_base_shape_fp32_greedy_matches_oracle(oracle):
     assert decoder.device_status() == 0
     ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, enc, prompt, 24)
     check_run(tokens, rows, ref_tokens, ref_rows, 1e-3)
+
+
+def test_widest_shape_bf16_matches_oracle(oracle):
+    # The large-v3 layer shape (d 1280, 20 heads, ffn 5120, bf16) with two
+    # layers and a short vocabulary: three poll slots per width-long vector,
+    # five LayerNorm runs, 64-lane logits rows, and 12 x 20 = 240 cross
+    # chunks on fewer row groups, so some row groups take two.
+    from whispereacp_amd.decoder import Decoder
+    shape = S.DecoderShape(1280, 20, 2, 5120, 5003, 448, 1500)
+    f = S.workload_decoder_file(shape, "BF16", 5000)
+    enc = S.normal_encoder_output(shape.cross_positions, shape.width, 11)
+    decoder = Decoder(shape, f, packing="ExactHalf")
+    assert decoder.uses_persistent_step
+    prompt = [1, 2, 3, 4]
+    tokens, rows = greedy_on_gpu(decoder, shape, enc, prompt, 12)
+    assert decoder.device_status() == 0
+    ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, enc, prompt, 12)
+    check_run(tokens, rows, ref_tokens, ref_rows, 2e-2)
 
 
 @pytest.mark.parametrize("dtype", ["BF16", "F16"])
