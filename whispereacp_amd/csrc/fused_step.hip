@@ -78,7 +78,12 @@ hipError_t acquire_area(int device, size_t bytes, void** out, size_t* held)
         }
     }
     *held = bytes;
-    return hipExtMallocWithFlags(out, bytes, hipDeviceMallocUncached);
+    if (hipExtMallocWithFlags(out, bytes, hipDeviceMallocUncached) == hipSuccess)
+        return hipSuccess;
+    // A device without uncached allocations: default memory, whose
+    // device-scope accesses are coherent too, only slower to hand over.
+    (void) hipGetLastError();
+    return hipMalloc(out, bytes);
 }
 
 void release_area(int device, size_t bytes, void* memory)
