@@ -342,6 +342,83 @@ __device__ __forceinline__ bool gather_blocked(const uint64_t* base, int rows, i
     return true;
 }
 
+// The same for the long feed-forward vector, two slots per 16-byte
+// device-scope load (half the load instructions of a poll round). Each 8-byte
+// word of the pair was stored whole, so each is old or new on its own. The
+// vector starts 16-byte aligned (every exchange region has an even size).
+template <int Q>
+__device__ __forceinline__ bool gather_pairs(const uint64_t* base, int rows, int log2_block, int stride, float* dst,
+                                             uint32_t epoch, int* status, Shared& sh)
+{
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const int pairs = (stride << log2_block) / 2;
+    const int mask = (1 << log2_block) - 1;
+    for (int first = 0; first < pairs; first += Q * kPollThreads)
+    {
+        bool failed = false;
+        if (threadIdx.x < kWave)
+            __builtin_amdgcn_s_waitcnt(0);
+        else
+        {
+            const int t = threadIdx.x - kWave;
+            uint32_t pending = 0;
+#pragma unroll
+            for (int q = 0; q < Q; ++q)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                {
+                    const int pair = first + t + q * kPollThreads;
+                    const int slot = 2 * pair + h;
+                    if (pair < pairs && (slot & mask) * stride + (slot >> log2_block) < rows)
+                        pending |= 1u << (2 * q + h);
+                }
+            int spins = 0;
+            while (pending != 0)
+            {
+                u32x4 v[Q];
+#pragma unroll
+                for (int q = 0; q < Q; ++q)
+                    if (pending & (3u << (2 * q)))
+                    {
+                        const uint64_t* p = base + 2 * (first + t + q * kPollThreads);
+                        asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v[q]) : "v"(p) : "memory");
+                    }
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int q = 0; q < Q; ++q)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        if ((pending & (1u << (2 * q + h))) && v[q][2 * h + 1] == epoch)
+                        {
+                            const int slot = 2 * (first + t + q * kPollThreads) + h;
+                            dst[(slot & mask) * stride + (slot >> log2_block)] = __uint_as_float(v[q][2 * h]);
+                            pending &= ~(1u << (2 * q + h));
+                        }
+                if (pending != 0 && (++spins & 63) == 0)
+                {
+                    if (spins > kSpinLimit)
+                    {
+                        __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        failed = true;
+                        break;
+                    }
+                    if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
+                    {
+                        failed = true;
+                        break;
+                    }
+                }
+            }
+        }
+        if (failed)
+            sh.abort = 1;
+        __syncthreads();
+        if (sh.abort != 0)
+            return false;
+    }
+    return true;
+}
+
 // Words per polling thread for the vectors a phase awaits: kPollBlocked and
 // kPollBlockedFF (step_kernel.h) per chunk of a blocked vector; a larger
 // vector is polled chunk after chunk.
@@ -1315,7 +1392,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         STEP_STAMP(11, l);
 
         // ---- fc2 + residual (weights in pb) ------------------------------------------------
-        if (!gather_blocked<kPollBlockedFF>(ex + a.off_ff, f, a.log2_f, stride, sh.x, epoch, a.status, sh))
+        if (!gather_pairs<kPollBlockedFF / 2>(ex + a.off_ff, f, a.log2_f, stride, sh.x, epoch, a.status, sh))
             return false;
         STEP_STAMP(12, l);
         {
