@@ -1216,10 +1216,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
     const uint32_t epoch = a.epoch;
     const PhaseShape qkv_shape = phase_shape<WT>(3 * d, d, group, stride, true); // read per head
     const PhaseShape square_shape = phase_shape<WT>(d, d, group, stride);
-    // The cross query is read per head too, but its blocks cost the bf16
-    // variant (whose dot products need more registers) vector-register spills.
-    constexpr bool kBlockedQuery = WT != kBF16;
-    const PhaseShape xq_shape = kBlockedQuery ? phase_shape<WT>(d, d, group, stride, true) : square_shape;
+    const PhaseShape xq_shape = phase_shape<WT>(d, d, group, stride, true); // read per head
     const PhaseShape fc1_shape = phase_shape<WT>(f, d, group, stride);
     const PhaseShape fc2_shape = phase_shape<WT>(d, f, group, stride);
     // One cross-attention chunk per row group when the split allows it; more
@@ -1347,8 +1344,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
             if (!poll<1>(
                     ex + a.off_xq, hd,
                     [&](int i, int& offset, int& index) {
-                        offset = kBlockedQuery ? blocked_slot(h * hd + i, xq_shape.block, a.log2_d)
-                                               : block_slot(h * hd + i, stride, a.log2_d);
+                        offset = blocked_slot(h * hd + i, xq_shape.block, a.log2_d);
                         index = i;
                         return true;
                     },
