@@ -48,7 +48,7 @@ constexpr int kCrossPasses = kCrossKeys / kKeySlots;
 constexpr int kRowLanes = 32;                      // lanes per projection row
 constexpr int kRowGroups = kThreads / kRowLanes;   // rows in flight per workgroup
 constexpr int kChunks = 3;                         // 16-byte chunks per lane per row slice
-constexpr int kRing = 4;                           // logits rows in flight per row group
+constexpr int kRing = 5;                           // logits rows in flight per row group
 constexpr int kWaves = kThreads / kWave;
 constexpr int kSpinLimit = 1 << 21;                // poll rounds before the watchdog trips
 constexpr uint32_t kUnchosen = 0xFFFFFFFFu;
