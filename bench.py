@@ -2,18 +2,27 @@
 
 Workload (default): the small shape — d_model 768, 12 heads, 12 layers, vocab
 51865, fp16-stored weights (fp32 accumulate), encoder states 1500 x 768 N(0,1),
-batch 1 — decoding from a 4-token start-of-transcript prefix, cross K/V
-projected once per sequence. A "step" is one single-token decoder step plus its
-greedy argmax, the token fed back on the device (Decoder::step followed by
-Argmax::encode, as Whisper::encodeStep records them). The timed region is
-exactly --steps such steps, bracketed by synchronisation, inputs resident in
-HBM; warm-up steps run in a sequence of their own first. With the default 224
-steps the self-attention KV grows 5..228 keys over the timed steps.
+batch 1 — decoding 224 single-token greedy steps after a 4-token
+start-of-transcript prefix, cross K/V projected once per sequence. A "step" is
+one single-token decoder step plus its greedy argmax, the token fed back on the
+device (Decoder::step followed by Argmax::encode, as Whisper::encodeStep
+records them). Inputs are resident in HBM; warm-up steps run in a sequence of
+their own first.
+
+Timing: with --steps equal to the workload's own step count (the default) the
+whole sequence is one event-bracketed region, the self-attention KV growing
+5..228 keys. With fewer, the whole sequence still runs, and --steps steps
+spread evenly over it are each bracketed by HIP events on the decoder's stream
+(nothing synchronises between them, so the launch queue never drains); the
+bytes per step are averaged over the same positions.
 
 The JSON line reports decode tokens/s, ms/step, the HBM roofline of the step
 (algorithmic bytes per step / measured step time against 8 TB/s) and the CPU
-oracle timed on the host cores over a bounded sample of the same workload,
-whose tokens are also checked against the GPU's.
+oracle timed on the host cores over a bounded sample of the same workload —
+on one thread (the reference oracle's own model) and on every usable core —
+whose tokens are also checked against the GPU's. `--workload tiny.en
+--cpu-only` runs only the oracle at the tiny.en shape, the configuration the
+reference runs on the CPU.
 """
 
 from __future__ import annotations
@@ -28,6 +37,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+METRIC = "decode tokens/s and ms/step at batch 1, % of HBM roofline (d=768 shapes)"
 
 
 def step_bytes(shape, weight_bytes: int, position: int, streams: int = 1) -> int:
@@ -46,54 +56,189 @@ def step_bytes(shape, weight_bytes: int, position: int, streams: int = 1) -> int
 def measured_traffic(workload: str, unfused: bool):
     """HBM bytes per step-kernel launch as the FETCH_SIZE and WRITE_SIZE
     counters measured them (each scaled by its reading for a plain copy of
-    known size), from the summary committed under profiles/; None when there
-    is no summary for this workload and path."""
+    known size), and the positions they were measured over, from the summary
+    committed under profiles/; (None, None) when there is none."""
     if unfused:
-        return None
+        return None, None
     path = os.path.join(ROOT, "profiles", f"step_kernel_{workload}_traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, None
     with open(path) as f:
-        return json.load(f).get("bytes_per_launch")
+        data = json.load(f)
+    return data.get("bytes_per_launch"), data.get("positions")
+
+
+def sampled_steps(total: int, count: int):
+    """`count` step indices (0-based, of `total`) spread evenly, each the
+    middle of its share."""
+    return sorted({int((i + 0.5) * total / count) for i in range(count)})
+
+
+def host_description():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return {"nproc": os.cpu_count(), "usable_cpus": usable, "cpu_model": model}
+
+
+def all_cores(host) -> int:
+    """Every CPU this process may run on, within the OMP_NUM_THREADS share
+    when the environment sets one."""
+    cores = host["usable_cpus"]
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        cores = min(cores, int(env))
+    return max(1, cores)
 
 
 def cpu_baseline(shape, decoder_file, encoder, prompt, gpu_tokens, budget_s: float):
     """The oracle (the C restatement of the reference's double-precision
-    decoder) on the host cores over a bounded sample: the prompt step, then
-    single-token steps until the time budget is spent."""
+    decoder, KV-cached) on the host: begin_sequence and the prompt step on every
+    usable core, then single-token steps on every core for half the budget and
+    on one thread for the other half, continuing the same sequence (the
+    oracle's threaded loops keep each output's summation order, so the threads
+    change nothing in the results). begin_sequence on one thread is timed over
+    a tenth of the encoder rows and scaled (its cost is linear in the rows).
+    The tokens are compared with the GPU's."""
     import numpy as np
     from oracle import load_oracle
     from whispereacp_amd import synthetic as S
 
+    host = host_description()
+    cores = all_cores(host)
     oracle = load_oracle()
-    cores = min(16, os.cpu_count() or 1)
-    oracle.set_threads(cores)
     tensors = [decoder_file[n].floats() for n in S.canonical_names(shape.layers)]
+
+    oracle.set_threads(1)
+    sub_rows = max(1, shape.cross_positions // 10)
+    probe = oracle.session(shape, tensors)
+    t0 = time.perf_counter()
+    probe.begin(encoder, sub_rows)
+    begin_single_s = (time.perf_counter() - t0) * shape.cross_positions / sub_rows
+    del probe
+
+    oracle.set_threads(cores)
     session = oracle.session(shape, tensors)
     t0 = time.perf_counter()
     session.begin(encoder)
     begin_s = time.perf_counter() - t0
     _, logits = session.step(prompt)
     tokens = [int(np.argmax(logits[-1]))]
-    steps, spent = 0, 0.0
-    while spent < budget_s and steps < len(gpu_tokens) - 1:
-        t = time.perf_counter()
-        _, logits = session.step([tokens[-1]])
-        spent += time.perf_counter() - t
-        tokens.append(int(np.argmax(logits[0])))
-        steps += 1
-    per_step = spent / max(steps, 1)
+    limit = len(gpu_tokens) - 1
+
+    def run(threads, budget, most):
+        oracle.set_threads(threads)
+        steps, spent = 0, 0.0
+        first = session.position
+        while spent < budget and steps < most and len(tokens) - 1 < limit:
+            t = time.perf_counter()
+            _, step_logits = session.step([tokens[-1]])
+            spent += time.perf_counter() - t
+            tokens.append(int(np.argmax(step_logits[0])))
+            steps += 1
+        return steps, spent, first
+
+    # The threaded sample leaves at least half the sequence to the single-thread one.
+    many_steps, many_s, many_first = run(cores, budget_s / 2, max(1, limit // 2))
+    one_steps, one_s, one_first = run(1, budget_s / 2, limit)
+    oracle.set_threads(cores)
+    many_per = many_s / max(many_steps, 1)
+    one_per = one_s / max(one_steps, 1)
     match = tokens == gpu_tokens[:len(tokens)]
     return {
-        "value": round(1.0 / per_step, 3),
+        "value": round(1.0 / many_per, 3),
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"{steps} single-token steps after the 4-token prompt (positions 4..{3 + steps}) of the same "
-                   f"workload in double precision; begin_sequence (cross K/V over 1500 rows) took "
-                   f"{begin_s:.1f} s and is excluded"),
-        "ms_per_step": round(per_step * 1e3, 2),
+        "sample": (f"{many_steps} single-token steps (positions {many_first}..{many_first + many_steps - 1}) on "
+                   f"{cores} threads, then {one_steps} (positions {one_first}..{one_first + one_steps - 1}) on one "
+                   f"thread, of the same workload's sequence in double precision; begin_sequence (cross K/V over "
+                   f"{shape.cross_positions} rows) timed apart"),
+        "ms_per_step": round(many_per * 1e3, 2),
+        "begin_sequence_s": round(begin_s, 3),
+        "single_thread": {"value": round(1.0 / one_per, 3), "unit": "tokens/s", "cores": 1,
+                          "ms_per_step": round(one_per * 1e3, 2),
+                          "begin_sequence_s": round(begin_single_s, 3),
+                          "begin_sequence_note": f"timed over {sub_rows} of {shape.cross_positions} rows, scaled"},
+        "host": host,
     }, {"steps_checked": len(tokens), "tokens_match": bool(match)}
+
+
+def cpu_only(args, w):
+    """The reference's CPU configuration: the oracle alone, on one thread, over
+    the workload's whole sequence (begin_sequence, the prompt step and every
+    single-token step), the median of --repeats runs after one warm-up run, as
+    the reference's benchmark takes it."""
+    import numpy as np
+    from oracle import load_oracle
+    from whispereacp_amd import synthetic as S
+
+    shape = S.workload_shape(args.workload)
+    prompt = S.SOT_PREFIX[shape.vocabulary_size]
+    steps = args.steps
+    print(f"[bench] generating {args.workload} weights ({w['dtype']})", file=sys.stderr, flush=True)
+    decoder_file = S.workload_decoder_file(shape, w["dtype"], w["seed"])
+    encoder = S.normal_encoder_output(shape.cross_positions, shape.width, 7)
+    host = host_description()
+    oracle = load_oracle()
+    oracle.set_threads(1)
+    tensors = [decoder_file[n].floats() for n in S.canonical_names(shape.layers)]
+    runs = []
+    tokens = None
+    for r in range(args.repeats + 1):
+        print(f"[bench] oracle run {r} ({'warm-up' if r == 0 else 'timed'})", file=sys.stderr, flush=True)
+        session = oracle.session(shape, tensors)
+        t0 = time.perf_counter()
+        session.begin(encoder)
+        t1 = time.perf_counter()
+        _, logits = session.step(prompt)
+        seq = [int(np.argmax(logits[-1]))]
+        t2 = time.perf_counter()
+        for _ in range(steps):
+            _, logits = session.step([seq[-1]])
+            seq.append(int(np.argmax(logits[0])))
+        t3 = time.perf_counter()
+        if tokens is not None:
+            assert seq == tokens, "the oracle's tokens differ between runs"
+        tokens = seq
+        if r > 0:
+            runs.append((t1 - t0, t2 - t1, t3 - t2))
+    runs.sort(key=lambda x: x[2])
+    begin_s, prompt_s, steps_s = runs[len(runs) // 2]
+    per = steps_s / steps
+    print(json.dumps({
+        "metric": METRIC,
+        "value": round(1.0 / per, 3),
+        "unit": "tokens/s",
+        "n_gpus": 0,
+        "steps": steps,
+        "warmup": 1,
+        "ms_per_step": round(per * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic: N(0,0.02) weights (LayerNorm gamma 1, beta 0), N(0,1) encoder states, fixed seeds",
+        "config": {"workload": f"{args.workload} decoder on the CPU oracle (one thread, double precision): d_model "
+                               f"{shape.width}, {shape.heads} heads, {shape.layers} layers, vocab "
+                               f"{shape.vocabulary_size}, {w['dtype']} weights, 1500 cross positions, batch 1, "
+                               f"{steps} single-token greedy steps after a 4-token prefix",
+                   "path": "oracle (CPU)", "global_batch": 1, "seq_len": len(prompt) + steps,
+                   "parallelism": "none (one thread)"},
+        "begin_sequence_s": round(begin_s, 3),
+        "prompt_step_s": round(prompt_s, 4),
+        "decode_s": round(steps_s, 4),
+        "repeats": args.repeats,
+        "tokens": tokens,
+        "host": host,
+    }))
 
 
 def main():
@@ -101,8 +246,11 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=None, help="timed steps (default: the workload's own)")
     parser.add_argument("--warmup", type=int, default=16)
-    parser.add_argument("--workload", default="small", choices=["base.en", "small", "medium", "large-v3"])
-    parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of oracle time (0: skip)")
+    parser.add_argument("--workload", default="small", choices=["tiny.en", "base.en", "small", "medium", "large-v3"])
+    parser.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of oracle time (0: skip)")
+    parser.add_argument("--cpu-only", action="store_true",
+                        help="run only the oracle on one thread (the reference's CPU configuration)")
+    parser.add_argument("--repeats", type=int, default=5, help="timed oracle runs with --cpu-only")
     parser.add_argument("--unfused", action="store_true", help="time the per-op kernel sequence instead")
     parser.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                         help="only run a plain device-to-device copy of BYTES (the reference reading for the "
@@ -125,20 +273,42 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    from whispereacp_amd import synthetic as S
+
+    w = S.WORKLOADS[args.workload]
+    if args.steps is None:
+        args.steps = w["steps"]
+    if args.steps <= 0 or args.warmup < 0:
+        print("--steps must be positive and --warmup not negative", file=sys.stderr)
+        sys.exit(2)
+    if args.cpu_only:
+        cpu_only(args, w)
+        return
+    if w["streams"] > 1:
+        bench_streams(args, w)
+        return
+    bench_single(args, w)
+
+
+def check_watchdog(decoder, where: str):
+    status = decoder.device_status()
+    if status != 0:
+        decoder.device_status(clear=True)
+        print(f"[bench] the persistent step's watchdog tripped during the {where}: its steps ended early and the "
+              f"run is not a measurement", file=sys.stderr)
+        sys.exit(3)
+
+
+def bench_single(args, w):
     import numpy as np
     import torch
     from whispereacp_amd import synthetic as S
     from whispereacp_amd.decoder import Decoder, to_device
 
-    w = S.WORKLOADS[args.workload]
-    if args.steps is None:
-        args.steps = w["steps"]
-    if w["streams"] > 1:
-        bench_streams(args, w)
-        return
     shape = S.workload_shape(args.workload)
     prompt = S.SOT_PREFIX[shape.vocabulary_size]
-    if len(prompt) + args.steps > shape.max_positions or len(prompt) + args.warmup > shape.max_positions:
+    total = max(args.steps, w["steps"])
+    if len(prompt) + total > shape.max_positions or len(prompt) + args.warmup > shape.max_positions:
         print(f"--steps and --warmup each fit {shape.max_positions - len(prompt)} steps in one sequence",
               file=sys.stderr)
         sys.exit(2)
@@ -146,7 +316,7 @@ def main():
     weight_bytes = 4 if dtype == "F32" else 2
 
     print(f"[bench] generating {args.workload} weights ({dtype})", file=sys.stderr, flush=True)
-    decoder_file = S.workload_decoder_file(shape, dtype, 1000)
+    decoder_file = S.workload_decoder_file(shape, dtype, w["seed"])
     encoder = S.normal_encoder_output(shape.cross_positions, shape.width, 7)
     torch.cuda.set_device(0)
     decoder = Decoder(shape, decoder_file, packing="ExactHalf")
@@ -156,53 +326,74 @@ def main():
     slots = torch.zeros(shape.max_positions + 1, dtype=torch.int32, device="cuda")
     prompt_logits = torch.empty((len(prompt), V), dtype=torch.float32, device="cuda")
     step_logits = torch.empty((1, V), dtype=torch.float32, device="cuda")
+    base = len(prompt)
 
     def open_sequence():
-        slots[:len(prompt)] = torch.tensor(prompt, dtype=torch.int32, device="cuda")
+        slots[:base] = torch.tensor(prompt, dtype=torch.int32, device="cuda")
         decoder.begin_sequence(enc)
-        decoder.step(slots[:len(prompt)], len(prompt), prompt_logits)
-        decoder.argmax(prompt_logits[-1:], 1, V, None, slots[len(prompt):len(prompt) + 1])
+        decoder.step(slots[:base], base, prompt_logits)
+        decoder.argmax(prompt_logits[-1:], 1, V, None, slots[base:base + 1])
 
-    def run_steps(count):
-        base = len(prompt)
-        for j in range(1, count + 1):
-            decoder.step_and_sample(slots[base + j - 1:base + j], step_logits, None, slots[base + j:base + j + 1])
+    def one_step(j):
+        # step j (1-based) reads the token at position base + j - 1
+        decoder.step_and_sample(slots[base + j - 1:base + j], step_logits, None, slots[base + j:base + j + 1])
 
     print("[bench] warm-up", file=sys.stderr, flush=True)
     open_sequence()
-    run_steps(args.warmup)
+    for j in range(1, args.warmup + 1):
+        one_step(j)
     torch.cuda.synchronize()
+    check_watchdog(decoder, "warm-up")
 
     print("[bench] timed region", file=sys.stderr, flush=True)
     open_sequence()
     torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    contiguous = args.steps == total
+    timed = list(range(total)) if contiguous else sampled_steps(total, args.steps)
     host0 = time.perf_counter()
-    start.record()
-    run_steps(args.steps)
-    stop.record()
+    if contiguous:
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for j in range(1, total + 1):
+            one_step(j)
+        stop.record()
+        events = [(start, stop)]
+    else:
+        wanted = set(timed)
+        events = []
+        for j in range(1, total + 1):
+            if j - 1 in wanted:
+                pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                pair[0].record()
+                one_step(j)
+                pair[1].record()
+                events.append(pair)
+            else:
+                one_step(j)
     enqueue_s = time.perf_counter() - host0
     torch.cuda.synchronize()
     host_s = time.perf_counter() - host0
-    gpu_ms = start.elapsed_time(stop)
+    check_watchdog(decoder, "timed region")
+    gpu_ms = sum(a.elapsed_time(b) for a, b in events)
     ms_per_step = gpu_ms / args.steps
-    gpu_tokens = slots[len(prompt):len(prompt) + args.steps + 1].cpu().numpy().tolist()
+    gpu_tokens = slots[base:base + total + 1].cpu().numpy().tolist()
 
-    positions = range(len(prompt), len(prompt) + args.steps)
-    bytes_total = sum(step_bytes(shape, weight_bytes, p) for p in positions)
-    bytes_per_step = bytes_total / args.steps
+    positions = [base + j for j in timed]
+    bytes_per_step = sum(step_bytes(shape, weight_bytes, p) for p in positions) / len(positions)
     achieved = bytes_per_step / (ms_per_step * 1e-3) / 1e9
 
-    traffic = measured_traffic(args.workload, args.unfused)
+    traffic, traffic_positions = measured_traffic(args.workload, args.unfused)
 
     baseline, parity = None, None
     if args.cpu_budget > 0:
         print("[bench] cpu baseline (oracle)", file=sys.stderr, flush=True)
         baseline, parity = cpu_baseline(shape, decoder_file, encoder, prompt, gpu_tokens, args.cpu_budget)
 
+    sampling = ("every step" if contiguous else
+                f"{args.steps} steps spread evenly over the {total}, each bracketed by HIP events")
     line = {
-        "metric": "decode tokens/s and ms/step at batch 1, % of HBM roofline (d=768 shapes)",
-        "value": round(args.steps / (gpu_ms * 1e-3), 2),
+        "metric": METRIC,
+        "value": round(1e3 / ms_per_step, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -211,15 +402,19 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16-weights/f32" if dtype == "F16" else "f32",
+        "dtype": {"F16": "f16-weights/f32", "BF16": "bf16-weights/f32"}.get(dtype, "f32"),
         "data": "synthetic: N(0,0.02) weights (LayerNorm gamma 1, beta 0), N(0,1) encoder states, fixed seeds",
         "config": {"workload": f"{args.workload} decoder: d_model {shape.width}, {shape.heads} heads, "
                                f"{shape.layers} layers, vocab {V}, {dtype} weights, 1500 cross positions, "
-                               f"batch 1, {args.steps} single-token greedy steps after a 4-token prefix",
+                               f"batch 1, {total} single-token greedy steps after a 4-token prefix "
+                               f"(timed: {sampling})",
                    "path": "per-op kernel sequence" if args.unfused else "fused single-token step",
-                   "global_batch": 1, "seq_len": len(prompt) + args.steps, "parallelism": "none (one GPU)"},
+                   "global_batch": 1, "seq_len": base + total, "parallelism": "none (one GPU)",
+                   "timed_positions": f"{positions[0]}..{positions[-1]}" if contiguous
+                   else positions},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_positions": traffic_positions,
                      "kernel": "step_kernel (one persistent launch per decode step)" if not args.unfused
                      else "per-op kernel sequence",
                      "bytes_per_step": round(bytes_per_step)},
@@ -251,7 +446,7 @@ def bench_streams(args, w):
     begin_timed = args.workload == "large-v3"
     print(f"[bench] generating {args.workload} weights ({dtype}) and {streams} encoder outputs", file=sys.stderr,
           flush=True)
-    decoder_file = S.workload_decoder_file(shape, dtype, 1000)
+    decoder_file = S.workload_decoder_file(shape, dtype, w["seed"])
     encoders = [S.normal_encoder_output(shape.cross_positions, shape.width, 7 + s) for s in range(streams)]
     torch.cuda.set_device(0)
     decoder = BatchedDecoder(shape, decoder_file, streams=streams)

@@ -43,6 +43,7 @@ private:
     DeviceBuffer sequenceTokens; // uint32 [maxPositions + 1]
     DeviceBuffer logitRows;      // float [maxPositions, vocabularySize]
     unsigned* hostSlots = nullptr; // pinned, one per step in flight
+    int* hostStatus = nullptr;     // pinned watchdog words, one per step in flight
     std::vector<void*> events;
 };
 } // namespace WSP

@@ -81,6 +81,9 @@ int wsp_decoder_step_persistent(const wsp_decoder* decoder);
 /* The persistent step's watchdog word (see wsp_hip_device_status). */
 int wsp_decoder_device_status(wsp_decoder* decoder, int* status, int clear);
 
+/* Sets the watchdog word (see wsp_hip_raise_device_status). */
+int wsp_decoder_raise_device_status(wsp_decoder* decoder);
+
 /* Argmax::encode (Kernels/Argmax.h:236-241) into out (device uint32 [rows]). */
 int wsp_decoder_argmax(wsp_decoder* decoder, const float* logits, int rows, int row_length,
                        const float* mask, uint32_t* out);
@@ -88,7 +91,11 @@ int wsp_decoder_argmax(wsp_decoder* decoder, const float* logits, int rows, int 
 /* The greedy loop of Whisper::decodeTranscript (Whisper/Whisper.cpp:1361-1443)
  * over encoder_rows (device), prompt (host ints), with masks on the device
  * (or null). end_of_text < 0 never stops early. Writes up to `capacity`
- * tokens to tokens_out (host) and their count to *count_out. */
+ * tokens to tokens_out (host) and the transcript's full token count to
+ * *count_out; a transcript longer than `capacity` returns WSP_ERR_CAPACITY
+ * (its first `capacity` tokens written). A step whose device-side hand-over
+ * timed out (wsp_hip_device_status) ends the call with WSP_ERR_HIP, kind
+ * runtime error, and clears the word. */
 int wsp_decoder_greedy(wsp_decoder* decoder, const float* encoder_rows, int cross_position_count,
                        const int* prompt, int prompt_count, int maximum_tokens, int end_of_text,
                        const float* first_mask, const float* later_mask, int* tokens_out, int capacity,

@@ -197,6 +197,20 @@ int wsp_hip_step_persistent(const wsp_hip_ctx* ctx);
  * passes cannot time out. */
 int wsp_hip_device_status(wsp_hip_ctx* ctx, int* status, int clear);
 
+/* Enqueues a copy of the watchdog word into *dst (host memory, pinned for the
+ * copy to stay asynchronous) on the context's stream, so a caller reading a
+ * step's outputs behind an event reads the word of the same point in the
+ * stream. Writes 0 at once when the context runs no persistent step. No
+ * reference counterpart (see wsp_hip_device_status). */
+int wsp_hip_device_status_copy(wsp_hip_ctx* ctx, int* dst);
+
+/* Sets the watchdog word as a tripped wait does: later persistent steps on
+ * this context leave at their first long wait, and every caller that reads
+ * the word reports the failure, until it is cleared. No reference
+ * counterpart: for a caller abandoning a context's work, and for tests of the
+ * failure path, which then run without a real time-out. */
+int wsp_hip_raise_device_status(wsp_hip_ctx* ctx);
+
 /* ---- batched independent streams ------------------------------------------
  * No reference counterpart: the reference decodes one sequence per Decoder.
  * A batch holds `streams` independent sequences that share one weight read

@@ -32,19 +32,24 @@ def small_workload():
     return shape, S.workload_decoder_file(shape, "F16", 1000), S.normal_encoder_output(1500, 768, 7)
 
 
+@pytest.mark.timeout(300)
 def test_small_shape_greedy_matches_oracle(oracle, small_workload):
-    # d 768, 12 heads, 12 layers, vocab 51865, fp16 weights, 1500 cross rows
+    # The small configuration at its stated length: d 768, 12 heads, 12
+    # layers, vocab 51865, fp16 weights, 1500 cross rows, 224 single-token
+    # steps after the 4-token prefix (self keys 5..228).
     from whispereacp_amd.decoder import Decoder
     shape, f, enc = small_workload
     decoder = Decoder(shape, f, packing="ExactHalf")
     assert decoder.uses_fused and decoder.uses_persistent_step
     prompt = S.SOT_PREFIX[shape.vocabulary_size]
-    steps = 32
+    steps = S.WORKLOADS["small"]["steps"]
     tokens, rows = greedy_on_gpu(decoder, shape, enc, prompt, steps)
     assert decoder.device_status() == 0
     ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, enc, prompt, steps)
     rel, worst = check_run(tokens, rows, ref_tokens, ref_rows, 2e-2)
-    print(f"small shape, {steps} persistent steps: max relative {rel:.2e}, worst {worst:.2e}")
+    assert len(set(tokens)) >= 4
+    print(f"small shape, {steps} persistent steps: max relative {rel:.2e}, worst {worst:.2e}, "
+          f"{len(set(tokens))} distinct tokens")
 
 
 def test_small_shape_persistent_and_per_op_steps_agree(small_workload):
@@ -62,7 +67,8 @@ def test_small_shape_persistent_and_per_op_steps_agree(small_workload):
 
 
 def test_base_shape_fp32_greedy_matches_oracle(oracle):
-    # d 512, 8 heads, 6 layers, vocab 51864, fp32 weights
+    # The base.en configuration at its stated length: d 512, 8 heads, 6
+    # layers, vocab 51864, fp32 weights, 64 single-token steps.
     from whispereacp_amd.decoder import Decoder
     shape = S.workload_shape("base.en")
     f = S.workload_decoder_file(shape, "F32", 2000)
@@ -70,10 +76,57 @@ def test_base_shape_fp32_greedy_matches_oracle(oracle):
     decoder = Decoder(shape, f, packing="Float")
     assert decoder.uses_persistent_step
     prompt = S.SOT_PREFIX[shape.vocabulary_size]
-    tokens, rows = greedy_on_gpu(decoder, shape, enc, prompt, 24)
+    steps = S.WORKLOADS["base.en"]["steps"]
+    tokens, rows = greedy_on_gpu(decoder, shape, enc, prompt, steps)
     assert decoder.device_status() == 0
-    ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, enc, prompt, 24)
-    check_run(tokens, rows, ref_tokens, ref_rows, 1e-3)
+    ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, enc, prompt, steps)
+    rel, worst = check_run(tokens, rows, ref_tokens, ref_rows, 1e-3)
+    print(f"base.en shape, {steps} persistent steps: max relative {rel:.2e}, worst {worst:.2e}, "
+          f"{len(set(tokens))} distinct tokens")
+
+
+def test_tiny_en_configuration_matches_oracle_and_golden(oracle):
+    # The tiny.en configuration (d 384, 6 heads, 4 layers, vocab 51864, fp32,
+    # the 4-token prefix, 25 greedy steps) on the persistent step: against the
+    # oracle, and against the independent float64 model's tokens.
+    from helpers import load_fixture
+    from whispereacp_amd.decoder import Decoder
+    fx = load_fixture("tiny_en_greedy.json")
+    w = S.WORKLOADS["tiny.en"]
+    shape = S.workload_shape("tiny.en")
+    f = S.workload_decoder_file(shape, w["dtype"], w["seed"])
+    enc = S.normal_encoder_output(shape.cross_positions, shape.width, fx["encoder_seed"])
+    decoder = Decoder(shape, f, packing="Float")
+    assert decoder.uses_persistent_step
+    prompt = S.SOT_PREFIX[shape.vocabulary_size]
+    tokens, rows = greedy_on_gpu(decoder, shape, enc, prompt, w["steps"])
+    assert decoder.device_status() == 0
+    ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, enc, prompt, w["steps"])
+    rel, worst = check_run(tokens, rows, ref_tokens, ref_rows, 1e-3)
+    assert tokens == fx["tokens"]
+    assert len(set(tokens)) >= 4
+    print(f"tiny.en, {w['steps']} persistent steps: max relative {rel:.2e}, worst {worst:.2e}")
+
+
+def test_greedy_reports_a_tripped_watchdog(small_workload):
+    # The watchdog word set from the host, as a timed-out hand-over sets it:
+    # the greedy loop must not hand back the unwritten tokens of such steps
+    # (every wait in the step is bounded, so the launches still end). The word
+    # is cleared by the report, and the next run decodes normally.
+    from whispereacp_amd.decoder import Decoder, to_device
+    shape, f, enc = small_workload
+    decoder = Decoder(shape, f, packing="ExactHalf")
+    assert decoder.uses_persistent_step
+    enc_d = to_device(enc)
+    prompt = S.SOT_PREFIX[shape.vocabulary_size]
+    expected, _ = decoder.greedy(enc_d, prompt, 6)
+    decoder.raise_device_status()
+    assert decoder.device_status() == 1
+    with pytest.raises(RuntimeError, match="timed out"):
+        decoder.greedy(enc_d, prompt, 6)
+    assert decoder.device_status() == 0
+    again, _ = decoder.greedy(enc_d, prompt, 6)
+    assert again == expected
 
 
 def test_widest_shape_bf16_matches_oracle(oracle):

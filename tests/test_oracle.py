@@ -79,6 +79,7 @@ def input_digest(decoder_file, encoder, layers):
 
 PROMPT_FIXTURES = sorted(os.path.basename(p) for p in glob.glob(os.path.join(GOLDEN, "small_*.json")))
 GREEDY_FIXTURES = sorted(os.path.basename(p) for p in glob.glob(os.path.join(GOLDEN, "mid_*.json")))
+TINY_EN_FIXTURE = "tiny_en_greedy.json"
 
 
 def test_fixture_sets_present():
@@ -107,7 +108,43 @@ def test_oracle_greedy_matches_golden(oracle, name):
     tokens, margins, last = session.greedy(fx["prompt"], fx["steps"])
     assert list(tokens) == fx["tokens"]
     assert np.allclose(margins, fx["margins"], rtol=0, atol=1e-12)
-    assert worst_error(last, from_hex(fx["last_logits"])) < 1e-12
+    assert worst_error(last[fx["last_logits_index"]], from_hex(fx["last_logits"])) < 1e-12
+
+
+def test_greedy_fixtures_feed_back_changing_tokens():
+    # A sequence stuck on one token would not show that the fed-back token is
+    # the sampled one: every workload fixture holds at least four.
+    for name in GREEDY_FIXTURES + [TINY_EN_FIXTURE]:
+        assert len(set(load_fixture(name)["tokens"])) >= 4, name
+
+
+def test_oracle_runs_the_tiny_en_configuration(oracle):
+    # The reference's CPU configuration: tiny.en shape (d 384, 6 heads, 4
+    # layers, vocab 51864), fp32 weights N(0, 0.02), 1500 encoder rows, the
+    # 4-token start-of-transcript prefix and 25 greedy steps, on one thread as
+    # the reference's oracle runs (Tests/Decoder/Common.h:360-468), against the
+    # independent float64 model's tokens, margins and last logits.
+    import time
+    fx = load_fixture(TINY_EN_FIXTURE)
+    shape, decoder_file, enc = fixture_inputs(fx)
+    assert shape == S.workload_shape("tiny.en")
+    assert fx["prompt"] == S.SOT_PREFIX[shape.vocabulary_size] and fx["steps"] == 26
+    assert input_digest(decoder_file, enc, shape.layers) == fx["input_sha256"]
+    tensors = tensors_in_order(decoder_file, S.canonical_names(shape.layers))
+    oracle.set_threads(1)
+    try:
+        session = oracle.session(shape, tensors)
+        t0 = time.perf_counter()
+        session.begin(enc)
+        t1 = time.perf_counter()
+        tokens, margins, last = session.greedy(fx["prompt"], fx["steps"])
+        t2 = time.perf_counter()
+    finally:
+        oracle.set_threads(min(8, os.cpu_count() or 1))
+    print(f"tiny.en on one thread: begin_sequence {t1 - t0:.2f} s, prompt + 25 steps {t2 - t1:.2f} s")
+    assert list(tokens) == fx["tokens"]
+    assert np.allclose(margins, fx["margins"], rtol=0, atol=1e-12)
+    assert worst_error(last[fx["last_logits_index"]], from_hex(fx["last_logits"])) < 1e-12
 
 
 # --- ReferenceDecoderTests' four properties (Tests/Decoder/ReferenceDecoderTests.cpp) ---

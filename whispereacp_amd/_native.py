@@ -78,6 +78,8 @@ SIGNATURES = {
                                      c_void_p, c_void_p, c_void_p, c_void_p]),
     "wsp_hip_step_persistent": (c_int, [c_void_p]),
     "wsp_hip_device_status": (c_int, [c_void_p, ctypes.POINTER(c_int), c_int]),
+    "wsp_hip_device_status_copy": (c_int, [c_void_p, ctypes.POINTER(c_int)]),
+    "wsp_hip_raise_device_status": (c_int, [c_void_p]),
     "wsp_decoder_create": (c_int, [ctypes.POINTER(wsp_decoder_shape), ctypes.POINTER(wsp_tensor_entry), c_int,
                                    c_int, c_int, c_void_p, ctypes.POINTER(c_void_p)]),
     "wsp_decoder_destroy": (None, [c_void_p]),
@@ -93,6 +95,7 @@ SIGNATURES = {
     "wsp_decoder_uses_fused": (c_int, [c_void_p]),
     "wsp_decoder_step_persistent": (c_int, [c_void_p]),
     "wsp_decoder_device_status": (c_int, [c_void_p, ctypes.POINTER(c_int), c_int]),
+    "wsp_decoder_raise_device_status": (c_int, [c_void_p]),
     "wsp_decoder_argmax": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p]),
     "wsp_decoder_greedy": (c_int, [c_void_p, c_void_p, c_int, ctypes.POINTER(c_int), c_int, c_int, c_int, c_void_p,
                                    c_void_p, ctypes.POINTER(c_int), c_int, ctypes.POINTER(c_int),

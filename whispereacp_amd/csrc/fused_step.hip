@@ -499,6 +499,30 @@ int fused_status(Context* ctx, int* status, int clear)
         e = hipMemset(state->status, 0, sizeof(int));
     return context_hip(ctx, e, "step status word");
 }
+
+int fused_status_copy(Context* ctx, int* dst)
+{
+    auto* state = static_cast<FusedState*>(ctx->fused);
+    if (state == nullptr || state->status == nullptr)
+    {
+        *dst = 0;
+        return WSP_OK;
+    }
+    return context_hip(ctx, hipMemcpyAsync(dst, state->status, sizeof(int), hipMemcpyDeviceToHost, ctx->stream),
+                       "step status word");
+}
+
+int fused_raise_status(Context* ctx)
+{
+    auto* state = static_cast<FusedState*>(ctx->fused);
+    if (state == nullptr || state->status == nullptr)
+        return context_fail(ctx, WSP_ERR_LOGIC, "the context runs no persistent step");
+    static const int tripped = 1;
+    hipError_t e = hipMemcpyAsync(state->status, &tripped, sizeof(int), hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(ctx->stream);
+    return context_hip(ctx, e, "step status word");
+}
 } // namespace wsp
 
 extern "C" int wsp_hip_decoder_step(wsp_hip_ctx* ctx, const wsp_decoder_tensors* tensors,
@@ -537,4 +561,18 @@ extern "C" int wsp_hip_device_status(wsp_hip_ctx* ctx, int* status, int clear)
     if (ctx == nullptr || status == nullptr)
         return WSP_ERR_ARGUMENT;
     return wsp::fused_status(ctx, status, clear);
+}
+
+extern "C" int wsp_hip_device_status_copy(wsp_hip_ctx* ctx, int* dst)
+{
+    if (ctx == nullptr || dst == nullptr)
+        return WSP_ERR_ARGUMENT;
+    return wsp::fused_status_copy(ctx, dst);
+}
+
+extern "C" int wsp_hip_raise_device_status(wsp_hip_ctx* ctx)
+{
+    if (ctx == nullptr)
+        return WSP_ERR_ARGUMENT;
+    return wsp::fused_raise_status(ctx);
 }

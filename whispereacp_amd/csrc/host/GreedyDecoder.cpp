@@ -4,7 +4,9 @@
 // sampled into and samples under the later-step mask. The sampled token never
 // leaves the device on its way to the next step; the host reads each step's
 // slot through a pinned copy behind that step's event, stepsInFlight steps
-// ahead.
+// ahead. The persistent step's watchdog word is read behind the same event: a
+// step whose hand-over timed out left its slot unwritten, so its token is
+// never used and the run ends in std::runtime_error (the word is cleared).
 #include "../../../include/whispereacp/GreedyDecoder.h"
 
 #include <hip/hip_runtime_api.h>
@@ -12,6 +14,7 @@
 #include <algorithm>
 #include <chrono>
 #include <stdexcept>
+#include <string>
 
 namespace WSP
 {
@@ -24,6 +27,8 @@ GreedyDecoder::GreedyDecoder(Decoder& decoderToUse, const DecoderWeights& weight
     sequenceTokens = DeviceBuffer(device, (std::size_t) (shape.maxPositions + 1) * sizeof(std::uint32_t));
     logitRows = DeviceBuffer(device, (std::size_t) shape.maxPositions * shape.vocabularySize * sizeof(float));
     checkHip(hipHostMalloc(reinterpret_cast<void**>(&hostSlots), stepsInFlight * sizeof(unsigned), 0),
+             "hipHostMalloc");
+    checkHip(hipHostMalloc(reinterpret_cast<void**>(&hostStatus), stepsInFlight * sizeof(int), 0),
              "hipHostMalloc");
     for (int i = 0; i < stepsInFlight; ++i)
     {
@@ -39,6 +44,8 @@ GreedyDecoder::~GreedyDecoder()
         (void) hipEventDestroy(static_cast<hipEvent_t>(e));
     if (hostSlots != nullptr)
         (void) hipHostFree(hostSlots);
+    if (hostStatus != nullptr)
+        (void) hipHostFree(hostStatus);
 }
 
 GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int crossPositionCount,
@@ -56,6 +63,7 @@ GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int 
             throw ModelError("prompt token " + std::to_string(id) + " is outside the vocabulary");
 
     const auto stream = static_cast<hipStream_t>(pass.hipStream());
+    wsp_hip_ctx* const context = decoder.net().context();
     const int stepLimit = std::min(maximumTokens, shape.maxPositions - promptLength + 1);
     const std::size_t slotBytes = sizeof(std::uint32_t);
     const std::size_t rowBytes = (std::size_t) shape.vocabularySize * sizeof(float);
@@ -83,6 +91,9 @@ GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int 
         checkHip(hipMemcpyAsync(&hostSlots[step % stepsInFlight], slot(target).data(), slotBytes,
                                 hipMemcpyDeviceToHost, stream),
                  "read token");
+        const int copied = wsp_hip_device_status_copy(context, &hostStatus[step % stepsInFlight]);
+        if (copied != WSP_OK)
+            throw std::runtime_error(std::string("read the step watchdog: ") + wsp_hip_last_error(context));
         checkHip(hipEventRecord(static_cast<hipEvent_t>(events[(std::size_t) (step % stepsInFlight)]), stream),
                  "hipEventRecord");
     };
@@ -97,6 +108,15 @@ GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int 
     {
         checkHip(hipEventSynchronize(static_cast<hipEvent_t>(events[(std::size_t) (step % stepsInFlight)])),
                  "hipEventSynchronize");
+        if (hostStatus[step % stepsInFlight] != 0)
+        {
+            // Drain what is in flight, then clear the word for the next run.
+            (void) hipStreamSynchronize(stream);
+            int status = 0;
+            (void) wsp_hip_device_status(context, &status, 1);
+            throw std::runtime_error("greedy decode: step " + std::to_string(step)
+                                     + " timed out on the device (its hand-over watchdog tripped)");
+        }
         const int sampled = (int) hostSlots[step % stepsInFlight];
         ++run.steps;
         if (sampled == endOfText)

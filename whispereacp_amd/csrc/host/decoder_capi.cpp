@@ -122,7 +122,8 @@ WSP::WeightPacking packingOf(int packing)
     return packing == 1 ? WSP::WeightPacking::ExactHalf : WSP::WeightPacking::Float;
 }
 
-// DecoderWeights + Decoder + Argmax, every buffer sized once.
+// DecoderWeights + Decoder + Argmax + the greedy loop's buffers, every buffer
+// sized once, so no later call allocates.
 void buildDecoder(wsp_decoder* d, const WSP::TensorSource& source, int packing, void* stream)
 {
     d->weights = std::make_unique<WSP::DecoderWeights>(source, d->shape, packingOf(packing), d->device);
@@ -130,6 +131,7 @@ void buildDecoder(wsp_decoder* d, const WSP::TensorSource& source, int packing, 
     d->decoder->prepare(d->device, stream);
     d->selection = std::make_unique<WSP::Argmax>();
     d->selection->prepare(d->device, d->shape.maxPositions, d->shape.vocabularySize, stream);
+    d->greedy = std::make_unique<WSP::GreedyDecoder>(*d->decoder, *d->weights, d->device);
 }
 
 void buildBatch(wsp_batch_decoder* d, const WSP::TensorSource& source, int packing, int streams, int maxStepTokens,
@@ -162,6 +164,7 @@ int wsp_decoder_create(const wsp_decoder_shape* shape, const wsp_tensor_entry* t
     if (status != WSP_OK)
     {
         // Keep the object so the caller can read why; it is unusable otherwise.
+        d->greedy.reset();
         d->decoder.reset();
         d->weights.reset();
         *out = d;
@@ -189,6 +192,7 @@ int wsp_decoder_create_from_file(const char* path, const wsp_decoder_shape* shap
     });
     if (status != WSP_OK)
     {
+        d->greedy.reset();
         d->decoder.reset();
         d->weights.reset();
     }
@@ -287,6 +291,13 @@ int wsp_decoder_device_status(wsp_decoder* d, int* status, int clear)
     return wsp_hip_device_status(d->decoder->net().context(), status, clear);
 }
 
+int wsp_decoder_raise_device_status(wsp_decoder* d)
+{
+    if (d == nullptr || !d->decoder)
+        return WSP_ERR_ARGUMENT;
+    return wsp_hip_raise_device_status(d->decoder->net().context());
+}
+
 int wsp_decoder_argmax(wsp_decoder* d, const float* logits, int rows, int row_length, const float* mask,
                        uint32_t* out)
 {
@@ -310,18 +321,23 @@ int wsp_decoder_greedy(wsp_decoder* d, const float* encoder_rows, int cross_posi
         if (prompt == nullptr || prompt_count <= 0 || tokens_out == nullptr || count_out == nullptr)
             throw std::invalid_argument("greedy decode needs a prompt and somewhere to put the tokens");
         if (!d->greedy)
-            d->greedy = std::make_unique<WSP::GreedyDecoder>(*d->decoder, *d->weights, d->device);
+            throw std::logic_error("the decoder was not created");
         WSP::Pass pass(d->stream);
         const std::vector<int> promptTokens(prompt, prompt + prompt_count);
         const WSP::GreedyRun run = d->greedy->decode(
             pass, range(encoder_rows, (std::size_t) d->shape.crossElementCount() * 4), cross_position_count,
             promptTokens, maximum_tokens, end_of_text, first_mask, later_mask);
-        const int n = std::min<int>((int) run.tokens.size(), capacity);
+        const int total = (int) run.tokens.size();
+        const int n = std::min(total, std::max(capacity, 0));
         for (int i = 0; i < n; ++i)
             tokens_out[i] = run.tokens[(std::size_t) i];
-        *count_out = n;
+        *count_out = total;
         if (decode_seconds != nullptr)
             *decode_seconds = run.decodeSeconds;
+        if (total > n)
+            throw std::invalid_argument("greedy decode: " + std::to_string(total) + " tokens, room for "
+                                        + std::to_string(n) + " (the first " + std::to_string(n)
+                                        + " were written)");
     });
 }
 

@@ -346,13 +346,30 @@ __device__ __forceinline__ bool gather_blocked(const uint64_t* base, int rows, i
 // device-scope load (half the load instructions of a poll round). Each 8-byte
 // word of the pair was stored whole, so each is old or new on its own. The
 // vector starts 16-byte aligned (every exchange region has an even size).
+//
+// The loads are buffer loads over the vector's own bytes with the
+// device-scope (sc1) cache policy: the compiler tracks them, so its waits
+// cover exactly these loads. Each poll round starts with a compiler-level
+// memory clobber, so no round's loads are merged with another's or hoisted
+// out of the loop (the volatile form would add sc0, the slower system scope).
+// A load past the vector's end reads zeros, which no epoch matches.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kBufferWords3 = 0x00020000; // raw buffer access: 32-bit data format, no swizzle
+constexpr int kDeviceScope = 0x10;        // the sc1 cache-policy bit
+
+__device__ __forceinline__ u32x4 poll_load16(__amdgpu_buffer_rsrc_t vector, int byte_offset)
+{
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vector, byte_offset, 0, kDeviceScope));
+}
+
 template <int Q>
 __device__ __forceinline__ bool gather_pairs(const uint64_t* base, int rows, int log2_block, int stride, float* dst,
                                              uint32_t epoch, int* status, Shared& sh)
 {
-    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     const int pairs = (stride << log2_block) / 2;
     const int mask = (1 << log2_block) - 1;
+    const __amdgpu_buffer_rsrc_t vector =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(base), 0, pairs * 16, kBufferWords3);
     for (int first = 0; first < pairs; first += Q * kPollThreads)
     {
         bool failed = false;
@@ -375,15 +392,12 @@ __device__ __forceinline__ bool gather_pairs(const uint64_t* base, int rows, int
             int spins = 0;
             while (pending != 0)
             {
+                asm volatile("" ::: "memory"); // a fresh read every round
                 u32x4 v[Q];
 #pragma unroll
                 for (int q = 0; q < Q; ++q)
                     if (pending & (3u << (2 * q)))
-                    {
-                        const uint64_t* p = base + 2 * (first + t + q * kPollThreads);
-                        asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v[q]) : "v"(p) : "memory");
-                    }
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                        v[q] = poll_load16(vector, 16 * (first + t + q * kPollThreads));
 #pragma unroll
                 for (int q = 0; q < Q; ++q)
 #pragma unroll

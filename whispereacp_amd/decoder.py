@@ -208,6 +208,11 @@ class Decoder:
         self._check(self.lib.wsp_decoder_device_status(self.handle, ctypes.byref(status), int(clear)))
         return status.value
 
+    def raise_device_status(self):
+        """Sets the watchdog word as a timed-out wait would (later steps leave
+        early and greedy() raises until it is cleared)."""
+        self._check(self.lib.wsp_decoder_raise_device_status(self.handle))
+
     def argmax(self, logits: torch.Tensor, rows: int, row_length: int, mask: Optional[torch.Tensor],
                out: torch.Tensor):
         self._check(self.lib.wsp_decoder_argmax(self.handle, ptr(logits), rows, row_length, ptr(mask), ptr(out)))
@@ -224,7 +229,7 @@ class Decoder:
                                                 len(prompt), maximum_tokens, end_of_text, ptr(first_mask),
                                                 ptr(later_mask), out, maximum_tokens, ctypes.byref(count),
                                                 ctypes.byref(seconds)))
-        return list(out[:count.value]), seconds.value
+        return list(out[:min(count.value, maximum_tokens)]), seconds.value
 
 
 class BatchedDecoder:
