@@ -114,6 +114,20 @@ int wsp_hip_attention(wsp_hip_ctx* ctx, const float* q, int q_count, const float
                       const float* values, int k_count, int width, int heads, int causal,
                       float scale, float* out);
 
+/* wsp_hip_attention without a context, allocating nothing: the same kernels
+ * and results, ordered on `stream` (a hipStream_t, null for the default
+ * stream) on the caller's current device. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The split-key
+ * partials live in a fixed device array of 2^20 floats (4 MiB) per GPU, held
+ * until the process ends; a call whose partials exceed it returns
+ * WSP_ERR_CAPACITY. Calls that overlap on one GPU share that array and race;
+ * calls ordered on one stream do not. The reason for a non-zero status goes to
+ * error (error_capacity bytes, may be null). */
+int wsp_hip_attention_static(const float* q, int q_count, const float* keys, const float* values,
+                             int k_count, int width, int heads, int causal, float scale, float* out,
+                             void* stream, char* error, int error_capacity);
+
 /* out[r] = the first j maximising logits[r * row_length + j] over the j with
  * mask[j] == 0 (mask may be null); all suppressed gives 0. Replaces Argmax
  * (Kernels/Argmax.h:46-262, Kernels/Argmax.cpp:43-81). */

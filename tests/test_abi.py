@@ -55,6 +55,22 @@ def test_context_refuses_bad_arguments_without_a_device():
     assert lib.wsp_hip_last_error(None) == b"no context"
 
 
+def test_static_attention_refuses_before_touching_a_device():
+    # Arguments and the fixed partials capacity are checked before any device
+    # call, with the reason in the caller's buffer.
+    from whispereacp_amd import _native as N
+    lib = ensure_library()
+    error = ctypes.create_string_buffer(256)
+    p = ctypes.c_void_p(16)
+    assert lib.wsp_hip_attention_static(None, 1, p, p, 1, 64, 1, 1, 1.0, p, None, error, 256) == N.WSP_ERR_ARGUMENT
+    assert lib.wsp_hip_attention_static(p, 1, p, p, 1, 128, 1, 1, 1.0, p, None, error, 256) == N.WSP_ERR_LOGIC
+    assert lib.wsp_hip_attention_static(p, 5, p, p, 4, 64, 1, 1, 1.0, p, None, error, 256) == N.WSP_ERR_SHAPE
+    # 20 heads x 4096 queries over 4096 keys: four chunks of partials, 21.6M floats
+    status = lib.wsp_hip_attention_static(p, 4096, p, p, 4096, 1280, 20, 0, 1.0, p, None, error, 256)
+    assert status == N.WSP_ERR_CAPACITY
+    assert b"without allocation" in error.value
+
+
 def test_decoder_refuses_a_bad_shape_as_a_model_error():
     from whispereacp_amd import _native as N
     from whispereacp_amd.decoder import Decoder, ModelError

@@ -71,6 +71,8 @@ SIGNATURES = {
     "wsp_hip_embed": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_int]),
     "wsp_hip_attention": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                                   c_float, c_void_p]),
+    "wsp_hip_attention_static": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float,
+                                         c_void_p, c_void_p, ctypes.c_char_p, c_int]),
     "wsp_hip_argmax": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p]),
     "wsp_hip_project_cross_kv": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int,
                                          c_void_p, c_void_p]),
