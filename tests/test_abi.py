@@ -124,3 +124,22 @@ def test_batch_refuses_bad_arguments_without_a_device():
     assert lib.wsp_batch_begin(None, None, N.WSP_F16, None, 0) == N.WSP_ERR_ARGUMENT
     assert lib.wsp_batch_last_error(None) == b"null batch"
     assert lib.wsp_batch_position(None) == -1
+
+
+def net_refusals():
+    path = os.path.join(ROOT, "tests", "native", "_build", "net_refusals")
+    if not os.path.exists(path):
+        import subprocess
+        ensure_library()
+        subprocess.run(["make", "-s", "_build/net_refusals"], cwd=os.path.join(ROOT, "tests", "native"), check=True)
+    return path
+
+
+def test_net_refusals_without_a_device():
+    # WSP::HipNet refuses with std::logic_error, as the reference's KernelNet
+    # does, what it can refuse before anything is prepared: recording or making
+    # a cache before prepare(), the encoder-only ops, a shape past four extents.
+    import subprocess
+    result = subprocess.run([net_refusals(), "host"], capture_output=True, text=True, timeout=60)
+    assert result.returncode == 0, result.stdout + result.stderr
+    assert result.stdout.count("ok ") == 6, result.stdout

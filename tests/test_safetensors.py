@@ -122,7 +122,7 @@ def test_unknown_tensor_lookup():
         open_bytes(assemble(SINGLE, f32(1, 2, 3, 4, 5, 6))).read_floats("nope", 6)
 
 
-@pytest.mark.parametrize("data", [
+MALFORMED = [
     b"\0" * 7,                                                      # shorter than the length prefix
     assemble("{}", length=3),                                        # header length past the end
     assemble("{}", length=2 ** 64 - 1),
@@ -145,7 +145,10 @@ def test_unknown_tensor_lookup():
     assemble('{"__metadata__":{"format":7}}'),                                       # metadata not strings
     assemble('{"__metadata__":7}'),
     assemble('{"w":{"dtype":"F32","shape":[1],"data_offsets":[0,4]}} x', f32(1)),     # trailing text
-], ids=lambda d: str(len(d)))
+]
+
+
+@pytest.mark.parametrize("data", MALFORMED, ids=lambda d: str(len(d)))
 def test_malformed_headers_are_refused_when_opened(data):
     refused(data)
 
@@ -262,3 +265,74 @@ def test_config_tokens_outside_the_vocabulary_are_refused(tmp_path, change):
     path.write_text(json.dumps(dict(SMALL_CONFIG, **change)))
     with pytest.raises(ModelError):
         decoding_from_config(str(path), 51865)
+
+
+# --- the same readers under AddressSanitizer and UndefinedBehaviorSanitizer ---
+
+def sanitized_reader():
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "native", "_build", "safetensors_check")
+    if not os.path.exists(path):
+        import subprocess
+        subprocess.run(["make", "-s", "_build/safetensors_check"], cwd=os.path.dirname(os.path.dirname(path)),
+                       check=True)
+    return path
+
+
+def run_sanitized(mode, paths):
+    import subprocess
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0:exitcode=86",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1:exitcode=87")
+    result = subprocess.run([sanitized_reader(), mode] + [str(p) for p in paths], capture_output=True, text=True,
+                            env=env, timeout=120)
+    assert result.returncode == 0, result.stdout + result.stderr
+    assert "runtime error" not in result.stderr and "AddressSanitizer" not in result.stderr, result.stderr
+    lines = result.stdout.splitlines()
+    assert len(lines) == len(paths), result.stdout
+    return lines
+
+
+def test_malformed_headers_are_refused_under_sanitizers(tmp_path):
+    # host/SafeTensors.cpp (its own JSON reader over a mapped file) built with
+    # -fsanitize=address,undefined: every malformed header of the cases above
+    # is refused with a ModelError and no sanitizer report, and well-formed
+    # files (empty tensors, metadata, every widened dtype) read in full.
+    bad = []
+    for i, data in enumerate(MALFORMED):
+        path = tmp_path / f"bad_{i}.safetensors"
+        path.write_bytes(data)
+        bad.append(path)
+    lines = run_sanitized("open", bad)
+    assert all(line.startswith("refused: ") for line in lines), lines
+    good = {
+        "single": assemble(SINGLE, f32(1, 2, 3, 4, 5, 6)),
+        "empty": assemble('{"empty":{"dtype":"F32","shape":[0,4],"data_offsets":[0,0]}}'),
+        "metadata": assemble('{"__metadata__":{"format":"pt"},"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}}',
+                             f32(1, 2)),
+        "widened": assemble('{"h":{"dtype":"F16","shape":[2],"data_offsets":[0,4]},'
+                            '"b":{"dtype":"BF16","shape":[2],"data_offsets":[4,8]},'
+                            '"d":{"dtype":"F64","shape":[1],"data_offsets":[8,16]}}',
+                            u16(0x3C00, 0x7C00) + u16(0x3F80, 0xC000) + np.array([0.5], "<f8").tobytes()),
+    }
+    paths = []
+    for name, data in good.items():
+        path = tmp_path / f"{name}.safetensors"
+        path.write_bytes(data)
+        paths.append(path)
+    lines = run_sanitized("open", paths + [tmp_path / "absent.safetensors"])
+    assert [line.split(",")[0] for line in lines[:4]] == ["read: 1 tensors", "read: 1 tensors", "read: 1 tensors",
+                                                          "read: 3 tensors"], lines
+    assert lines[4].startswith("refused: ")
+
+
+def test_config_readers_under_sanitizers(tmp_path):
+    good = tmp_path / "config.json"
+    good.write_text(json.dumps(dict(SMALL_CONFIG, suppress_tokens=[1, 2], begin_suppress_tokens=[3])))
+    broken = []
+    for i, text in enumerate(["", "{", "[]", '{"d_model": "wide"}', json.dumps(dict(SMALL_CONFIG, d_model=-1)),
+                              json.dumps(dict(SMALL_CONFIG, suppress_tokens=[10 ** 9]))]):
+        path = tmp_path / f"broken_{i}.json"
+        path.write_text(text)
+        broken.append(path)
+    lines = run_sanitized("config", [good] + broken)
+    assert lines[0].startswith("config: 768 12 12 3072 51865 448 1500"), lines
+    assert all(line.startswith("refused: ") for line in lines[1:]), lines

@@ -594,6 +594,8 @@ void SafeTensors::readFloats(const std::string& name, float* destination, std::s
     if (capacity < n)
         throw ModelError("tensor '" + name + "' holds " + std::to_string(n) + " values, more than the "
                          + std::to_string(capacity) + " the destination takes");
+    if (n == 0)
+        return; // an empty tensor's destination may be null, which memcpy must not see
     const std::uint8_t* p = rawBytes(t);
     switch (t.type)
     {
