@@ -154,7 +154,13 @@ def test_embed_refuses_positions_past_the_table(ctx):
 @pytest.mark.parametrize("q_count,k_count,width,heads,causal", [
     (1, 1, 64, 4, True), (1, 11, 768, 12, True), (1, 203, 64, 1, True), (1, 257, 384, 6, True),
     (1, 700, 64, 4, False), (1, 1500, 768, 12, False), (1, 448, 512, 8, True), (4, 4, 8, 2, True),
-    (4, 9, 8, 2, True), (16, 16, 64, 4, True), (3, 1500, 64, 4, False), (2, 6, 8, 2, False)])
+    (4, 9, 8, 2, True), (16, 16, 64, 4, True), (3, 1500, 64, 4, False), (2, 6, 8, 2, False),
+    # prompt steps (2..16 queries in one launch): causal self attention at the
+    # sequence start and further in, cross attention over full and reduced
+    # encoder rows, at the decode configurations' head counts and narrower heads
+    (2, 2, 768, 12, True), (4, 4, 768, 12, True), (7, 40, 512, 8, True), (16, 300, 1280, 20, True),
+    (5, 448, 384, 6, True), (4, 1500, 768, 12, False), (16, 1500, 1280, 20, False), (9, 77, 768, 12, False),
+    (3, 65, 256, 4, False), (12, 129, 128, 4, True), (16, 1500, 128, 32, False), (8, 3, 64, 16, False)])
 def test_attention_matches_oracle(ctx, oracle, q_count, k_count, width, heads, causal):
     q = S.normal_values(q_count * width, 1, 1.0).reshape(q_count, width)
     k = S.normal_values(k_count * width, 2, 1.0).reshape(k_count, width)
@@ -283,3 +289,20 @@ def test_cross_kv_projection_matches_oracle(ctx, oracle, dtype, width):
     xd = x.astype(np.float64)
     assert worst_error(k_out.cpu().numpy(), oracle.linear(xd, wk, None)) < 1e-5
     assert worst_error(v_out.cpu().numpy(), oracle.linear(xd, wv, bv)) < 1e-5
+
+
+def test_prompt_attention_is_deterministic_and_independent_of_the_last_block(ctx):
+    # 16 queries over 1500 keys split across blocks whose partials the last one
+    # to finish combines in split order: repeated launches give the same bits,
+    # and the per-head counters stay usable (zero between launches).
+    q = S.normal_values(16 * 768, 4, 1.0).reshape(16, 768)
+    k = S.normal_values(1500 * 768, 5, 1.0).reshape(1500, 768)
+    v = S.normal_values(1500 * 768, 6, 1.0).reshape(1500, 768)
+    qd, kd, vd = dev(q), dev(k), dev(v)
+    outs = []
+    for _ in range(5):
+        out = dev(np.zeros((16, 768), np.float32))
+        ctx.attention(qd, 16, kd, vd, 1500, 768, 12, False, 0.125, out)
+        sync()
+        outs.append(out.cpu().numpy())
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])

@@ -1,7 +1,8 @@
 // wsp_hip_attention_static: wsp_hip_attention without a context, for callers
 // that cannot allocate device memory (code under HIP graph capture, tight
 // serving loops, harnesses that forbid hipMalloc). It runs the same kernels
-// (ops.hip attention_chunk_kernel / attention_combine_kernel); their split-key
+// (ops.hip: prompt_attention_kernel for 2 to 16 queries, else
+// attention_chunk_kernel and attention_combine_kernel); their split-key
 // partials, which the context-bound entry point keeps in a workspace allocated
 // at wsp_hip_ctx_create, live here in one file-scope device array per GPU.
 //
@@ -9,8 +10,10 @@
 // by every GPU the library runs on until the process ends. Every call on a GPU
 // shares that GPU's array, so calls that overlap on one GPU (two streams, two
 // threads) race on it; calls ordered on one stream do not. The partials are
-// written in full by the chunk kernel before the combine reads them, so
-// nothing in the array needs clearing between calls.
+// written in full before they are read. The first kAttentionCounters words are
+// the prompt attention's per-head counters: zero when the array is loaded, and
+// every launch leaves them zero again, so nothing needs clearing between
+// calls.
 #include "ops.h"
 #include "../../include/wsp_hip.h"
 

@@ -83,6 +83,12 @@ int wsp_hip_ctx_create(const wsp_decoder_shape* shape, int device, void* stream,
         ctx->attention_floats = std::max<size_t>(floats, 1);
         status = hip_status(ctx, hipMalloc(&ctx->attention_workspace, ctx->attention_floats * sizeof(float)),
                             "attention workspace");
+        // The prompt attention's per-head counters start at zero (each launch
+        // leaves them zero again).
+        if (status == WSP_OK)
+            status = hip_status(ctx, hipMemset(ctx->attention_workspace, 0,
+                                               wsp::ops::kAttentionCounters * sizeof(unsigned int)),
+                                "attention workspace");
     }
     if (status == WSP_OK)
     {

@@ -52,9 +52,20 @@ hipError_t embed(hipStream_t stream, const uint32_t* tokens, int count, const fl
                  const float* position_table, int first_position, float* y, int width,
                  int vocabulary);
 
+// Queries a prompt step's attention takes in one launch (prompt_attention).
+constexpr int kMaxPromptQueries = 16;
+// The attention workspace starts with this many per-head counters (the
+// prompt attention's last-block election); they are zero between launches,
+// and whoever provides a workspace zeroes them once before its first use.
+constexpr int kAttentionCounters = 256;
+
 // How many key chunks the split-key attention uses for this shape, and the
-// workspace (floats) it needs: chunks * (head_width + 2) per (head, query).
+// workspace (floats) it needs: the counters, then the partials —
+// chunks * (head_width + 2) per (head, query) for one query or more than
+// kMaxPromptQueries, splits * kMaxPromptQueries * (kMaxHeadWidth + 2) per head
+// for a prompt step.
 int attention_chunks(int heads, int q_count, int k_count);
+int prompt_attention_splits(int heads, int k_count);
 size_t attention_workspace_floats(int heads, int q_count, int k_count, int head_width);
 
 hipError_t attention(hipStream_t stream, const float* q, int q_count, const float* keys,

@@ -370,6 +370,182 @@ __global__ void attention_combine_kernel(const float* __restrict__ partials, int
 }
 
 // ---------------------------------------------------------------------------
+// Multi-query attention of a prompt step (2..16 queries): the scores, the
+// softmax and the weighted value sum of Kernels/Attention.h:75-209, with its
+// causal rule (query i of q stands at absolute position k - q + i and sees the
+// keys up to it, Kernels/Attention.h:34-47), in one launch. Block (head,
+// split) takes every query of its head over keys [split·span, +span) in tiles
+// of 64 keys staged in LDS, and keeps per query an online (max, sum, row) with
+// exact exp(m_old - m_new) rescaling: masked keys get weight exactly 0. Wave w
+// owns queries 4w .. 4w + 3 in every phase (lane = key for the scores, lane =
+// channel for the values), so a query's statistics never leave its wave. With
+// several splits each block writes its (max, sum, row) per query, and the last
+// block of the head to finish (a per-head counter it resets to zero) combines
+// them in split order, so the result does not depend on which block is last.
+// ---------------------------------------------------------------------------
+constexpr int kPromptTile = 64;
+constexpr int kPromptKeyStride = kMaxHeadWidth + 4; // padded rows: lanes reading key rows spread over the banks
+constexpr int kPromptPartial = kMaxHeadWidth + 2;
+static_assert(kMaxPromptQueries == 4 * kWavesPerBlock, "four queries per wave");
+
+__global__ void __launch_bounds__(kBlock) prompt_attention_kernel(
+    const float* __restrict__ q, int q_count, const float* __restrict__ keys, const float* __restrict__ values,
+    int k_count, int width, int head_width, int causal, float scale, int splits, int span, float* __restrict__ out,
+    float* __restrict__ partials, unsigned int* __restrict__ counters)
+{
+    __shared__ __attribute__((aligned(16))) float qs[kMaxPromptQueries][kMaxHeadWidth];
+    __shared__ __attribute__((aligned(16))) float ks[kPromptTile][kPromptKeyStride];
+    __shared__ float vs[kPromptTile][kMaxHeadWidth];
+    __shared__ float ps[kMaxPromptQueries][kPromptTile];
+    __shared__ int last_block;
+
+    const int split = blockIdx.x % splits, head = blockIdx.x / splits;
+    const int column = head * head_width;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int first = split * span, end = min(first + span, k_count);
+
+    for (int i = threadIdx.x; i < kMaxPromptQueries * kMaxHeadWidth; i += kBlock)
+    {
+        const int r = i / kMaxHeadWidth, c = i % kMaxHeadWidth;
+        qs[r][c] = r < q_count && c < head_width ? q[(size_t) r * width + column + c] : 0.f;
+    }
+
+    float m[4], l[4], acc[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+    {
+        m[k] = -INFINITY;
+        l[k] = 0.f;
+        acc[k] = 0.f;
+    }
+    for (int t0 = first; t0 < end; t0 += kPromptTile)
+    {
+        const int n = min(kPromptTile, end - t0);
+        __syncthreads(); // the previous tile's readers are done (and the queries are in)
+        for (int i = threadIdx.x; i < kPromptTile * kMaxHeadWidth / 4; i += kBlock)
+        {
+            const int j = i / (kMaxHeadWidth / 4), c4 = 4 * (i % (kMaxHeadWidth / 4));
+            float4v kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+            if (j < n && c4 < head_width)
+            {
+                const size_t at = (size_t) (t0 + j) * width + column + c4;
+                kv = *reinterpret_cast<const float4v*>(keys + at);
+                vv = *reinterpret_cast<const float4v*>(values + at);
+            }
+            *reinterpret_cast<float4v*>(&ks[j][c4]) = kv;
+            *reinterpret_cast<float4v*>(&vs[j][c4]) = vv;
+        }
+        __syncthreads();
+
+        // Scores of key t0 + lane against this wave's four queries.
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < head_width; c += 4)
+        {
+            const float4v kv = *reinterpret_cast<const float4v*>(&ks[lane][c]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                const float4v qv = *reinterpret_cast<const float4v*>(&qs[4 * wave + k][c]);
+                s[k] += (qv[0] * kv[0] + qv[1] * kv[1]) + (qv[2] * kv[2] + qv[3] * kv[3]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            const int query = 4 * wave + k;
+            const int key = t0 + lane;
+            const bool seen = query < q_count && lane < n && (!causal || key <= k_count - q_count + query);
+            const float score = seen ? scale * s[k] : -INFINITY;
+            const float m_new = fmaxf(m[k], wave_max(score));
+            const float alpha = m_new == -INFINITY ? 1.f : expf(m[k] - m_new);
+            const float p = seen ? expf(score - m_new) : 0.f;
+            l[k] = l[k] * alpha + wave_sum(p);
+            acc[k] *= alpha;
+            m[k] = m_new;
+            ps[query][lane] = p;
+        }
+        __syncthreads();
+
+        // Values: lane = channel.
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            float sum = 0.f;
+            for (int j = 0; j < n; ++j)
+                sum += ps[4 * wave + k][j] * vs[j][lane];
+            acc[k] += sum;
+        }
+    }
+
+    if (splits == 1)
+    {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            const int query = 4 * wave + k;
+            if (query < q_count && lane < head_width)
+                out[(size_t) query * width + column + lane] = acc[k] / l[k];
+        }
+        return;
+    }
+
+    float* const head_parts = partials + (size_t) head * splits * kMaxPromptQueries * kPromptPartial;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+    {
+        const int query = 4 * wave + k;
+        float* part = head_parts + ((size_t) split * kMaxPromptQueries + query) * kPromptPartial;
+        if (query < q_count)
+        {
+            if (lane < head_width)
+                part[2 + lane] = acc[k];
+            if (lane == 0)
+            {
+                part[0] = m[k];
+                part[1] = l[k];
+            }
+        }
+    }
+    __threadfence(); // the partial is visible device-wide before the count says so
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last_block = atomicAdd(&counters[head], 1u) == (unsigned) (splits - 1);
+    __syncthreads();
+    if (!last_block)
+        return;
+    __threadfence(); // every other block's partial is visible from here on
+
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+    {
+        const int query = 4 * wave + k;
+        if (query >= q_count)
+            continue;
+        float largest = -INFINITY;
+        for (int sp = 0; sp < splits; ++sp)
+        {
+            const float* part = head_parts + ((size_t) sp * kMaxPromptQueries + query) * kPromptPartial;
+            if (part[1] != 0.f)
+                largest = fmaxf(largest, part[0]);
+        }
+        float numerator = 0.f, denominator = 0.f;
+        for (int sp = 0; sp < splits; ++sp)
+        {
+            const float* part = head_parts + ((size_t) sp * kMaxPromptQueries + query) * kPromptPartial;
+            if (part[1] == 0.f)
+                continue;
+            const float factor = expf(part[0] - largest);
+            numerator += factor * (lane < head_width ? part[2 + lane] : 0.f);
+            denominator += factor * part[1];
+        }
+        if (lane < head_width)
+            out[(size_t) query * width + column + lane] = numerator / denominator;
+    }
+    if (threadIdx.x == 0)
+        counters[head] = 0u; // zero again for the next launch
+}
+
+// ---------------------------------------------------------------------------
 // Argmax (Kernels/Argmax.h:46-262): candidates are (value, index) pairs; a
 // larger value wins and equal values keep the lower index, so the fold ends on
 // the index a left-to-right scan stops at. Suppressed entries never compete;
@@ -572,10 +748,36 @@ int attention_chunks(int heads, int q_count, int k_count)
     return chunks;
 }
 
+// Keys per split of a prompt step's attention: a whole number of 64-key tiles,
+// as few as give about one round of blocks over the chip (256).
+int prompt_attention_span(int heads, int k_count)
+{
+    const int tiles = std::max(1, (k_count + kPromptTile - 1) / kPromptTile);
+    const int wanted = std::max(1, std::min(tiles, (256 + heads - 1) / heads));
+    return (tiles + wanted - 1) / wanted * kPromptTile;
+}
+
+int prompt_attention_splits(int heads, int k_count)
+{
+    const int span = prompt_attention_span(heads, k_count);
+    return std::max(1, (k_count + span - 1) / span);
+}
+
+bool takes_prompt_attention(int q_count, int heads)
+{
+    return q_count >= 2 && q_count <= kMaxPromptQueries && heads <= kAttentionCounters;
+}
+
 size_t attention_workspace_floats(int heads, int q_count, int k_count, int head_width)
 {
+    if (takes_prompt_attention(q_count, heads))
+    {
+        const int splits = prompt_attention_splits(heads, k_count);
+        return kAttentionCounters
+               + (splits > 1 ? (size_t) heads * splits * kMaxPromptQueries * kPromptPartial : 0);
+    }
     const int chunks = attention_chunks(heads, q_count, k_count);
-    return chunks > 1 ? (size_t) heads * q_count * chunks * (head_width + 2) : 0;
+    return kAttentionCounters + (chunks > 1 ? (size_t) heads * q_count * chunks * (head_width + 2) : 0);
 }
 
 hipError_t attention(hipStream_t stream, const float* q, int q_count, const float* keys,
@@ -583,6 +785,17 @@ hipError_t attention(hipStream_t stream, const float* q, int q_count, const floa
                      float scale, float* out, float* workspace)
 {
     const int head_width = width / heads;
+    unsigned int* const counters = reinterpret_cast<unsigned int*>(workspace);
+    float* const partials = workspace + kAttentionCounters;
+    if (takes_prompt_attention(q_count, heads))
+    {
+        const int splits = prompt_attention_splits(heads, k_count);
+        hipLaunchKernelGGL(prompt_attention_kernel, dim3(heads * splits), dim3(kBlock), 0, stream, q, q_count, keys,
+                           values, k_count, width, head_width, causal, scale, splits,
+                           prompt_attention_span(heads, k_count), out, partials, counters);
+        return hipGetLastError();
+    }
+    workspace = partials;
     const int chunks = attention_chunks(heads, q_count, k_count);
     const int chunk_length = (k_count + chunks - 1) / chunks;
     hipLaunchKernelGGL(attention_chunk_kernel, dim3(heads * q_count * chunks), dim3(kBlock), 0, stream,
