@@ -125,4 +125,40 @@ struct DecodingConfig
 
 DecodingConfig decodingConfigFromConfig(const std::string& json);
 DecodingConfig decodingConfigFromConfigFile(const std::string& path);
+
+// The tokens that steer decoding, by name, out of a HuggingFace
+// tokenizer.json's added_tokens (Tokenizer/SpecialTokens.h:16-44,
+// Tokenizer/Tokenizer.cpp:102-138): an entry `<|name|>` fills the field of
+// that name, a two- or three-letter lowercase name is a language, and
+// `<|12.34|>` is a timestamp (the lowest id and its seconds start the run, the
+// interval is the seconds spanned over the ids spanned). -1: absent.
+struct SpecialTokens
+{
+    int endOfText = -1;
+    int startOfTranscript = -1;
+    int startOfPrevious = -1;
+    int startOfLanguageModel = -1;
+    int translate = -1;
+    int transcribe = -1;
+    int noTimestamps = -1;
+    int noSpeech = -1; // <|nospeech|>, or <|nocaptions|> in older vocabularies
+    int firstTimestamp = -1;
+    int timestampCount = 0;
+    float timestampInterval = 0.0f;
+    std::map<std::string, int> languages;
+
+    bool isTimestamp(int token) const;
+    int timestampForSeconds(float seconds) const; // -1 outside the run
+    float secondsForTimestamp(int token) const;   // -1 for a token outside the run
+    int forLanguage(const std::string& code) const;
+};
+
+SpecialTokens specialTokensFromTokenizerJson(const std::string& json);
+SpecialTokens specialTokensFromTokenizerFile(const std::string& path);
+
+// Whisper::buildPrompt (Whisper/Whisper.cpp:202-225): the English-only prompt
+// [start, <|notimestamps|>], the start being config.json's
+// decoder_start_token_id when it names one, else the vocabulary's
+// <|startoftranscript|>. A ModelError when either is missing.
+std::vector<int> transcriptPrompt(const DecodingConfig& config, const SpecialTokens& specials);
 } // namespace WSP

@@ -142,6 +142,38 @@ int wsp_shape_from_config(const char* config_path, int cross_positions, wsp_deco
 int wsp_decoding_from_config(const char* config_path, float* first_mask, float* later_mask, int capacity,
                              int* start_token, int* end_token, char* error, int error_capacity);
 
+/* The special tokens of a HuggingFace tokenizer.json's added_tokens
+ * (WSP::SpecialTokens; Tokenizer/SpecialTokens.h:16-44): -1 where the
+ * vocabulary names none. english is the <|en|> language token. */
+typedef struct wsp_special_tokens
+{
+    int end_of_text;
+    int start_of_transcript;
+    int start_of_previous;
+    int start_of_language_model;
+    int translate;
+    int transcribe;
+    int no_timestamps;
+    int no_speech;
+    int first_timestamp;
+    int timestamp_count;
+    float timestamp_interval;
+    int language_count;
+    int english;
+} wsp_special_tokens;
+
+int wsp_special_tokens_from_file(const char* tokenizer_path, wsp_special_tokens* out, char* error,
+                                 int error_capacity);
+
+/* Whisper::buildPrompt (Whisper/Whisper.cpp:202-225): the English-only
+ * prompt [start, <|notimestamps|>] from a config.json (decoder_start_token_id,
+ * else the vocabulary's <|startoftranscript|>) and a tokenizer.json. Writes up
+ * to `capacity` ids to prompt_out and their count to *count_out; a vocabulary
+ * that names no <|notimestamps|>, or neither file a start token, is refused
+ * with the reason in error. */
+int wsp_prompt_from_files(const char* config_path, const char* tokenizer_path, int* prompt_out, int capacity,
+                          int* count_out, char* error, int error_capacity);
+
 /* wsp_decoder_create / wsp_batch_decoder_create over the tensors of a
  * safetensors file (mapped while the weights upload). */
 int wsp_decoder_create_from_file(const char* path, const wsp_decoder_shape* shape, int packing, int device,

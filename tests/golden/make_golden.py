@@ -163,7 +163,27 @@ def greedy_fixture(name, shape, dtype, seed, encoder_seed, prompt, steps):
         tokens=tokens, margins=margins, last_logits_index=keep, last_logits=hexes(row[keep])))
 
 
+REFERENCE_TOKENIZER_FIXTURE = "/root/reference/Tests/Tokenizer/Fixtures/MiniTokenizer.json"
+
+
+def tokenizer_specials_fixture(name):
+    """The added_tokens of the reference's own tokenizer test fixture
+    (Tests/Tokenizer/Fixtures/MiniTokenizer.json, data its tests load), kept
+    with the values its special-token test asserts
+    (Tests/Tokenizer/TokenizerTests.cpp:400-420)."""
+    with open(REFERENCE_TOKENIZER_FIXTURE) as f:
+        source = json.load(f)
+    write(name, dict(
+        source="Tests/Tokenizer/Fixtures/MiniTokenizer.json (added_tokens only)",
+        added_tokens=[{"id": t["id"], "content": t["content"], "special": t.get("special", True)}
+                      for t in source["added_tokens"]],
+        expected=dict(end_of_text=263, start_of_transcript=264, translate=266, transcribe=267, no_timestamps=268,
+                      english=265, first_timestamp=269, timestamp_count=3)))
+
+
 def main():
+    if os.path.exists(REFERENCE_TOKENIZER_FIXTURE):
+        tokenizer_specials_fixture("mini_tokenizer_specials.json")
     torch.set_default_dtype(torch.float64)
     prompt_fixture("small_shape_prompt_float.json", "Float", "sweep", [5, 17, 3, 11])
     prompt_fixture("small_shape_prompt_packed_half.json", "PackedHalf", "sweep", [5, 17, 3, 11])

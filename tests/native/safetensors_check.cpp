@@ -8,6 +8,7 @@
 //                                       of every floating tensor
 //   safetensors_check config FILE...   decoderShapeFromConfigFile and
 //                                       decodingConfigFromConfigFile (with masks)
+//   safetensors_check tokenizer FILE... specialTokensFromTokenizerFile
 //
 // Prints one line per file: "refused: <message>", "read: <n> tensors, <m>
 // floats" or "config: <width> <heads> ..."; exits 0 unless something other
@@ -53,21 +54,32 @@ void readConfig(const char* path)
                 s.feedForwardWidth, s.vocabularySize, s.maxPositions, s.crossPositions, d.suppressedTokens.size(),
                 d.initiallySuppressedTokens.size());
 }
+void readTokenizer(const char* path)
+{
+    const WSP::SpecialTokens t = WSP::specialTokensFromTokenizerFile(path);
+    std::printf("tokenizer: %d %d %d, %zu languages, %d timestamps\n", t.endOfText, t.startOfTranscript,
+                t.noTimestamps, t.languages.size(), t.timestampCount);
+}
 } // namespace
 
 int main(int argc, char** argv)
 {
-    if (argc < 3 || (std::strcmp(argv[1], "open") != 0 && std::strcmp(argv[1], "config") != 0))
+    if (argc < 3
+        || (std::strcmp(argv[1], "open") != 0 && std::strcmp(argv[1], "config") != 0
+            && std::strcmp(argv[1], "tokenizer") != 0))
     {
-        std::fprintf(stderr, "usage: %s open|config FILE...\n", argv[0]);
+        std::fprintf(stderr, "usage: %s open|config|tokenizer FILE...\n", argv[0]);
         return 2;
     }
     const bool config = std::strcmp(argv[1], "config") == 0;
+    const bool tokenizer = std::strcmp(argv[1], "tokenizer") == 0;
     for (int i = 2; i < argc; ++i)
     {
         try
         {
-            if (config)
+            if (tokenizer)
+                readTokenizer(argv[i]);
+            else if (config)
                 readConfig(argv[i]);
             else
                 openFile(argv[i]);

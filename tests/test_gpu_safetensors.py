@@ -107,16 +107,22 @@ def test_a_file_missing_a_tensor_is_a_model_error_naming_it(tmp_path):
 def test_greedy_from_a_checkpoint_directory_follows_the_config(tmp_path, oracle):
     # The product loop end to end from files: shape, suppression masks, start
     # and end-of-text ids from config.json, weights from model.safetensors, the
-    # prompt [decoder_start_token_id, 2, 3, 4] — against the oracle's greedy
-    # loop under the same masks (first step: suppress_tokens and
+    # prompt [decoder_start_token_id, <|notimestamps|>] from config.json and
+    # tokenizer.json (Whisper::buildPrompt) — against the oracle's greedy loop
+    # under the same masks (first step: suppress_tokens and
     # begin_suppress_tokens; later: suppress_tokens) and the same stop.
     from helpers import oracle_tensors
-    from whispereacp_amd.decoder import Decoder, decoding_from_config, shape_from_config, to_device
+    from whispereacp_amd.decoder import (Decoder, decoding_from_config, prompt_from_files, shape_from_config,
+                                         to_device)
     shape = S.DecoderShape(256, 4, 2, 1024, 4099, 64, 120)
     f = S.workload_decoder_file(shape, "F16", 47)
     enc = S.normal_encoder_output(120, shape.width, 13)
     save(f, tmp_path / "model.safetensors")
-    prompt = [4000, 2, 3, 4]
+    (tmp_path / "tokenizer.json").write_text(json.dumps({"added_tokens": [
+        {"id": 4001, "content": "<|endoftext|>"}, {"id": 4000, "content": "<|startoftranscript|>"},
+        {"id": 4002, "content": "<|en|>"}, {"id": 4050, "content": "<|notimestamps|>"},
+        {"id": 4051, "content": "<|0.00|>"}, {"id": 4052, "content": "<|0.02|>"}]}))
+    prompt = [4000, 4050]
 
     def oracle_run(first_ids, later_ids, end=None, limit=30):
         session = oracle.session(shape, oracle_tensors(f, shape))
@@ -145,8 +151,10 @@ def test_greedy_from_a_checkpoint_directory_follows_the_config(tmp_path, oracle)
     loaded = shape_from_config(str(tmp_path / "config.json"))
     first, later, start, eot = decoding_from_config(str(tmp_path / "config.json"), loaded.vocabulary_size)
     assert (start, eot) == (4000, end)
+    assert prompt_from_files(str(tmp_path / "config.json"), str(tmp_path / "tokenizer.json")) == prompt
     decoder = Decoder(loaded, packing="ExactHalf", path=str(tmp_path / "model.safetensors"))
-    tokens, _ = decoder.greedy(to_device(enc), [start, 2, 3, 4], 30, end_of_text=eot,
-                               first_mask=to_device(first), later_mask=to_device(later))
+    tokens, _ = decoder.greedy(to_device(enc), prompt_from_files(str(tmp_path / "config.json"),
+                                                                 str(tmp_path / "tokenizer.json")), 30,
+                               end_of_text=eot, first_mask=to_device(first), later_mask=to_device(later))
     assert tokens == expected
     assert tokens[0] != free[0] and free[2] not in tokens

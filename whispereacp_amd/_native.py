@@ -60,6 +60,13 @@ class wsp_cross_tensors(ctypes.Structure):
     _fields_ = [("key_w", c_void_p), ("value_w", c_void_p), ("value_b", c_void_p)]
 
 
+class wsp_special_tokens(ctypes.Structure):
+    _fields_ = [(name, c_int) for name in ("end_of_text", "start_of_transcript", "start_of_previous",
+                                           "start_of_language_model", "translate", "transcribe", "no_timestamps",
+                                           "no_speech", "first_timestamp", "timestamp_count")] + [
+        ("timestamp_interval", c_float), ("language_count", c_int), ("english", c_int)]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "wsp_hip_ctx_create": (c_int, [ctypes.POINTER(wsp_decoder_shape), c_int, c_void_p, ctypes.POINTER(c_void_p)]),
@@ -140,6 +147,9 @@ SIGNATURES = {
     "wsp_decoding_from_config": (c_int, [c_char_p, c_void_p, c_void_p, c_int, ctypes.POINTER(c_int),
                                          ctypes.POINTER(c_int), ctypes.c_char_p, c_int]),
     "wsp_shape_from_config": (c_int, [c_char_p, c_int, ctypes.POINTER(wsp_decoder_shape), ctypes.c_char_p, c_int]),
+    "wsp_special_tokens_from_file": (c_int, [c_char_p, ctypes.POINTER(wsp_special_tokens), ctypes.c_char_p, c_int]),
+    "wsp_prompt_from_files": (c_int, [c_char_p, c_char_p, ctypes.POINTER(c_int), c_int, ctypes.POINTER(c_int),
+                                      ctypes.c_char_p, c_int]),
     "wsp_batch_decoder_hidden_states": (c_void_p, [c_void_p]),
 }
 

@@ -1,5 +1,6 @@
-// The safetensors reader and the config.json decoder shape. The JSON reader
-// below takes exactly what these two files use — objects, arrays, strings,
+// The safetensors reader, the config.json decoder shape and decoding fields, and
+// the special tokens of a tokenizer.json. The JSON reader below takes exactly
+// what these files use — objects, arrays, strings,
 // numbers, true/false/null — and remembers whether a number was written as an
 // integer, which the header's shapes and offsets must be.
 #include "../../../include/whispereacp/SafeTensors.h"
@@ -733,6 +734,148 @@ DecodingConfig decodingConfigFromConfig(const std::string& json)
 DecodingConfig decodingConfigFromConfigFile(const std::string& path)
 {
     return decodingConfigFromConfig(readText(path));
+}
+
+namespace
+{
+// The name inside `<|...|>`, or empty.
+std::string specialName(const std::string& content)
+{
+    if (content.size() < 5 || content.compare(0, 2, "<|") != 0 || content.compare(content.size() - 2, 2, "|>") != 0)
+        return {};
+    return content.substr(2, content.size() - 4);
+}
+
+bool languageCode(const std::string& name)
+{
+    if (name.size() != 2 && name.size() != 3)
+        return false;
+    return std::all_of(name.begin(), name.end(), [](char c) { return c >= 'a' && c <= 'z'; });
+}
+
+// "12.34" as seconds: digits, one dot with digits on both sides, nothing else.
+bool timestampSeconds(const std::string& name, float& seconds)
+{
+    const std::size_t dot = name.find('.');
+    if (dot == std::string::npos || dot == 0 || dot + 1 == name.size() || name.find('.', dot + 1) != std::string::npos)
+        return false;
+    if (!std::all_of(name.begin(), name.end(), [](char c) { return c == '.' || (c >= '0' && c <= '9'); }))
+        return false;
+    double whole = 0, fraction = 0, scale = 1;
+    for (std::size_t i = 0; i < dot; ++i)
+        whole = whole * 10 + (name[i] - '0');
+    for (std::size_t i = dot + 1; i < name.size(); ++i)
+    {
+        fraction = fraction * 10 + (name[i] - '0');
+        scale *= 10;
+    }
+    seconds = (float) (whole + fraction / scale);
+    return true;
+}
+} // namespace
+
+bool SpecialTokens::isTimestamp(int token) const
+{
+    return firstTimestamp >= 0 && token >= firstTimestamp && token < firstTimestamp + timestampCount;
+}
+
+int SpecialTokens::timestampForSeconds(float seconds) const
+{
+    if (timestampCount == 0 || timestampInterval <= 0.0f)
+        return -1;
+    const long step = std::lround(seconds / timestampInterval);
+    return step < 0 || step >= timestampCount ? -1 : firstTimestamp + (int) step;
+}
+
+float SpecialTokens::secondsForTimestamp(int token) const
+{
+    return isTimestamp(token) ? (float) (token - firstTimestamp) * timestampInterval : -1.0f;
+}
+
+int SpecialTokens::forLanguage(const std::string& code) const
+{
+    const auto it = languages.find(code);
+    return it == languages.end() ? -1 : it->second;
+}
+
+SpecialTokens specialTokensFromTokenizerJson(const std::string& json)
+{
+    const Json root = JsonReader(json.data(), json.data() + json.size(), "tokenizer.json").document();
+    if (root.kind != Json::Kind::Object)
+        throw ModelError("tokenizer.json is not a JSON object");
+    SpecialTokens t;
+    const Json* added = root.member("added_tokens");
+    if (added == nullptr || added->kind == Json::Kind::Null)
+        return t;
+    if (added->kind != Json::Kind::Array)
+        throw ModelError("tokenizer.json 'added_tokens' is not a list");
+    float firstSeconds = 0.0f, lastSeconds = 0.0f;
+    int lastTimestamp = -1;
+    for (const Json& entry: added->items)
+    {
+        const Json* id = entry.kind == Json::Kind::Object ? entry.member("id") : nullptr;
+        const Json* content = entry.kind == Json::Kind::Object ? entry.member("content") : nullptr;
+        if (id == nullptr || id->kind != Json::Kind::Number || !id->integral || id->integer < 0
+            || id->integer > std::numeric_limits<int>::max())
+            throw ModelError("tokenizer.json has an added token without a token id");
+        if (content == nullptr || content->kind != Json::Kind::String)
+            throw ModelError("tokenizer.json has an added token without its text");
+        const int token = (int) id->integer;
+        const std::string name = specialName(content->text);
+        if (name.empty())
+            continue;
+        float seconds = 0.0f;
+        if (timestampSeconds(name, seconds))
+        {
+            if (t.firstTimestamp < 0 || token < t.firstTimestamp)
+            {
+                t.firstTimestamp = token;
+                firstSeconds = seconds;
+            }
+            if (token > lastTimestamp)
+            {
+                lastTimestamp = token;
+                lastSeconds = seconds;
+            }
+            ++t.timestampCount;
+            continue;
+        }
+        static const std::pair<const char*, int SpecialTokens::*> named[] = {
+            {"endoftext", &SpecialTokens::endOfText},         {"startoftranscript", &SpecialTokens::startOfTranscript},
+            {"startofprev", &SpecialTokens::startOfPrevious}, {"startoflm", &SpecialTokens::startOfLanguageModel},
+            {"translate", &SpecialTokens::translate},         {"transcribe", &SpecialTokens::transcribe},
+            {"notimestamps", &SpecialTokens::noTimestamps},   {"nospeech", &SpecialTokens::noSpeech},
+            {"nocaptions", &SpecialTokens::noSpeech}};
+        bool matched = false;
+        for (const auto& [key, field]: named)
+            if (name == key)
+            {
+                t.*field = token;
+                matched = true;
+            }
+        if (!matched && languageCode(name))
+            t.languages.emplace(name, token);
+    }
+    if (t.timestampCount > 1 && lastTimestamp > t.firstTimestamp)
+        t.timestampInterval = (lastSeconds - firstSeconds) / (float) (lastTimestamp - t.firstTimestamp);
+    return t;
+}
+
+SpecialTokens specialTokensFromTokenizerFile(const std::string& path)
+{
+    return specialTokensFromTokenizerJson(readText(path));
+}
+
+std::vector<int> transcriptPrompt(const DecodingConfig& config, const SpecialTokens& specials)
+{
+    const int start = config.decoderStartToken >= 0 ? config.decoderStartToken : specials.startOfTranscript;
+    if (start < 0)
+        throw ModelError("neither config.json nor tokenizer.json names <|startoftranscript|>");
+    if (specials.noTimestamps < 0)
+        throw ModelError("tokenizer.json names no <|notimestamps|> token");
+    if (config.vocabularySize > 0 && (start >= config.vocabularySize || specials.noTimestamps >= config.vocabularySize))
+        throw ModelError("the prompt's tokens lie outside the vocabulary");
+    return {start, specials.noTimestamps};
 }
 
 void DecodingConfig::suppressionMasks(std::vector<float>& firstStep, std::vector<float>& laterSteps) const

@@ -570,6 +570,64 @@ int wsp_decoding_from_config(const char* config_path, float* first_mask, float* 
     }
 }
 
+namespace
+{
+int reportModelError(const std::exception& e, char* error, int error_capacity)
+{
+    if (error != nullptr && error_capacity > 0)
+    {
+        std::strncpy(error, e.what(), (std::size_t) error_capacity - 1);
+        error[error_capacity - 1] = 0;
+    }
+    return WSP_ERR_SHAPE;
+}
+} // namespace
+
+int wsp_special_tokens_from_file(const char* tokenizer_path, wsp_special_tokens* out, char* error,
+                                 int error_capacity)
+{
+    if (tokenizer_path == nullptr || out == nullptr)
+        return WSP_ERR_ARGUMENT;
+    try
+    {
+        const WSP::SpecialTokens t = WSP::specialTokensFromTokenizerFile(tokenizer_path);
+        *out = wsp_special_tokens {t.endOfText,     t.startOfTranscript,
+                                   t.startOfPrevious, t.startOfLanguageModel,
+                                   t.translate,     t.transcribe,
+                                   t.noTimestamps,  t.noSpeech,
+                                   t.firstTimestamp, t.timestampCount,
+                                   t.timestampInterval, (int) t.languages.size(),
+                                   t.forLanguage("en")};
+        return WSP_OK;
+    }
+    catch (const std::exception& e)
+    {
+        return reportModelError(e, error, error_capacity);
+    }
+}
+
+int wsp_prompt_from_files(const char* config_path, const char* tokenizer_path, int* prompt_out, int capacity,
+                          int* count_out, char* error, int error_capacity)
+{
+    if (config_path == nullptr || tokenizer_path == nullptr || prompt_out == nullptr || count_out == nullptr)
+        return WSP_ERR_ARGUMENT;
+    try
+    {
+        const std::vector<int> prompt = WSP::transcriptPrompt(WSP::decodingConfigFromConfigFile(config_path),
+                                                              WSP::specialTokensFromTokenizerFile(tokenizer_path));
+        *count_out = (int) prompt.size();
+        if ((int) prompt.size() > capacity)
+            throw WSP::ModelError("the prompt holds " + std::to_string(prompt.size()) + " tokens, more than the "
+                                  + std::to_string(capacity) + " the buffer takes");
+        std::copy(prompt.begin(), prompt.end(), prompt_out);
+        return WSP_OK;
+    }
+    catch (const std::exception& e)
+    {
+        return reportModelError(e, error, error_capacity);
+    }
+}
+
 int wsp_shape_from_config(const char* config_path, int cross_positions, wsp_decoder_shape* out, char* error,
                           int error_capacity)
 {

@@ -379,6 +379,30 @@ def decoding_from_config(path: str, vocabulary_size: int):
     return first, later, start.value, end.value
 
 
+def special_tokens_from_file(path: str) -> Dict[str, float]:
+    """WSP::SpecialTokens of a tokenizer.json (its added_tokens), by field
+    name; -1 where the vocabulary names none."""
+    lib = N.load()
+    out = N.wsp_special_tokens()
+    error = ctypes.create_string_buffer(512)
+    if lib.wsp_special_tokens_from_file(path.encode(), ctypes.byref(out), error, 512) != N.WSP_OK:
+        raise ModelError(error.value.decode())
+    return {name: getattr(out, name) for name, _ in N.wsp_special_tokens._fields_}
+
+
+def prompt_from_files(config_path: str, tokenizer_path: str) -> List[int]:
+    """Whisper::buildPrompt: [decoder_start_token_id or <|startoftranscript|>,
+    <|notimestamps|>] from a config.json and a tokenizer.json."""
+    lib = N.load()
+    out = (ctypes.c_int * 8)()
+    count = ctypes.c_int(0)
+    error = ctypes.create_string_buffer(512)
+    if lib.wsp_prompt_from_files(config_path.encode(), tokenizer_path.encode(), out, 8, ctypes.byref(count), error,
+                                 512) != N.WSP_OK:
+        raise ModelError(error.value.decode())
+    return list(out[:count.value])
+
+
 _hip = None
 
 
