@@ -183,7 +183,8 @@ enum Epilogue : int
     kStore = 0,     // y = acc + bias
     kResidual = 1,  // y += acc + bias
     kGeluSplit = 2, // split parts of gelu(acc + bias) into xs_out [parts][rows_padded][out]
-    kQkv = 3        // q | self key row | self value row
+    kQkv = 3,       // q | self key row | self value row
+    kGelu = 4       // y = gelu(acc + bias), fp32
 };
 
 struct Product
@@ -220,6 +221,7 @@ __device__ __forceinline__ void finish(const Product& a, int m, int n, float acc
         case kStore: a.y[(size_t) m * a.ldy + n] = v; break;
         case kResidual: a.y[(size_t) m * a.ldy + n] += v; break;
         case kGeluSplit: store_split<WT>(a.xs_out, a.xs_out_part, (size_t) m * a.out + n, exact_gelu(v)); break;
+        case kGelu: a.y[(size_t) m * a.ldy + n] = exact_gelu(v); break;
         default:
         {
             const int d = a.width;
@@ -494,6 +496,374 @@ __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product
 }
 
 // ---------------------------------------------------------------------------
+// LayerNorm statistics of h from 64-column groups: a residual tile product's
+// epilogue writes, for every 64-column group of a row, the group's mean and
+// its centred sum of squares. A consumer combines the groups in order with
+// Chan's pairwise update (exact algebra, stable in fp32), which gives the
+// row's mean and centred biased variance (Kernels/LayerNorm.h:44-89) without
+// reading the whole row.
+// ---------------------------------------------------------------------------
+constexpr int kGroupColumns = 64;
+
+__device__ __forceinline__ void row_statistics(const float* stats, int groups, int width, float eps, float& mean,
+                                               float& scale)
+{
+    float m = 0.f, m2 = 0.f, count = 0.f;
+    for (int c = 0; c < groups; ++c)
+    {
+        const float nb = (float) min(kGroupColumns, width - c * kGroupColumns);
+        const float mb = stats[2 * c], qb = stats[2 * c + 1];
+        const float total = count + nb;
+        const float delta = mb - m;
+        m += delta * (nb / total);
+        m2 += qb + delta * delta * (count * nb / total);
+        count = total;
+    }
+    mean = m;
+    scale = rsqrtf(m2 / (float) width + eps);
+}
+
+// The final LayerNorm written out as the step's hidden rows (Decoder/
+// Decoder.cpp:174, readable until the next step, Decoder/Decoder.h:111-115).
+__global__ void __launch_bounds__(kNormThreads) hidden_kernel(const float* h, const float* stats, int groups,
+                                                              int width, const float* gamma, const float* beta,
+                                                              float eps, float* out)
+{
+    const int row = blockIdx.x;
+    float mean, scale;
+    row_statistics(stats + (size_t) row * groups * 2, groups, width, eps, mean, scale);
+    for (int c = threadIdx.x; c < width; c += kNormThreads)
+        out[(size_t) row * width + c] = (h[(size_t) row * width + c] - mean) * scale * gamma[c] + beta[c];
+}
+
+// ---------------------------------------------------------------------------
+// Skinny products y[m, n] = Σ_k x[m, k]·W[n, k] + b[n] for up to 128 rows, on
+// the matrix cores (v_mfma_f32_16x16x32: A = activations, lane l row l % 16;
+// B = weights, lane l column l % 16; both with k = 8(l / 16) + j).
+//
+// A block owns 64 output columns (one 16-column tile per wave) and a run of
+// the inner dimension (a split). It stages its rows' fp32 activations for
+// the run into LDS once — LayerNorm applied on the way in when the product
+// has one, each value cut into its exact 16-bit parts — and every wave reads
+// its A fragments from there, so the activations are fetched once per block
+// instead of once per 16 columns. Weight fragments for a batch of k-blocks
+// are loaded before the batch's activations.
+//
+// Splits: when 64-column groups alone leave the chip idle, the inner
+// dimension is cut into `splits` runs. Each block writes its partial tile
+// with device-scope stores, waits for them, and counts itself in on the
+// group's counter; the block that counts last sums the partials in split
+// order (so the result does not depend on which block finishes last), runs
+// the epilogue and sets the counter back to zero for the next launch.
+// ---------------------------------------------------------------------------
+constexpr int kTileColumns = 64;
+constexpr int kTileThreads = 256;
+constexpr int kStageBytes = 64 * 1024; // LDS for a block's split activations
+
+struct Tile
+{
+    const float* x;        // [rows][ldx] fp32 activations
+    int ldx;
+    int rows, inner, out;
+    const void* w;         // [out][inner], 16-bit
+    const float* bias;
+    const float* gamma;    // LayerNorm on the way in when non-null
+    const float* beta;
+    const float* stats_in; // [rows][stat_groups][2]
+    int stat_groups;
+    float eps;
+    int epilogue;
+    float* y;
+    int ldy;
+    float* stats_out;      // kResidual: [rows][out / 64][2]
+    float* q;              // kQkv
+    float* keys;           // stream 0's cache of this layer
+    float* values;
+    size_t stream_stride;
+    const int* state;      // device word: the position of the step's first token
+    int step_tokens, width;
+    int splits, kb_per_split;
+    float* partials;       // [blocks][kTileThreads][columns per thread]
+    unsigned* counters;    // [column groups], zero between launches
+};
+
+// k-blocks (32 inner values) a block stages per batch: what the LDS holds,
+// and at most 10 float4 activation runs per thread in registers.
+template <int P, int MT>
+constexpr int stage_kblocks()
+{
+    constexpr int fit = (kStageBytes - P * MT * 16 * 16) / (P * MT * 16 * 64);
+    constexpr int runs = 20 / MT;
+    constexpr int kb = fit < runs ? fit : runs;
+    return kb < 1 ? 1 : (kb > 10 ? 10 : kb);
+}
+
+template <int WT, int MT>
+__global__ void __launch_bounds__(kTileThreads) tile_kernel(Tile a)
+{
+    constexpr int P = parts_of<WT>();
+    constexpr int R = MT * 16;                // rows held (padding rows are zero)
+    constexpr int KB = stage_kblocks<P, MT>();
+    constexpr int RS = KB * 32 + 8;           // LDS row stride in 16-bit values (16 bytes of padding)
+    constexpr int RUNS = R * KB * 8 / kTileThreads; // float4 runs a thread stages per batch
+    constexpr int TPR = kTileThreads / R;     // epilogue threads per row
+    constexpr int CPT = kTileColumns / TPR;   // columns per epilogue thread
+    static_assert(R * KB * 8 % kTileThreads == 0, "whole runs per thread");
+    __shared__ __attribute__((aligned(16))) u16 xs[P][R][RS];
+    __shared__ float tile[R][kTileColumns + 1];
+    __shared__ float row_mean[R], row_scale[R];
+    __shared__ int last_block;
+
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int li = lane % 16, g = lane / 16;
+    const int cg = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
+    const int n0 = cg * kTileColumns;
+    // The epilogue's row and columns; a residual product reads its h values
+    // now, so the epilogue's read-modify-write waits for nothing.
+    const int m = threadIdx.x / TPR, c0 = (threadIdx.x % TPR) * CPT;
+    const bool row_in = m < a.rows;
+    float resid[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c)
+    {
+        const int n = min(n0 + c0 + c, a.out - 1);
+        resid[c] = a.epilogue == kResidual ? a.y[(size_t) min(m, a.rows - 1) * a.ldy + n] : 0.f;
+    }
+    const int kblocks = a.inner / 32;
+    const int kb_begin = split * a.kb_per_split;
+    const int kb_end = min(kb_begin + a.kb_per_split, kblocks);
+    // Columns past `out` (the last group of a vocabulary) re-read the last
+    // weight row; their sums are never stored.
+    const u16* wrow = static_cast<const u16*>(a.w) + (size_t) min(n0 + 16 * wave + li, a.out - 1) * a.inner + 8 * g;
+
+    if (a.gamma != nullptr)
+    {
+        if (threadIdx.x < R)
+        {
+            float mean = 0.f, scale = 0.f;
+            if ((int) threadIdx.x < a.rows)
+                row_statistics(a.stats_in + (size_t) threadIdx.x * a.stat_groups * 2, a.stat_groups, a.inner, a.eps,
+                               mean, scale);
+            row_mean[threadIdx.x] = mean;
+            row_scale[threadIdx.x] = scale;
+        }
+        __syncthreads();
+    }
+
+    float4v acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+        acc[t] = float4v {0.f, 0.f, 0.f, 0.f};
+
+    u32x4 wv[KB];
+    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += KB)
+    {
+        const int nkb = min(KB, kb_end - kb0);
+#pragma unroll
+        for (int u = 0; u < KB; ++u)
+            wv[u] = *reinterpret_cast<const u32x4*>(wrow + (size_t) (kb0 + min(u, nkb - 1)) * 32);
+        // Stage rows [0, R) x inner [32 kb0, 32 (kb0 + nkb)) as float4 runs:
+        // run i is row i / (KB * 8), run i % (KB * 8) of the row.
+        float4v xv[RUNS];
+#pragma unroll
+        for (int r = 0; r < RUNS; ++r)
+        {
+            const int i = (int) threadIdx.x + r * kTileThreads;
+            const int m = i / (KB * 8), j = i % (KB * 8);
+            xv[r] = float4v {0.f, 0.f, 0.f, 0.f};
+            if (m < a.rows && j < nkb * 8)
+                xv[r] = *reinterpret_cast<const float4v*>(a.x + (size_t) m * a.ldx + kb0 * 32 + 4 * j);
+        }
+#pragma unroll
+        for (int r = 0; r < RUNS; ++r)
+        {
+            const int i = (int) threadIdx.x + r * kTileThreads;
+            const int m = i / (KB * 8), j = i % (KB * 8);
+            float4v v = xv[r];
+            if (a.gamma != nullptr && m < a.rows && j < nkb * 8)
+            {
+                const int k = kb0 * 32 + 4 * j;
+                const float4v gm = *reinterpret_cast<const float4v*>(a.gamma + k);
+                const float4v bt = *reinterpret_cast<const float4v*>(a.beta + k);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    v[e] = (v[e] - row_mean[m]) * row_scale[m] * gm[e] + bt[e];
+            }
+            uint32_t lo[P], hi[P];
+#pragma unroll
+            for (int half = 0; half < 2; ++half)
+            {
+                u16 pa[P], pb[P];
+                split_value<WT>(v[2 * half], pa);
+                split_value<WT>(v[2 * half + 1], pb);
+#pragma unroll
+                for (int p = 0; p < P; ++p)
+                    (half == 0 ? lo : hi)[p] = (uint32_t) pa[p] | ((uint32_t) pb[p] << 16);
+            }
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+                *reinterpret_cast<uint2*>(&xs[p][m][4 * j]) = uint2 {lo[p], hi[p]};
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < KB; ++u)
+            if (u < nkb)
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+#pragma unroll
+                    for (int p = 0; p < P; ++p)
+                        acc[t] = mfma16<WT>(*reinterpret_cast<const u32x4*>(&xs[p][t * 16 + li][u * 32 + 8 * g]),
+                                            wv[u], acc[t]);
+        __syncthreads();
+    }
+
+    // acc[t][r] of lane (g, li) in wave w is C[16 t + 4 g + r][16 w + li].
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            tile[t * 16 + 4 * g + r][16 * wave + li] = acc[t][r];
+    __syncthreads();
+    float v[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c)
+        v[c] = tile[m][c0 + c];
+
+    if (a.splits > 1)
+    {
+        // This split's partial, in the order the reducing thread reads it.
+        uint64_t* mine = reinterpret_cast<uint64_t*>(a.partials + ((size_t) blockIdx.x * kTileThreads + threadIdx.x) * CPT);
+#pragma unroll
+        for (int c = 0; c < CPT; c += 2)
+            __hip_atomic_store(mine + c / 2,
+                               (uint64_t) __float_as_uint(v[c]) | ((uint64_t) __float_as_uint(v[c + 1]) << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0); // the stores are performed before the block counts itself in
+        __syncthreads();
+        if (threadIdx.x == 0)
+        {
+            const unsigned before = __hip_atomic_fetch_add(a.counters + cg, 1u, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = before == (unsigned) a.splits - 1;
+            if (last)
+                __hip_atomic_store(a.counters + cg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_block = last;
+        }
+        __syncthreads();
+        if (!last_block)
+            return;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c)
+            v[c] = 0.f;
+        for (int s0 = 0; s0 < a.splits; s0 += 4)
+        {
+            uint64_t part[4][CPT / 2];
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                if (s0 + s < a.splits)
+                {
+                    const uint64_t* theirs = reinterpret_cast<const uint64_t*>(
+                        a.partials + (((size_t) cg * a.splits + s0 + s) * kTileThreads + threadIdx.x) * CPT);
+#pragma unroll
+                    for (int c = 0; c < CPT / 2; ++c)
+                        part[s][c] = __hip_atomic_load(const_cast<uint64_t*>(theirs) + c, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                if (s0 + s < a.splits)
+#pragma unroll
+                    for (int c = 0; c < CPT / 2; ++c)
+                    {
+                        v[2 * c] += __uint_as_float((uint32_t) part[s][c]);
+                        v[2 * c + 1] += __uint_as_float((uint32_t) (part[s][c] >> 32));
+                    }
+        }
+    }
+
+    // Epilogue: row m, columns n0 + c0 .. + CPT.
+#pragma unroll
+    for (int c = 0; c < CPT; ++c)
+    {
+        const int n = n0 + c0 + c;
+        if (n < a.out)
+            v[c] += a.bias != nullptr ? a.bias[n] : 0.f;
+    }
+    switch (a.epilogue)
+    {
+        case kStore:
+        case kGelu:
+            if (row_in)
+#pragma unroll
+                for (int c = 0; c < CPT; ++c)
+                {
+                    const int n = n0 + c0 + c;
+                    if (n < a.out)
+                        a.y[(size_t) m * a.ldy + n] = a.epilogue == kGelu ? exact_gelu(v[c]) : v[c];
+                }
+            break;
+        case kResidual:
+        {
+            float sum = 0.f;
+#pragma unroll
+            for (int c = 0; c < CPT; ++c)
+            {
+                const int n = n0 + c0 + c;
+                if (row_in && n < a.out)
+                {
+                    v[c] += resid[c];
+                    a.y[(size_t) m * a.ldy + n] = v[c];
+                    sum += v[c];
+                }
+            }
+            // The group's statistics over the TPR threads of the row (lanes
+            // next to each other), every pair added symmetrically.
+#pragma unroll
+            for (int offset = 1; offset < TPR; offset <<= 1)
+                sum += __shfl_xor(sum, offset, TPR);
+            const float count = (float) min(kGroupColumns, a.out - n0);
+            const float mean = sum / count;
+            float m2 = 0.f;
+#pragma unroll
+            for (int c = 0; c < CPT; ++c)
+            {
+                const int n = n0 + c0 + c;
+                if (row_in && n < a.out)
+                    m2 += (v[c] - mean) * (v[c] - mean);
+            }
+#pragma unroll
+            for (int offset = 1; offset < TPR; offset <<= 1)
+                m2 += __shfl_xor(m2, offset, TPR);
+            const int groups = (a.out + kGroupColumns - 1) / kGroupColumns;
+            if (row_in && threadIdx.x % TPR == 0)
+            {
+                a.stats_out[((size_t) m * groups + cg) * 2] = mean;
+                a.stats_out[((size_t) m * groups + cg) * 2 + 1] = m2;
+            }
+            break;
+        }
+        default:
+            if (row_in)
+            {
+                const int d = a.width;
+                const int stream = m / a.step_tokens, i = m % a.step_tokens;
+                const size_t row = (size_t) stream * a.stream_stride + (size_t) (*a.state + i) * d;
+#pragma unroll
+                for (int c = 0; c < CPT; ++c)
+                {
+                    const int n = n0 + c0 + c;
+                    if (n < d)
+                        a.q[(size_t) m * d + n] = v[c];
+                    else if (n < 2 * d)
+                        a.keys[row + (n - d)] = v[c];
+                    else if (n < 3 * d)
+                        a.values[row + (n - 2 * d)] = v[c];
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Split-key attention for (row, head, chunk): the row's query against keys
 // [chunk·len, min((chunk + 1)·len, visible)) of its stream's cache, visible
 // being the causal limit position + i + 1 for self attention (the query at
@@ -739,6 +1109,36 @@ hipError_t launch_norm(hipStream_t stream, const Norm& a, int rows, bool embed)
     return hipGetLastError();
 }
 
+// Splits of the inner dimension for a tile product: eight runs (as measured
+// best for fc2 at the medium and large-v3 shapes), whole k-blocks each.
+void plan_splits(Tile& a, bool can_split)
+{
+    const int kblocks = a.inner / 32;
+    const int splits = can_split ? std::min(8, kblocks) : 1;
+    a.kb_per_split = (kblocks + splits - 1) / splits;
+    a.splits = (kblocks + a.kb_per_split - 1) / a.kb_per_split;
+}
+
+template <int WT, int MT>
+void launch_tile_rows(hipStream_t stream, const Tile& a)
+{
+    const int groups = (a.out + kTileColumns - 1) / kTileColumns;
+    hipLaunchKernelGGL((tile_kernel<WT, MT>), dim3(groups * a.splits), dim3(kTileThreads), 0, stream, a);
+}
+
+template <int WT>
+hipError_t launch_tile(hipStream_t stream, const Tile& a)
+{
+    switch (row_tiles(a.rows))
+    {
+        case 1: launch_tile_rows<WT, 1>(stream, a); break;
+        case 2: launch_tile_rows<WT, 2>(stream, a); break;
+        case 4: launch_tile_rows<WT, 4>(stream, a); break;
+        default: launch_tile_rows<WT, 8>(stream, a); break;
+    }
+    return hipGetLastError();
+}
+
 // Key chunks for `units` (row, head) pairs over k_count keys: about `target`
 // blocks in all, no chunk shorter than one 128-key tile. Cross attention
 // (1500 keys a stream) aims at one full round of resident blocks (blocks per
@@ -790,8 +1190,11 @@ struct wsp_batch
     float* h = nullptr;           // [rows_padded][width] residual stream
     float* q = nullptr;           // [rows_padded][width] queries
     uint16_t* xs = nullptr;       // [parts][rows_padded][width]
-    uint16_t* xs_ff = nullptr;    // [parts][rows_padded][feed_forward]
-    float* partials = nullptr;
+    float* ff = nullptr;          // [rows_padded][feed_forward] gelu(fc1) rows
+    float* stats = nullptr;       // [rows_padded][width / 64][2] LayerNorm statistics of h after fc2
+    float* partials = nullptr;    // attention chunk partials
+    float* tile_partials = nullptr; // split products' partial tiles
+    unsigned* counters = nullptr; // split products' per-group counters (zero between launches)
     float* argmax_values = nullptr;
     uint32_t* argmax_indices = nullptr;
     int* state = nullptr;         // device word: the position of the next step's first token
@@ -893,7 +1296,8 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
     const wsp_decoder_shape& s = b->shape;
     const int d = s.width, f = s.feed_forward_width, H = s.heads, hd = d / H;
     const int rows = b->streams * count;
-    const size_t xs_part = (size_t) b->rows_padded * d, ff_part = (size_t) b->rows_padded * f;
+    const size_t xs_part = (size_t) b->rows_padded * d;
+    const int groups = (d + kGroupColumns - 1) / kGroupColumns;
     const float eps = 1e-5f;
     const float scale = 1.f / std::sqrt((float) hd);
     hipError_t e = hipSuccess;
@@ -918,6 +1322,15 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
     p.x_part = xs_part;
     p.rows = rows;
     p.inner = d;
+
+    Tile tile {};
+    tile.rows = rows;
+    tile.stats_in = b->stats;
+    tile.stat_groups = groups;
+    tile.eps = eps;
+    tile.stats_out = b->stats;
+    tile.partials = b->tile_partials;
+    tile.counters = b->counters;
 
     Attend at {};
     at.q = b->q;
@@ -1031,41 +1444,54 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         p.out = f;
         p.w = L.fc1_w;
         p.bias = L.fc1_b;
-        p.epilogue = kGeluSplit;
-        p.xs_out = b->xs_ff;
-        p.xs_out_part = ff_part;
+        p.epilogue = kGelu;
+        p.y = b->ff;
+        p.ldy = f;
         if ((e = product_after_norm(L.final_norm_w, L.final_norm_b)) != hipSuccess)
             return hip_fail(b, e, "fc1 product");
 
-        p.x = b->xs_ff;
-        p.x_part = ff_part;
-        p.inner = f;
-        p.out = d;
-        p.w = L.fc2_w;
-        p.bias = L.fc2_b;
-        p.epilogue = kResidual;
-        p.y = b->h;
-        if ((e = launch_product<WT>(st, p)) != hipSuccess)
+        // fc2 (inner 4d) as a split tile product: its epilogue also leaves
+        // the LayerNorm statistics of h for the final norm and the logits.
+        Tile t = tile;
+        t.x = b->ff;
+        t.ldx = f;
+        t.inner = f;
+        t.out = d;
+        t.w = L.fc2_w;
+        t.bias = L.fc2_b;
+        t.epilogue = kResidual;
+        t.y = b->h;
+        t.ldy = d;
+        plan_splits(t, true);
+        if ((e = launch_tile<WT>(st, t)) != hipSuccess)
             return hip_fail(b, e, "fc2 product");
     }
 
-    n.gamma = T->final_norm_w;
-    n.beta = T->final_norm_b;
-    n.y = hidden;
-    if ((e = launch_norm<WT>(st, n, rows, false)) != hipSuccess)
-        return hip_fail(b, e, "final norm");
-
-    p.x = b->xs;
-    p.x_part = xs_part;
-    p.inner = d;
-    p.out = s.vocabulary_size;
-    p.w = T->logits_weight;
-    p.bias = nullptr;
-    p.epilogue = kStore;
-    p.y = logits;
-    p.ldy = s.vocabulary_size;
-    if ((e = launch_product<WT>(st, p)) != hipSuccess)
-        return hip_fail(b, e, "logits product");
+    if (hidden != nullptr)
+    {
+        hipLaunchKernelGGL(hidden_kernel, dim3(rows), dim3(kNormThreads), 0, st, b->h, b->stats, groups, d,
+                           T->final_norm_w, T->final_norm_b, eps, hidden);
+        if ((e = hipGetLastError()) != hipSuccess)
+            return hip_fail(b, e, "final norm");
+    }
+    {
+        // The tied logits over the final LayerNorm of h, folded into the tile
+        // product (64 vocabulary rows a block).
+        Tile t = tile;
+        t.x = b->h;
+        t.ldx = d;
+        t.inner = d;
+        t.out = s.vocabulary_size;
+        t.w = T->logits_weight;
+        t.gamma = T->final_norm_w;
+        t.beta = T->final_norm_b;
+        t.epilogue = kStore;
+        t.y = logits;
+        t.ldy = s.vocabulary_size;
+        plan_splits(t, false);
+        if ((e = launch_tile<WT>(st, t)) != hipSuccess)
+            return hip_fail(b, e, "logits product");
+    }
 
     uint32_t* const argmax_out = io.ring != nullptr ? b->next : io.argmax_out;
     if (argmax_out != nullptr)
@@ -1176,6 +1602,8 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
 
     const int P = parts_for(wdtype);
     const size_t d = (size_t) s.width, H = (size_t) s.heads, hd = d / H;
+    const size_t stat_groups = (d + wsp::batch::kGroupColumns - 1) / wsp::batch::kGroupColumns;
+    const size_t split_groups = (d + wsp::batch::kTileColumns - 1) / wsp::batch::kTileColumns; // fc2
     const int most_chunks = std::max((s.cross_positions + wsp::batch::kTileKeys - 1) / wsp::batch::kTileKeys,
                                      (s.max_positions + wsp::batch::kTileKeys - 1) / wsp::batch::kTileKeys);
     const int groups = wsp::ops::argmax_groups(s.vocabulary_size);
@@ -1195,7 +1623,15 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
     if (e == hipSuccess)
         e = allocate(b, &b->xs, (size_t) P * b->rows_padded * d);
     if (e == hipSuccess)
-        e = allocate(b, &b->xs_ff, (size_t) P * b->rows_padded * s.feed_forward_width);
+        e = allocate(b, &b->ff, (size_t) b->rows_padded * s.feed_forward_width);
+    if (e == hipSuccess)
+        e = allocate(b, &b->stats, (size_t) b->rows_padded * stat_groups * 2);
+    if (e == hipSuccess)
+        e = allocate(b, &b->tile_partials, (size_t) 8 * split_groups * b->rows_padded * wsp::batch::kTileColumns);
+    if (e == hipSuccess)
+        e = allocate(b, &b->counters, split_groups);
+    if (e == hipSuccess)
+        e = hipMemsetAsync(b->counters, 0, split_groups * sizeof(unsigned), b->stream);
     if (e == hipSuccess)
         e = allocate(b, &b->partials, (size_t) b->rows_cap * H * most_chunks * (hd + 2));
     if (e == hipSuccess)
@@ -1222,12 +1658,10 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
             && cus > 0 && per_cu > 0)
             b->cross_target = cus * per_cu;
     }
-    // Padding rows of the split buffers are read by the products (their sums
+    // Padding rows of the split buffer are read by the products (their sums
     // are discarded); zero them once so they hold finite values.
     if (e == hipSuccess)
         e = hipMemsetAsync(b->xs, 0, (size_t) P * b->rows_padded * d * sizeof(u16), b->stream);
-    if (e == hipSuccess)
-        e = hipMemsetAsync(b->xs_ff, 0, (size_t) P * b->rows_padded * s.feed_forward_width * sizeof(u16), b->stream);
     if (e == hipSuccess)
         e = hipStreamSynchronize(b->stream);
     if (e != hipSuccess)
