@@ -558,6 +558,7 @@ __global__ void __launch_bounds__(kNormThreads) hidden_kernel(const float* h, co
 // ---------------------------------------------------------------------------
 constexpr int kTileColumns = 64;
 constexpr int kTileThreads = 256;
+constexpr int kMaxSplits = 8;
 constexpr int kStageBytes = 64 * 1024; // LDS for a block's split activations
 
 struct Tile
@@ -585,6 +586,7 @@ struct Tile
     int splits, kb_per_split;
     float* partials;       // [blocks][kTileThreads][columns per thread]
     unsigned* counters;    // [column groups], zero between launches
+    size_t partials_capacity, counters_capacity; // floats and counters the buffers hold
 };
 
 // k-blocks (32 inner values) a block stages per batch: what the LDS holds,
@@ -1114,7 +1116,7 @@ hipError_t launch_norm(hipStream_t stream, const Norm& a, int rows, bool embed)
 void plan_splits(Tile& a, bool can_split)
 {
     const int kblocks = a.inner / 32;
-    const int splits = can_split ? std::min(8, kblocks) : 1;
+    const int splits = can_split ? std::min(kMaxSplits, kblocks) : 1;
     a.kb_per_split = (kblocks + splits - 1) / splits;
     a.splits = (kblocks + a.kb_per_split - 1) / a.kb_per_split;
 }
@@ -1129,6 +1131,16 @@ void launch_tile_rows(hipStream_t stream, const Tile& a)
 template <int WT>
 hipError_t launch_tile(hipStream_t stream, const Tile& a)
 {
+    // A split launch writes 64 x (16 row tiles) partial floats per block and
+    // counts on one counter per column group: refuse it when the buffers are
+    // smaller than that.
+    if (a.splits > 1)
+    {
+        const size_t groups = (size_t) (a.out + kTileColumns - 1) / kTileColumns;
+        const size_t floats = groups * a.splits * kTileColumns * 16 * (size_t) row_tiles(a.rows);
+        if (floats > a.partials_capacity || groups > a.counters_capacity)
+            return hipErrorInvalidValue;
+    }
     switch (row_tiles(a.rows))
     {
         case 1: launch_tile_rows<WT, 1>(stream, a); break;
@@ -1195,6 +1207,7 @@ struct wsp_batch
     float* partials = nullptr;    // attention chunk partials
     float* tile_partials = nullptr; // split products' partial tiles
     unsigned* counters = nullptr; // split products' per-group counters (zero between launches)
+    size_t tile_partials_capacity = 0, counters_capacity = 0; // floats, counters
     float* argmax_values = nullptr;
     uint32_t* argmax_indices = nullptr;
     int* state = nullptr;         // device word: the position of the next step's first token
@@ -1331,6 +1344,8 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
     tile.stats_out = b->stats;
     tile.partials = b->tile_partials;
     tile.counters = b->counters;
+    tile.partials_capacity = b->tile_partials_capacity;
+    tile.counters_capacity = b->counters_capacity;
 
     Attend at {};
     at.q = b->q;
@@ -1626,8 +1641,11 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
         e = allocate(b, &b->ff, (size_t) b->rows_padded * s.feed_forward_width);
     if (e == hipSuccess)
         e = allocate(b, &b->stats, (size_t) b->rows_padded * stat_groups * 2);
+    b->tile_partials_capacity = (size_t) wsp::batch::kMaxSplits * split_groups * b->rows_padded
+                                * wsp::batch::kTileColumns;
+    b->counters_capacity = split_groups;
     if (e == hipSuccess)
-        e = allocate(b, &b->tile_partials, (size_t) 8 * split_groups * b->rows_padded * wsp::batch::kTileColumns);
+        e = allocate(b, &b->tile_partials, b->tile_partials_capacity);
     if (e == hipSuccess)
         e = allocate(b, &b->counters, split_groups);
     if (e == hipSuccess)
