@@ -290,6 +290,79 @@ int wsp_batch_ring_step(wsp_batch* batch, const wsp_decoder_tensors* tensors, ui
 int wsp_batch_self_cache(const wsp_batch* batch, int layer, const float** keys, const float** values);
 int wsp_batch_cross_cache(const wsp_batch* batch, int layer, const float** keys, const float** values);
 
+/* ---------------------------------------------------------------------------
+ * The encoder: the step before the decode path (Encoder/Encoder.h:8-71,
+ * Encoder/Encoder.cpp:82-175). A mel [mel_bins, input_frames] band-major in,
+ * [positions, width] rows out, positions = input_frames / 2 for Whisper's
+ * stride-two second convolution (Encoder/EncoderShape.cpp:19-33).
+ * ------------------------------------------------------------------------- */
+
+/* Encoder/EncoderShape.h:25-67 */
+typedef struct wsp_encoder_shape
+{
+    int mel_bins;
+    int width;
+    int heads;
+    int layers;
+    int feed_forward_width;
+    int input_frames;
+} wsp_encoder_shape;
+
+/* Encoder/EncoderWeights.h:19-36, HuggingFace's model.encoder.layers.<i>.*
+ * tensors: projections in `wdtype` storage, everything else fp32 (the
+ * reference widens every non-projection tensor, Encoder/EncoderWeights.h:44-52).
+ * k_proj has no bias. */
+typedef struct wsp_encoder_layer_tensors
+{
+    const float* attention_norm_w;
+    const float* attention_norm_b;
+    const void* q_w;
+    const float* q_b;
+    const void* k_w;
+    const void* v_w;
+    const float* v_b;
+    const void* out_w;
+    const float* out_b;
+    const float* final_norm_w;
+    const float* final_norm_b;
+    const void* fc1_w;
+    const float* fc1_b;
+    const void* fc2_w;
+    const float* fc2_b;
+} wsp_encoder_layer_tensors;
+
+/* Encoder/EncoderWeights.h:70-93: conv1 [width, mel_bins, 3], conv2 [width,
+ * width, 3] and their biases, embed_positions [>= positions, width] and the
+ * final LayerNorm, all fp32. */
+typedef struct wsp_encoder_tensors
+{
+    int wdtype; /* the projections' storage (WSP_F32, WSP_F16, WSP_BF16) */
+    const float* conv1_w;
+    const float* conv1_b;
+    const float* conv2_w;
+    const float* conv2_b;
+    const float* positions;
+    const float* final_norm_w;
+    const float* final_norm_b;
+    const wsp_encoder_layer_tensors* layers; /* host array, `layers` long */
+} wsp_encoder_tensors;
+
+typedef struct wsp_encoder wsp_encoder;
+
+/* Encoder::prepare (Encoder/Encoder.cpp:113-146): every intermediate sized for
+ * the shape's window, on `device`, ordered on `stream`. */
+int wsp_encoder_create(const wsp_encoder_shape* shape, int device, void* stream, wsp_encoder** out);
+void wsp_encoder_destroy(wsp_encoder* encoder);
+const char* wsp_encoder_last_error(const wsp_encoder* encoder);
+
+/* Encoder::encode (Encoder/Encoder.cpp:148-174): reads the first
+ * min(2 * position_count, input_frames) frames of each band of `mel` (device,
+ * [mel_bins, input_frames]) and writes position_count rows of width floats to
+ * `output` (device); position_count 0 is the whole window. A count past the
+ * window is WSP_ERR_SHAPE before anything is launched. No allocation. */
+int wsp_encoder_encode(wsp_encoder* encoder, const wsp_encoder_tensors* tensors, const float* mel, float* output,
+                       int position_count);
+
 #ifdef __cplusplus
 }
 #endif

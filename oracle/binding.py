@@ -29,6 +29,11 @@ class _Shape(ctypes.Structure):
         "cross_positions")]
 
 
+class _EncoderShape(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "mel_bins", "width", "heads", "layers", "feed_forward_width", "input_frames")]
+
+
 def build_oracle(force: bool = False) -> str:
     """Compile oracle.c with its Makefile (gcc) into oracle/_build/."""
     if force or not os.path.exists(_LIB_PATH):
@@ -76,6 +81,11 @@ class Oracle:
         lib.oracle_session_position.argtypes = [ctypes.c_void_p]
         lib.oracle_greedy.argtypes = [ctypes.c_void_p, _ip, ctypes.c_int, ctypes.c_int, _fp, _ip,
                                       _dp, _dp]
+        lib.oracle_conv1d_output_length.argtypes = [ctypes.c_int, ctypes.c_int]
+        lib.oracle_conv1d_output_length.restype = ctypes.c_int
+        lib.oracle_conv1d.argtypes = [_dp, ctypes.c_int, ctypes.c_int, _fp, _fp, ctypes.c_int, ctypes.c_int,
+                                      _dp]
+        lib.oracle_encode.argtypes = [ctypes.POINTER(_EncoderShape), ctypes.POINTER(_fp), _fp, _dp]
 
     # -- primitives -------------------------------------------------------
     def set_threads(self, threads: int) -> int:
@@ -194,6 +204,38 @@ class Oracle:
 
     def session(self, shape, tensors: Sequence[np.ndarray]) -> "OracleSession":
         return OracleSession(self, shape, tensors)
+
+    # -- the encoder ------------------------------------------------------
+    def conv1d_output_length(self, length: int, stride: int) -> int:
+        return int(self.lib.oracle_conv1d_output_length(length, stride))
+
+    def conv1d(self, x: np.ndarray, weight: np.ndarray, bias: np.ndarray, stride: int) -> np.ndarray:
+        """[in_channels, length] channel-major -> [out_channels, out_length]."""
+        xs = np.ascontiguousarray(x, dtype=np.float64)
+        w = np.ascontiguousarray(weight, dtype=np.float32)
+        b = np.ascontiguousarray(bias, dtype=np.float32)
+        out_channels = w.shape[0]
+        out = np.empty((out_channels, self.conv1d_output_length(xs.shape[1], stride)), dtype=np.float64)
+        self.lib.oracle_conv1d(_ptr(xs, _dp), xs.shape[0], xs.shape[1], _ptr(w, _fp), _ptr(b, _fp),
+                               out_channels, stride, _ptr(out, _dp))
+        return out
+
+    def encode(self, shape, tensors: Sequence[np.ndarray], mel: np.ndarray) -> np.ndarray:
+        """The whole encoder (oracle_encode): ``shape`` has mel_bins, width,
+        heads, layers, feed_forward_width and input_frames; ``tensors`` are in
+        the canonical encoder order; ``mel`` is [mel_bins, input_frames]."""
+        keep = [np.ascontiguousarray(t, dtype=np.float32) for t in tensors]
+        table = (_fp * len(keep))(*[_ptr(t, _fp) for t in keep])
+        m = np.ascontiguousarray(mel, dtype=np.float32)
+        cs = _EncoderShape(shape.mel_bins, shape.width, shape.heads, shape.layers, shape.feed_forward_width,
+                           shape.input_frames)
+        positions = self.conv1d_output_length(self.conv1d_output_length(shape.input_frames, 1), 2)
+        out = np.empty((positions, shape.width), dtype=np.float64)
+        status = self.lib.oracle_encode(ctypes.byref(cs), table, _ptr(m, _fp), _ptr(out, _dp))
+        del keep
+        if status != 0:
+            raise ValueError("oracle_encode refused the inputs")
+        return out
 
 
 class OracleSession:

@@ -630,3 +630,133 @@ int oracle_greedy(oracle_session* s, const int* prompt, int prompt_count, int st
     free(logits);
     return status;
 }
+
+/* ------------------------------------------------------------------------ */
+/* The encoder                                                               */
+/* ------------------------------------------------------------------------ */
+
+int oracle_conv1d_output_length(int input_length, int stride)
+{
+    return (input_length + 2 * 1 - 3) / stride + 1;
+}
+
+/* Tests/Encoder/Common.h:398-441 */
+void oracle_conv1d(const double* input, int input_channels, int input_length,
+                   const float* weight, const float* bias, int output_channels,
+                   int stride, double* out)
+{
+    const int output_length = oracle_conv1d_output_length(input_length, stride);
+    const long long total = (long long) output_channels * output_length;
+
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (g_threads > 1 && total * input_channels > 65536)
+#endif
+    for (long long element = 0; element < total; ++element)
+    {
+        const int channel = (int) (element / output_length);
+        const int frame = (int) (element % output_length);
+        double sum = (double) bias[channel];
+
+        for (int source = 0; source < input_channels; ++source)
+            for (int tap = 0; tap < 3; ++tap)
+            {
+                const int at = frame * stride + tap - 1;
+                if (at < 0 || at >= input_length)
+                    continue;
+                sum += (double) weight[((size_t) channel * input_channels + source) * 3 + tap]
+                       * input[(size_t) source * input_length + at];
+            }
+        out[(size_t) channel * output_length + frame] = sum;
+    }
+}
+
+static const float* encoder_layer_tensor(const float* const* tensors, int layer, int which)
+{
+    return tensors[ORACLE_ENC_MODEL_TENSORS + layer * ORACLE_ENC_TENSORS_PER_LAYER + which];
+}
+
+/* Tests/Encoder/Common.h:596-688 */
+int oracle_encode(const oracle_encoder_shape* shape, const float* const* tensors,
+                  const float* mel, double* out)
+{
+    const int width = shape->width, bins = shape->mel_bins, frames = shape->input_frames;
+    const int f = shape->feed_forward_width;
+    const int conv_frames = oracle_conv1d_output_length(frames, 1);
+    const int positions = oracle_conv1d_output_length(conv_frames, 2);
+    if (width <= 0 || shape->heads <= 0 || width % shape->heads != 0 || positions <= 0)
+        return -1;
+
+    double* input = alloc_doubles((size_t) bins * frames);
+    double* convolved = alloc_doubles((size_t) width * conv_frames);
+    double* projected = alloc_doubles((size_t) width * positions);
+    double* hidden = alloc_doubles((size_t) positions * width);
+    double* normalised = alloc_doubles((size_t) positions * width);
+    double* queries = alloc_doubles((size_t) positions * width);
+    double* keys = alloc_doubles((size_t) positions * width);
+    double* values = alloc_doubles((size_t) positions * width);
+    double* attended = alloc_doubles((size_t) positions * width);
+    double* projection = alloc_doubles((size_t) positions * width);
+    double* feed = alloc_doubles((size_t) positions * f);
+
+    for (size_t i = 0; i < (size_t) bins * frames; ++i)
+        input[i] = mel[i];
+
+    oracle_conv1d(input, bins, frames, tensors[ORACLE_ENC_CONV1_W], tensors[ORACLE_ENC_CONV1_B], width, 1,
+                  convolved);
+    for (size_t i = 0; i < (size_t) width * conv_frames; ++i)
+        convolved[i] = oracle_gelu(convolved[i]);
+    oracle_conv1d(convolved, width, conv_frames, tensors[ORACLE_ENC_CONV2_W], tensors[ORACLE_ENC_CONV2_B], width,
+                  2, projected);
+    for (size_t i = 0; i < (size_t) width * positions; ++i)
+        projected[i] = oracle_gelu(projected[i]);
+
+    /* channel-major out of the convolution, row-major into the transformer */
+    const float* table = tensors[ORACLE_ENC_POSITIONS];
+    for (int p = 0; p < positions; ++p)
+        for (int c = 0; c < width; ++c)
+            hidden[(size_t) p * width + c] = projected[(size_t) c * positions + p] + table[(size_t) p * width + c];
+
+    for (int l = 0; l < shape->layers; ++l)
+    {
+        oracle_layernorm(hidden, positions, width, encoder_layer_tensor(tensors, l, ORACLE_EL_ATTN_NORM_W),
+                         encoder_layer_tensor(tensors, l, ORACLE_EL_ATTN_NORM_B), normalised);
+        oracle_linear(normalised, positions, width, encoder_layer_tensor(tensors, l, ORACLE_EL_Q_W),
+                      encoder_layer_tensor(tensors, l, ORACLE_EL_Q_B), width, queries);
+        oracle_linear(normalised, positions, width, encoder_layer_tensor(tensors, l, ORACLE_EL_K_W), NULL, width,
+                      keys);
+        oracle_linear(normalised, positions, width, encoder_layer_tensor(tensors, l, ORACLE_EL_V_W),
+                      encoder_layer_tensor(tensors, l, ORACLE_EL_V_B), width, values);
+        oracle_attention(queries, positions, 0, keys, values, positions, width, shape->heads, 0, attended);
+        oracle_linear(attended, positions, width, encoder_layer_tensor(tensors, l, ORACLE_EL_O_W),
+                      encoder_layer_tensor(tensors, l, ORACLE_EL_O_B), width, projection);
+        for (size_t i = 0; i < (size_t) positions * width; ++i)
+            hidden[i] += projection[i];
+
+        oracle_layernorm(hidden, positions, width, encoder_layer_tensor(tensors, l, ORACLE_EL_FINAL_NORM_W),
+                         encoder_layer_tensor(tensors, l, ORACLE_EL_FINAL_NORM_B), normalised);
+        oracle_linear(normalised, positions, width, encoder_layer_tensor(tensors, l, ORACLE_EL_FC1_W),
+                      encoder_layer_tensor(tensors, l, ORACLE_EL_FC1_B), f, feed);
+        for (size_t i = 0; i < (size_t) positions * f; ++i)
+            feed[i] = oracle_gelu(feed[i]);
+        oracle_linear(feed, positions, f, encoder_layer_tensor(tensors, l, ORACLE_EL_FC2_W),
+                      encoder_layer_tensor(tensors, l, ORACLE_EL_FC2_B), width, projection);
+        for (size_t i = 0; i < (size_t) positions * width; ++i)
+            hidden[i] += projection[i];
+    }
+
+    oracle_layernorm(hidden, positions, width, tensors[ORACLE_ENC_FINAL_NORM_W], tensors[ORACLE_ENC_FINAL_NORM_B],
+                     out);
+
+    free(input);
+    free(convolved);
+    free(projected);
+    free(hidden);
+    free(normalised);
+    free(queries);
+    free(keys);
+    free(values);
+    free(attended);
+    free(projection);
+    free(feed);
+    return 0;
+}

@@ -31,6 +31,12 @@
  *                          every finite pattern class.
  *   oracle_mt19937_fill    the C++ standard's known answer (10000th draw of a
  *                          5489-seeded engine is 4123659995).
+ *   oracle_conv1d          hand-worked taps (identity kernel, the padded
+ *                          ends, stride two) and torch conv1d in float64.
+ *   oracle_encode          tests/golden fixture from an independent torch
+ *                          float64 encoder (conv1d, gelu, layer_norm,
+ *                          softmax), and the reduced-context property
+ *                          (Tests/Encoder/EncoderTests.cpp:259-304).
  *
  * Tensors are passed as one array of float pointers in the canonical order
  * below (floats are the stored weights widened exactly, as the reference's
@@ -194,6 +200,68 @@ int oracle_session_position(const oracle_session* session);
 int oracle_greedy(oracle_session* session, const int* prompt, int prompt_count,
                   int steps, const float* mask_or_null, int* tokens_out,
                   double* margins_or_null, double* last_logits_or_null);
+
+/* ---- the encoder (the step before the path: Encoder/Encoder.cpp:82-111) ---- */
+
+typedef struct oracle_encoder_shape
+{
+    int mel_bins;
+    int width;
+    int heads;
+    int layers;
+    int feed_forward_width;
+    int input_frames;
+} oracle_encoder_shape;
+
+/* Canonical encoder tensor order: model-level tensors, then
+ * ORACLE_ENC_TENSORS_PER_LAYER per layer (HF names model.encoder.*). */
+enum
+{
+    ORACLE_ENC_CONV1_W = 0, /* [width, mel_bins, 3] */
+    ORACLE_ENC_CONV1_B,     /* [width] */
+    ORACLE_ENC_CONV2_W,     /* [width, width, 3] */
+    ORACLE_ENC_CONV2_B,
+    ORACLE_ENC_POSITIONS,   /* [>= positions, width] */
+    ORACLE_ENC_FINAL_NORM_W,
+    ORACLE_ENC_FINAL_NORM_B,
+    ORACLE_ENC_MODEL_TENSORS
+};
+
+enum
+{
+    ORACLE_EL_ATTN_NORM_W = 0,
+    ORACLE_EL_ATTN_NORM_B,
+    ORACLE_EL_Q_W,
+    ORACLE_EL_Q_B,
+    ORACLE_EL_K_W,
+    ORACLE_EL_V_W,
+    ORACLE_EL_V_B,
+    ORACLE_EL_O_W,
+    ORACLE_EL_O_B,
+    ORACLE_EL_FINAL_NORM_W,
+    ORACLE_EL_FINAL_NORM_B,
+    ORACLE_EL_FC1_W,
+    ORACLE_EL_FC1_B,
+    ORACLE_EL_FC2_W,
+    ORACLE_EL_FC2_B,
+    ORACLE_ENC_TENSORS_PER_LAYER
+};
+
+/* Kernels/Conv1d.h:121-124: (length + 2 padding - kernel) / stride + 1, with
+ * kernel 3 and padding 1 (Encoder/EncoderShape.h:20-23). */
+int oracle_conv1d_output_length(int input_length, int stride);
+
+/* Tests/Encoder/Common.h:398-441: [output_channels, output_length] out of
+ * [input_channels, input_length], both channel-major; weight [output_channels,
+ * input_channels, 3]; padded taps are skipped. */
+void oracle_conv1d(const double* input, int input_channels, int input_length,
+                   const float* weight, const float* bias, int output_channels,
+                   int stride, double* out);
+
+/* Tests/Encoder/Common.h:596-688: the whole encoder over a band-major mel
+ * [mel_bins, input_frames]; out receives [positions, width] row-major. */
+int oracle_encode(const oracle_encoder_shape* shape, const float* const* tensors,
+                  const float* mel, double* out);
 
 #ifdef __cplusplus
 }

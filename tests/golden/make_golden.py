@@ -8,11 +8,17 @@ rather than against itself. Inputs are regenerated from seeds by
 whispereacp_amd.synthetic; each fixture stores a SHA-256 of the stored input
 bytes so a drifting generator is caught rather than silently re-based.
 
-Run: python tests/golden/make_golden.py
+The encoder fixtures (encoder_*.json) come the
+same way from a float64 WhisperEncoder.forward (``F.conv1d``, exact ``F.gelu``,
+``F.layer_norm``, ``torch.softmax``).
+
+Run: python tests/golden/make_golden.py          (every fixture)
+     python tests/golden/make_golden.py encoder  (the encoder fixtures only)
 """
 
 from __future__ import annotations
 
+import dataclasses
 import hashlib
 import json
 import math
@@ -181,7 +187,83 @@ def tokenizer_specials_fixture(name):
                       english=265, first_timestamp=269, timestamp_count=3)))
 
 
+def torch_encode(shape: S.EncoderShape, encoder_file, mel: np.ndarray):
+    """WhisperEncoder.forward in float64 from torch library ops (conv1d with
+    padding 1, exact gelu, layer_norm, softmax), over the first
+    shape.input_frames frames of ``mel``."""
+    W = {n: torch.from_numpy(t.floats().astype(np.float64)) for n, t in encoder_file.items()}
+    d, H = shape.width, shape.heads
+    D = d // H
+    x = torch.from_numpy(mel[:, :shape.input_frames].astype(np.float64))[None]
+    x = F.gelu(F.conv1d(x, W["model.encoder.conv1.weight"], W["model.encoder.conv1.bias"], stride=1, padding=1))
+    x = F.gelu(F.conv1d(x, W["model.encoder.conv2.weight"], W["model.encoder.conv2.bias"], stride=2, padding=1))
+    h = x[0].T + W["model.encoder.embed_positions.weight"][:x.shape[2]]
+    P = h.shape[0]
+
+    def ln(v, prefix):
+        return F.layer_norm(v, (d,), W[prefix + ".weight"], W[prefix + ".bias"], eps=EPS)
+
+    for layer in range(shape.layers):
+        p = lambda s: S.encoder_layer_name(layer, s)  # noqa: E731
+        n = ln(h, p("self_attn_layer_norm"))
+        q = (n @ W[p("self_attn.q_proj.weight")].T + W[p("self_attn.q_proj.bias")]).view(P, H, D).transpose(0, 1)
+        k = (n @ W[p("self_attn.k_proj.weight")].T).view(P, H, D).transpose(0, 1)
+        v = (n @ W[p("self_attn.v_proj.weight")].T + W[p("self_attn.v_proj.bias")]).view(P, H, D).transpose(0, 1)
+        probs = torch.softmax(torch.matmul(q, k.transpose(1, 2)) * (1.0 / math.sqrt(D)), dim=-1)
+        a = torch.matmul(probs, v).transpose(0, 1).reshape(P, d)
+        h = h + a @ W[p("self_attn.out_proj.weight")].T + W[p("self_attn.out_proj.bias")]
+        n = ln(h, p("final_layer_norm"))
+        g = F.gelu(n @ W[p("fc1.weight")].T + W[p("fc1.bias")])
+        h = h + g @ W[p("fc2.weight")].T + W[p("fc2.bias")]
+    return ln(h, "model.encoder.layer_norm").numpy()
+
+
+def encoder_digest(encoder_file, names, mel: np.ndarray) -> str:
+    h = hashlib.sha256()
+    for name in names:
+        t = encoder_file[name]
+        h.update(name.encode())
+        h.update(t.dtype.encode())
+        h.update(np.ascontiguousarray(t.data).tobytes())
+    h.update(np.ascontiguousarray(mel, dtype=np.float32).tobytes())
+    return h.hexdigest()
+
+
+def encoder_fixture(name, shape, kind, storage_or_dtype, seed=0, positions=0):
+    """The reference test-suite's small encoder (kind "reference-fixture") or
+    a workload-style one; ``positions`` runs a reduced context as the
+    reference's reducedContextMatchesTheShorterShape does: the expected rows
+    are the shorter shape's own encode over the mel's first frames."""
+    if kind == "reference-fixture":
+        encoder_file = S.synthetic_encoder_file(shape, storage_or_dtype)
+        mel = S.synthetic_mel(shape)
+    else:
+        encoder_file = S.workload_encoder_file(shape, storage_or_dtype, seed)
+        mel = S.normal_mel(shape, seed + 500)
+    run = shape.with_frames(shape.frames_for_positions(positions)) if positions else shape
+    rows = torch_encode(run, encoder_file, mel)
+    write(name, dict(
+        shape=dataclasses.asdict(shape), weights=dict(kind=kind, storage=storage_or_dtype, seed=seed),
+        positions=positions, input_sha256=encoder_digest(encoder_file, S.encoder_canonical_names(shape.layers), mel),
+        rows=hexes(rows)))
+
+
+def encoder_fixtures():
+    small = S.small_encoder_shape()
+    encoder_fixture("encoder_small_float.json", small, "reference-fixture", "Float")
+    encoder_fixture("encoder_small_packed_half.json", small, "reference-fixture", "PackedHalf")
+    encoder_fixture("encoder_small_all_half.json", small, "reference-fixture", "EveryTensorHalf")
+    encoder_fixture("encoder_small_reduced.json", small, "reference-fixture", "Float", positions=3)
+    # Whisper's 80 mel bins and head width 64 at a reduced width and window.
+    mid = S.EncoderShape(80, 128, 2, 2, 512, 64)
+    encoder_fixture("encoder_mid_f16.json", mid, "workload", "F16", seed=3000)
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "encoder":
+        torch.set_default_dtype(torch.float64)
+        encoder_fixtures()
+        return
     if os.path.exists(REFERENCE_TOKENIZER_FIXTURE):
         tokenizer_specials_fixture("mini_tokenizer_specials.json")
     torch.set_default_dtype(torch.float64)
@@ -206,6 +288,7 @@ def main():
     w = S.WORKLOADS["tiny.en"]
     greedy_fixture("tiny_en_greedy.json", S.workload_shape("tiny.en"), w["dtype"], w["seed"], 7,
                    S.SOT_PREFIX[w["vocab"]], w["steps"] + 1)
+    encoder_fixtures()
 
 
 if __name__ == "__main__":

@@ -60,6 +60,22 @@ class wsp_cross_tensors(ctypes.Structure):
     _fields_ = [("key_w", c_void_p), ("value_w", c_void_p), ("value_b", c_void_p)]
 
 
+class wsp_encoder_shape(ctypes.Structure):
+    _fields_ = [(n, c_int) for n in ("mel_bins", "width", "heads", "layers", "feed_forward_width", "input_frames")]
+
+
+class wsp_encoder_layer_tensors(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in (
+        "attention_norm_w", "attention_norm_b", "q_w", "q_b", "k_w", "v_w", "v_b", "out_w", "out_b",
+        "final_norm_w", "final_norm_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b")]
+
+
+class wsp_encoder_tensors(ctypes.Structure):
+    _fields_ = [("wdtype", c_int)] + [(n, c_void_p) for n in (
+        "conv1_w", "conv1_b", "conv2_w", "conv2_b", "positions", "final_norm_w", "final_norm_b")] + [
+        ("layers", ctypes.POINTER(wsp_encoder_layer_tensors))]
+
+
 class wsp_special_tokens(ctypes.Structure):
     _fields_ = [(name, c_int) for name in ("end_of_text", "start_of_transcript", "start_of_previous",
                                            "start_of_language_model", "translate", "transcribe", "no_timestamps",
@@ -151,6 +167,10 @@ SIGNATURES = {
     "wsp_prompt_from_files": (c_int, [c_char_p, c_char_p, ctypes.POINTER(c_int), c_int, ctypes.POINTER(c_int),
                                       ctypes.c_char_p, c_int]),
     "wsp_batch_decoder_hidden_states": (c_void_p, [c_void_p]),
+    "wsp_encoder_create": (c_int, [ctypes.POINTER(wsp_encoder_shape), c_int, c_void_p, ctypes.POINTER(c_void_p)]),
+    "wsp_encoder_destroy": (None, [c_void_p]),
+    "wsp_encoder_last_error": (c_char_p, [c_void_p]),
+    "wsp_encoder_encode": (c_int, [c_void_p, ctypes.POINTER(wsp_encoder_tensors), c_void_p, c_void_p, c_int]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -362,3 +362,203 @@ def synthetic_encoder_output(shape: DecoderShape) -> np.ndarray:
 def normal_encoder_output(rows: int, width: int, seed: int) -> np.ndarray:
     """[rows, width] float32 N(0, 1) encoder states."""
     return normal_values(rows * width, seed, 1.0).reshape(rows, width)
+
+
+# ---------------------------------------------------------------------------
+# The encoder (the step before the decode path)
+# ---------------------------------------------------------------------------
+
+def conv_length(length: int, stride: int) -> int:
+    """Kernels/Conv1d.h:121-124 with kernel 3 and padding 1."""
+    return (length + 2 - 3) // stride + 1
+
+
+@dataclasses.dataclass(frozen=True)
+class EncoderShape:
+    """Encoder/EncoderShape.h:25-67."""
+
+    mel_bins: int
+    width: int
+    heads: int
+    layers: int
+    feed_forward_width: int
+    input_frames: int
+
+    @property
+    def head_width(self) -> int:
+        return self.width // self.heads
+
+    def convolution_frames(self, frames: Optional[int] = None) -> int:
+        return conv_length(self.input_frames if frames is None else frames, 1)
+
+    def positions(self, frames: Optional[int] = None) -> int:
+        return conv_length(self.convolution_frames(frames), 2)
+
+    def frames_for_positions(self, count: int) -> int:
+        """Encoder/EncoderShape.cpp:35-38."""
+        return min(2 * count, self.input_frames)
+
+    def attention_scale(self) -> float:
+        return float(np.float32(1.0) / np.sqrt(np.float32(self.head_width)))
+
+    def with_frames(self, frames: int) -> "EncoderShape":
+        return dataclasses.replace(self, input_frames=frames)
+
+
+def small_encoder_shape() -> EncoderShape:
+    """Tests/Encoder/EncoderTests.cpp:15-24: no two extents equal."""
+    return EncoderShape(6, 8, 2, 2, 16, 12)
+
+
+ENCODER_WORKLOADS = {
+    # name: (mel bins, width, heads, layers) of the public checkpoints' encoders; ffn = 4 width, 3000 frames
+    "tiny.en": (80, 384, 6, 4),
+    "base.en": (80, 512, 8, 6),
+    "small": (80, 768, 12, 12),
+    "medium": (80, 1024, 16, 24),
+    "large-v3": (128, 1280, 20, 32),
+}
+
+
+def encoder_workload_shape(name: str, frames: int = 3000) -> EncoderShape:
+    bins, width, heads, layers = ENCODER_WORKLOADS[name]
+    return EncoderShape(bins, width, heads, layers, 4 * width, frames)
+
+
+ENCODER_MODEL_NAMES = [
+    "model.encoder.conv1.weight", "model.encoder.conv1.bias",
+    "model.encoder.conv2.weight", "model.encoder.conv2.bias",
+    "model.encoder.embed_positions.weight",
+    "model.encoder.layer_norm.weight", "model.encoder.layer_norm.bias",
+]
+
+ENCODER_LAYER_SUFFIXES = [
+    "self_attn_layer_norm.weight", "self_attn_layer_norm.bias",
+    "self_attn.q_proj.weight", "self_attn.q_proj.bias",
+    "self_attn.k_proj.weight",
+    "self_attn.v_proj.weight", "self_attn.v_proj.bias",
+    "self_attn.out_proj.weight", "self_attn.out_proj.bias",
+    "final_layer_norm.weight", "final_layer_norm.bias",
+    "fc1.weight", "fc1.bias", "fc2.weight", "fc2.bias",
+]
+
+
+def encoder_layer_name(index: int, suffix: str) -> str:
+    return f"model.encoder.layers.{index}.{suffix}"
+
+
+def encoder_canonical_names(layers: int) -> List[str]:
+    """Model tensors, then the 15 per-layer tensors: the oracle's order."""
+    names = list(ENCODER_MODEL_NAMES)
+    for layer in range(layers):
+        names += [encoder_layer_name(layer, s) for s in ENCODER_LAYER_SUFFIXES]
+    return names
+
+
+def encoder_tensor_extents(shape: EncoderShape, name: str, table_rows: Optional[int] = None) -> Tuple[int, ...]:
+    d, f = shape.width, shape.feed_forward_width
+    if name.endswith("conv1.weight"):
+        return (d, shape.mel_bins, 3)
+    if name.endswith("conv2.weight"):
+        return (d, d, 3)
+    if name.endswith("embed_positions.weight"):
+        return (table_rows if table_rows is not None else shape.positions(), d)
+    if name.endswith("fc1.weight"):
+        return (f, d)
+    if name.endswith("fc1.bias"):
+        return (f,)
+    if name.endswith("fc2.weight"):
+        return (d, f)
+    if name.endswith("proj.weight"):
+        return (d, d)
+    return (d,)
+
+
+def synthetic_encoder_file(shape: EncoderShape, storage: str = "Float") -> DecoderFile:
+    """Tests/Encoder/Common.h:205-302: seeds count up from 1000 in file order;
+    convolutions +-0.4, positions +-0.3, projections +-0.5, biases +-0.2,
+    LayerNorm gamma 1 +- 0.2. ``storage`` is "Float", "PackedHalf" or
+    "EveryTensorHalf" as in the decoder file."""
+    seed = [1000]
+    out: DecoderFile = {}
+
+    def nxt(count, value_range):
+        v = spread_values(count, seed[0], value_range)
+        seed[0] += 1
+        return v
+
+    def shifted(count, value_range):
+        v = shifted_values(count, seed[0], value_range)
+        seed[0] += 1
+        return v
+
+    def add(name, values, projection=False):
+        extents = encoder_tensor_extents(shape, name)
+        half = storage == "EveryTensorHalf" or (projection and storage != "Float")
+        dtype = "F16" if half else "F32"
+        out[name] = StoredTensor(name, dtype, extents, store(values, dtype))
+
+    d, f, bins = shape.width, shape.feed_forward_width, shape.mel_bins
+    add(ENCODER_MODEL_NAMES[0], nxt(d * bins * 3, 0.4))
+    add(ENCODER_MODEL_NAMES[1], nxt(d, 0.2))
+    add(ENCODER_MODEL_NAMES[2], nxt(d * d * 3, 0.4))
+    add(ENCODER_MODEL_NAMES[3], nxt(d, 0.2))
+    add(ENCODER_MODEL_NAMES[4], nxt(shape.positions() * d, 0.3))
+    for layer in range(shape.layers):
+        n = lambda suffix: encoder_layer_name(layer, suffix)  # noqa: E731
+        add(n("self_attn_layer_norm.weight"), shifted(d, 0.2))
+        add(n("self_attn_layer_norm.bias"), nxt(d, 0.2))
+        add(n("self_attn.q_proj.weight"), nxt(d * d, 0.5), True)
+        add(n("self_attn.q_proj.bias"), nxt(d, 0.2))
+        add(n("self_attn.k_proj.weight"), nxt(d * d, 0.5), True)
+        add(n("self_attn.v_proj.weight"), nxt(d * d, 0.5), True)
+        add(n("self_attn.v_proj.bias"), nxt(d, 0.2))
+        add(n("self_attn.out_proj.weight"), nxt(d * d, 0.5), True)
+        add(n("self_attn.out_proj.bias"), nxt(d, 0.2))
+        add(n("final_layer_norm.weight"), shifted(d, 0.2))
+        add(n("final_layer_norm.bias"), nxt(d, 0.2))
+        add(n("fc1.weight"), nxt(f * d, 0.5), True)
+        add(n("fc1.bias"), nxt(f, 0.2))
+        add(n("fc2.weight"), nxt(d * f, 0.5), True)
+        add(n("fc2.bias"), nxt(d, 0.2))
+    add(ENCODER_MODEL_NAMES[5], shifted(d, 0.2))
+    add(ENCODER_MODEL_NAMES[6], nxt(d, 0.2))
+    return out
+
+
+def synthetic_mel(shape: EncoderShape) -> np.ndarray:
+    """Tests/Encoder/Common.h:749-765: [mel_bins, input_frames] in about [-1.5, 1.5]."""
+    band = np.arange(shape.mel_bins, dtype=np.float64)[:, None]
+    frame = np.arange(shape.input_frames, dtype=np.float64)[None, :]
+    phase = 0.11 * band + 0.037 * frame
+    return (np.sin(phase) + 0.5 * np.cos(2.3 * phase)).astype(np.float32)
+
+
+def workload_encoder_file(shape: EncoderShape, dtype: str, base_seed: int = 3000) -> DecoderFile:
+    """Benchmark encoder weights: N(0, 0.02) convolutions, projections, biases
+    and positions (1500 rows), LayerNorm gamma 1 and beta 0; projections in
+    ``dtype``, everything else F32 (as the reference widens them). Tensor i in
+    canonical order gets seed base_seed + i."""
+    names = encoder_canonical_names(shape.layers)
+
+    def make(index: int, name: str) -> StoredTensor:
+        extents = encoder_tensor_extents(shape, name)
+        count = int(np.prod(extents))
+        if is_norm_weight(name):
+            values = np.ones(count, dtype=np.float32)
+        elif is_norm_bias(name):
+            values = np.zeros(count, dtype=np.float32)
+        else:
+            values = normal_values(count, base_seed + index, 0.02)
+        stored = dtype if is_projection(name) else "F32"
+        return StoredTensor(name, stored, extents, store(values, stored))
+
+    with concurrent.futures.ThreadPoolExecutor(max_workers=4) as pool:
+        tensors = list(pool.map(make, range(len(names)), names))
+    return {t.name: t for t in tensors}
+
+
+def normal_mel(shape: EncoderShape, seed: int) -> np.ndarray:
+    """A [mel_bins, input_frames] log-mel-sized input: N(0, 0.5) clipped to [-1.5, 1.5]."""
+    values = normal_values(shape.mel_bins * shape.input_frames, seed, 0.5)
+    return np.clip(values, -1.5, 1.5).reshape(shape.mel_bins, shape.input_frames)
