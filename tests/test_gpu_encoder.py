@@ -85,11 +85,13 @@ def test_short_positional_table_is_a_model_error():
         EncoderWeights(shape.with_frames(40), encoder_file)
 
 
-@pytest.mark.parametrize("dtype", ["F16", "BF16", "F32"])
-def test_whisper_width_encoder_matches_oracle(oracle, dtype):
-    # 80 mel bins, head width 64, 32 positions: the projections (more than 16
-    # rows) take the matrix-core product for 16-bit weights.
-    shape = S.EncoderShape(80, 128, 2, 2, 512, 64)
+@pytest.mark.parametrize("dtype,frames", [("F16", 64), ("BF16", 64), ("F32", 64), ("F16", 74), ("BF16", 27)])
+def test_whisper_width_encoder_matches_oracle(oracle, dtype, frames):
+    # 80 mel bins and head width 64: the projections (more than 16 rows) take
+    # the matrix-core product for 16-bit weights, and the attention the
+    # matrix-core flash kernel — over 32 positions, and over 37 and 14, which
+    # leave part-filled query blocks and key tiles.
+    shape = S.EncoderShape(80, 128, 2, 2, 512, frames)
     encoder_file = S.workload_encoder_file(shape, dtype, 3000)
     mel = S.normal_mel(shape, 3500)
     got = gpu_rows(shape, encoder_file, mel)

@@ -33,6 +33,7 @@ namespace wsp::encoder
 namespace
 {
 constexpr int kColumnThreads = 256;
+constexpr int kFlashWaves = 4; // queries per attention block: 16 per wave
 
 // Kernels/Conv1d.h:121-124 with kernel 3 and padding 1.
 int conv_length(int length, int stride)
@@ -53,6 +54,207 @@ __global__ void __launch_bounds__(kColumnThreads) mel_columns_kernel(const float
     {
         const int s = i / 3, at = t + i % 3 - 1;
         columns[(size_t) t * inner + i] = at >= 0 && at < frames ? mel[(size_t) s * stride + at] : 0.f;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Self attention of the encoder (Tests/Encoder/Common.h:547-594: every query
+// sees every key, softmax(scale q.k) v per head) for head width 64, on the
+// matrix cores, one pass over the keys with an online softmax.
+//
+// A block takes 16 queries per wave of one head; key tiles of 32 rows of K
+// and V go through LDS once for all its waves. Every fp32 operand is cut
+// into fp16 parts, hi = fp16(x) and lo = fp16(x - hi), and a product takes
+// the three terms hi·hi + hi·lo + lo·hi (v_mfma_f32_16x16x32_f16, fp32
+// accumulation): what is dropped, lo·lo, is about 2^-22 of the product, so
+// the sums stay at fp32 rather than fp16 accuracy.
+//
+// Layout: the wave computes S^T = K·Q^T, so lane (g, l) holds the scores of
+// keys 4g..4g+3 and 16+4g..16+4g+3 of the tile for query l — exactly the B
+// operand of O^T = V^T·P^T once the tile's key order inside the 32-key
+// k-block is taken as (4g..4g+3, 16+4g..16+4g+3) for both operands, so P
+// never leaves its registers. V is staged transposed for that A operand.
+// Scores are in base-2 units (scale·log2 e folded in); each new tile
+// rescales the running row by exp2(m_old - m_new) (exact online softmax).
+// ---------------------------------------------------------------------------
+constexpr int kFlashKeys = 32;
+constexpr int kFlashWidth = 64;
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ _Float16 half_hi(float x)
+{
+    return (_Float16) x;
+}
+
+__device__ __forceinline__ _Float16 half_lo(float x)
+{
+    return (_Float16) (x - (float) (_Float16) x);
+}
+
+__device__ __forceinline__ f32x4 mfma3(const f16x8& ah, const f16x8& al, const f16x8& bh, const f16x8& bl, f32x4 c)
+{
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
+}
+
+template <int WAVES>
+__global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float* __restrict__ q,
+                                                                    const float* __restrict__ k,
+                                                                    const float* __restrict__ v, int count,
+                                                                    int width, float scale2, float* __restrict__ out)
+{
+    constexpr int kThreadsHere = WAVES * 64;
+    constexpr int kUnits = kFlashKeys * kFlashWidth / 4; // float4 runs of a K (or V) tile
+    constexpr int kPerThread = (kUnits + kThreadsHere - 1) / kThreadsHere;
+    __shared__ __attribute__((aligned(16))) _Float16 ks[2][kFlashKeys][kFlashWidth + 8];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][kFlashWidth][kFlashKeys + 8];
+
+    const int head = blockIdx.y;
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, li = lane % 16, g = lane / 16;
+    const int column = head * kFlashWidth;
+    const int query = blockIdx.x * 16 * WAVES + 16 * wave + li;
+    const bool query_in = query < count;
+
+    // This lane's B fragments of Q^T: query `query`, dims 32 s + 8 g .. + 7.
+    f16x8 qh[2], ql[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+    {
+        const float* src = q + (size_t) min(query, count - 1) * width + column + 32 * s + 8 * g;
+        const f32x4 a = *reinterpret_cast<const f32x4*>(src);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+        {
+            qh[s][e] = half_hi(a[e]);
+            ql[s][e] = half_lo(a[e]);
+            qh[s][4 + e] = half_hi(b[e]);
+            ql[s][4 + e] = half_lo(b[e]);
+        }
+    }
+
+    float m = -INFINITY, l = 0.f;
+    f32x4 o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        o[t] = f32x4 {0.f, 0.f, 0.f, 0.f};
+
+    // The next tile's K and V runs, loaded while the current one is used.
+    f32x4 kn[kPerThread], vn[kPerThread];
+    auto load_tile = [&](int first) {
+#pragma unroll
+        for (int i = 0; i < kPerThread; ++i)
+        {
+            const int unit = (int) threadIdx.x + i * kThreadsHere;
+            const int key = first + (unit % kUnits) / 16, d4 = 4 * (unit % 16);
+            const size_t at = (size_t) min(key, count - 1) * width + column + d4;
+            kn[i] = *reinterpret_cast<const f32x4*>(k + at);
+            vn[i] = *reinterpret_cast<const f32x4*>(v + at);
+        }
+    };
+    load_tile(0);
+
+    for (int first = 0; first < count; first += kFlashKeys)
+    {
+        __syncthreads(); // the previous tile has been read
+#pragma unroll
+        for (int i = 0; i < kPerThread; ++i)
+        {
+            const int unit = (int) threadIdx.x + i * kThreadsHere;
+            if (unit < kUnits)
+            {
+                const int row = unit / 16, d4 = 4 * (unit % 16);
+                const bool in = first + row < count;
+                f16x4 kh, kl;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                {
+                    const float kv = in ? kn[i][e] : 0.f, vv = in ? vn[i][e] : 0.f;
+                    kh[e] = half_hi(kv);
+                    kl[e] = half_lo(kv);
+                    vt[0][d4 + e][row] = half_hi(vv);
+                    vt[1][d4 + e][row] = half_lo(vv);
+                }
+                *reinterpret_cast<f16x4*>(&ks[0][row][d4]) = kh;
+                *reinterpret_cast<f16x4*>(&ks[1][row][d4]) = kl;
+            }
+        }
+        __syncthreads();
+        if (first + kFlashKeys < count)
+            load_tile(first + kFlashKeys);
+
+        // S^T for keys 16 mt + 4 g + r of the tile, query li.
+        f32x4 st[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+        {
+            st[mt] = f32x4 {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+            {
+                const f16x8 kh = *reinterpret_cast<const f16x8*>(&ks[0][16 * mt + li][32 * s + 8 * g]);
+                const f16x8 kl = *reinterpret_cast<const f16x8*>(&ks[1][16 * mt + li][32 * s + 8 * g]);
+                st[mt] = mfma3(kh, kl, qh[s], ql[s], st[mt]);
+            }
+        }
+        float x[8];
+        float tile_max = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+            {
+                const int key = first + 16 * mt + 4 * g + r;
+                x[4 * mt + r] = key < count ? st[mt][r] * scale2 : -INFINITY;
+                tile_max = fmaxf(tile_max, x[4 * mt + r]);
+            }
+        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
+        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+        const float m_new = fmaxf(m, tile_max);
+        const float alpha = exp2f(m - m_new);
+        float p[8], own = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+        {
+            p[j] = exp2f(x[j] - m_new);
+            own += p[j];
+        }
+        l = l * alpha + own;
+        m = m_new;
+        f16x8 ph, pl;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+        {
+            ph[j] = half_hi(p[j]);
+            pl[j] = half_lo(p[j]);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+        {
+            o[t] *= alpha;
+            const f16x4 a0 = *reinterpret_cast<const f16x4*>(&vt[0][16 * t + li][4 * g]);
+            const f16x4 a1 = *reinterpret_cast<const f16x4*>(&vt[0][16 * t + li][16 + 4 * g]);
+            const f16x4 b0 = *reinterpret_cast<const f16x4*>(&vt[1][16 * t + li][4 * g]);
+            const f16x4 b1 = *reinterpret_cast<const f16x4*>(&vt[1][16 * t + li][16 + 4 * g]);
+            const f16x8 vh = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+            const f16x8 vl = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+            o[t] = mfma3(vh, vl, ph, pl, o[t]);
+        }
+    }
+    // The row sum over the four lanes of query li, then O = O^T / l.
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (query_in)
+    {
+        const float inv = 1.f / l;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                out[(size_t) query * width + column + 16 * t + 4 * g + r] = o[t][r] * inv;
     }
 }
 
@@ -247,8 +449,18 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
             || (status = ops::linear(st, e->normed, positions, d, L.k_w, wt, nullptr, e->k, d, 0)) != hipSuccess
             || (status = ops::linear(st, e->normed, positions, d, L.v_w, wt, L.v_b, e->v, d, 0)) != hipSuccess)
             return encoder_hip(e, status, "self-attention projections");
-        if ((status = ops::attention(st, e->q, positions, e->k, e->v, positions, d, heads, 0, scale, e->att,
-                                     e->workspace)) != hipSuccess)
+        if (d / heads == kFlashWidth && d % 4 == 0)
+        {
+            hipLaunchKernelGGL(flash_attention_kernel<kFlashWaves>, dim3((positions + 16 * kFlashWaves - 1)
+                                                                            / (16 * kFlashWaves), heads),
+                               dim3(64 * kFlashWaves), 0, st, e->q, e->k, e->v, positions, d,
+                               scale * 1.44269504088896340736f, e->att);
+            status = hipGetLastError();
+        }
+        else
+            status = ops::attention(st, e->q, positions, e->k, e->v, positions, d, heads, 0, scale, e->att,
+                                    e->workspace);
+        if (status != hipSuccess)
             return encoder_hip(e, status, "self attention");
         if ((status = ops::linear(st, e->att, positions, d, L.out_w, wt, L.out_b, e->hidden, d, 2)) != hipSuccess)
             return encoder_hip(e, status, "attention output");
