@@ -363,6 +363,34 @@ const char* wsp_encoder_last_error(const wsp_encoder* encoder);
 int wsp_encoder_encode(wsp_encoder* encoder, const wsp_encoder_tensors* tensors, const float* mel, float* output,
                        int position_count);
 
+/* ---------------------------------------------------------------------------
+ * The mel front end (Mel/MelSpectrogram.h:12-25, Mel/MelShape.h:16-30): 30 s
+ * of 16 kHz samples in, the [mel_count, frame_count] normalised log-mel the
+ * encoder reads out. The filterbank ([mel_count, fft_length / 2 + 1],
+ * preprocessor_config.json's matrix) is an argument of every call, as in the
+ * reference.
+ * ------------------------------------------------------------------------- */
+typedef struct wsp_mel_shape
+{
+    int sample_count; /* 480000 */
+    int fft_length;   /* 400 */
+    int hop_length;   /* 160 */
+    int frame_count;  /* 3000 */
+    int mel_count;    /* 80 */
+} wsp_mel_shape;
+
+typedef struct wsp_mel wsp_mel;
+
+/* MelSpectrogram::prepare: the window, the DFT basis and every intermediate. */
+int wsp_mel_create(const wsp_mel_shape* shape, int device, void* stream, wsp_mel** out);
+void wsp_mel_destroy(wsp_mel* mel);
+const char* wsp_mel_last_error(const wsp_mel* mel);
+
+/* MelSpectrogram::encode: samples [sample_count], filters [mel_count,
+ * fft_length / 2 + 1] and output [mel_count, frame_count], all device
+ * memory. No allocation. */
+int wsp_mel_encode(wsp_mel* mel, const float* samples, const float* filters, float* output);
+
 #ifdef __cplusplus
 }
 #endif

@@ -86,6 +86,8 @@ class Oracle:
         lib.oracle_conv1d.argtypes = [_dp, ctypes.c_int, ctypes.c_int, _fp, _fp, ctypes.c_int, ctypes.c_int,
                                       _dp]
         lib.oracle_encode.argtypes = [ctypes.POINTER(_EncoderShape), ctypes.POINTER(_fp), _fp, _dp]
+        lib.oracle_mel_spectrogram.argtypes = [_fp, ctypes.c_int, _fp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_int, _dp]
 
     # -- primitives -------------------------------------------------------
     def set_threads(self, threads: int) -> int:
@@ -218,6 +220,18 @@ class Oracle:
         out = np.empty((out_channels, self.conv1d_output_length(xs.shape[1], stride)), dtype=np.float64)
         self.lib.oracle_conv1d(_ptr(xs, _dp), xs.shape[0], xs.shape[1], _ptr(w, _fp), _ptr(b, _fp),
                                out_channels, stride, _ptr(out, _dp))
+        return out
+
+    def mel_spectrogram(self, samples: np.ndarray, filters: np.ndarray, fft_length: int, hop_length: int,
+                        frame_count: int) -> np.ndarray:
+        """[mel_count, frame_count] normalised log-mel (oracle_mel_spectrogram)."""
+        x = np.ascontiguousarray(samples, dtype=np.float32)
+        f = np.ascontiguousarray(filters, dtype=np.float32)
+        out = np.empty((f.shape[0], frame_count), dtype=np.float64)
+        status = self.lib.oracle_mel_spectrogram(_ptr(x, _fp), x.shape[0], _ptr(f, _fp), fft_length, hop_length,
+                                                 frame_count, f.shape[0], _ptr(out, _dp))
+        if status != 0:
+            raise ValueError("oracle_mel_spectrogram refused the inputs")
         return out
 
     def encode(self, shape, tensors: Sequence[np.ndarray], mel: np.ndarray) -> np.ndarray:

@@ -760,3 +760,67 @@ int oracle_encode(const oracle_encoder_shape* shape, const float* const* tensors
     free(feed);
     return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* The mel front end (Tests/Mel/ScalarMel.h:14-134)                          */
+/* ------------------------------------------------------------------------ */
+
+int oracle_mel_spectrogram(const float* samples, int sample_count, const float* filters, int fft_length,
+                           int hop_length, int frame_count, int mel_count, double* out)
+{
+    const int pad = fft_length / 2, bins = fft_length / 2 + 1;
+    if (sample_count <= pad || fft_length <= 0 || hop_length <= 0 || frame_count <= 0 || mel_count <= 0)
+        return -1;
+    const double two_pi = 2.0 * 3.14159265358979323846;
+    double* window = alloc_doubles((size_t) fft_length);
+    double* padded = alloc_doubles((size_t) sample_count + 2 * (size_t) pad);
+    double* power = alloc_doubles((size_t) frame_count * bins);
+
+    for (int n = 0; n < fft_length; ++n)
+        window[n] = 0.5 * (1.0 - cos(two_pi * n / fft_length));
+    /* numpy "reflect": mirrors about the first and last sample, neither repeated */
+    for (int i = 0; i < pad; ++i)
+        padded[i] = samples[pad - i];
+    for (int i = 0; i < sample_count; ++i)
+        padded[pad + i] = samples[i];
+    for (int i = 0; i < pad; ++i)
+        padded[pad + sample_count + i] = samples[sample_count - 2 - i];
+
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (g_threads > 1)
+#endif
+    for (int frame = 0; frame < frame_count; ++frame)
+        for (int bin = 0; bin < bins; ++bin)
+        {
+            double re = 0.0, im = 0.0;
+            for (int tap = 0; tap < fft_length; ++tap)
+            {
+                const double a = padded[(size_t) frame * hop_length + tap] * window[tap];
+                const double angle = two_pi * bin * tap / fft_length;
+                re += a * cos(angle);
+                im -= a * sin(angle);
+            }
+            power[(size_t) frame * bins + bin] = re * re + im * im;
+        }
+
+    double peak = -INFINITY;
+    for (int band = 0; band < mel_count; ++band)
+        for (int frame = 0; frame < frame_count; ++frame)
+        {
+            double total = 0.0;
+            for (int bin = 0; bin < bins; ++bin)
+                total += (double) filters[(size_t) band * bins + bin] * power[(size_t) frame * bins + bin];
+            const double v = log10(total > 1e-10 ? total : 1e-10);
+            out[(size_t) band * frame_count + frame] = v;
+            peak = v > peak ? v : peak;
+        }
+    for (size_t i = 0; i < (size_t) mel_count * frame_count; ++i)
+    {
+        const double v = out[i] > peak - 8.0 ? out[i] : peak - 8.0;
+        out[i] = (v + 4.0) / 4.0;
+    }
+    free(window);
+    free(padded);
+    free(power);
+    return 0;
+}

@@ -33,6 +33,8 @@
  *                          5489-seeded engine is 4123659995).
  *   oracle_conv1d          hand-worked taps (identity kernel, the padded
  *                          ends, stride two) and torch conv1d in float64.
+ *   oracle_mel_spectrogram numpy rfft power spectrum, the librosa-style log
+ *                          and clamp written independently in the test.
  *   oracle_encode          tests/golden fixture from an independent torch
  *                          float64 encoder (conv1d, gelu, layer_norm,
  *                          softmax), and the reduced-context property
@@ -262,6 +264,16 @@ void oracle_conv1d(const double* input, int input_channels, int input_length,
  * [mel_bins, input_frames]; out receives [positions, width] row-major. */
 int oracle_encode(const oracle_encoder_shape* shape, const float* const* tensors,
                   const float* mel, double* out);
+
+/* ---- the mel front end (Mel/MelSpectrogram.h:12-25) ---- */
+
+/* Tests/Mel/ScalarMel.h:14-134: periodic Hann window, numpy-"reflect" padding
+ * of fft_length / 2 each side, |DFT|^2 of every hop_length-th window (the
+ * textbook sum), the [mel_count, bin_count] filterbank, log10(max(x, 1e-10)),
+ * then (max(v, peak - 8) + 4) / 4 over the whole spectrogram. out receives
+ * [mel_count, frame_count] (band-major). */
+int oracle_mel_spectrogram(const float* samples, int sample_count, const float* filters, int fft_length,
+                           int hop_length, int frame_count, int mel_count, double* out);
 
 #ifdef __cplusplus
 }

@@ -76,6 +76,10 @@ class wsp_encoder_tensors(ctypes.Structure):
         ("layers", ctypes.POINTER(wsp_encoder_layer_tensors))]
 
 
+class wsp_mel_shape(ctypes.Structure):
+    _fields_ = [(n, c_int) for n in ("sample_count", "fft_length", "hop_length", "frame_count", "mel_count")]
+
+
 class wsp_special_tokens(ctypes.Structure):
     _fields_ = [(name, c_int) for name in ("end_of_text", "start_of_transcript", "start_of_previous",
                                            "start_of_language_model", "translate", "transcribe", "no_timestamps",
@@ -171,6 +175,10 @@ SIGNATURES = {
     "wsp_encoder_destroy": (None, [c_void_p]),
     "wsp_encoder_last_error": (c_char_p, [c_void_p]),
     "wsp_encoder_encode": (c_int, [c_void_p, ctypes.POINTER(wsp_encoder_tensors), c_void_p, c_void_p, c_int]),
+    "wsp_mel_create": (c_int, [ctypes.POINTER(wsp_mel_shape), c_int, c_void_p, ctypes.POINTER(c_void_p)]),
+    "wsp_mel_destroy": (None, [c_void_p]),
+    "wsp_mel_last_error": (c_char_p, [c_void_p]),
+    "wsp_mel_encode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

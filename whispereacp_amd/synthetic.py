@@ -562,3 +562,52 @@ def normal_mel(shape: EncoderShape, seed: int) -> np.ndarray:
     """A [mel_bins, input_frames] log-mel-sized input: N(0, 0.5) clipped to [-1.5, 1.5]."""
     values = normal_values(shape.mel_bins * shape.input_frames, seed, 0.5)
     return np.clip(values, -1.5, 1.5).reshape(shape.mel_bins, shape.input_frames)
+
+
+# ---------------------------------------------------------------------------
+# The mel front end's inputs
+# ---------------------------------------------------------------------------
+
+@dataclasses.dataclass(frozen=True)
+class MelShape:
+    """Mel/MelShape.h:16-30: Whisper's 30 s of 16 kHz audio, 400-point
+    windows every 160 samples, 3000 frames, 80 bands by default."""
+
+    sample_count: int = 480000
+    fft_length: int = 400
+    hop_length: int = 160
+    frame_count: int = 3000
+    mel_count: int = 80
+
+    @property
+    def bin_count(self) -> int:
+        return self.fft_length // 2 + 1
+
+
+def reduced_mel_shape() -> MelShape:
+    """Tests/Mel/MelSpectrogramTests.cpp:27-36."""
+    return MelShape(3200, 64, 16, 200, 12)
+
+
+def tone_and_noise(sample_count: int) -> np.ndarray:
+    """Tests/Mel/MelTestSupport.h:47-66: two tones and a 32-bit LCG's noise,
+    with no exact spectral null."""
+    state = np.empty(sample_count, dtype=np.uint64)
+    s = 12345
+    for i in range(sample_count):
+        s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
+        state[i] = s
+    noise = (state >> np.uint64(8)).astype(np.float64) / float(1 << 24) - 0.5
+    phase = 2.0 * math.pi * np.arange(sample_count, dtype=np.float64)
+    return (0.6 * np.sin(phase * 440.0 / 16000) + 0.3 * np.sin(phase * 1237.0 / 16000) + 0.1 * noise).astype(
+        np.float32)
+
+
+def triangular_filters(mel_count: int, bin_count: int) -> np.ndarray:
+    """Tests/Mel/MelTestSupport.h:70-88: overlapping triangles shaped like the
+    published filterbank."""
+    span = (bin_count - 1) / (mel_count + 1)
+    bins = np.arange(bin_count, dtype=np.float64)[None, :]
+    centre = span * (np.arange(mel_count, dtype=np.float64)[:, None] + 1)
+    distance = np.abs(bins - centre) / span
+    return np.where(distance < 1.0, 1.0 - distance, 0.0).astype(np.float32)
