@@ -174,6 +174,30 @@ int wsp_special_tokens_from_file(const char* tokenizer_path, wsp_special_tokens*
 int wsp_prompt_from_files(const char* config_path, const char* tokenizer_path, int* prompt_out, int capacity,
                           int* count_out, char* error, int error_capacity);
 
+/* ---- the tokenizer (Tokenizer/Tokenizer.h:27-80) --------------------------
+ * Whisper's byte-level BPE from a tokenizer.json: host code. Every added token
+ * is special (skipped by decode unless keep_special). Errors are negative
+ * codes with the reason in `error` (open) or WSP_ERR_CAPACITY when an output
+ * does not fit, with the needed count or length still reported. */
+typedef struct wsp_tokenizer wsp_tokenizer;
+
+int wsp_tokenizer_open(const char* path, wsp_tokenizer** out, char* error, int error_capacity);
+int wsp_tokenizer_open_bytes(const char* json, size_t length, wsp_tokenizer** out, char* error, int error_capacity);
+void wsp_tokenizer_close(wsp_tokenizer* tokenizer);
+int wsp_tokenizer_size(const wsp_tokenizer* tokenizer);
+int wsp_tokenizer_is_special(const wsp_tokenizer* tokenizer, int token);
+/* The id of a token spelled `text` in the vocabulary's printable alphabet
+ * (e.g. "\xc4\xa0the"), or -1. */
+int wsp_tokenizer_token_for_text(const wsp_tokenizer* tokenizer, const char* text, size_t length);
+/* Tokenizer::encode: UTF-8 (or any bytes) in, ids out; *count_out is the full
+ * count even when it exceeds capacity. */
+int wsp_tokenizer_encode(const wsp_tokenizer* tokenizer, const char* text, size_t length, int* ids_out, int capacity,
+                         int* count_out);
+/* Tokenizer::decode / decodeKeepingSpecialTokens: the bytes and a NUL in
+ * text_out; *length_out is the byte count without the NUL. */
+int wsp_tokenizer_decode(const wsp_tokenizer* tokenizer, const int* ids, int count, int keep_special, char* text_out,
+                         int capacity, int* length_out);
+
 /* wsp_decoder_create / wsp_batch_decoder_create over the tensors of a
  * safetensors file (mapped while the weights upload). */
 int wsp_decoder_create_from_file(const char* path, const wsp_decoder_shape* shape, int packing, int device,

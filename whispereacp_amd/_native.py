@@ -179,6 +179,17 @@ SIGNATURES = {
     "wsp_mel_destroy": (None, [c_void_p]),
     "wsp_mel_last_error": (c_char_p, [c_void_p]),
     "wsp_mel_encode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    "wsp_tokenizer_open": (c_int, [c_char_p, ctypes.POINTER(c_void_p), ctypes.c_char_p, c_int]),
+    "wsp_tokenizer_open_bytes": (c_int, [c_char_p, ctypes.c_size_t, ctypes.POINTER(c_void_p), ctypes.c_char_p,
+                                         c_int]),
+    "wsp_tokenizer_close": (None, [c_void_p]),
+    "wsp_tokenizer_size": (c_int, [c_void_p]),
+    "wsp_tokenizer_is_special": (c_int, [c_void_p, c_int]),
+    "wsp_tokenizer_token_for_text": (c_int, [c_void_p, c_char_p, ctypes.c_size_t]),
+    "wsp_tokenizer_encode": (c_int, [c_void_p, c_char_p, ctypes.c_size_t, ctypes.POINTER(c_int), c_int,
+                                     ctypes.POINTER(c_int)]),
+    "wsp_tokenizer_decode": (c_int, [c_void_p, ctypes.POINTER(c_int), c_int, c_int, ctypes.c_char_p, c_int,
+                                     ctypes.POINTER(c_int)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

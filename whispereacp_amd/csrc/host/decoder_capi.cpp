@@ -7,6 +7,7 @@
 #include "../../../include/whispereacp/Decoder.h"
 #include "../../../include/whispereacp/GreedyDecoder.h"
 #include "../../../include/whispereacp/SafeTensors.h"
+#include "../../../include/whispereacp/Tokenizer.h"
 
 #include <algorithm>
 #include <cstring>
@@ -647,6 +648,102 @@ int wsp_shape_from_config(const char* config_path, int cross_positions, wsp_deco
         }
         return WSP_ERR_SHAPE;
     }
+}
+
+} // extern "C"
+
+// ---------------------------------------------------------------------------
+// The tokenizer
+// ---------------------------------------------------------------------------
+struct wsp_tokenizer
+{
+    WSP::Tokenizer tokenizer;
+};
+
+extern "C" {
+
+int wsp_tokenizer_open_bytes(const char* json, size_t length, wsp_tokenizer** out, char* error, int error_capacity)
+{
+    if (json == nullptr || out == nullptr)
+        return WSP_ERR_ARGUMENT;
+    *out = nullptr;
+    try
+    {
+        *out = new wsp_tokenizer {WSP::Tokenizer::fromJsonText(std::string_view(json, length))};
+        return WSP_OK;
+    }
+    catch (const std::exception& e)
+    {
+        return reportModelError(e, error, error_capacity);
+    }
+}
+
+int wsp_tokenizer_open(const char* path, wsp_tokenizer** out, char* error, int error_capacity)
+{
+    if (path == nullptr || out == nullptr)
+        return WSP_ERR_ARGUMENT;
+    *out = nullptr;
+    try
+    {
+        *out = new wsp_tokenizer {WSP::Tokenizer::fromFile(path)};
+        return WSP_OK;
+    }
+    catch (const std::exception& e)
+    {
+        return reportModelError(e, error, error_capacity);
+    }
+}
+
+void wsp_tokenizer_close(wsp_tokenizer* t)
+{
+    delete t;
+}
+
+int wsp_tokenizer_size(const wsp_tokenizer* t)
+{
+    return t == nullptr ? WSP_ERR_ARGUMENT : t->tokenizer.size();
+}
+
+int wsp_tokenizer_is_special(const wsp_tokenizer* t, int token)
+{
+    return t != nullptr && t->tokenizer.isSpecial(token) ? 1 : 0;
+}
+
+int wsp_tokenizer_token_for_text(const wsp_tokenizer* t, const char* text, size_t length)
+{
+    if (t == nullptr || text == nullptr)
+        return WSP::invalidTokenId;
+    return t->tokenizer.tokenForText(std::string_view(text, length));
+}
+
+int wsp_tokenizer_encode(const wsp_tokenizer* t, const char* text, size_t length, int* ids_out, int capacity,
+                         int* count_out)
+{
+    if (t == nullptr || (text == nullptr && length > 0) || count_out == nullptr || capacity < 0
+        || (ids_out == nullptr && capacity > 0))
+        return WSP_ERR_ARGUMENT;
+    const std::vector<int> ids = t->tokenizer.encode(std::string_view(text == nullptr ? "" : text, length));
+    *count_out = (int) ids.size();
+    if ((int) ids.size() > capacity)
+        return WSP_ERR_CAPACITY;
+    std::copy(ids.begin(), ids.end(), ids_out);
+    return WSP_OK;
+}
+
+int wsp_tokenizer_decode(const wsp_tokenizer* t, const int* ids, int count, int keep_special, char* text_out,
+                         int capacity, int* length_out)
+{
+    if (t == nullptr || (ids == nullptr && count > 0) || count < 0 || length_out == nullptr || text_out == nullptr
+        || capacity <= 0)
+        return WSP_ERR_ARGUMENT;
+    const std::string text = keep_special ? t->tokenizer.decodeKeepingSpecialTokens(ids, count)
+                                          : t->tokenizer.decode(ids, count);
+    *length_out = (int) text.size();
+    if ((int) text.size() >= capacity)
+        return WSP_ERR_CAPACITY;
+    std::memcpy(text_out, text.data(), text.size());
+    text_out[text.size()] = 0;
+    return WSP_OK;
 }
 
 } // extern "C"
