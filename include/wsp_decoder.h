@@ -234,6 +234,53 @@ int wsp_batch_decoder_ring_step(wsp_batch_decoder* decoder, uint32_t* ring, floa
 int wsp_batch_decoder_position(const wsp_batch_decoder* decoder);
 const float* wsp_batch_decoder_hidden_states(const wsp_batch_decoder* decoder);
 
+/* ---- Whisper end to end (Whisper/Whisper.h:144-560, the kernels backend) --
+ * load parses config.json, preprocessor_config.json and tokenizer.json and
+ * maps model.safetensors (no GPU work); it builds the prompt and the two
+ * suppression masks. prepare uploads everything and sizes every
+ * intermediate on `device`, ordered on `stream`; transcribe allocates
+ * nothing. Errors are statuses with the reason in wsp_whisper_last_error:
+ * WSP_ERR_SHAPE for a ModelError, WSP_ERR_CAPACITY for an output that does
+ * not fit (the needed count still reported), WSP_ERR_LOGIC for a misuse. */
+typedef struct wsp_whisper wsp_whisper;
+
+int wsp_whisper_create(wsp_whisper** out);
+void wsp_whisper_destroy(wsp_whisper* whisper);
+const char* wsp_whisper_last_error(const wsp_whisper* whisper);
+int wsp_whisper_last_error_kind(const wsp_whisper* whisper);
+/* Whisper::load(directory): a missing file is refused naming it. */
+int wsp_whisper_load(wsp_whisper* whisper, const char* model_directory);
+/* Whisper::load(ModelFiles): the three JSON documents as NUL-terminated text
+ * and the weights as a safetensors file path. */
+int wsp_whisper_load_files(wsp_whisper* whisper, const char* config_json, const char* preprocessor_json,
+                           const char* tokenizer_json, const char* weights_path);
+/* Whisper::setPacksWeights, before prepare (1 = fp16 wherever exact, the default). */
+int wsp_whisper_set_packs_weights(wsp_whisper* whisper, int pack);
+int wsp_whisper_prepare(wsp_whisper* whisper, int device, void* stream);
+/* Whisper::prompt(): up to `capacity` ids; *count_out is the full count. */
+int wsp_whisper_prompt(wsp_whisper* whisper, int* tokens_out, int capacity, int* count_out);
+/* firstStepMask() / laterStepMask(): vocabulary_size floats each (host),
+ * nonzero = suppressed; either pointer may be null. */
+int wsp_whisper_masks(wsp_whisper* whisper, float* first_mask, float* later_mask, int capacity);
+int wsp_whisper_end_of_text(wsp_whisper* whisper, int* token_out);
+int wsp_whisper_set_maximum_tokens(wsp_whisper* whisper, int count);
+int wsp_whisper_maximum_tokens(wsp_whisper* whisper, int* count_out);
+/* Whisper::setAudioContext: 0 (the whole window) or 1..positions. */
+int wsp_whisper_set_audio_context(wsp_whisper* whisper, int positions);
+int wsp_whisper_audio_context_for_samples(wsp_whisper* whisper, int sample_count, double margin_seconds,
+                                          int* positions_out);
+/* Whisper::transcribe: at most one window of samples (host memory), the
+ * transcript's tokens (end-of-text excluded) to tokens_out. */
+int wsp_whisper_transcribe(wsp_whisper* whisper, const float* samples, int sample_count, int* tokens_out,
+                           int capacity, int* count_out);
+/* Whisper::textForTokens: the bytes and a NUL in text_out. */
+int wsp_whisper_text_for_tokens(wsp_whisper* whisper, const int* tokens, int count, char* text_out, int capacity,
+                                int* length_out);
+/* lastEncodeSeconds, lastDecodeSeconds, lastStepCount; any pointer may be null. */
+int wsp_whisper_timing(wsp_whisper* whisper, double* encode_seconds, double* decode_seconds, int* steps);
+/* The last run's encoded rows (device, [positions, width]). */
+int wsp_whisper_encoded_rows(wsp_whisper* whisper, const float** rows_out, int* positions_out, int* width_out);
+
 #ifdef __cplusplus
 }
 #endif

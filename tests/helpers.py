@@ -159,3 +159,75 @@ def check_run(gpu_tokens, gpu_rows, ref_tokens, ref_rows, relative_bar, mask=Non
     assert rel <= relative_bar, rel
     assert worst <= WORST, worst
     return rel, worst
+
+
+# ---------------------------------------------------------------------------
+# a whole Whisper directory at reduced shapes, and the oracle's transcript
+# ---------------------------------------------------------------------------
+
+# The reduced mel of Tests/Mel/MelSpectrogramTests.cpp:27-36 (3200 samples,
+# 64-point frames every 16, 200 frames, 12 bands) in front of a 128-wide,
+# two-head encoder (head width 64, so the flash kernel runs) and a decoder
+# over the 272-token fixture vocabulary (tests/golden/mini_tokenizer.json).
+WHISPER_MEL = S.reduced_mel_shape()
+WHISPER_ENCODER = S.EncoderShape(12, 128, 2, 2, 256, 200)
+WHISPER_DECODER = S.DecoderShape(128, 2, 2, 256, 272, 32, 100)
+# The fixture vocabulary's specials: 263 <|endoftext|>, 264
+# <|startoftranscript|>, 265 <|en|>, 266-267 tasks, 268 <|notimestamps|>,
+# 269-271 timestamps; id 32 is "Ġ" (a bare space).
+WHISPER_DECODING = dict(suppress_tokens=[264, 265, 266, 267, 268], begin_suppress_tokens=[32, 263],
+                        decoder_start_token_id=264, eos_token_id=263)
+
+
+def whisper_tensors():
+    tensors = dict(S.synthetic_encoder_file(WHISPER_ENCODER))
+    tensors.update(S.synthetic_decoder_file(WHISPER_DECODER))
+    return tensors
+
+
+def whisper_filters():
+    return S.triangular_filters(WHISPER_MEL.mel_count, WHISPER_MEL.bin_count)
+
+
+def write_whisper(path, tensors=None, filters=None, **decoding):
+    """The four files of a Whisper directory at the reduced shapes."""
+    with open(os.path.join(GOLDEN, "mini_tokenizer.json")) as f:
+        tokenizer_json = f.read()
+    config = S.whisper_config(WHISPER_ENCODER, WHISPER_DECODER, **dict(WHISPER_DECODING, **decoding))
+    pre = S.preprocessor_config(WHISPER_MEL, whisper_filters() if filters is None else filters)
+    return S.write_whisper_directory(str(path), config, pre, tokenizer_json,
+                                     whisper_tensors() if tensors is None else tensors)
+
+
+def oracle_transcript(oracle, tensors, samples, first_mask, later_mask, prompt, end_of_text, maximum_tokens,
+                      context=0):
+    """Whisper::transcribe restated on the oracle: samples zero-padded to the
+    window, oracle_mel_spectrogram, oracle_encode over the first
+    min(2 * context, frames) frames, then the greedy loop of
+    Whisper::decodeTranscript (Whisper/Whisper.cpp:1361-1443) on the KV-cached
+    oracle decoder. Returns the tokens and the top-2 margin of every step."""
+    m, e, d = WHISPER_MEL, WHISPER_ENCODER, WHISPER_DECODER
+    window = np.zeros(m.sample_count, dtype=np.float32)
+    window[:len(samples)] = samples
+    mel = oracle.mel_spectrogram(window, whisper_filters(), m.fft_length, m.hop_length, m.frame_count)
+    frames = e.input_frames if context == 0 else min(2 * context, e.input_frames)
+    run = e.with_frames(frames)
+    rows = oracle.encode(run, [tensors[n].floats() for n in S.encoder_canonical_names(e.layers)],
+                         np.ascontiguousarray(mel[:, :frames].astype(np.float32)))
+    session = oracle.session(d, [tensors[n].floats() for n in S.canonical_names(d.layers)])
+    session.begin(rows.astype(np.float32), run.positions())
+    limit = min(maximum_tokens, d.max_positions - len(prompt) + 1)
+    tokens, margins = [], []
+    _, logits = session.step(prompt)
+    row, mask = logits[-1], first_mask
+    for step in range(limit):
+        if step > 0:
+            _, logits = session.step([tokens[-1]])
+            row, mask = logits[0], later_mask
+        allowed = np.where(mask != 0, -np.inf, row)
+        token = int(np.argmax(allowed))
+        margins.append(margin(allowed[np.isfinite(allowed)]))
+        if token == end_of_text:
+            break
+        tokens.append(token)
+    return tokens, margins

@@ -190,6 +190,29 @@ SIGNATURES = {
                                      ctypes.POINTER(c_int)]),
     "wsp_tokenizer_decode": (c_int, [c_void_p, ctypes.POINTER(c_int), c_int, c_int, ctypes.c_char_p, c_int,
                                      ctypes.POINTER(c_int)]),
+    "wsp_whisper_create": (c_int, [ctypes.POINTER(c_void_p)]),
+    "wsp_whisper_destroy": (None, [c_void_p]),
+    "wsp_whisper_last_error": (c_char_p, [c_void_p]),
+    "wsp_whisper_last_error_kind": (c_int, [c_void_p]),
+    "wsp_whisper_load": (c_int, [c_void_p, c_char_p]),
+    "wsp_whisper_load_files": (c_int, [c_void_p, c_char_p, c_char_p, c_char_p, c_char_p]),
+    "wsp_whisper_set_packs_weights": (c_int, [c_void_p, c_int]),
+    "wsp_whisper_prepare": (c_int, [c_void_p, c_int, c_void_p]),
+    "wsp_whisper_prompt": (c_int, [c_void_p, ctypes.POINTER(c_int), c_int, ctypes.POINTER(c_int)]),
+    "wsp_whisper_masks": (c_int, [c_void_p, c_void_p, c_void_p, c_int]),
+    "wsp_whisper_end_of_text": (c_int, [c_void_p, ctypes.POINTER(c_int)]),
+    "wsp_whisper_set_maximum_tokens": (c_int, [c_void_p, c_int]),
+    "wsp_whisper_maximum_tokens": (c_int, [c_void_p, ctypes.POINTER(c_int)]),
+    "wsp_whisper_set_audio_context": (c_int, [c_void_p, c_int]),
+    "wsp_whisper_audio_context_for_samples": (c_int, [c_void_p, c_int, ctypes.c_double, ctypes.POINTER(c_int)]),
+    "wsp_whisper_transcribe": (c_int, [c_void_p, c_void_p, c_int, ctypes.POINTER(c_int), c_int,
+                                       ctypes.POINTER(c_int)]),
+    "wsp_whisper_text_for_tokens": (c_int, [c_void_p, ctypes.POINTER(c_int), c_int, ctypes.c_char_p, c_int,
+                                            ctypes.POINTER(c_int)]),
+    "wsp_whisper_timing": (c_int, [c_void_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                   ctypes.POINTER(c_int)]),
+    "wsp_whisper_encoded_rows": (c_int, [c_void_p, ctypes.POINTER(c_void_p), ctypes.POINTER(c_int),
+                                         ctypes.POINTER(c_int)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -24,7 +24,8 @@ DEVICE_SOURCES = ["ops.hip", "capi.hip", "cross_kv.hip", "fused_step.hip", "step
                   "mfma_product.hip", "attention_static.hip", "encoder.hip", "mel.hip"]
 HOST_SOURCES = ["host/Gpu.cpp", "host/Net.cpp", "host/Half.cpp", "host/HipNet.cpp", "host/DecoderWeights.cpp",
                 "host/Decoder.cpp", "host/Argmax.cpp", "host/GreedyDecoder.cpp", "host/BatchedDecoder.cpp",
-                "host/SafeTensors.cpp", "host/Tokenizer.cpp", "host/decoder_capi.cpp"]
+                "host/SafeTensors.cpp", "host/Tokenizer.cpp", "host/Encoder.cpp", "host/Whisper.cpp",
+                "host/decoder_capi.cpp"]
 
 COMMON = ["-std=c++20", "-fPIC", "-Wall", "-Wno-unused-result", "-I" + os.path.join(HERE, "..", "include")]
 DEVICE_FLAGS = ["-O3", "--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

@@ -8,6 +8,7 @@
 #include "../../../include/whispereacp/GreedyDecoder.h"
 #include "../../../include/whispereacp/SafeTensors.h"
 #include "../../../include/whispereacp/Tokenizer.h"
+#include "../../../include/whispereacp/Whisper.h"
 
 #include <algorithm>
 #include <cstring>
@@ -32,6 +33,13 @@ struct wsp_decoder
 struct wsp_safetensors
 {
     std::unique_ptr<WSP::SafeTensors> file;
+    std::string error;
+    int errorKind = WSP_KIND_NONE;
+};
+
+struct wsp_whisper
+{
+    WSP::Whisper whisper;
     std::string error;
     int errorKind = WSP_KIND_NONE;
 };
@@ -744,6 +752,216 @@ int wsp_tokenizer_decode(const wsp_tokenizer* t, const int* ids, int count, int 
     std::memcpy(text_out, text.data(), text.size());
     text_out[text.size()] = 0;
     return WSP_OK;
+}
+
+} // extern "C"
+
+// ---- Whisper end to end ---------------------------------------------------
+namespace
+{
+// A tokenizer.json the tokenizer refuses is a model file the load refuses.
+template <typename Body>
+int whisperGuarded(wsp_whisper* w, Body body)
+{
+    return guarded(w, [&] {
+        try
+        {
+            body();
+        }
+        catch (const WSP::TokenizerError& e)
+        {
+            throw WSP::ModelError(e.what());
+        }
+    });
+}
+} // namespace
+
+extern "C" {
+
+int wsp_whisper_create(wsp_whisper** out)
+{
+    if (out == nullptr)
+        return WSP_ERR_ARGUMENT;
+    *out = new (std::nothrow) wsp_whisper {};
+    return *out == nullptr ? WSP_ERR_CAPACITY : WSP_OK;
+}
+
+void wsp_whisper_destroy(wsp_whisper* w)
+{
+    delete w;
+}
+
+const char* wsp_whisper_last_error(const wsp_whisper* w)
+{
+    return w == nullptr ? "null whisper" : w->error.c_str();
+}
+
+int wsp_whisper_last_error_kind(const wsp_whisper* w)
+{
+    return w == nullptr ? WSP_KIND_NONE : w->errorKind;
+}
+
+int wsp_whisper_load(wsp_whisper* w, const char* model_directory)
+{
+    return whisperGuarded(w, [&] {
+        if (model_directory == nullptr)
+            throw std::invalid_argument("wsp_whisper_load: null directory");
+        w->whisper.load(std::string(model_directory));
+    });
+}
+
+int wsp_whisper_load_files(wsp_whisper* w, const char* config_json, const char* preprocessor_json,
+                           const char* tokenizer_json, const char* weights_path)
+{
+    return whisperGuarded(w, [&] {
+        if (config_json == nullptr || preprocessor_json == nullptr || tokenizer_json == nullptr
+            || weights_path == nullptr)
+            throw std::invalid_argument("wsp_whisper_load_files: a null file");
+        WSP::ModelFiles files;
+        files.config = config_json;
+        files.preprocessorConfig = preprocessor_json;
+        files.tokenizer = tokenizer_json;
+        files.weightsPath = weights_path;
+        w->whisper.load(files);
+    });
+}
+
+int wsp_whisper_set_packs_weights(wsp_whisper* w, int pack)
+{
+    return guarded(w, [&] { w->whisper.setPacksWeights(pack != 0); });
+}
+
+int wsp_whisper_prepare(wsp_whisper* w, int device, void* stream)
+{
+    return guarded(w, [&] { w->whisper.prepare(WSP::Device {device}, stream); });
+}
+
+int wsp_whisper_prompt(wsp_whisper* w, int* tokens_out, int capacity, int* count_out)
+{
+    return guarded(w, [&] {
+        if (count_out == nullptr || capacity < 0 || (tokens_out == nullptr && capacity > 0))
+            throw std::invalid_argument("wsp_whisper_prompt: no room described");
+        if (!w->whisper.isLoaded())
+            throw WSP::ModelError("this Whisper has not loaded a model yet");
+        const std::vector<int>& p = w->whisper.prompt();
+        *count_out = (int) p.size();
+        if ((int) p.size() > capacity)
+            throw std::invalid_argument("wsp_whisper_prompt: " + std::to_string(p.size()) + " tokens, room for "
+                                        + std::to_string(capacity));
+        std::copy(p.begin(), p.end(), tokens_out);
+    });
+}
+
+int wsp_whisper_masks(wsp_whisper* w, float* first_mask, float* later_mask, int capacity)
+{
+    return guarded(w, [&] {
+        if (!w->whisper.isLoaded())
+            throw WSP::ModelError("this Whisper has not loaded a model yet");
+        const auto& first = w->whisper.firstStepMask();
+        const auto& later = w->whisper.laterStepMask();
+        if ((first_mask != nullptr || later_mask != nullptr) && capacity < (int) first.size())
+            throw std::invalid_argument("wsp_whisper_masks: the masks are " + std::to_string(first.size())
+                                        + " floats long");
+        if (first_mask != nullptr)
+            std::copy(first.begin(), first.end(), first_mask);
+        if (later_mask != nullptr)
+            std::copy(later.begin(), later.end(), later_mask);
+    });
+}
+
+int wsp_whisper_end_of_text(wsp_whisper* w, int* token_out)
+{
+    return guarded(w, [&] {
+        if (token_out == nullptr)
+            throw std::invalid_argument("wsp_whisper_end_of_text: null output");
+        *token_out = w->whisper.endOfTextToken();
+    });
+}
+
+int wsp_whisper_set_maximum_tokens(wsp_whisper* w, int count)
+{
+    return guarded(w, [&] { w->whisper.setMaximumTokens(count); });
+}
+
+int wsp_whisper_maximum_tokens(wsp_whisper* w, int* count_out)
+{
+    return guarded(w, [&] {
+        if (count_out == nullptr)
+            throw std::invalid_argument("wsp_whisper_maximum_tokens: null output");
+        *count_out = w->whisper.maximumTokens();
+    });
+}
+
+int wsp_whisper_set_audio_context(wsp_whisper* w, int positions)
+{
+    return guarded(w, [&] { w->whisper.setAudioContext(positions); });
+}
+
+int wsp_whisper_audio_context_for_samples(wsp_whisper* w, int sample_count, double margin_seconds,
+                                          int* positions_out)
+{
+    return guarded(w, [&] {
+        if (positions_out == nullptr)
+            throw std::invalid_argument("wsp_whisper_audio_context_for_samples: null output");
+        *positions_out = w->whisper.audioContextForSamples(sample_count, margin_seconds);
+    });
+}
+
+int wsp_whisper_transcribe(wsp_whisper* w, const float* samples, int sample_count, int* tokens_out, int capacity,
+                           int* count_out)
+{
+    return guarded(w, [&] {
+        if (sample_count < 0 || count_out == nullptr || capacity < 0 || (tokens_out == nullptr && capacity > 0))
+            throw std::invalid_argument("wsp_whisper_transcribe: bad sample count or output");
+        const std::vector<int> tokens = w->whisper.transcribe(samples, (std::size_t) sample_count);
+        *count_out = (int) tokens.size();
+        const int n = std::min((int) tokens.size(), capacity);
+        std::copy(tokens.begin(), tokens.begin() + n, tokens_out);
+        if ((int) tokens.size() > capacity)
+            throw std::invalid_argument("wsp_whisper_transcribe: " + std::to_string(tokens.size())
+                                        + " tokens, room for " + std::to_string(capacity) + " (the first "
+                                        + std::to_string(n) + " were written)");
+    });
+}
+
+int wsp_whisper_text_for_tokens(wsp_whisper* w, const int* tokens, int count, char* text_out, int capacity,
+                                int* length_out)
+{
+    return guarded(w, [&] {
+        if (count < 0 || (tokens == nullptr && count > 0) || length_out == nullptr || text_out == nullptr
+            || capacity <= 0)
+            throw std::invalid_argument("wsp_whisper_text_for_tokens: bad tokens or output");
+        const std::string text = w->whisper.textForTokens(std::vector<int>(tokens, tokens + count));
+        *length_out = (int) text.size();
+        if ((int) text.size() >= capacity)
+            throw std::invalid_argument("wsp_whisper_text_for_tokens: " + std::to_string(text.size())
+                                        + " bytes and a NUL, room for " + std::to_string(capacity));
+        std::memcpy(text_out, text.data(), text.size());
+        text_out[text.size()] = 0;
+    });
+}
+
+int wsp_whisper_timing(wsp_whisper* w, double* encode_seconds, double* decode_seconds, int* steps)
+{
+    return guarded(w, [&] {
+        if (encode_seconds != nullptr)
+            *encode_seconds = w->whisper.lastEncodeSeconds();
+        if (decode_seconds != nullptr)
+            *decode_seconds = w->whisper.lastDecodeSeconds();
+        if (steps != nullptr)
+            *steps = w->whisper.lastStepCount();
+    });
+}
+
+int wsp_whisper_encoded_rows(wsp_whisper* w, const float** rows_out, int* positions_out, int* width_out)
+{
+    return guarded(w, [&] {
+        if (rows_out == nullptr || positions_out == nullptr || width_out == nullptr)
+            throw std::invalid_argument("wsp_whisper_encoded_rows: null output");
+        *rows_out = w->whisper.encodedRows();
+        *positions_out = w->whisper.encodedPositions();
+        *width_out = w->whisper.encoderShape().width;
+    });
 }
 
 } // extern "C"

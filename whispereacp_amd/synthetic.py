@@ -611,3 +611,69 @@ def triangular_filters(mel_count: int, bin_count: int) -> np.ndarray:
     centre = span * (np.arange(mel_count, dtype=np.float64)[:, None] + 1)
     distance = np.abs(bins - centre) / span
     return np.where(distance < 1.0, 1.0 - distance, 0.0).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# A whole Whisper model directory (config.json, preprocessor_config.json,
+# tokenizer.json, model.safetensors) from synthetic tensors
+# ---------------------------------------------------------------------------
+
+def safetensors_bytes(tensors: Dict[str, StoredTensor], metadata: Optional[Dict[str, str]] = None) -> bytes:
+    """The safetensors layout: an 8-byte little-endian header length, the JSON
+    header (name -> dtype, shape, data_offsets), then the tensors' bytes in
+    header order."""
+    import json
+    header: Dict[str, object] = {}
+    if metadata:
+        header["__metadata__"] = dict(metadata)
+    blobs = []
+    offset = 0
+    for name in sorted(tensors):
+        t = tensors[name]
+        raw = np.ascontiguousarray(t.data).tobytes()
+        header[name] = {"dtype": t.dtype, "shape": list(t.extents), "data_offsets": [offset, offset + len(raw)]}
+        blobs.append(raw)
+        offset += len(raw)
+    text = json.dumps(header, separators=(",", ":")).encode()
+    text += b" " * ((8 - len(text) % 8) % 8)
+    return len(text).to_bytes(8, "little") + text + b"".join(blobs)
+
+
+def whisper_config(encoder: EncoderShape, decoder: DecoderShape, **decoding) -> Dict[str, object]:
+    """A HuggingFace config.json for these two shapes; ``decoding`` adds
+    suppress_tokens, begin_suppress_tokens, decoder_start_token_id, eos_token_id."""
+    config: Dict[str, object] = {
+        "model_type": "whisper", "num_mel_bins": encoder.mel_bins, "d_model": decoder.width,
+        "encoder_attention_heads": encoder.heads, "encoder_layers": encoder.layers,
+        "encoder_ffn_dim": encoder.feed_forward_width, "decoder_attention_heads": decoder.heads,
+        "decoder_layers": decoder.layers, "decoder_ffn_dim": decoder.feed_forward_width,
+        "vocab_size": decoder.vocabulary_size, "max_target_positions": decoder.max_positions,
+        "max_source_positions": encoder.input_frames // 2,
+    }
+    config.update(decoding)
+    return config
+
+
+def preprocessor_config(mel: MelShape, filters: np.ndarray, sample_rate: int = 16000) -> Dict[str, object]:
+    return {
+        "feature_extractor_type": "WhisperFeatureExtractor", "sampling_rate": sample_rate,
+        "n_fft": mel.fft_length, "hop_length": mel.hop_length, "feature_size": mel.mel_count,
+        "chunk_length": max(1, mel.sample_count // sample_rate), "n_samples": mel.sample_count,
+        "nb_max_frames": mel.frame_count,
+        "mel_filters": np.asarray(filters, dtype=np.float64).tolist(),
+    }
+
+
+def write_whisper_directory(path: str, config: Dict[str, object], preprocessor: Dict[str, object],
+                            tokenizer_json: str, tensors: Dict[str, StoredTensor]) -> str:
+    import json
+    os.makedirs(path, exist_ok=True)
+    with open(os.path.join(path, "config.json"), "w") as f:
+        json.dump(config, f)
+    with open(os.path.join(path, "preprocessor_config.json"), "w") as f:
+        json.dump(preprocessor, f)
+    with open(os.path.join(path, "tokenizer.json"), "w") as f:
+        f.write(tokenizer_json)
+    with open(os.path.join(path, "model.safetensors"), "wb") as f:
+        f.write(safetensors_bytes(tensors, {"format": "pt"}))
+    return path
