@@ -677,3 +677,67 @@ def write_whisper_directory(path: str, config: Dict[str, object], preprocessor: 
     with open(os.path.join(path, "model.safetensors"), "wb") as f:
         f.write(safetensors_bytes(tensors, {"format": "pt"}))
     return path
+
+
+def byte_alphabet() -> List[str]:
+    """The byte-level BPE's printable stand-in for each byte (GPT-2's
+    bytes_to_unicode): printable Latin-1 bytes stand for themselves, the rest
+    take code points from 256 upwards in byte order."""
+    keep = list(range(ord("!"), ord("~") + 1)) + list(range(0xA1, 0xAC + 1)) + list(range(0xAE, 0xFF + 1))
+    out, extra = [], 0
+    for b in range(256):
+        if b in keep:
+            out.append(chr(b))
+        else:
+            out.append(chr(256 + extra))
+            extra += 1
+    return out
+
+
+def synthetic_tokenizer_json(vocabulary_size: int = 51864) -> str:
+    """A tokenizer.json laid out like tiny.en's: the 256 byte tokens, two-byte
+    tokens up to id 50255 (no merges), then the added tokens — <|endoftext|>
+    50256, <|startoftranscript|> 50257, <|en|> 50258, the task and prompt
+    tokens, <|notimestamps|> 50362 and the timestamps from 50363 — for a
+    vocabulary of ``vocabulary_size`` ids."""
+    import json
+    alphabet = byte_alphabet()
+    vocab = {alphabet[b]: b for b in range(256)}
+    for i in range(256, 50256):
+        j = i - 256
+        vocab[alphabet[j // 256] + alphabet[j % 256]] = i
+    named = {50256: "<|endoftext|>", 50257: "<|startoftranscript|>", 50258: "<|en|>", 50358: "<|translate|>",
+             50359: "<|transcribe|>", 50360: "<|startoflm|>", 50361: "<|startofprev|>", 50362: "<|notimestamps|>"}
+    added = []
+    for i in range(50256, vocabulary_size):
+        if i in named:
+            content = named[i]
+        elif i >= 50363:
+            content = f"<|{(i - 50363) * 0.02:.2f}|>"
+        else:
+            content = f"<|x{i}|>"
+        added.append({"id": i, "content": content, "single_word": False, "lstrip": False, "rstrip": False,
+                      "normalized": False, "special": True})
+    return json.dumps({"version": "1.0", "added_tokens": added,
+                       "model": {"type": "BPE", "vocab": vocab, "merges": []}})
+
+
+def tiny_en_whisper_directory(path: str, seed: int = 1003) -> str:
+    """A tiny.en-shaped Whisper directory with synthetic weights: N(0, 0.02)
+    projections rounded to fp16-exact floats in F32 storage (as OpenAI's fp16
+    checkpoints are after HuggingFace's conversion, so ExactHalf packs them),
+    the published mel shape (30 s, 400-point frames every 160, 80 bands) with
+    a triangular filterbank, and the synthetic vocabulary above."""
+    encoder = encoder_workload_shape("tiny.en")
+    decoder = workload_shape("tiny.en")
+    tensors: Dict[str, StoredTensor] = {}
+    for source in (workload_encoder_file(encoder, "F32", seed + 2000), workload_decoder_file(decoder, "F32", seed)):
+        for name, t in source.items():
+            exact = t.data.astype(np.float16).astype(np.float32)
+            tensors[name] = StoredTensor(name, "F32", t.extents, exact)
+    mel = MelShape()
+    config = whisper_config(encoder, decoder, suppress_tokens=[1, 2, 7, 8, 9, 10, 50257, 50360, 50361],
+                            begin_suppress_tokens=[220, 50256], decoder_start_token_id=50257,
+                            eos_token_id=50256)
+    return write_whisper_directory(path, config, preprocessor_config(mel, triangular_filters(80, mel.bin_count)),
+                                   synthetic_tokenizer_json(decoder.vocabulary_size), tensors)
