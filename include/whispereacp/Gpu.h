@@ -13,14 +13,22 @@
 namespace WSP
 {
 // The device a decoder runs on. One GPU per process is the supported model.
+// Device::host() places buffers in host memory instead (the reference's
+// WeightPlacement::Host, Model/TensorLoader.h:40-44): weights loaded there
+// serve a Net that runs on the host, and nothing touches a GPU.
 struct Device
 {
+    static constexpr int hostIndex = -1;
+
     int index = 0;
 
     static Device& shared();
+    static Device host() { return Device {hostIndex}; }
+    bool isHost() const { return index == hostIndex; }
 };
 
-// Device memory, allocated on construction and freed on destruction.
+// Device memory (host memory on Device::host()), allocated on construction
+// and freed on destruction.
 class DeviceBuffer
 {
 public:

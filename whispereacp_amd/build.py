@@ -23,7 +23,7 @@ ARCH = "gfx950"
 DEVICE_SOURCES = ["ops.hip", "capi.hip", "cross_kv.hip", "fused_step.hip", "step_kernel.hip", "batch.hip",
                   "mfma_product.hip", "attention_static.hip", "encoder.hip", "mel.hip"]
 HOST_SOURCES = ["host/Gpu.cpp", "host/Net.cpp", "host/Half.cpp", "host/HipNet.cpp", "host/DecoderWeights.cpp",
-                "host/Decoder.cpp", "host/Argmax.cpp", "host/GreedyDecoder.cpp", "host/BatchedDecoder.cpp",
+                "host/Decoder.cpp", "host/DecoderRecording.cpp", "host/Argmax.cpp", "host/GreedyDecoder.cpp", "host/BatchedDecoder.cpp",
                 "host/SafeTensors.cpp", "host/Tokenizer.cpp", "host/Encoder.cpp", "host/Whisper.cpp",
                 "host/decoder_capi.cpp"]
 

@@ -1,5 +1,6 @@
-// The decoder body against Net and the Decoder class around it
-// (Decoder/Decoder.cpp:1-308), plus the fused single-token path.
+// The Decoder class around the decoder body (Decoder/Decoder.cpp:113-308):
+// caches and scratch sized once, the recorded steps on HipNet
+// (DecoderRecording.cpp), and the fused single-token path.
 #include "../../../include/whispereacp/Decoder.h"
 #include "host_common.h"
 
@@ -11,50 +12,6 @@ namespace WSP
 {
 namespace
 {
-// One pre-norm attention sublayer: normalise, project the queries (and, for
-// self-attention, append this step's keys and values from the same
-// normalised rows), attend, and add the output projection into the stream.
-Tensor attentionSublayer(Net& net, const DecoderShape& shape, const TensorBuffer& normWeight,
-                         const TensorBuffer& normBias, const TensorBuffer& queryWeight,
-                         const TensorBuffer& queryBias, const TensorBuffer& outputWeight,
-                         const TensorBuffer& outputBias, const Tensor& stream, bool causal,
-                         const std::function<std::pair<Tensor, Tensor>(const Tensor&)>& keysAndValues)
-{
-    const Tensor normalised = net.layerNorm(stream, normWeight, normBias);
-    const Tensor queries = net.linear(normalised, queryWeight, &queryBias, Activation::none);
-    const auto [keys, values] = keysAndValues(normalised);
-    const Tensor attended = net.attention(queries, keys, values, shape.heads, causal);
-    return net.linearAdd(attended, outputWeight, &outputBias, stream);
-}
-
-Tensor layerBody(Net& net, const DecoderShape& shape, const DecoderLayerWeights& w, DecoderCaches& caches,
-                 int layer, const Tensor& hidden)
-{
-    // Self-attention: keys and values come from this step's normalised rows,
-    // appended to the cache; the causal mask keeps each row out of its future.
-    const Tensor afterSelf = attentionSublayer(
-        net, shape, w.selfAttentionNormWeight, w.selfAttentionNormBias, w.selfQueryWeight, w.selfQueryBias,
-        w.selfAttentionOutputWeight, w.selfAttentionOutputBias, hidden, true, [&](const Tensor& normalised) {
-            Tensor keys = net.appendLinear(caches.selfKeys[(std::size_t) layer], normalised, w.selfKeyWeight, nullptr);
-            Tensor values = net.appendLinear(caches.selfValues[(std::size_t) layer], normalised, w.selfValueWeight,
-                                             &w.selfValueBias);
-            return std::make_pair(keys, values);
-        });
-
-    // Cross-attention: the keys and values were projected when the sequence
-    // opened; nothing is masked.
-    const Tensor afterCross = attentionSublayer(
-        net, shape, w.crossAttentionNormWeight, w.crossAttentionNormBias, w.crossQueryWeight, w.crossQueryBias,
-        w.crossAttentionOutputWeight, w.crossAttentionOutputBias, afterSelf, false, [&](const Tensor&) {
-            return std::make_pair(net.cached(caches.crossKeys[(std::size_t) layer]),
-                                  net.cached(caches.crossValues[(std::size_t) layer]));
-        });
-
-    const Tensor inner = net.linear(net.layerNorm(afterCross, w.finalNormWeight, w.finalNormBias),
-                                    w.feedForwardWeight, &w.feedForwardBias, Activation::gelu);
-    return net.linearAdd(inner, w.feedForwardOutputWeight, &w.feedForwardOutputBias, afterCross);
-}
-
 void addCaches(std::vector<Cache>& caches, Net& net, int layers, int rows, int width)
 {
     caches.clear();
@@ -62,38 +19,6 @@ void addCaches(std::vector<Cache>& caches, Net& net, int layers, int rows, int w
         caches.push_back(net.makeCache(rows, width));
 }
 } // namespace
-
-void recordSequenceStart(Net& net, const DecoderShape& shape, const DecoderWeights& weights, DecoderCaches& caches,
-                         const Binding& encoderRows, int rows)
-{
-    const Tensor encoded = net.input(encoderRows, {rows, shape.width}, DType::float32);
-    for (int layer = 0; layer < shape.layers; ++layer)
-    {
-        const auto& w = weights.layers[(std::size_t) layer];
-        const auto i = (std::size_t) layer;
-        caches.selfKeys[i].clear();
-        caches.selfValues[i].clear();
-        caches.crossKeys[i].clear();
-        caches.crossValues[i].clear();
-        net.appendLinear(caches.crossKeys[i], encoded, w.crossKeyWeight, nullptr);
-        net.appendLinear(caches.crossValues[i], encoded, w.crossValueWeight, &w.crossValueBias);
-    }
-}
-
-void recordDecoderStep(Net& net, const DecoderShape& shape, const DecoderWeights& weights, DecoderCaches& caches,
-                       const Binding& tokens, int tokenCount, int firstPosition, const Binding& hiddenStates,
-                       const Binding& logits)
-{
-    Tensor hidden = net.embed(net.input(tokens, {tokenCount}, DType::int32), weights.tokenEmbedding,
-                              weights.positionalEmbedding, firstPosition);
-    for (int layer = 0; layer < shape.layers; ++layer)
-        hidden = layerBody(net, shape, weights.layers[(std::size_t) layer], caches, layer, hidden);
-
-    const Tensor normalised = net.layerNorm(hidden, weights.finalNormWeight, weights.finalNormBias);
-    net.output(normalised, hiddenStates);
-    // Tied logits: embed_tokens itself, no bias (Decoder/DecoderWeights.h:66-79).
-    net.output(net.linear(normalised, weights.logitsWeight(), nullptr, Activation::none), logits);
-}
 
 Decoder::Decoder(const DecoderShape& shapeToUse) : decoderShape(shapeToUse) {}
 

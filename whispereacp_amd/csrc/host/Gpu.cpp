@@ -3,6 +3,10 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <cstdlib>
+#include <cstring>
+#include <new>
+
 namespace WSP
 {
 Device& Device::shared()
@@ -20,6 +24,13 @@ void checkHip(int status, const char* what)
 DeviceBuffer::DeviceBuffer(const Device& deviceToUse, std::size_t byteCount)
     : bytes(byteCount), device(deviceToUse.index)
 {
+    if (device == Device::hostIndex)
+    {
+        pointer = std::malloc(bytes > 0 ? bytes : 1);
+        if (pointer == nullptr)
+            throw std::bad_alloc();
+        return;
+    }
     checkHip(hipSetDevice(device), "hipSetDevice");
     checkHip(hipMalloc(&pointer, bytes > 0 ? bytes : 1), "hipMalloc");
 }
@@ -30,10 +41,22 @@ DeviceBuffer::DeviceBuffer(const Device& deviceToUse, const void* host, std::siz
     upload(host, byteCount);
 }
 
+namespace
+{
+void release(void* pointer, int device)
+{
+    if (pointer == nullptr)
+        return;
+    if (device == Device::hostIndex)
+        std::free(pointer);
+    else
+        (void) hipFree(pointer);
+}
+} // namespace
+
 DeviceBuffer::~DeviceBuffer()
 {
-    if (pointer != nullptr)
-        (void) hipFree(pointer);
+    release(pointer, device);
 }
 
 DeviceBuffer::DeviceBuffer(DeviceBuffer&& other) noexcept
@@ -47,8 +70,7 @@ DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& other) noexcept
 {
     if (this != &other)
     {
-        if (pointer != nullptr)
-            (void) hipFree(pointer);
+        release(pointer, device);
         pointer = other.pointer;
         bytes = other.bytes;
         device = other.device;
@@ -62,6 +84,11 @@ void DeviceBuffer::upload(const void* host, std::size_t count, std::size_t offse
 {
     if (offset + count > bytes)
         throw std::out_of_range("upload past the end of a device buffer");
+    if (device == Device::hostIndex)
+    {
+        std::memcpy(static_cast<char*>(pointer) + offset, host, count);
+        return;
+    }
     checkHip(hipMemcpy(static_cast<char*>(pointer) + offset, host, count, hipMemcpyHostToDevice),
              "hipMemcpy host to device");
 }
@@ -70,6 +97,11 @@ void DeviceBuffer::read(void* host, std::size_t count, std::size_t offset) const
 {
     if (offset + count > bytes)
         throw std::out_of_range("read past the end of a device buffer");
+    if (device == Device::hostIndex)
+    {
+        std::memcpy(host, static_cast<char*>(pointer) + offset, count);
+        return;
+    }
     checkHip(hipMemcpy(host, static_cast<char*>(pointer) + offset, count, hipMemcpyDeviceToHost),
              "hipMemcpy device to host");
 }
