@@ -444,10 +444,35 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
     {
         const wsp_encoder_layer_tensors& L = T->layers[l];
         if ((status = ops::layernorm(st, e->hidden, L.attention_norm_w, L.attention_norm_b, e->normed, positions, d,
-                                     eps)) != hipSuccess
-            || (status = ops::linear(st, e->normed, positions, d, L.q_w, wt, L.q_b, e->q, d, 0)) != hipSuccess
-            || (status = ops::linear(st, e->normed, positions, d, L.k_w, wt, nullptr, e->k, d, 0)) != hipSuccess
-            || (status = ops::linear(st, e->normed, positions, d, L.v_w, wt, L.v_b, e->v, d, 0)) != hipSuccess)
+                                     eps)) != hipSuccess)
+            return encoder_hip(e, status, "self-attention norm");
+        if (positions > 16 && ops::tile_product_fits(wt, d, 3 * d, d, e->normed) && d % 128 == 0)
+        {
+            // q, k and v side by side in one launch: three times the blocks of one.
+            ops::TileProduct p {};
+            p.x = e->normed;
+            p.rows = positions;
+            p.inner = d;
+            p.w0 = L.q_w;
+            p.w1 = L.k_w;
+            p.w2 = L.v_w;
+            p.split = d;
+            p.split2 = 2 * d;
+            p.out = 3 * d;
+            p.bias0 = L.q_b;
+            p.bias2 = L.v_b;
+            p.y0 = e->q;
+            p.y1 = e->k;
+            p.y2 = e->v;
+            p.ldy = d;
+            p.rows_per_group = positions;
+            p.wdtype = wt;
+            status = ops::tile_product(st, p);
+        }
+        else if ((status = ops::linear(st, e->normed, positions, d, L.q_w, wt, L.q_b, e->q, d, 0)) == hipSuccess
+                 && (status = ops::linear(st, e->normed, positions, d, L.k_w, wt, nullptr, e->k, d, 0)) == hipSuccess)
+            status = ops::linear(st, e->normed, positions, d, L.v_w, wt, L.v_b, e->v, d, 0);
+        if (status != hipSuccess)
             return encoder_hip(e, status, "self-attention projections");
         if (d / heads == kFlashWidth && d % 4 == 0)
         {

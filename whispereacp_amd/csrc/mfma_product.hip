@@ -8,11 +8,13 @@
 // product is exact and the fp32 sums match an fp32 product with widened
 // weights to fp32 rounding (the fp16 split needs |x| < 65504).
 //
-// A 256-thread block computes a 128 x 128 tile in 32-wide k-steps; each of its
-// four waves owns 64 x 64 (4 x 4 MFMA tiles of 16 x 16). The next k-step's
-// global loads are issued before the current step's products. LDS rows are
-// padded to 80 bytes, which keeps each 16-lane fragment read on distinct
-// banks.
+// A 256-thread block computes a 128 x 128 tile (or 64 x 128 when 128-row tiles
+// would leave CUs idle) in 32-wide k-steps; each of its four waves owns a
+// quarter (4 x 4 or 2 x 4 MFMA tiles of 16 x 16). The next k-step's global
+// loads are issued before the current step's products. LDS rows are padded to
+// 80 bytes, which keeps each 16-lane fragment read on distinct banks. Up to
+// three weight matrices share one launch side by side (the encoder's q, k and
+// v; the cross keys and values).
 #include "device_common.h"
 #include "ops.h"
 
@@ -69,41 +71,47 @@ __device__ __forceinline__ void split(float x, uint32_t (&bits)[3])
     }
 }
 
-template <int WT>
+// TM rows by 128 columns per block: four waves as 2 x 2, each TM/2 x 64.
+template <int WT, int TM>
 __global__ void __launch_bounds__(kThreads) tile_product_kernel(TileProduct a)
 {
     constexpr int P = parts_of<WT>();
-    __shared__ __attribute__((aligned(16))) u16 sa[P][kTile][kRow];
+    constexpr int MW = TM / 32;              // 16-row tiles per wave
+    constexpr int XPER = TM * kStep / kThreads; // X floats one thread stages per k-step (16 or 8)
+    constexpr int XTPR = kStep / XPER;       // threads per X row
+    __shared__ __attribute__((aligned(16))) u16 sa[P][TM][kRow];
     __shared__ __attribute__((aligned(16))) u16 sb[kTile][kRow];
 
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const int li = lane % 16, g = lane / 16;
     const int wm = wave / 2, wn = wave % 2;
-    const int n_block = blockIdx.x * kTile, m_block = blockIdx.y * kTile;
+    const int n_block = blockIdx.x * kTile, m_block = blockIdx.y * TM;
 
-    // Staging: thread (row sr, half sh) moves 16 consecutive k of one X row
-    // and one W row per k-step. Rows past the end re-read the last row.
-    const int sr = tid / 2, sh = (tid % 2) * 16;
+    // Staging: thread (row sr, offset sh) moves XPER consecutive k of one X
+    // row; thread (row br, half bh) moves 16 k of one W row. Rows past the end
+    // re-read the last row.
+    const int sr = tid / XTPR, sh = (tid % XTPR) * XPER;
     const float* ap = a.x + (size_t) min(m_block + sr, a.rows - 1) * a.inner + sh;
-    const int nrow = n_block + sr;
-    const u16* bp = (nrow < a.split ? static_cast<const u16*>(a.w0) + (size_t) nrow * a.inner
-                                    : static_cast<const u16*>(a.w1) + (size_t) (nrow - a.split) * a.inner)
-                    + sh;
+    const int br = tid / 2, bh = (tid % 2) * 16;
+    const int nrow = n_block + br;
+    const void* wbase = nrow < a.split ? a.w0 : nrow < a.split2 ? a.w1 : a.w2;
+    const int wrow = nrow < a.split ? nrow : nrow < a.split2 ? nrow - a.split : nrow - a.split2;
+    const u16* bp = static_cast<const u16*>(wbase) + (size_t) wrow * a.inner + bh;
 
-    float4v ar[4];
-    u32x4 br[2];
+    float4v ar[XPER / 4];
+    u32x4 br2[2];
 #define WSP_TILE_LOAD(k0)                                                            \
     do                                                                               \
     {                                                                                \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j) ar[j] =                        \
+        _Pragma("unroll") for (int j = 0; j < XPER / 4; ++j) ar[j] =                 \
             *reinterpret_cast<const float4v*>(ap + (k0) + 4 * j);                    \
-        br[0] = *reinterpret_cast<const u32x4*>(bp + (k0));                          \
-        br[1] = *reinterpret_cast<const u32x4*>(bp + (k0) + 8);                      \
+        br2[0] = *reinterpret_cast<const u32x4*>(bp + (k0));                         \
+        br2[1] = *reinterpret_cast<const u32x4*>(bp + (k0) + 8);                     \
     } while (0)
 
-    float4v acc[4][4];
+    float4v acc[MW][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MW; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             acc[i][j] = float4v {0.f, 0.f, 0.f, 0.f};
@@ -114,7 +122,7 @@ __global__ void __launch_bounds__(kThreads) tile_product_kernel(TileProduct a)
     {
         __syncthreads(); // the previous step's fragments are read
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < XPER / 8; ++h)
         {
             uint32_t packed[P][4];
 #pragma unroll
@@ -132,23 +140,23 @@ __global__ void __launch_bounds__(kThreads) tile_product_kernel(TileProduct a)
             for (int p = 0; p < P; ++p)
                 *reinterpret_cast<u32x4*>(&sa[p][sr][sh + 8 * h]) = u32x4 {packed[p][0], packed[p][1], packed[p][2], packed[p][3]};
         }
-        *reinterpret_cast<u32x4*>(&sb[sr][sh]) = br[0];
-        *reinterpret_cast<u32x4*>(&sb[sr][sh + 8]) = br[1];
+        *reinterpret_cast<u32x4*>(&sb[br][bh]) = br2[0];
+        *reinterpret_cast<u32x4*>(&sb[br][bh + 8]) = br2[1];
         __syncthreads();
         if (s + 1 < steps)
             WSP_TILE_LOAD((s + 1) * kStep);
 
-        u32x4 af[4][P], bf[4];
+        u32x4 af[MW][P], bf[4];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < MW; ++mt)
 #pragma unroll
             for (int p = 0; p < P; ++p)
-                af[mt][p] = *reinterpret_cast<const u32x4*>(&sa[p][wm * 64 + mt * 16 + li][8 * g]);
+                af[mt][p] = *reinterpret_cast<const u32x4*>(&sa[p][wm * (TM / 2) + mt * 16 + li][8 * g]);
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt)
             bf[nt] = *reinterpret_cast<const u32x4*>(&sb[wn * 64 + nt * 16 + li][8 * g]);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < MW; ++mt)
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
@@ -159,11 +167,11 @@ __global__ void __launch_bounds__(kThreads) tile_product_kernel(TileProduct a)
 
     // acc[mt][nt][r] of lane (g, li) is C[4g + r][li] of that 16 x 16 tile.
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < MW; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
         {
-            const int row = m_block + wm * 64 + mt * 16 + 4 * g + r;
+            const int row = m_block + wm * (TM / 2) + mt * 16 + 4 * g + r;
             if (row >= a.rows)
                 continue;
             const size_t base = (size_t) (row / a.rows_per_group) * a.group_stride
@@ -172,10 +180,10 @@ __global__ void __launch_bounds__(kThreads) tile_product_kernel(TileProduct a)
             for (int nt = 0; nt < 4; ++nt)
             {
                 const int n = n_block + wn * 64 + nt * 16 + li;
-                const bool first = n < a.split;
-                const int c = first ? n : n - a.split;
-                const float* bias = first ? a.bias0 : a.bias1;
-                float* y = first ? a.y0 : a.y1;
+                const int seg = n < a.split ? 0 : n < a.split2 ? 1 : 2;
+                const int c = seg == 0 ? n : seg == 1 ? n - a.split : n - a.split2;
+                const float* bias = seg == 0 ? a.bias0 : seg == 1 ? a.bias1 : a.bias2;
+                float* y = seg == 0 ? a.y0 : seg == 1 ? a.y1 : a.y2;
                 float v = acc[mt][nt][r];
                 if (bias != nullptr)
                     v += bias[c];
@@ -196,13 +204,40 @@ bool tile_product_fits(int wdtype, int inner, int out, int split, const void* x)
            && split <= out && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
 }
 
-hipError_t tile_product(hipStream_t stream, const TileProduct& a)
+// 128-row tiles unless that leaves most of the chip idle: a grid of fewer
+// blocks than CUs takes 64-row tiles (twice the blocks, each half the work).
+hipError_t tile_product(hipStream_t stream, const TileProduct& product)
 {
-    const dim3 grid(a.out / kTile, (a.rows + kTile - 1) / kTile);
+    TileProduct a = product;
+    if (a.split2 <= 0 || a.split2 > a.out)
+        a.split2 = a.out;
+    if (a.split2 < a.split || a.split2 % kTile != 0)
+        return hipErrorInvalidValue;
+    static const int units = [] {
+        int device = 0, count = 0;
+        if (hipGetDevice(&device) == hipSuccess
+            && hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && count > 0)
+            return count;
+        return 256;
+    }();
+    const int columns = a.out / kTile;
+    const bool narrow = (long long) columns * ((a.rows + kTile - 1) / kTile) < 4LL * units;
+    const int tm = narrow ? 64 : kTile;
+    const dim3 grid(columns, (a.rows + tm - 1) / tm);
     if (a.wdtype == kF16)
-        hipLaunchKernelGGL((tile_product_kernel<kF16>), grid, dim3(kThreads), 0, stream, a);
+    {
+        if (narrow)
+            hipLaunchKernelGGL((tile_product_kernel<kF16, 64>), grid, dim3(kThreads), 0, stream, a);
+        else
+            hipLaunchKernelGGL((tile_product_kernel<kF16, kTile>), grid, dim3(kThreads), 0, stream, a);
+    }
     else
-        hipLaunchKernelGGL((tile_product_kernel<kBF16>), grid, dim3(kThreads), 0, stream, a);
+    {
+        if (narrow)
+            hipLaunchKernelGGL((tile_product_kernel<kBF16, 64>), grid, dim3(kThreads), 0, stream, a);
+        else
+            hipLaunchKernelGGL((tile_product_kernel<kBF16, kTile>), grid, dim3(kThreads), 0, stream, a);
+    }
     return hipGetLastError();
 }
 } // namespace wsp::ops

@@ -26,6 +26,9 @@ struct TileProduct
 {
     const float* x;
     int rows, inner;
+    // Up to three weight matrices side by side: columns [0, split) read w0,
+    // [split, split2) w1 and [split2, out) w2, each with its bias and output
+    // (split2 0: two matrices, w1 running to out).
     const void* w0;
     const void* w1;
     int split, out;
@@ -38,9 +41,14 @@ struct TileProduct
     size_t group_stride;
     int flags;
     int wdtype;
+    const void* w2;
+    const float* bias2;
+    float* y2;
+    int split2;
 };
 
-// 16-bit weights, inner % 32 == 0, out and split multiples of 128, X 16-byte aligned.
+// 16-bit weights, inner % 32 == 0, out and split (and split2) multiples of
+// 128, X 16-byte aligned.
 bool tile_product_fits(int wdtype, int inner, int out, int split, const void* x);
 hipError_t tile_product(hipStream_t stream, const TileProduct& product);
 
