@@ -15,7 +15,8 @@ from typing import Optional
 import torch  # noqa: F401  (the process's one HIP runtime)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIBRARY = os.path.join(HERE, "_build", "libwhispereacp_hip.so")
+# The in-tree build, unless WSP_LIBRARY names another build of the same sources.
+LIBRARY = os.environ.get("WSP_LIBRARY") or os.path.join(HERE, "_build", "libwhispereacp_hip.so")
 
 c_int, c_float, c_void_p, c_char_p, c_double = ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_double
 

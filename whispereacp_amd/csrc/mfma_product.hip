@@ -9,10 +9,11 @@
 // weights to fp32 rounding (the fp16 split needs |x| < 65504).
 //
 // A 256-thread block computes a 128 x 128 tile (or 64 x 128 when 128-row tiles
-// would leave CUs idle) in 32-wide k-steps; each of its four waves owns a
+// would give fewer than four blocks per CU) in 32-wide k-steps; each of its four waves owns a
 // quarter (4 x 4 or 2 x 4 MFMA tiles of 16 x 16). The next k-step's global
 // loads are issued before the current step's products. LDS rows are padded to
-// 80 bytes, which keeps each 16-lane fragment read on distinct banks. Up to
+// 96 bytes: against 80-byte rows that halves the bank-conflict cycles
+// (SQ_LDS_BANK_CONFLICT) of the large-v3 fc1 product. Up to
 // three weight matrices share one launch side by side (the encoder's q, k and
 // v; the cross keys and values).
 #include "device_common.h"
@@ -29,7 +30,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 constexpr int kTile = 128;
 constexpr int kStep = 32;
-constexpr int kRow = kStep + 8; // halves per LDS row
+constexpr int kRow = kStep + 16; // halves per LDS row (96 bytes)
 
 template <int WT>
 constexpr int parts_of()
