@@ -90,8 +90,8 @@ void Decoder::beginSequence(Pass& pass, const BufferRange& encoderOutput, const 
 bool Decoder::usesFusedStep(const DecoderWeights& weights, int tokenCount) const
 {
     const int headWidth = decoderShape.headWidth();
-    return fusedSteps && tokenCount == 1 && weights.uniformProjectionStorage().has_value() && headWidth % 4 == 0
-           && headWidth <= 64;
+    return fusedSteps && tokenCount >= 1 && tokenCount <= fusedPromptTokens
+           && weights.uniformProjectionStorage().has_value() && headWidth % 4 == 0 && headWidth <= 64;
 }
 
 void Decoder::step(Pass& pass, const BufferRange& tokens, int tokenCount, const DecoderWeights& weights,
@@ -102,7 +102,10 @@ void Decoder::step(Pass& pass, const BufferRange& tokens, int tokenCount, const 
 
     if (usesFusedStep(weights, tokenCount))
     {
-        fusedStep(pass, tokens, weights, logits, nullptr, nullptr);
+        // Token i at position + i sees the keys of every token before it, as
+        // the causal recorded step would (Kernels/Attention.h:34-47).
+        for (int i = 0; i < tokenCount; ++i)
+            fusedStep(pass, tokens, weights, logits, nullptr, nullptr, i);
         return;
     }
 
@@ -133,7 +136,7 @@ void Decoder::stepAndSample(Pass& pass, const BufferRange& tokens, const Decoder
 }
 
 void Decoder::fusedStep(Pass& pass, const BufferRange& tokens, const DecoderWeights& weights,
-                        const BufferRange& logits, const float* mask, const BufferRange* argmaxSlot)
+                        const BufferRange& logits, const float* mask, const BufferRange* argmaxSlot, int row)
 {
     if (pass.hipStream() != wsp_hip_stream(hipNet.context()))
         throw std::logic_error("a decoder records into the stream it was prepared with");
@@ -151,9 +154,11 @@ void Decoder::fusedStep(Pass& pass, const BufferRange& tokens, const DecoderWeig
     }
     const wsp_decoder_tensors tensors = decoderTable(weights, fusedLayers);
 
+    const auto r = (std::size_t) row;
     const int status = wsp_hip_decoder_step(
-        hipNet.context(), &tensors, static_cast<const uint32_t*>(tokens.data()), decodedPositions,
-        activeCrossPositions, static_cast<float*>(normalisedRows->data()), static_cast<float*>(logits.data()), mask,
+        hipNet.context(), &tensors, static_cast<const uint32_t*>(tokens.data()) + r, decodedPositions,
+        activeCrossPositions, static_cast<float*>(normalisedRows->data()) + r * (std::size_t) decoderShape.width,
+        static_cast<float*>(logits.data()) + r * (std::size_t) decoderShape.vocabularySize, mask,
         argmaxSlot != nullptr ? static_cast<uint32_t*>(argmaxSlot->data()) : nullptr);
     if (status != WSP_OK)
         throwForStatus(status, wsp_hip_last_error(hipNet.context()));
