@@ -355,7 +355,10 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
 constexpr int kNormedBlocks = 5;   // k-blocks per wave: inner <= 8 waves * 5 * 32 = 1280
 constexpr int kNormedWidth = kProductWaves * kNormedBlocks * 32;
 
-template <int WT, int MT>
+// NT column tiles of 16 per block: 2 when one tile a block would give more
+// blocks than CUs, so every block still has a CU of its own and the h rows are
+// loaded and normalised once for both tiles.
+template <int WT, int MT, int NT>
 __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product a)
 {
     constexpr int P = parts_of<WT>();
@@ -365,22 +368,27 @@ __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product
 
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int li = lane % 16, g = lane / 16;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * 16 * NT;
     const int kblocks = a.inner / 32;
     const int kb_begin = wave * kblocks / kProductWaves;
     const int kb_end = (wave + 1) * kblocks / kProductWaves;
     const int nkb = kb_end - kb_begin;
-    const u16* wrow = static_cast<const u16*>(a.w) + (size_t) min(n0 + li, a.out - 1) * a.inner + 8 * g;
+    const u16* wrow[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+        wrow[nt] = static_cast<const u16*>(a.w) + (size_t) min(n0 + nt * 16 + li, a.out - 1) * a.inner + 8 * g;
     const float* hrow = a.h + (size_t) li * a.inner + 8 * g;
 
-    u32x4 wv[kNormedBlocks];
+    u32x4 wv[kNormedBlocks][NT];
     float4v hv[kNormedBlocks][MT][2];
 #pragma unroll
     for (int u = 0; u < kNormedBlocks; ++u)
         if (u < nkb)
         {
             const int k = (kb_begin + u) * 32;
-            wv[u] = *reinterpret_cast<const u32x4*>(wrow + k);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+                wv[u][nt] = *reinterpret_cast<const u32x4*>(wrow[nt] + k);
 #pragma unroll
             for (int t = 0; t < MT; ++t)
             {
@@ -435,10 +443,12 @@ __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product
         }
     }
 
-    float4v acc[MT];
+    float4v acc[NT][MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-        acc[t] = float4v {0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+            acc[nt][t] = float4v {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < kNormedBlocks; ++u)
         if (u < nkb)
@@ -468,31 +478,36 @@ __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product
                         packed[p][e2] = lo16[p] | (hi16[p] << 16);
                 }
 #pragma unroll
-                for (int p = 0; p < P; ++p)
-                    acc[t] = mfma16<WT>(u32x4 {packed[p][0], packed[p][1], packed[p][2], packed[p][3]}, wv[u], acc[t]);
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int p = 0; p < P; ++p)
+                        acc[nt][t] = mfma16<WT>(u32x4 {packed[p][0], packed[p][1], packed[p][2], packed[p][3]},
+                                                wv[u][nt], acc[nt][t]);
             }
 
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-    {
-        __syncthreads();
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            partial[wave][lane * 4 + r] = acc[t][r];
-        __syncthreads();
-        if (threadIdx.x < 256)
+        for (int t = 0; t < MT; ++t)
         {
-            const int row = threadIdx.x / 16, col = threadIdx.x % 16;
-            const int src = ((row / 4) * 16 + col) * 4 + row % 4;
-            float v = 0.f;
+            __syncthreads();
 #pragma unroll
-            for (int w = 0; w < kProductWaves; ++w)
-                v += partial[w][src];
-            const int m = t * 16 + row, n = n0 + col;
-            if (m < a.rows && n < a.out)
-                finish<WT>(a, m, n, v);
+            for (int r = 0; r < 4; ++r)
+                partial[wave][lane * 4 + r] = acc[nt][t][r];
+            __syncthreads();
+            if (threadIdx.x < 256)
+            {
+                const int row = threadIdx.x / 16, col = threadIdx.x % 16;
+                const int src = ((row / 4) * 16 + col) * 4 + row % 4;
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < kProductWaves; ++w)
+                    v += partial[w][src];
+                const int m = t * 16 + row, n = n0 + nt * 16 + col;
+                if (m < a.rows && n < a.out)
+                    finish<WT>(a, m, n, v);
+            }
         }
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1090,14 +1105,33 @@ bool normed_fits(int rows, int inner)
     return row_tiles(rows) <= 2 && inner <= kNormedWidth && inner % 32 == 0;
 }
 
+int compute_units()
+{
+    static const int units = [] {
+        int device = 0, count = 0;
+        if (hipGetDevice(&device) == hipSuccess
+            && hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && count > 0)
+            return count;
+        return 256;
+    }();
+    return units;
+}
+
 template <int WT>
 hipError_t launch_normed_product(hipStream_t stream, const Product& a)
 {
-    const dim3 grid((a.out + 15) / 16);
-    if (row_tiles(a.rows) == 1)
-        hipLaunchKernelGGL((normed_product_kernel<WT, 1>), grid, dim3(kProductThreads), 0, stream, a);
+    const int tiles = (a.out + 15) / 16;
+    const bool pair = tiles > compute_units();
+    const dim3 grid(pair ? (tiles + 1) / 2 : tiles);
+    const bool two_rows = row_tiles(a.rows) != 1;
+    if (!pair && !two_rows)
+        hipLaunchKernelGGL((normed_product_kernel<WT, 1, 1>), grid, dim3(kProductThreads), 0, stream, a);
+    else if (!pair)
+        hipLaunchKernelGGL((normed_product_kernel<WT, 2, 1>), grid, dim3(kProductThreads), 0, stream, a);
+    else if (!two_rows)
+        hipLaunchKernelGGL((normed_product_kernel<WT, 1, 2>), grid, dim3(kProductThreads), 0, stream, a);
     else
-        hipLaunchKernelGGL((normed_product_kernel<WT, 2>), grid, dim3(kProductThreads), 0, stream, a);
+        hipLaunchKernelGGL((normed_product_kernel<WT, 2, 2>), grid, dim3(kProductThreads), 0, stream, a);
     return hipGetLastError();
 }
 
