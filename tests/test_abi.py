@@ -143,3 +143,18 @@ def test_net_refusals_without_a_device():
     result = subprocess.run([net_refusals(), "host"], capture_output=True, text=True, timeout=60)
     assert result.returncode == 0, result.stdout + result.stderr
     assert result.stdout.count("ok ") == 6, result.stdout
+
+
+def test_headers_compile_as_c99(tmp_path):
+    # The C ABI is meant for C callers (cgo, ctypes, plain C): both headers
+    # must stand alone as C99, with no C++ in their C view.
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    source = tmp_path / "check.c"
+    source.write_text('#include "wsp_hip.h"\n#include "wsp_decoder.h"\n'
+                      "int main(void) { wsp_whisper* w = 0; wsp_decoder* d = 0; (void) w; (void) d; return 0; }\n")
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    "-fsyntax-only", str(source)], check=True)
