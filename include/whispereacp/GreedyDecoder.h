@@ -39,11 +39,9 @@ public:
 private:
     Decoder& decoder;
     const DecoderWeights& weights;
-    Argmax selection;
     DeviceBuffer sequenceTokens; // uint32 [maxPositions + 1]
     DeviceBuffer logitRows;      // float [maxPositions, vocabularySize]
-    unsigned* hostSlots = nullptr; // pinned, one per step in flight
-    int* hostStatus = nullptr;     // pinned watchdog words, one per step in flight
+    int* hostReports = nullptr; // pinned (token, watchdog word) pairs, one per step in flight
     std::vector<void*> events;
 };
 } // namespace WSP

@@ -218,6 +218,15 @@ int wsp_hip_device_status(wsp_hip_ctx* ctx, int* status, int clear);
  * reference counterpart (see wsp_hip_device_status). */
 int wsp_hip_device_status_copy(wsp_hip_ctx* ctx, int* dst);
 
+/* One launch that writes, ordered after the work already on the context's
+ * stream, host_pair[0] = *slot (a sampled token, device memory) and
+ * host_pair[1] = the watchdog word (0 when the context runs no persistent
+ * step). host_pair is pinned host memory (hipHostMalloc). It replaces a token
+ * copy and a wsp_hip_device_status_copy in a greedy loop that reads each
+ * token behind an event: one small launch instead of two copies. No
+ * reference counterpart (see wsp_hip_device_status). */
+int wsp_hip_step_report(wsp_hip_ctx* ctx, const uint32_t* slot, int* host_pair);
+
 /* Sets the watchdog word as a tripped wait does: later persistent steps on
  * this context leave at their first long wait, and every caller that reads
  * the word reports the failure, until it is cleared. No reference

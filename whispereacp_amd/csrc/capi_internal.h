@@ -40,6 +40,7 @@ bool fused_persistent(const Context* ctx);
 int fused_status(Context* ctx, int* status, int clear);
 int fused_status_copy(Context* ctx, int* dst);
 int fused_raise_status(Context* ctx);
+int fused_report(Context* ctx, const uint32_t* slot, int* host_pair);
 
 // cross_kv.hip: K = X·Wkᵀ and V = X·Wvᵀ + bv for `rows` rows of `width`.
 int cross_kv_projection(Context* ctx, const float* x, int rows, int width, const void* wk, const void* wv,

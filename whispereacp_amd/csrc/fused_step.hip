@@ -512,6 +512,24 @@ int fused_status_copy(Context* ctx, int* dst)
                        "step status word");
 }
 
+// A sampled token and the watchdog word into pinned host memory: one thread,
+// system-scope stores, so the host reads both behind one event.
+__global__ void report_kernel(const uint32_t* slot, const int* status, int* host_pair)
+{
+    const int token = (int) __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int word = status != nullptr ? __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+    __hip_atomic_store(host_pair, token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(host_pair + 1, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+int fused_report(Context* ctx, const uint32_t* slot, int* host_pair)
+{
+    auto* state = static_cast<FusedState*>(ctx->fused);
+    const int* status = state != nullptr ? state->status : nullptr;
+    hipLaunchKernelGGL(report_kernel, dim3(1), dim3(1), 0, ctx->stream, slot, status, host_pair);
+    return context_hip(ctx, hipGetLastError(), "step report");
+}
+
 int fused_raise_status(Context* ctx)
 {
     auto* state = static_cast<FusedState*>(ctx->fused);
@@ -568,6 +586,13 @@ extern "C" int wsp_hip_device_status_copy(wsp_hip_ctx* ctx, int* dst)
     if (ctx == nullptr || dst == nullptr)
         return WSP_ERR_ARGUMENT;
     return wsp::fused_status_copy(ctx, dst);
+}
+
+extern "C" int wsp_hip_step_report(wsp_hip_ctx* ctx, const uint32_t* slot, int* host_pair)
+{
+    if (ctx == nullptr || slot == nullptr || host_pair == nullptr)
+        return WSP_ERR_ARGUMENT;
+    return wsp::fused_report(ctx, slot, host_pair);
 }
 
 extern "C" int wsp_hip_raise_device_status(wsp_hip_ctx* ctx)

@@ -3,10 +3,11 @@
 // last row under the first-step mask; step j decodes the slot step j-1
 // sampled into and samples under the later-step mask. The sampled token never
 // leaves the device on its way to the next step; the host reads each step's
-// slot through a pinned copy behind that step's event, stepsInFlight steps
-// ahead. The persistent step's watchdog word is read behind the same event: a
-// step whose hand-over timed out left its slot unwritten, so its token is
-// never used and the run ends in std::runtime_error (the word is cleared).
+// slot and the persistent step's watchdog word, written together into pinned
+// memory by one small launch behind the step, after that step's event,
+// stepsInFlight steps ahead. A step whose hand-over timed out left its slot
+// unwritten, so its token is never used and the run ends in
+// std::runtime_error (the word is cleared).
 #include "../../../include/whispereacp/GreedyDecoder.h"
 
 #include <hip/hip_runtime_api.h>
@@ -22,13 +23,9 @@ GreedyDecoder::GreedyDecoder(Decoder& decoderToUse, const DecoderWeights& weight
     : decoder(decoderToUse), weights(weightsToUse)
 {
     const DecoderShape& shape = decoder.shape();
-    void* stream = wsp_hip_stream(decoder.net().context());
-    selection.prepare(device, shape.maxPositions, shape.vocabularySize, stream);
     sequenceTokens = DeviceBuffer(device, (std::size_t) (shape.maxPositions + 1) * sizeof(std::uint32_t));
     logitRows = DeviceBuffer(device, (std::size_t) shape.maxPositions * shape.vocabularySize * sizeof(float));
-    checkHip(hipHostMalloc(reinterpret_cast<void**>(&hostSlots), stepsInFlight * sizeof(unsigned), 0),
-             "hipHostMalloc");
-    checkHip(hipHostMalloc(reinterpret_cast<void**>(&hostStatus), stepsInFlight * sizeof(int), 0),
+    checkHip(hipHostMalloc(reinterpret_cast<void**>(&hostReports), 2 * stepsInFlight * sizeof(int), 0),
              "hipHostMalloc");
     for (int i = 0; i < stepsInFlight; ++i)
     {
@@ -42,10 +39,8 @@ GreedyDecoder::~GreedyDecoder()
 {
     for (void* e : events)
         (void) hipEventDestroy(static_cast<hipEvent_t>(e));
-    if (hostSlots != nullptr)
-        (void) hipHostFree(hostSlots);
-    if (hostStatus != nullptr)
-        (void) hipHostFree(hostStatus);
+    if (hostReports != nullptr)
+        (void) hipHostFree(hostReports);
 }
 
 GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int crossPositionCount,
@@ -80,20 +75,24 @@ GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int 
         const int target = promptLength + step;
         if (step == 0)
         {
+            // The prompt but its last token, then the last token with the
+            // first step's sampling fused in: the same rows and the same token
+            // as the whole prompt followed by an argmax of its last row.
             decoder.beginSequence(pass, encoderRows, weights, crossPositionCount);
-            decoder.step(pass, BufferRange {sequenceTokens.data(), 0, (std::size_t) promptLength * slotBytes},
-                         promptLength, weights, BufferRange::of(logitRows));
-            selection.encode(pass, BufferRange {logitRows.data(), (std::size_t) (promptLength - 1) * rowBytes, rowBytes},
-                             firstMask, slot(target), 1, shape.vocabularySize);
+            if (promptLength > 1)
+                decoder.step(pass, BufferRange {sequenceTokens.data(), 0, (std::size_t) (promptLength - 1) * slotBytes},
+                             promptLength - 1, weights, BufferRange::of(logitRows));
+            decoder.stepAndSample(pass, slot(promptLength - 1), weights,
+                                  BufferRange {logitRows.data(), (std::size_t) (promptLength - 1) * rowBytes, rowBytes},
+                                  firstMask, slot(target));
         }
         else
             decoder.stepAndSample(pass, slot(target - 1), weights, BufferRange::of(logitRows), laterMask, slot(target));
-        checkHip(hipMemcpyAsync(&hostSlots[step % stepsInFlight], slot(target).data(), slotBytes,
-                                hipMemcpyDeviceToHost, stream),
-                 "read token");
-        const int copied = wsp_hip_device_status_copy(context, &hostStatus[step % stepsInFlight]);
-        if (copied != WSP_OK)
-            throw std::runtime_error(std::string("read the step watchdog: ") + wsp_hip_last_error(context));
+        // The token and the watchdog word in one launch behind the step.
+        const int reported = wsp_hip_step_report(context, static_cast<const std::uint32_t*>(slot(target).data()),
+                                                 &hostReports[2 * (step % stepsInFlight)]);
+        if (reported != WSP_OK)
+            throw std::runtime_error(std::string("report the step's token: ") + wsp_hip_last_error(context));
         checkHip(hipEventRecord(static_cast<hipEvent_t>(events[(std::size_t) (step % stepsInFlight)]), stream),
                  "hipEventRecord");
     };
@@ -108,7 +107,8 @@ GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int 
     {
         checkHip(hipEventSynchronize(static_cast<hipEvent_t>(events[(std::size_t) (step % stepsInFlight)])),
                  "hipEventSynchronize");
-        if (hostStatus[step % stepsInFlight] != 0)
+        const int* report = &hostReports[2 * (step % stepsInFlight)];
+        if (report[1] != 0)
         {
             // Drain what is in flight, then clear the word for the next run.
             (void) hipStreamSynchronize(stream);
@@ -117,7 +117,7 @@ GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int 
             throw std::runtime_error("greedy decode: step " + std::to_string(step)
                                      + " timed out on the device (its hand-over watchdog tripped)");
         }
-        const int sampled = (int) hostSlots[step % stepsInFlight];
+        const int sampled = report[0];
         ++run.steps;
         if (sampled == endOfText)
             break;
