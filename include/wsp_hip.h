@@ -254,7 +254,7 @@ typedef struct wsp_cross_tensors
 typedef struct wsp_batch wsp_batch;
 
 /* Allocates every stream's caches (self [layers][streams][max_positions][width],
- * cross [layers][streams][cross_positions][width], f32) and the step buffers
+ * cross [layers][cross_positions][streams][width] — key-major — f32) and the step buffers
  * for up to max_step_tokens tokens per stream per step; streams ×
  * max_step_tokens ≤ 128. wdtype is the projections' storage (WSP_F16 or
  * WSP_BF16). Decoder::prepare's role (Decoder/Decoder.cpp:194-227), per stream. */
@@ -295,7 +295,8 @@ int wsp_batch_ring_step(wsp_batch* batch, const wsp_decoder_tensors* tensors, ui
                         const float* mask);
 
 /* Layer `layer`'s caches of stream 0; stream s starts max_positions·width
- * (self) or cross_positions·width (cross) floats later. */
+ * (self) floats later, key k of stream s of the cross caches sits at
+ * (k·streams + s)·width. */
 int wsp_batch_self_cache(const wsp_batch* batch, int layer, const float** keys, const float** values);
 int wsp_batch_cross_cache(const wsp_batch* batch, int layer, const float** keys, const float** values);
 

@@ -32,16 +32,18 @@ def library():
     ensure_library()
 
 
-def batched_greedy(decoder, shape, encoders, prompt, steps, mask=None, cross_rows=0):
+def batched_greedy(decoder, shape, encoders, prompt, steps, mask=None, cross_rows=0, encoder_rows=None):
     """begin for every stream, the prompt as one causal step per stream, then
     `steps` single-token steps whose argmax feeds the next step on the device.
     Returns per stream: tokens (prompt argmax first), the single-token steps'
-    logits rows [steps, V] and the prompt step's logits [t, V]."""
+    logits rows [steps, V] and the prompt step's logits [t, V]. encoder_rows,
+    when given, is the device block begin reads instead of `encoders`."""
     import torch
     from whispereacp_amd.decoder import to_device
     streams, V, t = len(encoders), shape.vocabulary_size, len(prompt)
-    enc = to_device(np.ascontiguousarray(np.stack(encoders), dtype=np.float32))
-    decoder.begin(enc, cross_rows)
+    if encoder_rows is None:
+        encoder_rows = to_device(np.ascontiguousarray(np.stack(encoders), dtype=np.float32))
+    decoder.begin(encoder_rows, cross_rows)
     tokens = torch.tensor([list(prompt)] * streams, dtype=torch.int32, device="cuda")
     slots = torch.zeros((steps + 1, streams), dtype=torch.int32, device="cuda")
     prompt_logits = torch.empty((streams * t, V), dtype=torch.float32, device="cuda")
@@ -211,6 +213,28 @@ def test_long_sequence_splits_self_keys(oracle):
     tokens, rows, _ = batched_greedy(decoder, shape, encoders, prompt, 300)
     for s in range(2):
         ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, encoders[s], prompt, 300)
+        check_run(tokens[s], rows[s], ref_tokens, ref_rows, 2e-2)
+
+
+def test_unaligned_encoder_rows_take_the_per_stream_projection(oracle):
+    # Encoder rows 4 bytes past a 16-byte boundary cannot feed the tile
+    # product: each stream's cross keys and values are projected alone into a
+    # scratch block and copied into the key-major cache.
+    import torch
+    from whispereacp_amd.decoder import BatchedDecoder
+    shape = S.DecoderShape(128, 2, 2, 512, 1000, 448, 64)
+    f = S.workload_decoder_file(shape, "F16", 93)
+    encoders = [S.normal_encoder_output(64, shape.width, 900 + s) for s in range(3)]
+    prompt, steps = [1, 2, 3, 4], 10
+    flat = np.ascontiguousarray(np.stack(encoders), dtype=np.float32).ravel()
+    buffer = torch.empty(flat.size + 1, dtype=torch.float32, device="cuda")
+    buffer[1:].copy_(torch.from_numpy(flat))
+    rows_view = buffer[1:].view(3, 64, shape.width)
+    assert rows_view.data_ptr() % 16 == 4
+    decoder = BatchedDecoder(shape, f, streams=3)
+    tokens, rows, _ = batched_greedy(decoder, shape, [None] * 3, prompt, steps, encoder_rows=rows_view)
+    for s in range(3):
+        ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, encoders[s], prompt, steps)
         check_run(tokens[s], rows[s], ref_tokens, ref_rows, 2e-2)
 
 

@@ -897,7 +897,8 @@ struct Attend
     const float* q;       // [rows][width]
     const float* keys;    // stream 0's cache of this layer, [capacity][width]
     const float* values;
-    size_t stream_stride; // elements between streams' caches
+    size_t stream_stride; // elements between streams' first keys
+    size_t key_stride;    // elements between one stream's consecutive keys
     const int* state;     // device word: the position of the step's first token
     int k_count, step_tokens, causal, heads, head_width, width; // k_count: cross rows (causal: unused)
     float scale;
@@ -942,8 +943,8 @@ __global__ void __launch_bounds__(kAttendThreads) attend_kernel(Attend a)
         for (int u = 0; u < 8; ++u)
         {
             const size_t key = (size_t) min(ts + group + 16 * u, last - 1);
-            kv[u] = *reinterpret_cast<const float4v*>(kbase + key * a.width);
-            vv[u] = *reinterpret_cast<const float4v*>(vbase + key * a.width);
+            kv[u] = *reinterpret_cast<const float4v*>(kbase + key * a.key_stride);
+            vv[u] = *reinterpret_cast<const float4v*>(vbase + key * a.key_stride);
         }
         float s[8];
         float tile_max = -INFINITY;
@@ -1018,30 +1019,176 @@ __global__ void __launch_bounds__(kAttendThreads) attend_kernel(Attend a)
     }
 }
 
+// The chunks of one (row, head) combined in chunk order: every chunk's
+// maximum is read at once (one chunk a lane) and reduced, then the factors
+// exp(m_k - m) of a run of up to 64 chunks go through LDS, so the row's loads
+// for the whole run are independent of each other.
 template <int WT>
 __global__ void __launch_bounds__(kWave) combine_kernel(const float* __restrict__ partials, int heads,
                                                         int head_width, int chunks, int width, u16* xs,
                                                         size_t xs_part)
 {
+    __shared__ float factor[kWave], weight[kWave];
     const int head = blockIdx.x % heads, row = blockIdx.x / heads;
-    const int c = threadIdx.x;
-    if (c >= head_width)
-        return;
-    const float* base = partials + ((size_t) row * heads + head) * chunks * (head_width + 2);
+    const int lane = threadIdx.x;
+    const size_t stride = (size_t) head_width + 2;
+    const float* base = partials + ((size_t) row * heads + head) * chunks * stride;
     float largest = -INFINITY;
-    for (int k = 0; k < chunks; ++k)
-        largest = fmaxf(largest, base[(size_t) k * (head_width + 2)]);
+    for (int k = lane; k < chunks; k += kWave)
+        largest = fmaxf(largest, base[k * stride]);
+#pragma unroll
+    for (int offset = 1; offset < kWave; offset <<= 1)
+        largest = fmaxf(largest, __shfl_xor(largest, offset));
     float numerator = 0.f, denominator = 0.f;
-    for (int k = 0; k < chunks; ++k)
+    for (int k0 = 0; k0 < chunks; k0 += kWave)
     {
-        const float* part = base + (size_t) k * (head_width + 2);
-        if (part[1] == 0.f)
-            continue;
-        const float factor = expf(part[0] - largest);
-        numerator += factor * part[2 + c];
-        denominator += factor * part[1];
+        float f = 0.f, sum = 0.f;
+        if (k0 + lane < chunks)
+        {
+            sum = base[(k0 + lane) * stride + 1];
+            if (sum != 0.f) // an empty chunk (no visible key) adds nothing
+                f = expf(base[(k0 + lane) * stride] - largest);
+        }
+        __syncthreads();
+        factor[lane] = f;
+        weight[lane] = f * sum;
+        __syncthreads();
+        const int run = min(kWave, chunks - k0);
+        if (lane < head_width)
+        {
+            const float* column = base + (size_t) k0 * stride + 2 + lane;
+#pragma unroll 8
+            for (int i = 0; i < run; ++i)
+            {
+                numerator += factor[i] * column[i * stride];
+                denominator += weight[i];
+            }
+        }
     }
-    store_split<WT>(xs, xs_part, (size_t) row * width + head * head_width + c, numerator / denominator);
+    if (lane < head_width)
+        store_split<WT>(xs, xs_part, (size_t) row * width + head * head_width + lane, numerator / denominator);
+}
+
+// ---------------------------------------------------------------------------
+// Cross attention of one query row per stream by key sweep. The cross caches
+// are key-major ([key][stream][width]), and block (stream, j) takes every head
+// of its stream over the key passes j, j + G, j + 2G, ... of KR·8 keys each
+// (G blocks a stream, blocks of one key range adjacent), so at any time the
+// chip reads one front of whole rows moving through memory instead of one
+// short strided run per (head, chunk). One block a CU with nontemporal loads
+// keeps about 80-128 KB of loads in flight per CU, which streams faster than
+// more blocks with more loads in flight. Thread (kr, quad) holds channels
+// 4·quad.. (head quad / 16) of keys first + kr + KR·u; each 16-lane row keeps
+// its own running (max, sum, row) over its keys, so the loop has no barrier.
+// The KR key lanes are folded in order through LDS at the end; the block then
+// writes one (max, sum, row) partial per head for combine_kernel
+// (Kernels/SingleQueryAttention.h:27-37), or with G = 1 the normalised row
+// itself. Head width 64.
+// ---------------------------------------------------------------------------
+constexpr int kSweepKeys = 8;       // keys per lane per pass
+constexpr int kSweepBlocksPerCU = 1;
+constexpr int kSweepThreads = 512;  // most threads a sweep block takes
+constexpr int kMaxSweepGroups = 32; // most blocks per stream
+
+template <int WT>
+__global__ void __launch_bounds__(kSweepThreads) sweep_attend_kernel(Attend a, int key_lanes, int groups)
+{
+    extern __shared__ float4v fold[]; // [key_lanes][quads] rows, then [key_lanes][heads] maxima and sums
+    const int quads = a.width / 4;
+    const int quad = threadIdx.x % quads, kr = threadIdx.x / quads;
+    const int streams = gridDim.x / groups;
+    const int stream = blockIdx.x % streams, j = blockIdx.x / streams; // blocks of one key range adjacent
+    const int head = quad / 16, lane16 = quad % 16;
+    const float4v qv = *reinterpret_cast<const float4v*>(a.q + (size_t) stream * a.width + 4 * quad);
+    const float* kbase = a.keys + (size_t) stream * a.stream_stride + 4 * quad;
+    const float* vbase = a.values + (size_t) stream * a.stream_stride + 4 * quad;
+    const int pass_keys = key_lanes * kSweepKeys;
+
+    float run_max = -INFINITY, run_sum = 0.f;
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+    for (int first = j * pass_keys; first < a.k_count; first += groups * pass_keys)
+    {
+        float4v kv[kSweepKeys], vv[kSweepKeys];
+#pragma unroll
+        for (int u = 0; u < kSweepKeys; ++u)
+        {
+            const size_t key = (size_t) min(first + kr + key_lanes * u, a.k_count - 1);
+            kv[u] = __builtin_nontemporal_load(reinterpret_cast<const float4v*>(kbase + key * a.key_stride));
+            vv[u] = __builtin_nontemporal_load(reinterpret_cast<const float4v*>(vbase + key * a.key_stride));
+        }
+        float s[kSweepKeys];
+        float tile_max = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < kSweepKeys; ++u)
+        {
+            const float part = sum16(qv[0] * kv[u][0] + qv[1] * kv[u][1] + qv[2] * kv[u][2] + qv[3] * kv[u][3]);
+            s[u] = first + kr + key_lanes * u < a.k_count ? a.scale * part : -INFINITY;
+            tile_max = fmaxf(tile_max, s[u]);
+        }
+        const float new_max = fmaxf(run_max, tile_max);
+        if (new_max != -INFINITY) // every key of this lane's pass past the end: nothing to fold
+        {
+            const float factor = expf(run_max - new_max);
+            float psum = 0.f;
+            float4v pv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < kSweepKeys; ++u)
+            {
+                const float p = expf(s[u] - new_max);
+                psum += p;
+                pv += p * vv[u];
+            }
+            run_sum = run_sum * factor + psum;
+            acc = acc * factor + pv;
+            run_max = new_max;
+        }
+    }
+
+    if (key_lanes > 1)
+    {
+        const int heads = quads / 16;
+        float* maxima = reinterpret_cast<float*>(fold + key_lanes * quads);
+        float* sums = maxima + key_lanes * heads;
+        fold[kr * quads + quad] = acc;
+        if (lane16 == 0)
+        {
+            maxima[kr * heads + head] = run_max;
+            sums[kr * heads + head] = run_sum;
+        }
+        __syncthreads();
+        if (kr != 0)
+            return;
+        float largest = -INFINITY;
+        for (int k = 0; k < key_lanes; ++k)
+            largest = fmaxf(largest, maxima[k * heads + head]);
+        run_sum = 0.f;
+        acc = float4v {0.f, 0.f, 0.f, 0.f};
+        if (largest != -INFINITY)
+            for (int k = 0; k < key_lanes; ++k)
+            {
+                const float factor = expf(maxima[k * heads + head] - largest);
+                run_sum += factor * sums[k * heads + head];
+                acc += factor * fold[k * quads + quad];
+            }
+        run_max = largest;
+    }
+
+    if (groups == 1)
+    {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            store_split<WT>(a.xs, a.xs_part, (size_t) stream * a.width + 4 * quad + r, acc[r] / run_sum);
+        return;
+    }
+    float* part = a.partials + (((size_t) stream * a.heads + head) * groups + j) * (a.head_width + 2);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        part[2 + 4 * lane16 + r] = acc[r];
+    if (lane16 == 0)
+    {
+        part[0] = run_max;
+        part[1] = run_sum;
+    }
 }
 
 // The step's last launch: with a ring, each stream's greedy token goes to the
@@ -1214,6 +1361,47 @@ hipError_t launch_attend(hipStream_t stream, Attend a, int rows, int span, int c
                        a.head_width, a.chunks, a.width, a.xs, a.xs_part);
     return hipGetLastError();
 }
+
+// Key lanes of a sweep block for this width: the fewest that make whole
+// waves, doubled while the block stays within kSweepThreads; 0 when the
+// shape does not fit (head width other than 64, or one key lane already too
+// wide).
+int sweep_key_lanes(int width, int heads)
+{
+    if (heads <= 0 || width != heads * 64)
+        return 0;
+    const int quads = width / 4;
+    int lanes = 1;
+    while ((quads * lanes) % kWave != 0)
+        lanes *= 2;
+    if (quads * lanes > kSweepThreads)
+        return 0;
+    while (quads * lanes * 2 <= kSweepThreads)
+        lanes *= 2;
+    return lanes;
+}
+
+// Cross attention of one row per stream by key sweep: about `target` blocks
+// (a whole number per stream, at most kMaxSweepGroups and at most one per key
+// pass), then the combine of each (stream, head)'s partials.
+template <int WT>
+hipError_t launch_sweep_attend(hipStream_t stream, Attend a, int streams, int lanes, int target)
+{
+    const int quads = a.width / 4;
+    const int pass_keys = lanes * kSweepKeys;
+    const int passes = (a.k_count + pass_keys - 1) / pass_keys;
+    const int groups = std::max(1, std::min({kMaxSweepGroups, passes, (target + streams / 2) / streams}));
+    const size_t lds = lanes > 1 ? (size_t) lanes * quads * sizeof(float4v) + 2 * (size_t) lanes * a.heads * sizeof(float)
+                                 : 0;
+    hipLaunchKernelGGL((sweep_attend_kernel<WT>), dim3(streams * groups), dim3(quads * lanes), lds, stream, a, lanes,
+                       groups);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || groups == 1)
+        return e;
+    hipLaunchKernelGGL((combine_kernel<WT>), dim3(streams * a.heads), dim3(kWave), 0, stream, a.partials, a.heads,
+                       a.head_width, groups, a.width, a.xs, a.xs_part);
+    return hipGetLastError();
+}
 } // namespace
 } // namespace wsp::batch
 
@@ -1228,11 +1416,13 @@ struct wsp_batch
     int rows_cap = 0, rows_padded = 0;
     int position = 0, cross_rows = 0;
     int cross_target = 1536; // cross-attention blocks per launch: one round of resident blocks
+    int sweep_target = 512;  // key-sweep cross-attention blocks per launch
 
     float* self_keys = nullptr;   // [layers][streams][max_positions][width]
     float* self_values = nullptr;
-    float* cross_keys = nullptr;  // [layers][streams][cross_positions][width]
+    float* cross_keys = nullptr;  // [layers][cross_positions][streams][width]
     float* cross_values = nullptr;
+    float* cross_scratch = nullptr; // [cross_positions][width], made by the first begin that needs it
     float* h = nullptr;           // [rows_padded][width] residual stream
     float* q = nullptr;           // [rows_padded][width] queries
     uint16_t* xs = nullptr;       // [parts][rows_padded][width]
@@ -1293,6 +1483,19 @@ size_t self_layer_stride(const wsp_batch* b)
 size_t cross_layer_stride(const wsp_batch* b)
 {
     return (size_t) b->streams * b->shape.cross_positions * b->shape.width;
+}
+
+// Cross caches are key-major, [cross_positions][streams][width]: key k of
+// every stream is one contiguous run, so the blocks of a key sweep that take
+// the same keys of all streams read one front of memory together.
+size_t cross_stream_stride(const wsp_batch* b)
+{
+    return (size_t) b->shape.width;
+}
+
+size_t cross_key_stride(const wsp_batch* b)
+{
+    return (size_t) b->streams * b->shape.width;
 }
 
 void release(wsp_batch* b)
@@ -1393,6 +1596,8 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
     at.partials = b->partials;
     at.state = b->state;
     const int self_span = io.fixed_grid ? s.max_positions : b->position + count;
+    // One query row per stream: the cross attention sweeps each stream's keys.
+    const int sweep_lanes = count == 1 ? wsp::batch::sweep_key_lanes(d, H) : 0;
 
     // Decode steps fold each LayerNorm into the product that consumes it.
     const bool normed = wsp::batch::normed_fits(rows, d);
@@ -1444,6 +1649,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         at.keys = self_k;
         at.values = self_v;
         at.stream_stride = (size_t) s.max_positions * d;
+        at.key_stride = d;
         at.k_count = 0;
         at.causal = 1;
         if ((e = launch_attend<WT>(st, at, rows, self_span, b->cross_target)) != hipSuccess)
@@ -1472,10 +1678,13 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
 
         at.keys = cross_k;
         at.values = cross_v;
-        at.stream_stride = (size_t) s.cross_positions * d;
+        at.stream_stride = cross_stream_stride(b);
+        at.key_stride = cross_key_stride(b);
         at.k_count = b->cross_rows;
         at.causal = 0;
-        if ((e = launch_attend<WT>(st, at, rows, b->cross_rows, b->cross_target)) != hipSuccess)
+        e = sweep_lanes > 0 ? launch_sweep_attend<WT>(st, at, rows, sweep_lanes, b->sweep_target)
+                            : launch_attend<WT>(st, at, rows, b->cross_rows, b->cross_target);
+        if (e != hipSuccess)
             return hip_fail(b, e, "cross attention");
 
         p.w = L.cross_out_w;
@@ -1653,8 +1862,9 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
     const size_t d = (size_t) s.width, H = (size_t) s.heads, hd = d / H;
     const size_t stat_groups = (d + wsp::batch::kGroupColumns - 1) / wsp::batch::kGroupColumns;
     const size_t split_groups = (d + wsp::batch::kTileColumns - 1) / wsp::batch::kTileColumns; // fc2
-    const int most_chunks = std::max((s.cross_positions + wsp::batch::kTileKeys - 1) / wsp::batch::kTileKeys,
-                                     (s.max_positions + wsp::batch::kTileKeys - 1) / wsp::batch::kTileKeys);
+    const int most_chunks = std::max({(s.cross_positions + wsp::batch::kTileKeys - 1) / wsp::batch::kTileKeys,
+                                      (s.max_positions + wsp::batch::kTileKeys - 1) / wsp::batch::kTileKeys,
+                                      wsp::batch::kMaxSweepGroups});
     const int groups = wsp::ops::argmax_groups(s.vocabulary_size);
     hipError_t e = hipSetDevice(device);
     if (e == hipSuccess)
@@ -1709,6 +1919,8 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
                                                             wsp::batch::kAttendThreads, 0) == hipSuccess
             && cus > 0 && per_cu > 0)
             b->cross_target = cus * per_cu;
+        if (cus > 0)
+            b->sweep_target = wsp::batch::kSweepBlocksPerCU * cus;
     }
     // Padding rows of the split buffer are read by the products (their sums
     // are discarded); zero them once so they hold finite values.
@@ -1792,9 +2004,9 @@ int wsp_batch_begin(wsp_batch* b, const wsp_cross_tensors* layers, int wdtype, c
             p.bias1 = L.value_b;
             p.y0 = keys;
             p.y1 = values;
-            p.ldy = d;
+            p.ldy = (int) cross_key_stride(b);
             p.rows_per_group = cross_rows;
-            p.group_stride = (size_t) b->shape.cross_positions * d;
+            p.group_stride = cross_stream_stride(b);
             p.wdtype = wdtype;
             e = wsp::ops::tile_product(b->stream, p);
         }
@@ -1802,10 +2014,23 @@ int wsp_batch_begin(wsp_batch* b, const wsp_cross_tensors* layers, int wdtype, c
             for (int c = 0; c < b->streams && e == hipSuccess; ++c)
             {
                 const float* x = encoder_rows + (size_t) c * cross_rows * d;
-                const size_t at = (size_t) c * b->shape.cross_positions * d;
-                e = wsp::ops::linear(b->stream, x, cross_rows, d, L.key_w, wdtype, nullptr, keys + at, d, 0);
+                // Dense rows into the scratch block, then strided into the
+                // key-major cache.
+                const size_t at = (size_t) c * cross_stream_stride(b);
+                const size_t pitch = cross_key_stride(b) * sizeof(float), row = (size_t) d * sizeof(float);
+                if (b->cross_scratch == nullptr)
+                    e = allocate(b, &b->cross_scratch, (size_t) b->shape.cross_positions * d);
                 if (e == hipSuccess)
-                    e = wsp::ops::linear(b->stream, x, cross_rows, d, L.value_w, wdtype, L.value_b, values + at, d, 0);
+                    e = wsp::ops::linear(b->stream, x, cross_rows, d, L.key_w, wdtype, nullptr, b->cross_scratch, d, 0);
+                if (e == hipSuccess)
+                    e = hipMemcpy2DAsync(keys + at, pitch, b->cross_scratch, row, row, cross_rows,
+                                         hipMemcpyDeviceToDevice, b->stream);
+                if (e == hipSuccess)
+                    e = wsp::ops::linear(b->stream, x, cross_rows, d, L.value_w, wdtype, L.value_b, b->cross_scratch,
+                                         d, 0);
+                if (e == hipSuccess)
+                    e = hipMemcpy2DAsync(values + at, pitch, b->cross_scratch, row, row, cross_rows,
+                                         hipMemcpyDeviceToDevice, b->stream);
             }
         if (e != hipSuccess)
             return hip_fail(b, e, "cross key/value projection");

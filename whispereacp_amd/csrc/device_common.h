@@ -40,6 +40,34 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* global_mut(T* p)
     return (__attribute__((address_space(1))) T*) p;
 }
 
+// Sums within a 16-lane DPP row in a fixed order: swap neighbours, swap
+// pairs, mirror within 8 and mirror within 16 leave the row total in every
+// lane, each step one v_add_f32_dpp. Every pair is added in an
+// order-independent way (a + b == b + a), so every lane of the row holds the
+// same bits. Every lane of the row must be active.
+// (bound_ctrl set: every pattern used reads a lane of the same row, so no lane
+// reads out of range, and the move folds into the consuming add as one
+// v_add_f32_dpp.)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+constexpr int kSwapNeighbours = 0xB1; // quad_perm [1,0,3,2]
+constexpr int kSwapPairs = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kMirrorHalfRow = 0x141; // row_half_mirror
+constexpr int kMirrorRow = 0x140;     // row_mirror
+
+__device__ __forceinline__ float sum16(float v)
+{
+    v += dpp<kSwapNeighbours>(v);
+    v += dpp<kSwapPairs>(v);
+    v += dpp<kMirrorHalfRow>(v);
+    v += dpp<kMirrorRow>(v);
+    return v;
+}
+
 // 16 bytes from global memory.
 __device__ __forceinline__ uint4 load_global16(const void* p)
 {

@@ -91,29 +91,14 @@ __device__ __forceinline__ uint64_t peek(const uint64_t* p)
 }
 
 // ---------------------------------------------------------------------------
-// Cross-lane sums and maxima in a fixed order. A DPP "row" is 16 lanes: swap
-// neighbours, swap pairs, mirror within 8 and mirror within 16 leave the row
-// total in every lane; a permlane16 swap then adds the neighbouring row (lane
-// l and lane l ^ 16) and a permlane32 swap the other half of the wave (lane l
-// and lane l ^ 32). Both swaps are VALU operations of gfx950: no LDS round
-// trip and no scalar register. Every pair is added in an order-independent
-// way (a + b == b + a), so every lane of the span holds the same bits. Every
-// lane of the span must be active.
+// Cross-lane sums and maxima in a fixed order. Within a 16-lane row, sum16
+// (device_common.h) leaves the row total in every lane; a permlane16 swap
+// then adds the neighbouring row (lane l and lane l ^ 16) and a permlane32
+// swap the other half of the wave (lane l and lane l ^ 32). Both swaps are
+// VALU operations of gfx950: no LDS round trip and no scalar register. Every
+// pair is added in an order-independent way (a + b == b + a), so every lane
+// of the span holds the same bits. Every lane of the span must be active.
 // ---------------------------------------------------------------------------
-// (bound_ctrl set: every pattern used reads a lane of the same row, so no lane
-// reads out of range, and the move folds into the consuming add as one
-// v_add_f32_dpp.)
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v)
-{
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
-}
-
-constexpr int kSwapNeighbours = 0xB1; // quad_perm [1,0,3,2]
-constexpr int kSwapPairs = 0x4E;      // quad_perm [2,3,0,1]
-constexpr int kMirrorHalfRow = 0x141; // row_half_mirror
-constexpr int kMirrorRow = 0x140;     // row_mirror
-
 // Lane l's value and lane (l ^ 16)'s, in an order that depends only on l.
 __device__ __forceinline__ void rows_pair_bits(uint32_t v, uint32_t& a, uint32_t& b)
 {
@@ -163,15 +148,6 @@ __device__ __forceinline__ float add32(float v)
 __device__ __forceinline__ float halves_sum(float v)
 {
     return add32(v);
-}
-
-__device__ __forceinline__ float sum16(float v)
-{
-    v += dpp<kSwapNeighbours>(v);
-    v += dpp<kSwapPairs>(v);
-    v += dpp<kMirrorHalfRow>(v);
-    v += dpp<kMirrorRow>(v);
-    return v;
 }
 
 __device__ __forceinline__ float sum32(float v)
