@@ -73,6 +73,18 @@ __device__ __forceinline__ void store_split(u16* out, size_t part_stride, size_t
     }
 }
 
+// Split activations ([parts][rows_padded][width]) are stored fragment-major:
+// the 16 rows x 32 inner values one v_mfma_f32_16x16x32 A-operand load covers
+// are 64 lanes x 16 contiguous bytes in lane order (lane 16g + r holds row r,
+// values 8g..8g+7), so a wave reads each fragment as one contiguous kilobyte.
+// Read row by row (16 rows x 64 bytes a load) the same activations took 6.5
+// of an 80-block product's 9.6 us; fragment-major, 1.9.
+__device__ __forceinline__ size_t fragment_index(int row, int col, int width)
+{
+    const int t = row / 16, r = row % 16, kb = col / 32, g = (col % 32) / 8, e = col % 8;
+    return (((size_t) t * (width / 32) + kb) * 64 + g * 16 + r) * 8 + e;
+}
+
 // The same parts as register values.
 template <int WT>
 __device__ __forceinline__ void split_value(float x, u16 (&out)[parts_of<WT>()])
@@ -119,7 +131,7 @@ struct Norm
     const float* gamma;
     const float* beta;
     float eps;
-    u16* xs;              // split output [parts][rows_padded][width]
+    u16* xs;              // split output [parts][rows_padded][width], fragment-major
     size_t xs_part;
     float* y;             // optional f32 copy of the normalised rows
     const uint32_t* tokens; // [streams][step_tokens], or null with a ring
@@ -162,7 +174,7 @@ __global__ void __launch_bounds__(kNormThreads) norm_kernel(Norm a)
     for (int c = threadIdx.x; c < a.width; c += kNormThreads)
     {
         const float v = (h[c] - mean) * scale * a.gamma[c] + a.beta[c];
-        store_split<WT>(a.xs, a.xs_part, (size_t) row * a.width + c, v);
+        store_split<WT>(a.xs, a.xs_part, fragment_index(row, c, a.width), v);
         if (a.y != nullptr)
             a.y[(size_t) row * a.width + c] = v;
     }
@@ -172,17 +184,16 @@ __global__ void __launch_bounds__(kNormThreads) norm_kernel(Norm a)
 // Skinny product y[m, n] = Σ_k x[m, k]·W[n, k] for up to 128 rows. A block
 // owns 16 output columns for every row tile; its 8 waves split the inner
 // dimension into contiguous runs of 32-wide k-blocks, each lane loading 16
-// bytes of one weight row and of each split activation row per k-block
+// bytes of one weight row and of each split activation fragment per k-block
 // (v_mfma_f32_16x16x32: A = activations, lane l row l % 16; B = weights,
 // lane l column l % 16; both with k = 8(l / 16) + j). KB k-blocks are loaded
-// before their products, the next batch's weights ahead of them. The 8 wave
-// partials are summed in wave order.
+// before their products, the next batch's weights ahead of them. The 8 run
+// partials are summed in run order.
 // ---------------------------------------------------------------------------
 enum Epilogue : int
 {
     kStore = 0,     // y = acc + bias
     kResidual = 1,  // y += acc + bias
-    kGeluSplit = 2, // split parts of gelu(acc + bias) into xs_out [parts][rows_padded][out]
     kQkv = 3,       // q | self key row | self value row
     kGelu = 4       // y = gelu(acc + bias), fp32
 };
@@ -197,8 +208,6 @@ struct Product
     int epilogue;
     float* y;
     int ldy;
-    u16* xs_out;
-    size_t xs_out_part;
     float* q;
     float* keys;      // stream 0's cache of this layer
     float* values;
@@ -212,15 +221,15 @@ struct Product
     float eps;
 };
 
+// `prior` is y[m][n] read before the product (kResidual; unused otherwise).
 template <int WT>
-__device__ __forceinline__ void finish(const Product& a, int m, int n, float acc)
+__device__ __forceinline__ void finish(const Product& a, int m, int n, float acc, float prior = 0.f)
 {
     const float v = acc + (a.bias != nullptr ? a.bias[n] : 0.f);
     switch (a.epilogue)
     {
         case kStore: a.y[(size_t) m * a.ldy + n] = v; break;
-        case kResidual: a.y[(size_t) m * a.ldy + n] += v; break;
-        case kGeluSplit: store_split<WT>(a.xs_out, a.xs_out_part, (size_t) m * a.out + n, exact_gelu(v)); break;
+        case kResidual: a.y[(size_t) m * a.ldy + n] = prior + v; break;
         case kGelu: a.y[(size_t) m * a.ldy + n] = exact_gelu(v); break;
         default:
         {
@@ -237,6 +246,18 @@ __device__ __forceinline__ void finish(const Product& a, int m, int n, float acc
     }
 }
 
+// The run of the inner dimension wave `wave` of this block takes. Every block
+// reads all of the activations, and the blocks of one XCD (every eighth
+// block) would otherwise read them in the same order at the same time, all
+// on the same few L2 channels: rotating the runs by the block's place on its
+// XCD spreads them (measured: the activation reads of an 80-block product
+// took 6.5 of its 9.6 us unrotated). Partials are kept by run and summed in
+// run order, so the arithmetic is the same for every rotation.
+__device__ __forceinline__ int inner_run(int wave)
+{
+    return (wave + (int) blockIdx.x / 8) % kProductWaves;
+}
+
 // k-blocks a wave loads at once: as many as about 160 registers of weight
 // and activation fragments hold (4 + 4·P·MT per k-block), at most 8.
 template <int P, int MT>
@@ -251,18 +272,19 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
 {
     constexpr int P = parts_of<WT>();
     constexpr int KB = kblocks_per_load<P, MT>();
-    __shared__ float partial[kProductWaves][256];
+    constexpr int OUTS = (MT * 256 + kProductThreads - 1) / kProductThreads; // outputs a thread finishes
+    __shared__ float partial[kProductWaves][MT * 256];
 
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int li = lane % 16, g = lane / 16;
     const int n0 = blockIdx.x * 16;
     const int kblocks = a.inner / 32;
-    const int kb_begin = wave * kblocks / kProductWaves;
-    const int kb_end = (wave + 1) * kblocks / kProductWaves;
+    const int run = inner_run(wave);
+    const int kb_begin = run * kblocks / kProductWaves;
+    const int kb_end = (run + 1) * kblocks / kProductWaves;
     // Columns past `out` (the last tile of a vocabulary) re-read the last row;
     // their sums are never stored.
     const u16* wrow = static_cast<const u16*>(a.w) + (size_t) min(n0 + li, a.out - 1) * a.inner + 8 * g;
-    const u16* xrow = a.x + (size_t) li * a.inner + 8 * g;
 
     float4v acc[MT];
 #pragma unroll
@@ -279,6 +301,18 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
 #pragma unroll
     for (int u = 0; u < KB; ++u)
         wv[u] = *reinterpret_cast<const u32x4*>(wrow + min(kb_begin + u, kb_last) * 32);
+    // The epilogue's outputs: output o of this thread is C[16 t + row][col]
+    // with t·256 + row·16 + col = threadIdx.x + o·512. A residual product
+    // reads their y values now, behind the first weight loads (ahead of them
+    // they would delay the weights), so its epilogue waits for no load.
+    float prior[OUTS];
+#pragma unroll
+    for (int o = 0; o < OUTS; ++o)
+    {
+        const int i = (int) threadIdx.x + o * kProductThreads;
+        const int m = min((i / 256) * 16 + (i % 256) / 16, a.rows - 1), n = min(n0 + i % 16, a.out - 1);
+        prior[o] = a.epilogue == kResidual ? a.y[(size_t) m * a.ldy + n] : 0.f;
+    }
     for (int kb = kb_begin; kb < kb_end; kb += KB)
     {
         u32x4 xv[KB][P][MT];
@@ -290,7 +324,8 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
             for (int p = 0; p < P; ++p)
 #pragma unroll
                 for (int t = 0; t < MT; ++t)
-                    xv[u][p][t] = *reinterpret_cast<const u32x4*>(xrow + p * a.x_part + (size_t) t * 16 * a.inner + k);
+                    xv[u][p][t] = *reinterpret_cast<const u32x4*>(
+                        a.x + p * a.x_part + (((size_t) t * kblocks + k / 32) * 64 + lane) * 8);
         }
         u32x4 wn[KB];
         if constexpr (PREFETCH)
@@ -321,27 +356,29 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
         }
     }
 
-    // acc[t][r] of lane (g, li) is C[4g + r][li] of row tile t.
+    // acc[t][r] of lane (g, li) is C[4g + r][li] of row tile t. Every tile
+    // goes to LDS at once; each output is then the 8 waves' sum in order.
 #pragma unroll
     for (int t = 0; t < MT; ++t)
-    {
-        __syncthreads();
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            partial[wave][lane * 4 + r] = acc[t][r];
-        __syncthreads();
-        if (threadIdx.x < 256)
-        {
-            const int row = threadIdx.x / 16, col = threadIdx.x % 16;
-            const int src = ((row / 4) * 16 + col) * 4 + row % 4;
-            float v = 0.f;
+            partial[run][t * 256 + lane * 4 + r] = acc[t][r];
+    __syncthreads();
 #pragma unroll
-            for (int w = 0; w < kProductWaves; ++w)
-                v += partial[w][src];
-            const int m = t * 16 + row, n = n0 + col;
-            if (m < a.rows && n < a.out)
-                finish<WT>(a, m, n, v);
-        }
+    for (int o = 0; o < OUTS; ++o)
+    {
+        const int i = (int) threadIdx.x + o * kProductThreads;
+        if (i >= MT * 256)
+            break;
+        const int t = i / 256, row = (i % 256) / 16, col = i % 16;
+        const int src = t * 256 + ((row / 4) * 16 + col) * 4 + row % 4;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < kProductWaves; ++w)
+            v += partial[w][src];
+        const int m = t * 16 + row, n = n0 + col;
+        if (m < a.rows && n < a.out)
+            finish<WT>(a, m, n, v, prior[o]);
     }
 }
 
@@ -362,7 +399,9 @@ template <int WT, int MT, int NT>
 __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product a)
 {
     constexpr int P = parts_of<WT>();
-    __shared__ float partial[kProductWaves][256];
+    constexpr int TILES = NT * MT;
+    constexpr int OUTS = (TILES * 256 + kProductThreads - 1) / kProductThreads; // outputs a thread finishes
+    __shared__ float partial[kProductWaves][TILES * 256];
     __shared__ float stats[2][kProductWaves][MT * 16];
     __shared__ float4v sh_gamma[kNormedWidth / 4], sh_beta[kNormedWidth / 4];
 
@@ -370,8 +409,9 @@ __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product
     const int li = lane % 16, g = lane / 16;
     const int n0 = blockIdx.x * 16 * NT;
     const int kblocks = a.inner / 32;
-    const int kb_begin = wave * kblocks / kProductWaves;
-    const int kb_end = (wave + 1) * kblocks / kProductWaves;
+    const int run = inner_run(wave);
+    const int kb_begin = run * kblocks / kProductWaves;
+    const int kb_end = (run + 1) * kblocks / kProductWaves;
     const int nkb = kb_end - kb_begin;
     const u16* wrow[NT];
 #pragma unroll
@@ -426,7 +466,7 @@ __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product
             s += __shfl_xor(s, 16);
             s += __shfl_xor(s, 32);
             if (g == 0)
-                stats[pass][wave][t * 16 + li] = s;
+                stats[pass][run][t * 16 + li] = s;
         }
         __syncthreads();
 #pragma unroll
@@ -485,29 +525,33 @@ __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product
                                                 wv[u][nt], acc[nt][t]);
             }
 
+    // Every tile goes to LDS at once (tile nt·MT + t); each output is then
+    // the 8 waves' sum in order. (No residual epilogue here.)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int t = 0; t < MT; ++t)
-        {
-            __syncthreads();
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                partial[wave][lane * 4 + r] = acc[nt][t][r];
-            __syncthreads();
-            if (threadIdx.x < 256)
-            {
-                const int row = threadIdx.x / 16, col = threadIdx.x % 16;
-                const int src = ((row / 4) * 16 + col) * 4 + row % 4;
-                float v = 0.f;
+                partial[run][(nt * MT + t) * 256 + lane * 4 + r] = acc[nt][t][r];
+    __syncthreads();
 #pragma unroll
-                for (int w = 0; w < kProductWaves; ++w)
-                    v += partial[w][src];
-                const int m = t * 16 + row, n = n0 + nt * 16 + col;
-                if (m < a.rows && n < a.out)
-                    finish<WT>(a, m, n, v);
-            }
-        }
+    for (int o = 0; o < OUTS; ++o)
+    {
+        const int i = (int) threadIdx.x + o * kProductThreads;
+        if (i >= TILES * 256)
+            break;
+        const int tile = i / 256, row = (i % 256) / 16, col = i % 16;
+        const int nt = tile / MT, t = tile % MT;
+        const int src = tile * 256 + ((row / 4) * 16 + col) * 4 + row % 4;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < kProductWaves; ++w)
+            v += partial[w][src];
+        const int m = t * 16 + row, n = n0 + nt * 16 + col;
+        if (m < a.rows && n < a.out)
+            finish<WT>(a, m, n, v);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -903,7 +947,7 @@ struct Attend
     int k_count, step_tokens, causal, heads, head_width, width; // k_count: cross rows (causal: unused)
     float scale;
     int chunks, chunk_len;
-    u16* xs;              // split output [parts][rows_padded][width] when chunks == 1
+    u16* xs;              // split output [parts][rows_padded][width] (fragment-major) when chunks == 1
     size_t xs_part;
     float* partials;      // [rows][heads][chunks][head_width + 2]
 };
@@ -1005,7 +1049,7 @@ __global__ void __launch_bounds__(kAttendThreads) attend_kernel(Attend a)
         const float total = (wave_sum[0] + wave_sum[1]) + (wave_sum[2] + wave_sum[3]);
         const float value = (wave_row[0][q4][r] + wave_row[1][q4][r]) + (wave_row[2][q4][r] + wave_row[3][q4][r]);
         if (a.chunks == 1)
-            store_split<WT>(a.xs, a.xs_part, (size_t) row * a.width + head * a.head_width + c, value / total);
+            store_split<WT>(a.xs, a.xs_part, fragment_index(row, head * a.head_width + c, a.width), value / total);
         else
         {
             float* part = a.partials + (((size_t) row * a.heads + head) * a.chunks + chunk) * (a.head_width + 2);
@@ -1066,7 +1110,7 @@ __global__ void __launch_bounds__(kWave) combine_kernel(const float* __restrict_
         }
     }
     if (lane < head_width)
-        store_split<WT>(xs, xs_part, (size_t) row * width + head * head_width + lane, numerator / denominator);
+        store_split<WT>(xs, xs_part, fragment_index(row, head * head_width + lane, width), numerator / denominator);
 }
 
 // ---------------------------------------------------------------------------
@@ -1177,7 +1221,7 @@ __global__ void __launch_bounds__(kSweepThreads) sweep_attend_kernel(Attend a, i
     {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            store_split<WT>(a.xs, a.xs_part, (size_t) stream * a.width + 4 * quad + r, acc[r] / run_sum);
+            store_split<WT>(a.xs, a.xs_part, fragment_index(stream, 4 * quad + r, a.width), acc[r] / run_sum);
         return;
     }
     float* part = a.partials + (((size_t) stream * a.heads + head) * groups + j) * (a.head_width + 2);
