@@ -85,6 +85,17 @@ __device__ __forceinline__ size_t fragment_index(int row, int col, int width)
     return (((size_t) t * (width / 32) + kb) * 64 + g * 16 + r) * 8 + e;
 }
 
+// The fp32 residual stream h ([rows_padded][width]) is stored fragment-major
+// as well: fragment (t, kb) holds rows 16t.. and inner values 32kb.. as two
+// 1 KB halves, half j holding values 8g + 4j .. 8g + 4j + 3 of row r at lane
+// 16g + r, so each of a wave's two fragment loads is one contiguous kilobyte
+// and four consecutive values of a row stay contiguous.
+__device__ __forceinline__ size_t residual_index(int row, int col, int width)
+{
+    const int t = row / 16, r = row % 16, kb = col / 32, g = (col % 32) / 8, e = col % 8;
+    return (((size_t) t * (width / 32) + kb) * 2 + e / 4) * 256 + (g * 16 + r) * 4 + e % 4;
+}
+
 // The same parts as register values.
 template <int WT>
 __device__ __forceinline__ void split_value(float x, u16 (&out)[parts_of<WT>()])
@@ -126,7 +137,7 @@ __device__ __forceinline__ float4v mfma16(u32x4 a, u32x4 b, float4v c)
 // ---------------------------------------------------------------------------
 struct Norm
 {
-    float* h;             // [rows, width] residual stream
+    float* h;             // [rows_padded, width] residual stream (residual_index layout)
     int width;
     const float* gamma;
     const float* beta;
@@ -147,33 +158,35 @@ __global__ void __launch_bounds__(kNormThreads) norm_kernel(Norm a)
 {
     __shared__ float scratch[kNormThreads / kWave];
     const int row = blockIdx.x;
-    float* h = a.h + (size_t) row * a.width;
+    float* h = a.h;
+    const auto at = [&](int c) { return residual_index(row, c, a.width); };
     if constexpr (EMBED)
     {
         const int first = *a.state;
         const uint32_t token = a.ring != nullptr ? a.ring[(size_t) first * a.streams + row] : a.tokens[row];
         const int position = first + row % a.step_tokens;
         for (int c = threadIdx.x; c < a.width; c += kNormThreads)
-            h[c] = token < (uint32_t) a.vocabulary
-                       ? a.token_table[(size_t) token * a.width + c] + a.position_table[(size_t) position * a.width + c]
-                       : __builtin_nanf("");
+            h[at(c)] = token < (uint32_t) a.vocabulary
+                           ? a.token_table[(size_t) token * a.width + c]
+                                 + a.position_table[(size_t) position * a.width + c]
+                           : __builtin_nanf("");
         if (a.xs == nullptr) // the embedding only: the next product normalises
             return;
     }
     float total = 0.f;
     for (int c = threadIdx.x; c < a.width; c += kNormThreads)
-        total += h[c];
+        total += h[at(c)];
     const float mean = block_sum(total, scratch) / (float) a.width;
     float squares = 0.f;
     for (int c = threadIdx.x; c < a.width; c += kNormThreads)
     {
-        const float centred = h[c] - mean;
+        const float centred = h[at(c)] - mean;
         squares += centred * centred;
     }
     const float scale = rsqrtf(block_sum(squares, scratch) / (float) a.width + a.eps);
     for (int c = threadIdx.x; c < a.width; c += kNormThreads)
     {
-        const float v = (h[c] - mean) * scale * a.gamma[c] + a.beta[c];
+        const float v = (h[at(c)] - mean) * scale * a.gamma[c] + a.beta[c];
         store_split<WT>(a.xs, a.xs_part, fragment_index(row, c, a.width), v);
         if (a.y != nullptr)
             a.y[(size_t) row * a.width + c] = v;
@@ -215,7 +228,7 @@ struct Product
     const int* state; // device word: the position of the step's first token
     int step_tokens, width;
     // normed_product_kernel: x = LayerNorm(h) computed in the product
-    const float* h;   // [rows_padded][inner] residual stream
+    const float* h;   // [rows_padded][inner] residual stream (residual_index layout)
     const float* gamma;
     const float* beta;
     float eps;
@@ -229,7 +242,7 @@ __device__ __forceinline__ void finish(const Product& a, int m, int n, float acc
     switch (a.epilogue)
     {
         case kStore: a.y[(size_t) m * a.ldy + n] = v; break;
-        case kResidual: a.y[(size_t) m * a.ldy + n] = prior + v; break;
+        case kResidual: a.y[residual_index(m, n, a.ldy)] = prior + v; break; // y is h
         case kGelu: a.y[(size_t) m * a.ldy + n] = exact_gelu(v); break;
         default:
         {
@@ -311,7 +324,7 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
     {
         const int i = (int) threadIdx.x + o * kProductThreads;
         const int m = min((i / 256) * 16 + (i % 256) / 16, a.rows - 1), n = min(n0 + i % 16, a.out - 1);
-        prior[o] = a.epilogue == kResidual ? a.y[(size_t) m * a.ldy + n] : 0.f;
+        prior[o] = a.epilogue == kResidual ? a.y[residual_index(m, n, a.ldy)] : 0.f;
     }
     for (int kb = kb_begin; kb < kb_end; kb += KB)
     {
@@ -417,7 +430,6 @@ __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
         wrow[nt] = static_cast<const u16*>(a.w) + (size_t) min(n0 + nt * 16 + li, a.out - 1) * a.inner + 8 * g;
-    const float* hrow = a.h + (size_t) li * a.inner + 8 * g;
 
     u32x4 wv[kNormedBlocks][NT];
     float4v hv[kNormedBlocks][MT][2];
@@ -432,8 +444,9 @@ __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product
 #pragma unroll
             for (int t = 0; t < MT; ++t)
             {
-                hv[u][t][0] = *reinterpret_cast<const float4v*>(hrow + (size_t) t * 16 * a.inner + k);
-                hv[u][t][1] = *reinterpret_cast<const float4v*>(hrow + (size_t) t * 16 * a.inner + k + 4);
+                const float* half0 = a.h + ((size_t) t * kblocks + k / 32) * 512 + lane * 4;
+                hv[u][t][0] = *reinterpret_cast<const float4v*>(half0);
+                hv[u][t][1] = *reinterpret_cast<const float4v*>(half0 + 256);
             }
         }
     for (int i = threadIdx.x; i < a.inner / 4; i += kProductThreads)
@@ -592,7 +605,7 @@ __global__ void __launch_bounds__(kNormThreads) hidden_kernel(const float* h, co
     float mean, scale;
     row_statistics(stats + (size_t) row * groups * 2, groups, width, eps, mean, scale);
     for (int c = threadIdx.x; c < width; c += kNormThreads)
-        out[(size_t) row * width + c] = (h[(size_t) row * width + c] - mean) * scale * gamma[c] + beta[c];
+        out[(size_t) row * width + c] = (h[residual_index(row, c, width)] - mean) * scale * gamma[c] + beta[c];
 }
 
 // ---------------------------------------------------------------------------
@@ -622,8 +635,9 @@ constexpr int kStageBytes = 64 * 1024; // LDS for a block's split activations
 
 struct Tile
 {
-    const float* x;        // [rows][ldx] fp32 activations
+    const float* x;        // [rows][ldx] fp32 activations (the residual stream's layout when x_residual)
     int ldx;
+    int x_residual;
     int rows, inner, out;
     const void* w;         // [out][inner], 16-bit
     const float* bias;
@@ -688,7 +702,7 @@ __global__ void __launch_bounds__(kTileThreads) tile_kernel(Tile a)
     for (int c = 0; c < CPT; ++c)
     {
         const int n = min(n0 + c0 + c, a.out - 1);
-        resid[c] = a.epilogue == kResidual ? a.y[(size_t) min(m, a.rows - 1) * a.ldy + n] : 0.f;
+        resid[c] = a.epilogue == kResidual ? a.y[residual_index(min(m, a.rows - 1), n, a.ldy)] : 0.f; // y is h
     }
     const int kblocks = a.inner / 32;
     const int kb_begin = split * a.kb_per_split;
@@ -733,7 +747,8 @@ __global__ void __launch_bounds__(kTileThreads) tile_kernel(Tile a)
             const int m = i / (KB * 8), j = i % (KB * 8);
             xv[r] = float4v {0.f, 0.f, 0.f, 0.f};
             if (m < a.rows && j < nkb * 8)
-                xv[r] = *reinterpret_cast<const float4v*>(a.x + (size_t) m * a.ldx + kb0 * 32 + 4 * j);
+                xv[r] = *reinterpret_cast<const float4v*>(
+                    a.x + (a.x_residual ? residual_index(m, kb0 * 32 + 4 * j, a.ldx) : (size_t) m * a.ldx + kb0 * 32 + 4 * j));
         }
 #pragma unroll
         for (int r = 0; r < RUNS; ++r)
@@ -873,7 +888,7 @@ __global__ void __launch_bounds__(kTileThreads) tile_kernel(Tile a)
                 if (row_in && n < a.out)
                 {
                     v[c] += resid[c];
-                    a.y[(size_t) m * a.ldy + n] = v[c];
+                    a.y[residual_index(m, n, a.ldy)] = v[c];
                     sum += v[c];
                 }
             }
@@ -1467,7 +1482,7 @@ struct wsp_batch
     float* cross_keys = nullptr;  // [layers][cross_positions][streams][width]
     float* cross_values = nullptr;
     float* cross_scratch = nullptr; // [cross_positions][width], made by the first begin that needs it
-    float* h = nullptr;           // [rows_padded][width] residual stream
+    float* h = nullptr;           // [rows_padded][width] residual stream, fragment-major (residual_index)
     float* q = nullptr;           // [rows_padded][width] queries
     uint16_t* xs = nullptr;       // [parts][rows_padded][width]
     float* ff = nullptr;          // [rows_padded][feed_forward] gelu(fc1) rows
@@ -1781,6 +1796,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         // product (64 vocabulary rows a block).
         Tile t = tile;
         t.x = b->h;
+        t.x_residual = 1;
         t.ldx = d;
         t.inner = d;
         t.out = s.vocabulary_size;
