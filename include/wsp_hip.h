@@ -254,7 +254,8 @@ typedef struct wsp_cross_tensors
 typedef struct wsp_batch wsp_batch;
 
 /* Allocates every stream's caches (self [layers][streams][max_positions][width],
- * cross [layers][cross_positions][streams][width] — key-major — f32) and the step buffers
+ * cross [layers][cross_positions][streams][width] — key-major — f32), a
+ * fragment-major copy of the projection and logits weights, and the step buffers
  * for up to max_step_tokens tokens per stream per step; streams ×
  * max_step_tokens ≤ 128. wdtype is the projections' storage (WSP_F16 or
  * WSP_BF16). Decoder::prepare's role (Decoder/Decoder.cpp:194-227), per stream. */
@@ -277,7 +278,11 @@ int wsp_batch_begin(wsp_batch* batch, const wsp_cross_tensors* layers, int wdtyp
  * (device f32 [streams·count][width]) or null. With argmax_out non-null,
  * argmax_out[s] receives the masked argmax of stream s's last row
  * (Argmax::encode, Kernels/Argmax.h:236-241), so it can feed the next step.
- * The layer table's cache pointers are not used: the batch owns its caches. */
+ * The layer table's cache pointers are not used: the batch owns its caches.
+ * The products read the batch's own fragment-major copy of the projection and
+ * logits weights, packed on the batch's stream the first time a table is
+ * passed (here or to wsp_batch_ring_step) and whenever its pointers change: a
+ * table with the same pointers is taken to hold the same weights. */
 int wsp_batch_step(wsp_batch* batch, const wsp_decoder_tensors* tensors, const uint32_t* tokens, int count,
                    float* hidden, float* logits, const float* mask, uint32_t* argmax_out);
 

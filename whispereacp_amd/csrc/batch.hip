@@ -96,6 +96,38 @@ __device__ __forceinline__ size_t residual_index(int row, int col, int width)
     return (((size_t) t * (width / 32) + kb) * 2 + e / 4) * 256 + (g * 16 + r) * 4 + e % 4;
 }
 
+// Projection weights W [n][k] (16-bit) are read from a fragment-major copy
+// made once per weight table: the 16 rows x 32 inner values one
+// v_mfma_f32_16x16x32 B-operand load covers are 64 lanes x 16 contiguous
+// bytes, lane 16g + r holding row r's values 8g..8g+7, tiles of 16 rows in
+// order and k-blocks in order within a tile (rows past the last padded with
+// zeros). Read from the row-major weights, each load touched 16 rows x 64
+// bytes; fragment-major, an 80-block product launch took 4.4 us instead of
+// 5.1. Element (tile, kb) starts at (tile * (k / 32) + kb) * 512.
+constexpr int kFragment = 512; // 16-bit values per fragment
+
+__global__ void __launch_bounds__(256) pack_fragments_kernel(const u16* __restrict__ w, int rows, int inner,
+                                                             u16* __restrict__ out, size_t chunks)
+{
+    const size_t i = (size_t) blockIdx.x * 256 + threadIdx.x; // 16-byte chunk of the output
+    if (i >= chunks)
+        return;
+    const int lane = (int) (i % 64), kbs = inner / 32;
+    const size_t fragment = i / 64;
+    const int kb = (int) (fragment % kbs), tile = (int) (fragment / kbs);
+    const int n = tile * 16 + lane % 16, k = kb * 32 + 8 * (lane / 16);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (n < rows)
+        v = *reinterpret_cast<const u32x4*>(w + (size_t) n * inner + k);
+    *reinterpret_cast<u32x4*>(out + i * 8) = v;
+}
+
+// 16-bit values of the fragment-major copy of a [rows][inner] weight.
+size_t packed_size(int rows, int inner)
+{
+    return (size_t) ((rows + 15) / 16) * 16 * inner;
+}
+
 // The same parts as register values.
 template <int WT>
 __device__ __forceinline__ void split_value(float x, u16 (&out)[parts_of<WT>()])
@@ -295,9 +327,8 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
     const int run = inner_run(wave);
     const int kb_begin = run * kblocks / kProductWaves;
     const int kb_end = (run + 1) * kblocks / kProductWaves;
-    // Columns past `out` (the last tile of a vocabulary) re-read the last row;
-    // their sums are never stored.
-    const u16* wrow = static_cast<const u16*>(a.w) + (size_t) min(n0 + li, a.out - 1) * a.inner + 8 * g;
+    // This block's weight tile, fragment-major (padding rows are zero).
+    const u16* wfrag = static_cast<const u16*>(a.w) + (size_t) blockIdx.x * kblocks * kFragment + lane * 8;
 
     float4v acc[MT];
 #pragma unroll
@@ -313,7 +344,7 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
     u32x4 wv[KB];
 #pragma unroll
     for (int u = 0; u < KB; ++u)
-        wv[u] = *reinterpret_cast<const u32x4*>(wrow + min(kb_begin + u, kb_last) * 32);
+        wv[u] = *reinterpret_cast<const u32x4*>(wfrag + (size_t) min(kb_begin + u, kb_last) * kFragment);
     // The epilogue's outputs: output o of this thread is C[16 t + row][col]
     // with t·256 + row·16 + col = threadIdx.x + o·512. A residual product
     // reads their y values now, behind the first weight loads (ahead of them
@@ -345,7 +376,7 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
         {
 #pragma unroll
             for (int u = 0; u < KB; ++u)
-                wn[u] = *reinterpret_cast<const u32x4*>(wrow + min(kb + KB + u, kb_end - 1) * 32);
+                wn[u] = *reinterpret_cast<const u32x4*>(wfrag + (size_t) min(kb + KB + u, kb_end - 1) * kFragment);
         }
 #pragma unroll
         for (int u = 0; u < KB; ++u)
@@ -365,7 +396,7 @@ __global__ void __launch_bounds__(kProductThreads) product_kernel(Product a)
         {
 #pragma unroll
             for (int u = 0; u < KB; ++u)
-                wv[u] = *reinterpret_cast<const u32x4*>(wrow + min(kb + KB + u, kb_end - 1) * 32);
+                wv[u] = *reinterpret_cast<const u32x4*>(wfrag + (size_t) min(kb + KB + u, kb_end - 1) * kFragment);
         }
     }
 
@@ -426,10 +457,13 @@ __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product
     const int kb_begin = run * kblocks / kProductWaves;
     const int kb_end = (run + 1) * kblocks / kProductWaves;
     const int nkb = kb_end - kb_begin;
-    const u16* wrow[NT];
+    // The block's weight tiles, fragment-major; a second tile past the last
+    // (an odd tile count) re-reads the last one and is never stored.
+    const u16* wfrag[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
-        wrow[nt] = static_cast<const u16*>(a.w) + (size_t) min(n0 + nt * 16 + li, a.out - 1) * a.inner + 8 * g;
+        wfrag[nt] = static_cast<const u16*>(a.w)
+                    + (size_t) min((int) blockIdx.x * NT + nt, (a.out + 15) / 16 - 1) * kblocks * kFragment + lane * 8;
 
     u32x4 wv[kNormedBlocks][NT];
     float4v hv[kNormedBlocks][MT][2];
@@ -440,7 +474,7 @@ __global__ void __launch_bounds__(kProductThreads) normed_product_kernel(Product
             const int k = (kb_begin + u) * 32;
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
-                wv[u][nt] = *reinterpret_cast<const u32x4*>(wrow[nt] + k);
+                wv[u][nt] = *reinterpret_cast<const u32x4*>(wfrag[nt] + (size_t) (kb_begin + u) * kFragment);
 #pragma unroll
             for (int t = 0; t < MT; ++t)
             {
@@ -707,9 +741,10 @@ __global__ void __launch_bounds__(kTileThreads) tile_kernel(Tile a)
     const int kblocks = a.inner / 32;
     const int kb_begin = split * a.kb_per_split;
     const int kb_end = min(kb_begin + a.kb_per_split, kblocks);
-    // Columns past `out` (the last group of a vocabulary) re-read the last
-    // weight row; their sums are never stored.
-    const u16* wrow = static_cast<const u16*>(a.w) + (size_t) min(n0 + 16 * wave + li, a.out - 1) * a.inner + 8 * g;
+    // This wave's weight tile, fragment-major; tiles past the last (the last
+    // group of a vocabulary) re-read the last tile and are never stored.
+    const u16* wfrag = static_cast<const u16*>(a.w)
+                       + (size_t) min(n0 / 16 + wave, (a.out + 15) / 16 - 1) * kblocks * kFragment + lane * 8;
 
     if (a.gamma != nullptr)
     {
@@ -736,7 +771,7 @@ __global__ void __launch_bounds__(kTileThreads) tile_kernel(Tile a)
         const int nkb = min(KB, kb_end - kb0);
 #pragma unroll
         for (int u = 0; u < KB; ++u)
-            wv[u] = *reinterpret_cast<const u32x4*>(wrow + (size_t) (kb0 + min(u, nkb - 1)) * 32);
+            wv[u] = *reinterpret_cast<const u32x4*>(wfrag + (size_t) (kb0 + min(u, nkb - 1)) * kFragment);
         // Stage rows [0, R) x inner [32 kb0, 32 (kb0 + nkb)) as float4 runs:
         // run i is row i / (KB * 8), run i % (KB * 8) of the row.
         float4v xv[RUNS];
@@ -1497,6 +1532,14 @@ struct wsp_batch
     uint32_t* next = nullptr;     // [streams] greedy tokens of a ring step
     std::vector<void*> owned;
 
+    // Fragment-major copies of the projection and tied logits weights the
+    // step's products read, packed from the caller's table when a table is
+    // first seen (packed_table: the table they came from).
+    uint16_t* packed = nullptr;
+    std::vector<char> packed_table;
+    std::vector<wsp_layer_tensors> packed_layers;
+    wsp_decoder_tensors packed_tensors {};
+
     // The single-token ring step, captured once as a HIP graph on a private
     // stream and replayed on `stream`; re-captured when anything it bakes in
     // (ring, logits, mask, cross rows, the weight table) changes.
@@ -1843,6 +1886,79 @@ std::vector<char> table_bytes(const wsp_decoder_tensors* T, int layers)
     return bytes;
 }
 
+// 16-bit values of every fragment-major weight copy of one batch.
+size_t packed_capacity(const wsp_decoder_shape& s)
+{
+    using wsp::batch::packed_size;
+    const int d = s.width, f = s.feed_forward_width;
+    return (size_t) s.layers * (packed_size(3 * d, d) + 3 * packed_size(d, d) + packed_size(f, d) + packed_size(d, f))
+           + packed_size(s.vocabulary_size, d);
+}
+
+// The caller's table with every projection and the logits weight replaced by
+// its fragment-major copy, packed (on the batch's stream) when this table has
+// not been seen before. A table with the same pointers is taken to hold the
+// same weights. Null on failure, with the status in `status`.
+const wsp_decoder_tensors* packed_weights(wsp_batch* b, const wsp_decoder_tensors* T, int& status)
+{
+    std::vector<char> table = table_bytes(T, b->shape.layers);
+    if (b->packed_table.size() == table.size() && std::memcmp(b->packed_table.data(), table.data(), table.size()) == 0)
+        return &b->packed_tensors;
+    const wsp_decoder_shape& s = b->shape;
+    const int d = s.width, f = s.feed_forward_width;
+    if (T->logits_weight == nullptr)
+    {
+        status = fail(b, WSP_ERR_ARGUMENT, "batch step: null logits weight");
+        return nullptr;
+    }
+    for (int l = 0; l < s.layers; ++l)
+    {
+        const wsp_layer_tensors& L = T->layers[l];
+        if (L.self_qkv_w == nullptr || L.self_out_w == nullptr || L.cross_q_w == nullptr || L.cross_out_w == nullptr
+            || L.fc1_w == nullptr || L.fc2_w == nullptr)
+        {
+            status = fail(b, WSP_ERR_ARGUMENT, "batch step: a layer without projection weights");
+            return nullptr;
+        }
+    }
+    b->packed_table.clear();
+    uint16_t* at = b->packed;
+    hipError_t e = hipSuccess;
+    auto pack = [&](const void* w, int rows, int inner) -> const void* {
+        const size_t values = wsp::batch::packed_size(rows, inner), chunks = values / 8;
+        if (e == hipSuccess)
+        {
+            hipLaunchKernelGGL(wsp::batch::pack_fragments_kernel, dim3((unsigned) ((chunks + 255) / 256)), dim3(256),
+                               0, b->stream, static_cast<const uint16_t*>(w), rows, inner, at, chunks);
+            e = hipGetLastError();
+        }
+        const void* out = at;
+        at += values;
+        return out;
+    };
+    b->packed_layers.assign(T->layers, T->layers + s.layers);
+    for (int l = 0; l < s.layers; ++l)
+    {
+        wsp_layer_tensors& L = b->packed_layers[l];
+        L.self_qkv_w = pack(L.self_qkv_w, 3 * d, d);
+        L.self_out_w = pack(L.self_out_w, d, d);
+        L.cross_q_w = pack(L.cross_q_w, d, d);
+        L.cross_out_w = pack(L.cross_out_w, d, d);
+        L.fc1_w = pack(L.fc1_w, f, d);
+        L.fc2_w = pack(L.fc2_w, d, f);
+    }
+    b->packed_tensors = *T;
+    b->packed_tensors.layers = b->packed_layers.data();
+    b->packed_tensors.logits_weight = pack(T->logits_weight, s.vocabulary_size, d);
+    if (e != hipSuccess)
+    {
+        status = hip_fail(b, e, "weight packing");
+        return nullptr;
+    }
+    b->packed_table = std::move(table);
+    return &b->packed_tensors;
+}
+
 void drop_graph(wsp_batch* b)
 {
     if (b->graph != nullptr)
@@ -1943,6 +2059,8 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
         e = allocate(b, &b->xs, (size_t) P * b->rows_padded * d);
     if (e == hipSuccess)
         e = allocate(b, &b->ff, (size_t) b->rows_padded * s.feed_forward_width);
+    if (e == hipSuccess)
+        e = allocate(b, &b->packed, packed_capacity(s));
     if (e == hipSuccess)
         e = allocate(b, &b->stats, (size_t) b->rows_padded * stat_groups * 2);
     b->tile_partials_capacity = (size_t) wsp::batch::kMaxSplits * split_groups * b->rows_padded
@@ -2120,9 +2238,13 @@ int wsp_batch_step(wsp_batch* b, const wsp_decoder_tensors* tensors, const uint3
     if (tensors->wdtype != b->wdtype || tensors->logits_wdtype != b->wdtype)
         return fail(b, WSP_ERR_LOGIC, "wsp_batch_step: projections and logits must share the batch's 16-bit storage");
     (void) hipSetDevice(b->device);
+    int status = WSP_OK;
+    const wsp_decoder_tensors* packed = packed_weights(b, tensors, status);
+    if (packed == nullptr)
+        return status;
     const StepIo io {tokens, nullptr, count, hidden, logits, mask, argmax_out, false};
-    const int status = b->wdtype == WSP_F16 ? run_step<wsp::kF16>(b, tensors, io, b->stream)
-                                            : run_step<wsp::kBF16>(b, tensors, io, b->stream);
+    status = b->wdtype == WSP_F16 ? run_step<wsp::kF16>(b, packed, io, b->stream)
+                                  : run_step<wsp::kBF16>(b, packed, io, b->stream);
     if (status == WSP_OK)
         b->position += count;
     return status;
@@ -2143,11 +2265,15 @@ int wsp_batch_ring_step(wsp_batch* b, const wsp_decoder_tensors* tensors, uint32
     if (tensors->wdtype != b->wdtype || tensors->logits_wdtype != b->wdtype)
         return fail(b, WSP_ERR_LOGIC, "wsp_batch_ring_step: projections and logits must share the batch's 16-bit storage");
     (void) hipSetDevice(b->device);
+    int packing = WSP_OK;
+    const wsp_decoder_tensors* packed = packed_weights(b, tensors, packing);
+    if (packed == nullptr)
+        return packing;
     if (b->graph == nullptr || b->graph_ring != ring || b->graph_logits != logits || b->graph_mask != mask
-        || b->graph_cross_rows != b->cross_rows || !same_table(b, table_bytes(tensors, b->shape.layers)))
+        || b->graph_cross_rows != b->cross_rows || !same_table(b, table_bytes(packed, b->shape.layers)))
     {
-        const int status = b->wdtype == WSP_F16 ? capture_ring_step<wsp::kF16>(b, tensors, ring, logits, mask)
-                                                : capture_ring_step<wsp::kBF16>(b, tensors, ring, logits, mask);
+        const int status = b->wdtype == WSP_F16 ? capture_ring_step<wsp::kF16>(b, packed, ring, logits, mask)
+                                                : capture_ring_step<wsp::kBF16>(b, packed, ring, logits, mask);
         if (status != WSP_OK)
             return status;
     }
