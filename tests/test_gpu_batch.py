@@ -201,6 +201,24 @@ def test_streams_with_mask_reduced_cross_rows_and_prompt_step(oracle, dtype):
         assert all(t % 3 != 0 for t in tokens[s][1:])
 
 
+@pytest.mark.parametrize("dtype", ["F16", "BF16"])
+def test_six_heads_sweep_with_four_key_lanes(oracle, dtype):
+    # tiny.en's width and head count (d 384, 6 heads): the cross-attention
+    # sweep runs 4 key lanes of 96 quads (384 threads) and folds them through
+    # LDS for an even-but-not-4-divisible head count; inner 384 gives the
+    # products 12 k-blocks over 8 runs (runs of one and two).
+    from whispereacp_amd.decoder import BatchedDecoder
+    shape = S.DecoderShape(384, 6, 2, 1536, 2001, 448, 150)
+    f = S.workload_decoder_file(shape, dtype, 94)
+    encoders = [S.normal_encoder_output(150, shape.width, 950 + s) for s in range(5)]
+    prompt, steps = [50, 60, 70, 80], 12
+    decoder = BatchedDecoder(shape, f, streams=5)
+    tokens, rows, _ = batched_greedy(decoder, shape, encoders, prompt, steps)
+    for s in range(5):
+        ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, encoders[s], prompt, steps)
+        check_run(tokens[s], rows[s], ref_tokens, ref_rows, 2e-2)
+
+
 def test_long_sequence_splits_self_keys(oracle):
     # 300 single-token steps: the self keys pass 128 and 256, so the split
     # attention runs several chunks and the combine.
