@@ -121,19 +121,47 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 // Tiled product for many rows: 64x64 output tiles, 16-deep K slices staged in
 // LDS (weights widened to float on the way in), 4x4 outputs per thread, k
-// ascending within each thread's sum. Same epilogue as the GEMV.
+// ascending within each thread's sum. Same epilogue as the GEMV. With VEC
+// (inner a multiple of 4, rows 16-byte aligned) each thread moves one row's
+// four consecutive k per operand per slice as one vector load, the next
+// slice's loads are in flight while the current one is multiplied, and the
+// fragments come out of LDS as float4 reads.
 // ---------------------------------------------------------------------------
 constexpr int kTile = 64;
 constexpr int kTileK = 16;
 
+// Four consecutive weights widened to float (VEC loads: 16 bytes for F32,
+// 8 for F16 and BF16).
 template <int WT>
+__device__ __forceinline__ float4v load4(const void* w, size_t index)
+{
+    if constexpr (WT == kF32)
+        return *reinterpret_cast<const float4v*>(static_cast<const float*>(w) + index);
+    else
+    {
+        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(w) + index);
+        const uint16_t h[4] = {(uint16_t) u.x, (uint16_t) (u.x >> 16), (uint16_t) u.y, (uint16_t) (u.y >> 16)};
+        float4v v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            if constexpr (WT == kF16)
+                v[i] = (float) __builtin_bit_cast(_Float16, h[i]);
+            else
+                v[i] = bf16_to_float(h[i]);
+        }
+        return v;
+    }
+}
+
+template <int WT, bool VEC>
 __global__ void __launch_bounds__(kBlock) gemm_kernel(const float* __restrict__ x, int rows,
                                                       int inner, const void* __restrict__ w,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ y, int out, int flags)
 {
-    __shared__ float xs[kTileK][kTile + 4];
-    __shared__ float ws[kTileK][kTile + 4];
+    __shared__ __attribute__((aligned(16))) float xs[kTileK][kTile + 4];
+    __shared__ __attribute__((aligned(16))) float ws[kTileK][kTile + 4];
 
     const int row0 = blockIdx.y * kTile;
     const int col0 = blockIdx.x * kTile;
@@ -141,38 +169,81 @@ __global__ void __launch_bounds__(kBlock) gemm_kernel(const float* __restrict__ 
 
     float acc[4][4] = {};
 
-    for (int k0 = 0; k0 < inner; k0 += kTileK)
+    if constexpr (VEC)
     {
-        // 64 x 16 of each operand: 1024 elements, 4 per thread.
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
+        // Thread t stages row (or weight row) t / 4, k = 4 (t % 4) .. + 3 of
+        // the slice.
+        const int sr = threadIdx.x / 4, sq = (threadIdx.x % 4) * 4;
+        const int gr = row0 + sr, gc = col0 + sr;
+        float4v xa = {0.f, 0.f, 0.f, 0.f}, wa = {0.f, 0.f, 0.f, 0.f};
+        auto fetch = [&](int k0) {
+            const int gk = k0 + sq;
+            xa = float4v {0.f, 0.f, 0.f, 0.f};
+            wa = float4v {0.f, 0.f, 0.f, 0.f};
+            if (gr < rows && gk < inner)
+                xa = *reinterpret_cast<const float4v*>(x + (size_t) gr * inner + gk);
+            if (gc < out && gk < inner)
+                wa = load4<WT>(w, (size_t) gc * inner + gk);
+        };
+        fetch(0);
+        for (int k0 = 0; k0 < inner; k0 += kTileK)
         {
-            const int e = threadIdx.x + i * kBlock;
-            const int r = e / kTileK, kk = e % kTileK;
-            const int gk = k0 + kk;
-            const int gr = row0 + r, gc = col0 + r;
-            xs[kk][r] = (gr < rows && gk < inner) ? x[(size_t) gr * inner + gk] : 0.f;
-            ws[kk][r] = (gc < out && gk < inner) ? load1<WT>(w, (size_t) gc * inner + gk) : 0.f;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < kTileK; ++kk)
-        {
-            float a[4], b[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
             {
-                a[i] = xs[kk][ty * 4 + i];
-                b[i] = ws[kk][tx * 4 + i];
+                xs[sq + i][sr] = xa[i];
+                ws[sq + i][sr] = wa[i];
             }
+            __syncthreads();
+            if (k0 + kTileK < inner)
+                fetch(k0 + kTileK);
+#pragma unroll
+            for (int kk = 0; kk < kTileK; ++kk)
+            {
+                const float4v a = *reinterpret_cast<const float4v*>(&xs[kk][ty * 4]);
+                const float4v b = *reinterpret_cast<const float4v*>(&ws[kk][tx * 4]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] += a[i] * b[j];
+            }
+            __syncthreads();
+        }
+    }
+    else
+        for (int k0 = 0; k0 < inner; k0 += kTileK)
+        {
+            // 64 x 16 of each operand: 1024 elements, 4 per thread.
 #pragma unroll
             for (int i = 0; i < 4; ++i)
+            {
+                const int e = threadIdx.x + i * kBlock;
+                const int r = e / kTileK, kk = e % kTileK;
+                const int gk = k0 + kk;
+                const int gr = row0 + r, gc = col0 + r;
+                xs[kk][r] = (gr < rows && gk < inner) ? x[(size_t) gr * inner + gk] : 0.f;
+                ws[kk][r] = (gc < out && gk < inner) ? load1<WT>(w, (size_t) gc * inner + gk) : 0.f;
+            }
+            __syncthreads();
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] += a[i] * b[j];
+            for (int kk = 0; kk < kTileK; ++kk)
+            {
+                float a[4], b[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    a[i] = xs[kk][ty * 4 + i];
+                    b[i] = ws[kk][tx * 4 + i];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] += a[i] * b[j];
+            }
+            __syncthreads();
         }
-        __syncthreads();
-    }
 
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -679,7 +750,15 @@ hipError_t launch_gemm(hipStream_t stream, const float* x, int rows, int inner, 
                        const float* bias, float* y, int out, int flags)
 {
     const dim3 grid((out + kTile - 1) / kTile, (rows + kTile - 1) / kTile);
-    hipLaunchKernelGGL((gemm_kernel<WT>), grid, dim3(kBlock), 0, stream, x, rows, inner, w, bias, y, out, flags);
+    const size_t w_align = WT == kF32 ? 16 : 8;
+    const bool vec = inner % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0
+                     && reinterpret_cast<uintptr_t>(w) % w_align == 0;
+    if (vec)
+        hipLaunchKernelGGL((gemm_kernel<WT, true>), grid, dim3(kBlock), 0, stream, x, rows, inner, w, bias, y, out,
+                           flags);
+    else
+        hipLaunchKernelGGL((gemm_kernel<WT, false>), grid, dim3(kBlock), 0, stream, x, rows, inner, w, bias, y, out,
+                           flags);
     return hipGetLastError();
 }
 } // namespace
