@@ -33,7 +33,8 @@ namespace wsp::encoder
 namespace
 {
 constexpr int kColumnThreads = 256;
-constexpr int kFlashWaves = 4; // queries per attention block: 16 per wave
+constexpr int kFlashWaves = 4;     // queries per attention block: 16 per wave
+constexpr int kFlashWideWaves = 8; // the same with twice the queries per K/V tile, when the blocks still fill the chip
 
 // Kernels/Conv1d.h:121-124 with kernel 3 and padding 1.
 int conv_length(int length, int stride)
@@ -98,6 +99,18 @@ __device__ __forceinline__ f32x4 mfma3(const f16x8& ah, const f16x8& al, const f
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, c, 0, 0, 0);
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, c, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, c, 0, 0, 0);
+}
+
+int compute_units()
+{
+    static const int units = [] {
+        int device = 0, count = 0;
+        if (hipGetDevice(&device) == hipSuccess
+            && hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && count > 0)
+            return count;
+        return 256;
+    }();
+    return units;
 }
 
 template <int WAVES>
@@ -476,10 +489,20 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
             return encoder_hip(e, status, "self-attention projections");
         if (d / heads == kFlashWidth && d % 4 == 0)
         {
-            hipLaunchKernelGGL(flash_attention_kernel<kFlashWaves>, dim3((positions + 16 * kFlashWaves - 1)
-                                                                            / (16 * kFlashWaves), heads),
-                               dim3(64 * kFlashWaves), 0, st, e->q, e->k, e->v, positions, d,
-                               scale * 1.44269504088896340736f, e->att);
+            // 128 queries a block share each K/V tile when that still leaves
+            // at most an eighth of the CUs idle (large-v3: 240 blocks,
+            // 14.2 -> 13.4 ms a window); else 64 (tiny.en's 72 blocks of 128
+            // queries measured slower than 144 of 64).
+            const int wide_blocks = (positions + 16 * kFlashWideWaves - 1) / (16 * kFlashWideWaves) * heads;
+            const float scale2 = scale * 1.44269504088896340736f;
+            if (8 * wide_blocks >= 7 * compute_units())
+                hipLaunchKernelGGL(flash_attention_kernel<kFlashWideWaves>,
+                                   dim3((positions + 16 * kFlashWideWaves - 1) / (16 * kFlashWideWaves), heads),
+                                   dim3(64 * kFlashWideWaves), 0, st, e->q, e->k, e->v, positions, d, scale2, e->att);
+            else
+                hipLaunchKernelGGL(flash_attention_kernel<kFlashWaves>,
+                                   dim3((positions + 16 * kFlashWaves - 1) / (16 * kFlashWaves), heads),
+                                   dim3(64 * kFlashWaves), 0, st, e->q, e->k, e->v, positions, d, scale2, e->att);
             status = hipGetLastError();
         }
         else
