@@ -62,6 +62,7 @@ private:
     void record(Pass& pass, const BufferRange& tokens, int tokenCount, const DecoderWeights& weights,
                 const BufferRange& logits, const float* mask, const BufferRange* argmaxSlots);
     void requireMatchingWeights(const DecoderWeights& weights) const;
+    wsp_decoder_tensors tablesFor(const DecoderWeights& weights);
 
     DecoderShape decoderShape;
     int streamCount = 0;

@@ -39,6 +39,18 @@ void BatchedDecoder::prepare(const DecoderWeights& weights, const Device& device
         layerTables.push_back(layerTable(layer));
 }
 
+// The table of the weights this step is given (Decoder::step's weights
+// argument, Decoder/Decoder.h:49-148): every layer's entries are taken from
+// them, not from the weights the batch was prepared with. The batch packs its
+// own copy again when the table's pointers change.
+wsp_decoder_tensors BatchedDecoder::tablesFor(const DecoderWeights& weights)
+{
+    layerTables.resize(weights.layers.size());
+    for (std::size_t i = 0; i < weights.layers.size(); ++i)
+        layerTables[i] = layerTable(weights.layers[i]);
+    return decoderTable(weights, layerTables);
+}
+
 void BatchedDecoder::requireMatchingWeights(const DecoderWeights& weights) const
 {
     if (!(weights.shape == decoderShape))
@@ -104,7 +116,7 @@ void BatchedDecoder::record(Pass& pass, const BufferRange& tokens, int tokenCoun
     if (argmaxSlots != nullptr && argmaxSlots->size < (std::size_t) streamCount * sizeof(uint32_t))
         throw ModelError("the argmax range holds fewer slots than streams");
 
-    const wsp_decoder_tensors tensors = decoderTable(weights, layerTables);
+    const wsp_decoder_tensors tensors = tablesFor(weights);
     const int status = wsp_batch_step(batch, &tensors, static_cast<const uint32_t*>(tokens.data()), tokenCount,
                                       static_cast<float*>(hidden.data()), static_cast<float*>(logits.data()), mask,
                                       argmaxSlots != nullptr ? static_cast<uint32_t*>(argmaxSlots->data()) : nullptr);
@@ -132,7 +144,7 @@ void BatchedDecoder::ringStep(Pass& pass, const BufferRange& ring, const Decoder
         throw ModelError("the token ring holds fewer than (maxPositions + 1) x streams slots");
     if (logits.size < (std::size_t) streamCount * decoderShape.vocabularySize * sizeof(float))
         throw ModelError("the logits range is smaller than streams rows");
-    const wsp_decoder_tensors tensors = decoderTable(weights, layerTables);
+    const wsp_decoder_tensors tensors = tablesFor(weights);
     const int status = wsp_batch_ring_step(batch, &tensors, static_cast<uint32_t*>(ring.data()),
                                            static_cast<float*>(logits.data()), mask);
     if (status != WSP_OK)
