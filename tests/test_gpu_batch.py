@@ -202,9 +202,9 @@ def test_streams_with_mask_reduced_cross_rows_and_prompt_step(oracle, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["F16", "BF16"])
-def test_six_heads_sweep_with_four_key_lanes(oracle, dtype):
+def test_six_heads_sweep_with_two_key_lanes(oracle, dtype):
     # tiny.en's width and head count (d 384, 6 heads): the cross-attention
-    # sweep runs 4 key lanes of 96 quads (384 threads) and folds them through
+    # sweep runs 2 key lanes of 96 quads (192 threads) and folds them through
     # LDS for an even-but-not-4-divisible head count; inner 384 gives the
     # products 12 k-blocks over 8 runs (runs of one and two).
     from whispereacp_amd.decoder import BatchedDecoder

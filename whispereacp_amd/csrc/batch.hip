@@ -1457,9 +1457,9 @@ hipError_t launch_attend(hipStream_t stream, Attend a, int rows, int span, int c
 }
 
 // Key lanes of a sweep block for this width: the fewest that make whole
-// waves, doubled while the block stays within kSweepThreads; 0 when the
-// shape does not fit (head width other than 64, or one key lane already too
-// wide).
+// waves (medium: one lane of 256 threads measured as fast as two of 512, or
+// two blocks a CU); 0 when the shape does not fit (head width other than 64,
+// or one key lane already too wide).
 int sweep_key_lanes(int width, int heads)
 {
     if (heads <= 0 || width != heads * 64)
@@ -1470,8 +1470,6 @@ int sweep_key_lanes(int width, int heads)
         lanes *= 2;
     if (quads * lanes > kSweepThreads)
         return 0;
-    while (quads * lanes * 2 <= kSweepThreads)
-        lanes *= 2;
     return lanes;
 }
 
