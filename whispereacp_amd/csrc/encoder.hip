@@ -35,6 +35,7 @@ namespace
 constexpr int kColumnThreads = 256;
 constexpr int kFlashWaves = 4;     // queries per attention block: 16 per wave
 constexpr int kFlashWideWaves = 8; // the same with twice the queries per K/V tile, when the blocks still fill the chip
+constexpr int kMaxFlashSplits = 4; // key splits of the attention when its 64-query blocks leave CUs idle
 
 // Kernels/Conv1d.h:121-124 with kernel 3 and padding 1.
 int conv_length(int length, int stride)
@@ -113,11 +114,16 @@ int compute_units()
     return units;
 }
 
+// Key splits: blockIdx.z takes keys [z·span, min((z + 1)·span, count)); with
+// one split the block writes the normalised rows to out, with several it
+// writes (max, sum, row) partials [split][head][query][66] for
+// flash_combine_kernel.
 template <int WAVES>
 __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float* __restrict__ q,
                                                                     const float* __restrict__ k,
                                                                     const float* __restrict__ v, int count,
-                                                                    int width, float scale2, float* __restrict__ out)
+                                                                    int width, float scale2, float* __restrict__ out,
+                                                                    int span, float* __restrict__ partials)
 {
     constexpr int kThreadsHere = WAVES * 64;
     constexpr int kUnits = kFlashKeys * kFlashWidth / 4; // float4 runs of a K (or V) tile
@@ -130,6 +136,7 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
     const int column = head * kFlashWidth;
     const int query = blockIdx.x * 16 * WAVES + 16 * wave + li;
     const bool query_in = query < count;
+    const int k_begin = (int) blockIdx.z * span, k_end = min(count, k_begin + span);
 
     // This lane's B fragments of Q^T: query `query`, dims 32 s + 8 g .. + 7.
     f16x8 qh[2], ql[2];
@@ -163,14 +170,15 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
         {
             const int unit = (int) threadIdx.x + i * kThreadsHere;
             const int key = first + (unit % kUnits) / 16, d4 = 4 * (unit % 16);
-            const size_t at = (size_t) min(key, count - 1) * width + column + d4;
+            const size_t at = (size_t) min(key, k_end - 1) * width + column + d4;
             kn[i] = *reinterpret_cast<const f32x4*>(k + at);
             vn[i] = *reinterpret_cast<const f32x4*>(v + at);
         }
     };
-    load_tile(0);
+    if (k_begin < k_end)
+        load_tile(k_begin);
 
-    for (int first = 0; first < count; first += kFlashKeys)
+    for (int first = k_begin; first < k_end; first += kFlashKeys)
     {
         __syncthreads(); // the previous tile has been read
 #pragma unroll
@@ -180,7 +188,7 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
             if (unit < kUnits)
             {
                 const int row = unit / 16, d4 = 4 * (unit % 16);
-                const bool in = first + row < count;
+                const bool in = first + row < k_end;
                 f16x4 kh, kl;
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
@@ -196,7 +204,7 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
             }
         }
         __syncthreads();
-        if (first + kFlashKeys < count)
+        if (first + kFlashKeys < k_end)
             load_tile(first + kFlashKeys);
 
         // S^T for keys 16 mt + 4 g + r of the tile, query li.
@@ -221,7 +229,7 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
             for (int r = 0; r < 4; ++r)
             {
                 const int key = first + 16 * mt + 4 * g + r;
-                x[4 * mt + r] = key < count ? st[mt][r] * scale2 : -INFINITY;
+                x[4 * mt + r] = key < k_end ? st[mt][r] * scale2 : -INFINITY;
                 tile_max = fmaxf(tile_max, x[4 * mt + r]);
             }
         tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
@@ -260,6 +268,25 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
     // The row sum over the four lanes of query li, then O = O^T / l.
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
+    if (partials != nullptr)
+    {
+        if (query_in)
+        {
+            const int heads = gridDim.y;
+            float* part = partials + (((size_t) blockIdx.z * heads + head) * count + query) * (kFlashWidth + 2);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    part[2 + 16 * t + 4 * g + r] = o[t][r];
+            if (g == 0)
+            {
+                part[0] = m;
+                part[1] = l;
+            }
+        }
+        return;
+    }
     if (query_in)
     {
         const float inv = 1.f / l;
@@ -269,6 +296,32 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
             for (int r = 0; r < 4; ++r)
                 out[(size_t) query * width + column + 16 * t + 4 * g + r] = o[t][r] * inv;
     }
+}
+
+// The key splits of every (query, head) combined in split order, in base-2
+// units: out = Σ 2^(m_s - m)·row_s / Σ 2^(m_s - m)·l_s. One 64-lane wave per
+// (query, head), a lane per channel.
+__global__ void __launch_bounds__(kFlashWidth) flash_combine_kernel(const float* __restrict__ partials, int count,
+                                                                    int heads, int splits, int width,
+                                                                    float* __restrict__ out)
+{
+    const int query = blockIdx.x, head = blockIdx.y, c = threadIdx.x;
+    const size_t stride = (size_t) heads * count * (kFlashWidth + 2);
+    const float* base = partials + ((size_t) head * count + query) * (kFlashWidth + 2);
+    float largest = -INFINITY;
+    for (int s = 0; s < splits; ++s)
+        largest = fmaxf(largest, base[s * stride]);
+    float numerator = 0.f, denominator = 0.f;
+    for (int s = 0; s < splits; ++s)
+    {
+        const float* part = base + s * stride;
+        if (part[1] == 0.f) // a split with no key
+            continue;
+        const float f = exp2f(part[0] - largest);
+        numerator += f * part[2 + c];
+        denominator += f * part[1];
+    }
+    out[(size_t) query * width + head * kFlashWidth + c] = numerator / denominator;
 }
 
 // Row p of the second convolution's columns over frame-major rows x
@@ -302,6 +355,7 @@ struct wsp_encoder
     float* att = nullptr;
     float* ff = nullptr;      // [positions, feed_forward_width]
     float* workspace = nullptr;
+    float* flash_partials = nullptr; // [kMaxFlashSplits][heads][positions][66], split-key attention
     std::vector<void*> owned;
     char error[512] = {0};
 };
@@ -370,6 +424,10 @@ int wsp_encoder_create(const wsp_encoder_shape* shape, int device, void* stream,
             status = encoder_allocate(e, r, positions * d);
     if (status == hipSuccess)
         status = encoder_allocate(e, &e->ff, positions * s.feed_forward_width);
+    if (status == hipSuccess && s.heads > 0 && s.width == s.heads * wsp::encoder::kFlashWidth)
+        status = encoder_allocate(e, &e->flash_partials,
+                                  (size_t) wsp::encoder::kMaxFlashSplits * s.heads * positions
+                                      * (wsp::encoder::kFlashWidth + 2));
     if (status == hipSuccess)
         status = encoder_allocate(e, &e->workspace,
                                   wsp::ops::attention_workspace_floats(s.heads, (int) positions, (int) positions,
@@ -495,15 +553,33 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
             // queries measured slower than 144 of 64).
             const int wide_blocks = (positions + 16 * kFlashWideWaves - 1) / (16 * kFlashWideWaves) * heads;
             const float scale2 = scale * 1.44269504088896340736f;
+            // Fewer 64-query blocks than CUs (tiny.en: 144): the keys are
+            // split over up to four blocks per query tile, at least 64 keys
+            // each, and the splits combined after.
+            const int narrow_blocks = (positions + 16 * kFlashWaves - 1) / (16 * kFlashWaves) * heads;
+            int splits = 1;
+            if (narrow_blocks < compute_units() && e->flash_partials != nullptr)
+                splits = std::max(1, std::min({kMaxFlashSplits, (compute_units() + narrow_blocks - 1) / narrow_blocks,
+                                               positions / 64}));
+            const int span = ((positions + splits - 1) / splits + kFlashKeys - 1) / kFlashKeys * kFlashKeys;
+            float* partials = splits > 1 ? e->flash_partials : nullptr;
             if (8 * wide_blocks >= 7 * compute_units())
                 hipLaunchKernelGGL(flash_attention_kernel<kFlashWideWaves>,
                                    dim3((positions + 16 * kFlashWideWaves - 1) / (16 * kFlashWideWaves), heads),
-                                   dim3(64 * kFlashWideWaves), 0, st, e->q, e->k, e->v, positions, d, scale2, e->att);
+                                   dim3(64 * kFlashWideWaves), 0, st, e->q, e->k, e->v, positions, d, scale2, e->att,
+                                   positions, nullptr);
             else
                 hipLaunchKernelGGL(flash_attention_kernel<kFlashWaves>,
-                                   dim3((positions + 16 * kFlashWaves - 1) / (16 * kFlashWaves), heads),
-                                   dim3(64 * kFlashWaves), 0, st, e->q, e->k, e->v, positions, d, scale2, e->att);
+                                   dim3((positions + 16 * kFlashWaves - 1) / (16 * kFlashWaves), heads, splits),
+                                   dim3(64 * kFlashWaves), 0, st, e->q, e->k, e->v, positions, d, scale2, e->att,
+                                   span, partials);
             status = hipGetLastError();
+            if (status == hipSuccess && splits > 1)
+            {
+                hipLaunchKernelGGL(flash_combine_kernel, dim3(positions, heads), dim3(kFlashWidth), 0, st,
+                                   e->flash_partials, positions, heads, splits, d, e->att);
+                status = hipGetLastError();
+            }
         }
         else
             status = ops::attention(st, e->q, positions, e->k, e->v, positions, d, heads, 0, scale, e->att,
