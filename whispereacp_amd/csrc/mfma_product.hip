@@ -122,6 +122,23 @@ __global__ void __launch_bounds__(kThreads) tile_product_kernel(TileProduct a)
     for (int s = 0; s < steps; ++s)
     {
         __syncthreads(); // the previous step's fragments are read
+        if constexpr (XPER == 4) // 32-row tiles: one float4 of a row per thread
+        {
+            uint32_t packed[P][2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+            {
+                uint32_t b0[3], b1[3];
+                split<WT>(ar[0][2 * j], b0);
+                split<WT>(ar[0][2 * j + 1], b1);
+#pragma unroll
+                for (int p = 0; p < P; ++p)
+                    packed[p][j] = b0[p] | (b1[p] << 16);
+            }
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+                *reinterpret_cast<uint2*>(&sa[p][sr][sh]) = uint2 {packed[p][0], packed[p][1]};
+        }
 #pragma unroll
         for (int h = 0; h < XPER / 8; ++h)
         {
@@ -223,18 +240,25 @@ hipError_t tile_product(hipStream_t stream, const TileProduct& product)
     }();
     const int columns = a.out / kTile;
     const bool narrow = (long long) columns * ((a.rows + kTile - 1) / kTile) < 4LL * units;
-    const int tm = narrow ? 64 : kTile;
+    // 32-row tiles when even 64-row tiles give fewer blocks than CUs (the
+    // tiny.en encoder's 384-column products: 72 blocks of 64 rows).
+    const bool narrowest = narrow && (long long) columns * ((a.rows + 63) / 64) < units;
+    const int tm = narrowest ? 32 : narrow ? 64 : kTile;
     const dim3 grid(columns, (a.rows + tm - 1) / tm);
     if (a.wdtype == kF16)
     {
-        if (narrow)
+        if (narrowest)
+            hipLaunchKernelGGL((tile_product_kernel<kF16, 32>), grid, dim3(kThreads), 0, stream, a);
+        else if (narrow)
             hipLaunchKernelGGL((tile_product_kernel<kF16, 64>), grid, dim3(kThreads), 0, stream, a);
         else
             hipLaunchKernelGGL((tile_product_kernel<kF16, kTile>), grid, dim3(kThreads), 0, stream, a);
     }
     else
     {
-        if (narrow)
+        if (narrowest)
+            hipLaunchKernelGGL((tile_product_kernel<kBF16, 32>), grid, dim3(kThreads), 0, stream, a);
+        else if (narrow)
             hipLaunchKernelGGL((tile_product_kernel<kBF16, 64>), grid, dim3(kThreads), 0, stream, a);
         else
             hipLaunchKernelGGL((tile_product_kernel<kBF16, kTile>), grid, dim3(kThreads), 0, stream, a);
