@@ -227,6 +227,16 @@ int wsp_hip_device_status_copy(wsp_hip_ctx* ctx, int* dst);
  * reference counterpart (see wsp_hip_device_status). */
 int wsp_hip_step_report(wsp_hip_ctx* ctx, const uint32_t* slot, int* host_pair);
 
+/* Hands host_pair to the next sampling step (wsp_hip_decoder_step with
+ * argmax_out) on this context: a persistent step writes the token and the
+ * watchdog word there itself when its argmax fold ends, so the
+ * wsp_hip_step_report(ctx, slot, host_pair) that follows it launches nothing.
+ * A step that trips its watchdog writes nothing: the caller puts a nonzero
+ * word in host_pair[1] beforehand and reads it as a trip. Other steps leave
+ * the report to wsp_hip_step_report as before. No reference counterpart (see
+ * wsp_hip_device_status). */
+int wsp_hip_step_report_next(wsp_hip_ctx* ctx, int* host_pair);
+
 /* Sets the watchdog word as a tripped wait does: later persistent steps on
  * this context leave at their first long wait, and every caller that reads
  * the word reports the failure, until it is cleared. No reference

@@ -52,6 +52,8 @@ def test_context_refuses_bad_arguments_without_a_device():
     assert lib.wsp_hip_linear(None, None, 1, 1, None, 0, None, None, 1, 0) == N.WSP_ERR_ARGUMENT
     assert lib.wsp_hip_argmax(None, None, 1, 1, None, None) == N.WSP_ERR_ARGUMENT
     assert lib.wsp_hip_decoder_step(None, None, None, 0, 1, None, None, None, None) == N.WSP_ERR_ARGUMENT
+    assert lib.wsp_hip_step_report(None, None, None) == N.WSP_ERR_ARGUMENT
+    assert lib.wsp_hip_step_report_next(None, None) == N.WSP_ERR_ARGUMENT
     assert lib.wsp_hip_last_error(None) == b"no context"
 
 

@@ -110,6 +110,7 @@ SIGNATURES = {
     "wsp_hip_device_status": (c_int, [c_void_p, ctypes.POINTER(c_int), c_int]),
     "wsp_hip_device_status_copy": (c_int, [c_void_p, ctypes.POINTER(c_int)]),
     "wsp_hip_step_report": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "wsp_hip_step_report_next": (c_int, [c_void_p, c_void_p]),
     "wsp_hip_raise_device_status": (c_int, [c_void_p]),
     "wsp_decoder_create": (c_int, [ctypes.POINTER(wsp_decoder_shape), ctypes.POINTER(wsp_tensor_entry), c_int,
                                    c_int, c_int, c_void_p, ctypes.POINTER(c_void_p)]),

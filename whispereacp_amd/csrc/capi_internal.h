@@ -23,6 +23,11 @@ struct wsp_hip_ctx
 
     void* fused = nullptr; // fused-step state (fused_step.hip)
 
+    // wsp_hip_step_report_next: the host pair the next sampling step writes
+    // (armed), and the one the last persistent step took over (reported).
+    int* armed_report = nullptr;
+    int* reported = nullptr;
+
     char error[512] = {0};
 };
 

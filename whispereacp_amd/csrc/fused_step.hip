@@ -369,6 +369,7 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     a.logits = logits;
     a.mask = mask;
     a.argmax_out = argmax_out;
+    a.host_pair = argmax_out != nullptr ? ctx->armed_report : nullptr;
     a.exchange = st->exchange;
     a.status = st->status;
     a.width = d;
@@ -417,6 +418,11 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
                                                           dim3(step::kThreads), args, 0, ctx->stream)
                              : hipLaunchKernel(step::kernel_for(tensors->wdtype), dim3(st->workgroups),
                                                dim3(step::kThreads), args, 0, ctx->stream);
+    if (e == hipSuccess && a.host_pair != nullptr)
+    {
+        ctx->reported = a.host_pair;
+        ctx->armed_report = nullptr;
+    }
     return context_hip(ctx, e, "decoder step launch");
 }
 } // namespace
@@ -524,6 +530,12 @@ __global__ void report_kernel(const uint32_t* slot, const int* status, int* host
 
 int fused_report(Context* ctx, const uint32_t* slot, int* host_pair)
 {
+    ctx->armed_report = nullptr;
+    if (ctx->reported == host_pair) // the persistent step wrote it when it ended
+    {
+        ctx->reported = nullptr;
+        return WSP_OK;
+    }
     auto* state = static_cast<FusedState*>(ctx->fused);
     const int* status = state != nullptr ? state->status : nullptr;
     hipLaunchKernelGGL(report_kernel, dim3(1), dim3(1), 0, ctx->stream, slot, status, host_pair);
@@ -593,6 +605,15 @@ extern "C" int wsp_hip_step_report(wsp_hip_ctx* ctx, const uint32_t* slot, int* 
     if (ctx == nullptr || slot == nullptr || host_pair == nullptr)
         return WSP_ERR_ARGUMENT;
     return wsp::fused_report(ctx, slot, host_pair);
+}
+
+extern "C" int wsp_hip_step_report_next(wsp_hip_ctx* ctx, int* host_pair)
+{
+    if (ctx == nullptr || host_pair == nullptr)
+        return WSP_ERR_ARGUMENT;
+    ctx->armed_report = host_pair;
+    ctx->reported = nullptr;
+    return WSP_OK;
 }
 
 extern "C" int wsp_hip_raise_device_status(wsp_hip_ctx* ctx)

@@ -73,6 +73,13 @@ GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int 
 
     auto startStep = [&](int step) {
         const int target = promptLength + step;
+        // The sampling step reports its token and watchdog word itself (a
+        // persistent step; else the report below launches); a step that
+        // trips writes nothing and leaves the nonzero word.
+        int* pair = &hostReports[2 * (step % stepsInFlight)];
+        pair[1] = -1;
+        if (wsp_hip_step_report_next(context, pair) != WSP_OK)
+            throw std::runtime_error(std::string("arm the step's report: ") + wsp_hip_last_error(context));
         if (step == 0)
         {
             // The prompt but its last token, then the last token with the
@@ -88,9 +95,10 @@ GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int 
         }
         else
             decoder.stepAndSample(pass, slot(target - 1), weights, BufferRange::of(logitRows), laterMask, slot(target));
-        // The token and the watchdog word in one launch behind the step.
+        // The token and the watchdog word: written by the step itself, or in
+        // one launch behind it.
         const int reported = wsp_hip_step_report(context, static_cast<const std::uint32_t*>(slot(target).data()),
-                                                 &hostReports[2 * (step % stepsInFlight)]);
+                                                 pair);
         if (reported != WSP_OK)
             throw std::runtime_error(std::string("report the step's token: ") + wsp_hip_last_error(context));
         checkHip(hipEventRecord(static_cast<hipEvent_t>(events[(std::size_t) (step % stepsInFlight)]), stream),

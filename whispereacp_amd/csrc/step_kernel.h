@@ -45,6 +45,7 @@ struct StepArgs
     float* logits;
     const float* mask;
     uint32_t* argmax_out;
+    int* host_pair;     // with argmax_out: the token and the watchdog word, written to pinned host memory, or null
     uint64_t* exchange;
     int* status;
 

@@ -1598,7 +1598,19 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
         }
         fold64(bv, bi);
         if (threadIdx.x == 0)
-            a.argmax_out[0] = bi == kUnchosen ? 0u : bi;
+        {
+            const uint32_t token = bi == kUnchosen ? 0u : bi;
+            a.argmax_out[0] = token;
+            // Every workgroup's candidate arrived, so none waits any more:
+            // the watchdog word is final for this step.
+            if (a.host_pair != nullptr)
+            {
+                __hip_atomic_store(a.host_pair, (int) token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(a.host_pair + 1,
+                                   __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
         STEP_STAMP(20, 0);
     }
 }
