@@ -47,15 +47,17 @@ __global__ void __launch_bounds__(kThreads) frames_kernel(const float* __restric
     }
 }
 
-__global__ void __launch_bounds__(kThreads) power_kernel(const float* __restrict__ spectrum, int bins, int total,
-                                                         float* __restrict__ power)
+// power rows have a stride of `padded` (bins rounded up to a multiple of 4,
+// the padding left at zero) so the filterbank product takes vector loads.
+__global__ void __launch_bounds__(kThreads) power_kernel(const float* __restrict__ spectrum, int bins, int padded,
+                                                         int total, float* __restrict__ power)
 {
     const int i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= total)
         return;
     const int f = i / bins, b = i % bins;
     const float re = spectrum[(size_t) f * 2 * bins + 2 * b], im = spectrum[(size_t) f * 2 * bins + 2 * b + 1];
-    power[i] = re * re + im * im;
+    power[(size_t) f * padded + b] = re * re + im * im;
 }
 
 // log10 of the [frames, mels] products into the band-major output, and each
@@ -101,7 +103,8 @@ struct wsp_mel
     float* basis = nullptr;    // [2 bins][fft]: cos, -sin
     float* frames = nullptr;   // [frames][fft]
     float* spectrum = nullptr; // [frames][2 bins]
-    float* power = nullptr;    // [frames][bins]
+    float* power = nullptr;    // [frames][padded bins], the padding zero
+    float* filters = nullptr;  // [mels][padded bins]: the call's filterbank, the padding zero
     float* rows = nullptr;     // [frames][mels]
     float* peaks = nullptr;    // [kLogBlocks]
     std::vector<void*> owned;
@@ -173,8 +176,15 @@ int wsp_mel_create(const wsp_mel_shape* shape, int device, void* stream, wsp_mel
         status = mel_allocate(m, &m->frames, (size_t) s.frame_count * fft);
     if (status == hipSuccess)
         status = mel_allocate(m, &m->spectrum, (size_t) s.frame_count * 2 * bins);
+    const int padded = (bins + 3) / 4 * 4;
     if (status == hipSuccess)
-        status = mel_allocate(m, &m->power, (size_t) s.frame_count * bins);
+        status = mel_allocate(m, &m->power, (size_t) s.frame_count * padded);
+    if (status == hipSuccess)
+        status = mel_allocate(m, &m->filters, (size_t) s.mel_count * padded);
+    if (status == hipSuccess)
+        status = hipMemset(m->power, 0, (size_t) s.frame_count * padded * sizeof(float));
+    if (status == hipSuccess)
+        status = hipMemset(m->filters, 0, (size_t) s.mel_count * padded * sizeof(float));
     if (status == hipSuccess)
         status = mel_allocate(m, &m->rows, (size_t) s.frame_count * s.mel_count);
     if (status == hipSuccess)
@@ -233,12 +243,18 @@ int wsp_mel_encode(wsp_mel* m, const float* samples, const float* filters, float
     if ((status = wsp::ops::linear(st, m->frames, frames, fft, m->basis, WSP_F32, nullptr, m->spectrum, 2 * bins, 0))
         != hipSuccess)
         return mel_hip(m, status, "spectrum");
-    const int cells = frames * bins;
+    const int cells = frames * bins, padded = (bins + 3) / 4 * 4;
     hipLaunchKernelGGL(power_kernel, dim3((cells + kThreads - 1) / kThreads), dim3(kThreads), 0, st, m->spectrum,
-                       bins, cells, m->power);
+                       bins, padded, cells, m->power);
     if ((status = hipGetLastError()) != hipSuccess)
         return mel_hip(m, status, "power");
-    if ((status = wsp::ops::linear(st, m->power, frames, bins, filters, WSP_F32, nullptr, m->rows, mels, 0))
+    // The filterbank into rows of the padded stride (the padding stays zero):
+    // the product then sums the same terms in the same order, plus zeros.
+    if ((status = hipMemcpy2DAsync(m->filters, (size_t) padded * sizeof(float), filters, (size_t) bins * sizeof(float),
+                                   (size_t) bins * sizeof(float), mels, hipMemcpyDeviceToDevice, st))
+        != hipSuccess)
+        return mel_hip(m, status, "filterbank copy");
+    if ((status = wsp::ops::linear(st, m->power, frames, padded, m->filters, WSP_F32, nullptr, m->rows, mels, 0))
         != hipSuccess)
         return mel_hip(m, status, "filterbank");
     const int total = frames * mels;

@@ -154,20 +154,24 @@ __device__ __forceinline__ float4v load4(const void* w, size_t index)
     }
 }
 
-template <int WT, bool VEC>
+// TM rows by 64 columns a block: RT = TM / 16 rows by 4 columns a thread
+// (TM 32, VEC only, when 64-row blocks leave CUs idle).
+template <int WT, bool VEC, int TM>
 __global__ void __launch_bounds__(kBlock) gemm_kernel(const float* __restrict__ x, int rows,
                                                       int inner, const void* __restrict__ w,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ y, int out, int flags)
 {
+    constexpr int RT = TM / 16;
+    static_assert(TM == kTile || (VEC && TM == 32), "32-row blocks take vector loads");
     __shared__ __attribute__((aligned(16))) float xs[kTileK][kTile + 4];
     __shared__ __attribute__((aligned(16))) float ws[kTileK][kTile + 4];
 
-    const int row0 = blockIdx.y * kTile;
+    const int row0 = blockIdx.y * TM;
     const int col0 = blockIdx.x * kTile;
     const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
 
-    float acc[4][4] = {};
+    float acc[RT][4] = {};
 
     if constexpr (VEC)
     {
@@ -180,7 +184,7 @@ __global__ void __launch_bounds__(kBlock) gemm_kernel(const float* __restrict__ 
             const int gk = k0 + sq;
             xa = float4v {0.f, 0.f, 0.f, 0.f};
             wa = float4v {0.f, 0.f, 0.f, 0.f};
-            if (gr < rows && gk < inner)
+            if (sr < TM && gr < rows && gk < inner)
                 xa = *reinterpret_cast<const float4v*>(x + (size_t) gr * inner + gk);
             if (gc < out && gk < inner)
                 wa = load4<WT>(w, (size_t) gc * inner + gk);
@@ -191,7 +195,8 @@ __global__ void __launch_bounds__(kBlock) gemm_kernel(const float* __restrict__ 
 #pragma unroll
             for (int i = 0; i < 4; ++i)
             {
-                xs[sq + i][sr] = xa[i];
+                if (sr < TM)
+                    xs[sq + i][sr] = xa[i];
                 ws[sq + i][sr] = wa[i];
             }
             __syncthreads();
@@ -200,10 +205,20 @@ __global__ void __launch_bounds__(kBlock) gemm_kernel(const float* __restrict__ 
 #pragma unroll
             for (int kk = 0; kk < kTileK; ++kk)
             {
-                const float4v a = *reinterpret_cast<const float4v*>(&xs[kk][ty * 4]);
+                float a[RT];
+                if constexpr (RT == 4)
+                {
+                    const float4v v = *reinterpret_cast<const float4v*>(&xs[kk][ty * 4]);
+                    a[0] = v[0]; a[1] = v[1]; a[2] = v[2]; a[3] = v[3];
+                }
+                else
+                {
+                    const float2 v = *reinterpret_cast<const float2*>(&xs[kk][ty * 2]);
+                    a[0] = v.x; a[1] = v.y;
+                }
                 const float4v b = *reinterpret_cast<const float4v*>(&ws[kk][tx * 4]);
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < RT; ++i)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         acc[i][j] += a[i] * b[j];
@@ -211,7 +226,7 @@ __global__ void __launch_bounds__(kBlock) gemm_kernel(const float* __restrict__ 
             __syncthreads();
         }
     }
-    else
+    else if constexpr (TM == kTile)
         for (int k0 = 0; k0 < inner; k0 += kTileK)
         {
             // 64 x 16 of each operand: 1024 elements, 4 per thread.
@@ -246,9 +261,9 @@ __global__ void __launch_bounds__(kBlock) gemm_kernel(const float* __restrict__ 
         }
 
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RT; ++i)
     {
-        const int r = row0 + ty * 4 + i;
+        const int r = row0 + ty * RT + i;
         if (r >= rows)
             continue;
 #pragma unroll
@@ -753,12 +768,22 @@ hipError_t launch_gemm(hipStream_t stream, const float* x, int rows, int inner, 
     const size_t w_align = WT == kF32 ? 16 : 8;
     const bool vec = inner % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0
                      && reinterpret_cast<uintptr_t>(w) % w_align == 0;
-    if (vec)
-        hipLaunchKernelGGL((gemm_kernel<WT, true>), grid, dim3(kBlock), 0, stream, x, rows, inner, w, bias, y, out,
-                           flags);
+    static const int units = [] {
+        int device = 0, count = 0;
+        if (hipGetDevice(&device) == hipSuccess
+            && hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && count > 0)
+            return count;
+        return 256;
+    }();
+    if (vec && (long long) grid.x * grid.y < units) // 32-row blocks: twice the blocks
+        hipLaunchKernelGGL((gemm_kernel<WT, true, 32>), dim3(grid.x, (rows + 31) / 32), dim3(kBlock), 0, stream, x,
+                           rows, inner, w, bias, y, out, flags);
+    else if (vec)
+        hipLaunchKernelGGL((gemm_kernel<WT, true, kTile>), grid, dim3(kBlock), 0, stream, x, rows, inner, w, bias, y,
+                           out, flags);
     else
-        hipLaunchKernelGGL((gemm_kernel<WT, false>), grid, dim3(kBlock), 0, stream, x, rows, inner, w, bias, y, out,
-                           flags);
+        hipLaunchKernelGGL((gemm_kernel<WT, false, kTile>), grid, dim3(kBlock), 0, stream, x, rows, inner, w, bias, y,
+                           out, flags);
     return hipGetLastError();
 }
 } // namespace
