@@ -772,14 +772,30 @@ __global__ void __launch_bounds__(kTileThreads) tile_kernel(Tile a)
 #pragma unroll
         for (int u = 0; u < KB; ++u)
             wv[u] = *reinterpret_cast<const u32x4*>(wfrag + (size_t) (kb0 + min(u, nkb - 1)) * kFragment);
-        // Stage rows [0, R) x inner [32 kb0, 32 (kb0 + nkb)) as float4 runs:
-        // run i is row i / (KB * 8), run i % (KB * 8) of the row.
+        // Stage rows [0, R) x inner [32 kb0, 32 (kb0 + nkb)) as float4 runs
+        // (row m, values 4j .. 4j + 3 of the batch), taken in the source's
+        // order so that a wave's loads are contiguous: row-major runs for a
+        // row-major x; for the residual stream, its fragment-major order
+        // (fragment (t, kb), half, lane slot 16g + r).
+        const auto run_at = [&](int i, int& m, int& j) {
+            if (a.x_residual)
+            {
+                const int t = i / (KB * 128), rest = i % (KB * 128), slot = rest % 64;
+                m = t * 16 + slot % 16;
+                j = (rest / 128) * 8 + (slot / 16) * 2 + (rest / 64) % 2;
+            }
+            else
+            {
+                m = i / (KB * 8);
+                j = i % (KB * 8);
+            }
+        };
         float4v xv[RUNS];
 #pragma unroll
         for (int r = 0; r < RUNS; ++r)
         {
-            const int i = (int) threadIdx.x + r * kTileThreads;
-            const int m = i / (KB * 8), j = i % (KB * 8);
+            int m, j;
+            run_at((int) threadIdx.x + r * kTileThreads, m, j);
             xv[r] = float4v {0.f, 0.f, 0.f, 0.f};
             if (m < a.rows && j < nkb * 8)
                 xv[r] = *reinterpret_cast<const float4v*>(
@@ -788,8 +804,8 @@ __global__ void __launch_bounds__(kTileThreads) tile_kernel(Tile a)
 #pragma unroll
         for (int r = 0; r < RUNS; ++r)
         {
-            const int i = (int) threadIdx.x + r * kTileThreads;
-            const int m = i / (KB * 8), j = i % (KB * 8);
+            int m, j;
+            run_at((int) threadIdx.x + r * kTileThreads, m, j);
             float4v v = xv[r];
             if (a.gamma != nullptr && m < a.rows && j < nkb * 8)
             {
