@@ -1,8 +1,12 @@
-// The misuse refusals of WSP::HipNet, the gfx950 Net backend, in the manner of
-// the reference's KernelNet (Net/KernelNet.cpp:228-244, 274-288, 313-335): each
-// case misuses a fresh net and must get std::logic_error with the reference's
-// message, before anything wrong reaches the device. Test infrastructure
-// (tests/test_gpu_net.py and tests/test_abi.py run it).
+// The misuse refusals of WSP::HipNet, the gfx950 Net backend. HipNet records a
+// program and places every value when the recording ends, so a misuse is
+// refused either at the op (no recording open, a stale or foreign handle, a
+// cache overflow, a bad output()) or at end() before the first launch (a value
+// with nowhere to live, scratch buffers too few for the values live at once).
+// Each case misuses a fresh net and must get std::logic_error naming the
+// problem. One proper recording runs on the device, and a chain of LayerNorms
+// whose handles all stay held shows buffers shared by liveness. Test
+// infrastructure (tests/test_gpu_net.py and tests/test_abi.py run it).
 //
 //   net_refusals host      the cases that need no device (nothing prepared)
 //   net_refusals device    the cases on a prepared net (device 0)
@@ -13,6 +17,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <functional>
@@ -81,12 +86,30 @@ DecoderShape tinyShape()
     return s;
 }
 
-HipNetLayout layout(int slots)
+HipNetLayout layout(int slots, int values = 4096)
 {
     HipNetLayout l;
     l.shape = tinyShape();
     l.scratch = {{kWidth, slots}};
+    l.valueCapacity = values;
     return l;
+}
+
+// LayerNorm of one row, gamma 1 and beta 0, in double (the oracle's formula).
+std::vector<double> hostLayerNorm(const std::vector<double>& x)
+{
+    double mean = 0;
+    for (double v : x)
+        mean += v;
+    mean /= (double) x.size();
+    double var = 0;
+    for (double v : x)
+        var += (v - mean) * (v - mean);
+    var /= (double) x.size();
+    std::vector<double> y(x.size());
+    for (std::size_t i = 0; i < x.size(); ++i)
+        y[i] = (x[i] - mean) / std::sqrt(var + 1e-5);
+    return y;
 }
 
 // A device vector of `count` floats, all `value`.
@@ -113,14 +136,18 @@ Binding bindingOf(const Weight& w, int rows, int columns)
 
 void hostCases()
 {
-    expectRefusal("begin before prepare", "records once it is prepared", [] {
+    expectRefusal("begin before prepare", "not prepared", [] {
         HipNet net;
         Pass pass;
         net.begin(pass);
     });
-    expectRefusal("cache before prepare", "makes a cache once it is prepared", [] {
+    expectRefusal("cache before prepare", "not prepared", [] {
         HipNet net;
         (void) net.makeCache(4, kWidth);
+    });
+    expectRefusal("an op before prepare", "no recording is open", [] {
+        HipNet net;
+        (void) net.input(Binding {}, Shape {1, kWidth}, DType::float32);
     });
     expectRefusal("transpose is an encoder op", "encoder op", [] {
         HipNet net;
@@ -145,15 +172,14 @@ void deviceCases()
     const Weight gamma = vectorOf(device, kWidth, 1.0f);
     const Weight beta = vectorOf(device, kWidth, 0.0f);
     const Weight square = matrixOf(device, kWidth, kWidth, 0.01f);
+    const Weight out = matrixOf(device, 1, kWidth, 0.0f);
 
-    expectRefusal("an op outside begin and end", "records between begin() and end()", [&] {
+    expectRefusal("an op with no recording open", "no recording is open", [&] {
         HipNet net;
         net.prepare(device, layout(2), nullptr);
-        Tensor in = net.input(bindingOf(x, 1, kWidth), Shape {1, kWidth}, DType::float32);
-        Tensor a = net.layerNorm(in, gamma, beta);
-        Tensor b = net.layerNorm(a, gamma, beta); // dispatches the first: no pass is open
+        (void) net.input(bindingOf(x, 1, kWidth), Shape {1, kWidth}, DType::float32);
     });
-    expectRefusal("a pass on another stream", "the stream it was prepared with", [&] {
+    expectRefusal("a pass on another stream", "another stream", [&] {
         hipStream_t other = nullptr;
         if (hipStreamCreate(&other) != hipSuccess)
             throw std::runtime_error("hipStreamCreate");
@@ -167,19 +193,27 @@ void deviceCases()
         Pass pass(other);
         net.begin(pass);
     });
-    expectRefusal("a value outliving its recording", "outlived the recording", [&] {
+    expectRefusal("a second begin", "already open", [&] {
         HipNet net;
         net.prepare(device, layout(2), nullptr);
         Pass pass;
-        Tensor kept;
         net.begin(pass);
-        {
-            Tensor in = net.input(bindingOf(x, 1, kWidth), Shape {1, kWidth}, DType::float32);
-            kept = net.layerNorm(in, gamma, beta);
-        }
-        net.end(); // kept still holds a scratch buffer
+        net.begin(pass);
     });
-    expectRefusal("every scratch buffer held", "every scratch buffer of 64 elements is holding a value", [&] {
+    expectRefusal("a handle kept past its recording", "recording that has ended", [&] {
+        HipNet net;
+        net.prepare(device, layout(2), nullptr);
+        Pass pass;
+        net.begin(pass);
+        Tensor in = net.input(bindingOf(x, 1, kWidth), Shape {1, kWidth}, DType::float32);
+        Tensor kept = net.layerNorm(in, gamma, beta);
+        net.output(kept, bindingOf(out, 1, kWidth));
+        net.end();
+        pass.synchronize();
+        net.begin(pass);
+        (void) net.layerNorm(kept, gamma, beta);
+    });
+    expectRefusal("more values live than scratch buffers", "are live than the 2 scratch buffers", [&] {
         HipNet net;
         net.prepare(device, layout(2), nullptr);
         Pass pass;
@@ -187,33 +221,40 @@ void deviceCases()
         Tensor in = net.input(bindingOf(x, 1, kWidth), Shape {1, kWidth}, DType::float32);
         Tensor a = net.layerNorm(in, gamma, beta);
         Tensor b = net.layerNorm(in, gamma, beta);
-        Tensor c = net.layerNorm(in, gamma, beta); // two buffers of this capacity were reserved
+        Tensor c = net.layerNorm(in, gamma, beta); // a and b are read later: three live here
+        (void) net.linearAdd(a, square, nullptr, c);
+        net.output(net.layerNorm(b, gamma, beta), bindingOf(out, 1, kWidth));
+        net.end();
     });
-    expectRefusal("more live values than records", "more values at once than it has records for", [&] {
+    expectRefusal("more values than the table holds", "already holds 8 values", [&] {
         HipNet net;
-        net.prepare(device, layout(2), nullptr);
-        std::vector<Tensor> held;
-        for (int i = 0; i < 65; ++i)
-            held.push_back(net.input(bindingOf(x, 1, kWidth), Shape {1, kWidth}, DType::float32));
+        net.prepare(device, layout(2, 8), nullptr);
+        Pass pass;
+        net.begin(pass);
+        for (int i = 0; i < 9; ++i)
+            (void) net.input(bindingOf(x, 1, kWidth), Shape {1, kWidth}, DType::float32);
     });
-    expectRefusal("a tensor of another net", "holds no value of this net", [&] {
+    expectRefusal("a tensor of another net", "not a value of this net", [&] {
         HipNet first, second;
         first.prepare(device, layout(2), nullptr);
         second.prepare(device, layout(2), nullptr);
+        Pass pass;
+        first.begin(pass);
+        second.begin(pass);
         Tensor in = first.input(bindingOf(x, 1, kWidth), Shape {1, kWidth}, DType::float32);
         (void) second.layerNorm(in, gamma, beta);
     });
-    expectRefusal("a value with no buffer of its capacity", "has to be placed by output()", [&] {
+    expectRefusal("a value with nowhere to live", "no scratch buffers of that capacity", [&] {
         HipNet net;
         net.prepare(device, layout(2), nullptr);
         Pass pass;
         net.begin(pass);
         const Weight rows = matrixOf(device, 2, kWidth, 0.25f);
         Tensor in = net.input(bindingOf(rows, 2, kWidth), Shape {2, kWidth}, DType::float32);
-        Tensor a = net.layerNorm(in, gamma, beta); // 128 elements: nothing was reserved at that capacity
-        Tensor b = net.layerNorm(in, gamma, beta);
+        (void) net.layerNorm(in, gamma, beta); // 128 floats: no class, never bound
+        net.end();
     });
-    expectRefusal("a cache appended past its capacity", "appended to past its capacity", [&] {
+    expectRefusal("a cache appended past its capacity", "would overflow a cache", [&] {
         HipNet net;
         net.prepare(device, layout(2), nullptr);
         Cache cache = net.makeCache(2, kWidth);
@@ -224,13 +265,20 @@ void deviceCases()
         Tensor r2 = net.appendLinear(cache, in, square, nullptr);
         Tensor r3 = net.appendLinear(cache, in, square, nullptr); // the cache holds two rows
     });
-    // The same recording used as the net intends passes, so the refusals above
-    // are the misuse and not the setup.
+    expectRefusal("output() of a view", "view of storage", [&] {
+        HipNet net;
+        net.prepare(device, layout(2), nullptr);
+        Pass pass;
+        net.begin(pass);
+        Tensor in = net.input(bindingOf(x, 1, kWidth), Shape {1, kWidth}, DType::float32);
+        net.output(in, bindingOf(out, 1, kWidth));
+    });
+    // The same ops used as the net intends pass, so the refusals above are the
+    // misuse and not the setup.
     expectNoRefusal("a proper recording", [&] {
         HipNet net;
         net.prepare(device, layout(2), nullptr);
         Cache cache = net.makeCache(2, kWidth);
-        const Weight out = matrixOf(device, 1, kWidth, 0.0f);
         Pass pass;
         net.begin(pass);
         {
@@ -241,6 +289,42 @@ void deviceCases()
         }
         net.end();
         pass.synchronize();
+    });
+    // Four chained LayerNorms whose handles all stay held: their spans meet
+    // pairwise only, so two buffers carry them, and the bound result matches
+    // four LayerNorms on the host.
+    expectNoRefusal("a chain sharing two buffers", [&] {
+        std::vector<float> row(kWidth);
+        for (int i = 0; i < kWidth; ++i)
+            row[(std::size_t) i] = (float) (i % 7) - 2.5f + 0.01f * (float) i;
+        Weight input;
+        input.storage = std::make_shared<DeviceBuffer>(device, row.data(), row.size() * sizeof(float));
+        input.extents = {1, kWidth};
+        HipNet net;
+        net.prepare(device, layout(2), nullptr);
+        Pass pass;
+        net.begin(pass);
+        Tensor in = net.input(bindingOf(input, 1, kWidth), Shape {1, kWidth}, DType::float32);
+        Tensor a = net.layerNorm(in, gamma, beta);
+        Tensor b = net.layerNorm(a, gamma, beta);
+        Tensor c = net.layerNorm(b, gamma, beta);
+        Tensor d = net.layerNorm(c, gamma, beta);
+        Tensor e = net.layerNorm(d, gamma, beta);
+        net.output(e, bindingOf(out, 1, kWidth));
+        net.end();
+        pass.synchronize();
+        if (net.scratchHighWater().at(0) != 2)
+            throw std::runtime_error("the chain used " + std::to_string(net.scratchHighWater().at(0))
+                                     + " buffers, not 2");
+        std::vector<float> got(kWidth);
+        out.storage->read(got.data(), got.size() * sizeof(float));
+        std::vector<double> want(row.begin(), row.end());
+        for (int k = 0; k < 5; ++k)
+            want = hostLayerNorm(want);
+        for (int i = 0; i < kWidth; ++i)
+            if (std::fabs(got[(std::size_t) i] - want[(std::size_t) i]) > 1e-4)
+                throw std::runtime_error("element " + std::to_string(i) + ": " + std::to_string(got[(std::size_t) i])
+                                         + " against " + std::to_string(want[(std::size_t) i]));
     });
 }
 } // namespace

@@ -138,13 +138,13 @@ def net_refusals():
 
 
 def test_net_refusals_without_a_device():
-    # WSP::HipNet refuses with std::logic_error, as the reference's KernelNet
-    # does, what it can refuse before anything is prepared: recording or making
-    # a cache before prepare(), the encoder-only ops, a shape past four extents.
+    # WSP::HipNet refuses with std::logic_error what it can refuse before
+    # anything is prepared: a recording, a cache or an op before prepare(), the
+    # encoder-only ops, a shape past four extents.
     import subprocess
     result = subprocess.run([net_refusals(), "host"], capture_output=True, text=True, timeout=60)
     assert result.returncode == 0, result.stdout + result.stderr
-    assert result.stdout.count("ok ") == 6, result.stdout
+    assert result.stdout.count("ok ") == 7, result.stdout
 
 
 def test_headers_compile_as_c99(tmp_path):

@@ -1,11 +1,12 @@
-"""WSP::HipNet's misuse refusals on a prepared net (device 0), in the manner of
-the reference's KernelNet (Net/KernelNet.cpp:228-244, 274-288, 313-335): an op
-recorded outside begin()/end(), a pass on another stream, a value outliving its
-recording, every scratch buffer of a capacity held, more live values than
-records, a tensor of another net, a value with no buffer of its capacity left
-unplaced, and a cache appended past its capacity each end in std::logic_error
-with the reference's message; the same recording used properly passes. The
-cases are C++ (tests/native/net_refusals.cpp), run in a process of their own."""
+"""WSP::HipNet's misuse refusals on a prepared net (device 0). HipNet records a
+program and places its values when the recording ends: an op with no recording
+open, a pass on another stream, a second begin(), a handle kept past its
+recording, more values live at one instruction than scratch buffers, a full
+value table, a tensor of another net, a value with nowhere to live, a cache
+appended past its capacity and output() of a view each end in
+std::logic_error; a proper recording passes, and a chain of five LayerNorms
+whose handles all stay held runs in two buffers and matches the host. The cases
+are C++ (tests/native/net_refusals.cpp), run in a process of their own."""
 
 import os
 import subprocess
@@ -25,4 +26,4 @@ def test_net_refusals_on_a_prepared_net():
     result = subprocess.run([path, "device"], capture_output=True, text=True, timeout=120)
     print(result.stdout)
     assert result.returncode == 0, result.stdout + result.stderr
-    assert result.stdout.count("ok ") == 9, result.stdout
+    assert result.stdout.count("ok ") == 12, result.stdout

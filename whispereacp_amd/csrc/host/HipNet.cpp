@@ -1,6 +1,7 @@
-// HipNet: the decoder profile of Net on gfx950 (include/whispereacp/HipNet.h).
-// The value bookkeeping follows Net/KernelNet.cpp:220-513; each op is one or
-// two C-ABI calls on the context's stream.
+// HipNet: Net on gfx950 as a recorded program (include/whispereacp/HipNet.h).
+// Ops append instructions; end() places every value (bindings, fixed views,
+// scratch buffers shared by liveness) and then issues the instructions in
+// order, each one or two C-ABI calls on the context's stream.
 #include "../../../include/whispereacp/HipNet.h"
 #include "host_common.h"
 
@@ -13,9 +14,18 @@ namespace WSP
 {
 namespace
 {
-std::size_t floatBytes(int elements)
+constexpr int kIndexBits = 16;
+constexpr int kIndexMask = (1 << kIndexBits) - 1;
+constexpr std::uint32_t kGenerationMask = 0x7FFF; // handles stay non-negative ints
+
+std::size_t floatBytes(long long elements)
 {
     return (std::size_t) elements * sizeof(float);
+}
+
+std::string floats(int elements)
+{
+    return std::to_string(elements) + " floats";
 }
 } // namespace
 
@@ -36,9 +46,10 @@ HipNet::~HipNet()
     wsp_hip_ctx_destroy(ctx);
 }
 
-void HipNet::prepare(const Device& deviceToUse, const HipNetLayout& layoutToUse, void* hipStream)
+void HipNet::prepare(const Device& deviceToUse, const HipNetLayout& layout, void* hipStream)
 {
-    layout = layoutToUse;
+    if (layout.valueCapacity <= 0 || layout.valueCapacity > kIndexMask + 1 || layout.instructionCapacity <= 0)
+        throw std::invalid_argument("HipNet::prepare: the value and instruction tables need a size in [1, 65536]");
     device = deviceToUse;
     wsp_hip_ctx_destroy(ctx);
     ctx = nullptr;
@@ -47,14 +58,41 @@ void HipNet::prepare(const Device& deviceToUse, const HipNetLayout& layoutToUse,
     if (status != WSP_OK)
         throwForStatus(status, "HipNet::prepare: the kernel context could not be created");
 
-    records.assign(maxRecords, Record {});
-    slots.clear();
+    // Reservations of one capacity join one class, so a layout may list a
+    // capacity twice.
+    scratchClasses.clear();
+    int total = 0;
     for (const auto& reservation : layout.scratch)
+    {
+        int c = scratchClassOf(reservation.elements);
+        if (c < 0)
+        {
+            scratchClasses.push_back(ScratchClass {reservation.elements, 0, {}});
+            c = (int) scratchClasses.size() - 1;
+        }
         for (int i = 0; i < reservation.count; ++i)
-            slots.push_back(ScratchSlot {DeviceBuffer(device, floatBytes(reservation.elements)),
-                                         reservation.elements, -1});
+            scratchClasses[(std::size_t) c].buffers.emplace_back(device, floatBytes(reservation.elements));
+        total += reservation.count;
+    }
+    for (std::size_t c = 0, first = 0; c < scratchClasses.size(); ++c)
+    {
+        scratchClasses[c].first = (int) first;
+        first += scratchClasses[c].buffers.size();
+    }
+    highWater.assign(scratchClasses.size(), 0);
+    held.assign((std::size_t) total, 0);
+
     caches.clear();
-    pending = {};
+    valueCapacity = layout.valueCapacity;
+    instructionCapacity = layout.instructionCapacity;
+    values.clear();
+    values.reserve((std::size_t) valueCapacity);
+    program.clear();
+    program.reserve((std::size_t) instructionCapacity);
+    starting.assign((std::size_t) instructionCapacity, -1);
+    ending.assign((std::size_t) instructionCapacity, -1);
+    pass = nullptr;
+    ++generation;
 }
 
 void HipNet::check(int status) const
@@ -66,8 +104,9 @@ void HipNet::check(int status) const
 Cache HipNet::makeCache(int capacityRows, int width)
 {
     if (ctx == nullptr)
-        throw std::logic_error("a net makes a cache once it is prepared");
-    caches.push_back(CacheStorage {DeviceBuffer(device, floatBytes(capacityRows * width)), capacityRows, width});
+        throw std::logic_error("HipNet::makeCache: the net is not prepared yet, so it has no device to hold a cache");
+    caches.push_back(CacheBlock {DeviceBuffer(device, floatBytes((long long) capacityRows * width)), capacityRows,
+                                 width});
     return {(int) caches.size() - 1, 0};
 }
 
@@ -76,364 +115,408 @@ float* HipNet::cacheData(const Cache& cache) const
     return static_cast<float*>(caches.at((std::size_t) cache.id).buffer.data());
 }
 
-void HipNet::begin(Pass& pass)
+// ---------------------------------------------------------------------------
+// Recording
+// ---------------------------------------------------------------------------
+void HipNet::begin(Pass& passToUse)
 {
     if (ctx == nullptr)
-        throw std::logic_error("a net records once it is prepared");
-    if (pass.hipStream() != wsp_hip_stream(ctx))
-        throw std::logic_error("a net records into the stream it was prepared with");
-    recordingPass = &pass;
-    pending = {};
+        throw std::logic_error("HipNet::begin: the net is not prepared yet");
+    if (pass != nullptr)
+        throw std::logic_error("HipNet::begin: a recording is already open; end() it first");
+    if (passToUse.hipStream() != wsp_hip_stream(ctx))
+        throw std::logic_error("HipNet::begin: the pass wraps another stream than the one the net was prepared with");
+    pass = &passToUse;
+    values.clear();
+    program.clear();
 }
 
-void HipNet::end()
+void HipNet::requireRecording(const char* op) const
 {
-    flush();
-    recordingPass = nullptr;
-    for (const auto& slot : slots)
-        if (slot.holder >= 0)
-            throw std::logic_error("a value outlived the recording that made it");
+    if (pass == nullptr)
+        throw std::logic_error(std::string("HipNet::") + op + ": no recording is open (ops go between begin() and end())");
 }
 
-void HipNet::retain(int index)
+void HipNet::closeRecording()
 {
-    ++records[(std::size_t) index].references;
+    pass = nullptr;
+    values.clear();
+    program.clear();
+    generation = (generation + 1) & kGenerationMask;
+    if (generation == 0)
+        generation = 1;
 }
 
-void HipNet::release(int index)
+int HipNet::scratchClassOf(int elements) const
 {
-    auto& record = records[(std::size_t) index];
-    if (--record.references > 0)
-        return;
-    record.live = false;
-    if (record.slot >= 0)
-    {
-        slots[(std::size_t) record.slot].holder = -1;
-        record.slot = -1;
-    }
-    if (record.base >= 0)
-    {
-        const int base = record.base;
-        record.base = -1;
-        release(base);
-    }
-}
-
-int HipNet::makeRecord()
-{
-    flush();
-    for (std::size_t i = 0; i < records.size(); ++i)
-        if (!records[i].live)
-        {
-            records[i] = Record {};
-            records[i].live = true;
-            return (int) i;
-        }
-    throw std::logic_error("a net recording holds more values at once than it has records for");
-}
-
-HipNet::Record& HipNet::recordOf(const Tensor& value)
-{
-    if (!value.isValid() || !value.isOwnedBy(*this))
-        throw std::logic_error("an op was given a tensor that holds no value of this net");
-    return records[(std::size_t) value.index()];
-}
-
-Tensor HipNet::view(const Record& source)
-{
-    const int index = makeRecord();
-    records[(std::size_t) index] = source;
-    records[(std::size_t) index].live = true;
-    records[(std::size_t) index].references = 0;
-    return {*this, index};
-}
-
-int HipNet::takeSlot(int elements)
-{
-    flush();
-    bool reserved = false;
-    for (std::size_t i = 0; i < slots.size(); ++i)
-    {
-        if (slots[i].elements != elements)
-            continue;
-        reserved = true;
-        if (slots[i].holder < 0)
-            return (int) i;
-    }
-    if (reserved)
-        throw std::logic_error("every scratch buffer of " + std::to_string(elements)
-                               + " elements is holding a value");
+    for (std::size_t c = 0; c < scratchClasses.size(); ++c)
+        if (scratchClasses[c].elements == elements)
+            return (int) c;
     return -1;
 }
 
-Tensor HipNet::fresh(const Shape& shape, const Shape& capacity)
+int HipNet::newValue(Home home, const BufferRange& range, const Shape& shape, int elements)
 {
-    const int slot = takeSlot(capacity.elementCount());
-    Record record;
-    record.shape = shape;
-    record.capacity = capacity;
-    record.slot = slot;
-    if (slot >= 0)
-        record.storage = BufferRange::of(slots[(std::size_t) slot].buffer);
-    Tensor value = view(record);
-    if (slot >= 0)
-        slots[(std::size_t) slot].holder = value.index();
-    return value;
+    if ((int) values.size() >= valueCapacity)
+        throw std::logic_error("HipNet: this recording already holds " + std::to_string(valueCapacity)
+                               + " values, the most the net was prepared for");
+    Value v;
+    v.home = home;
+    v.range = range;
+    v.shape = shape;
+    v.elements = elements;
+    if (home == Home::scratch)
+        v.cls = scratchClassOf(elements);
+    values.push_back(v);
+    return (int) values.size() - 1;
 }
 
-bool HipNet::makesNewValue(OpKind kind)
+Tensor HipNet::handleTo(int value)
 {
-    return kind == OpKind::linear || kind == OpKind::layerNorm || kind == OpKind::attention
-           || kind == OpKind::embed;
+    return {*this, (int) ((generation & kGenerationMask) << kIndexBits) | value};
 }
 
-void HipNet::flush()
+int HipNet::valueOf(const Tensor& handle, const char* op) const
 {
-    if (pending.kind == OpKind::none)
-        return;
-    const PendingOp op = pending;
-    pending = {};
-    if (makesNewValue(op.kind) && !records[(std::size_t) op.result].storage.isValid())
-        throw std::logic_error("a value with no scratch buffer of its capacity has to be placed by output()");
-    run(op);
+    requireRecording(op);
+    if (!handle.isValid() || !handle.isOwnedBy(*this))
+        throw std::logic_error(std::string("HipNet::") + op + ": the tensor is not a value of this net");
+    const int id = handle.index();
+    const int index = id & kIndexMask;
+    if ((std::uint32_t) (id >> kIndexBits) != (generation & kGenerationMask) || index >= (int) values.size())
+        throw std::logic_error(std::string("HipNet::") + op
+                               + ": the tensor belongs to a recording that has ended; values live for one recording");
+    return index;
 }
 
-void HipNet::run(const PendingOp& op)
+void HipNet::retain(int) {}
+
+void HipNet::release(int) {}
+
+void HipNet::touch(int value, int instruction)
 {
-    if (recordingPass == nullptr)
-        throw std::logic_error("a net records between begin() and end()");
-    switch (op.kind)
-    {
-        case OpKind::linear:
-        case OpKind::linearAdd:
-        case OpKind::append: runProjection(op); break;
-        case OpKind::add: runAdd(op); break;
-        case OpKind::layerNorm: runLayerNorm(op); break;
-        case OpKind::attention: runAttention(op); break;
-        case OpKind::embed: runEmbed(op); break;
-        case OpKind::none: break;
-    }
+    Value& v = values[(std::size_t) value];
+    if (v.writer < 0 && v.home == Home::scratch)
+        v.writer = instruction;
+    if (instruction > v.lastTouch)
+        v.lastTouch = instruction;
+}
+
+int HipNet::emit(const Instruction& instruction)
+{
+    if ((int) program.size() >= instructionCapacity)
+        throw std::logic_error("HipNet: this recording already holds " + std::to_string(instructionCapacity)
+                               + " instructions, the most the net was prepared for");
+    const int at = (int) program.size();
+    program.push_back(instruction);
+    // The written value first: its span starts here even when it is also read.
+    touch(instruction.dst, at);
+    for (int source : instruction.in)
+        if (source >= 0)
+            touch(source, at);
+    return at;
 }
 
 Tensor HipNet::input(const Binding& source, const Shape& shape, DType)
 {
-    flush();
-    Record record;
-    record.storage = source.range;
-    record.shape = shape;
-    record.capacity = source.capacity.rank() == 0 ? shape : source.capacity;
-    return view(record);
-}
-
-void HipNet::output(const Tensor& value, const Binding& target)
-{
-    auto& record = recordOf(value);
-    const bool madeByPending = pending.result == value.index() && makesNewValue(pending.kind);
-    if (madeByPending)
-    {
-        if (record.slot >= 0)
-            slots[(std::size_t) record.slot].holder = -1;
-        record.slot = -1;
-        record.storage = target.range;
-        flush();
-        return;
-    }
-    if (!record.storage.sameStart(target.range))
-        throw std::logic_error("the backend places an output by pointing the op just before it at the target");
-    flush();
+    requireRecording("input");
+    const Shape capacity = source.capacity.rank() == 0 ? shape : source.capacity;
+    return handleTo(newValue(Home::fixed, source.range, shape, capacity.elementCount()));
 }
 
 Tensor HipNet::rows(const Weight& table, int first, int count)
 {
-    flush();
+    requireRecording("rows");
     const int width = table.dimension(1);
-    Record record;
-    record.storage = {const_cast<void*>(table.data()), floatBytes(first * width),
-                      table.storage->size() - table.byteOffset - floatBytes(first * width)};
-    record.shape = {count, width};
-    record.capacity = record.shape;
-    return view(record);
-}
-
-Tensor HipNet::transpose(const Tensor&)
-{
-    throw std::logic_error("transpose is an encoder op; the decoder backend does not run it");
-}
-
-Tensor HipNet::conv1d(const Tensor&, const Weight&, const Weight&, int, int, Activation)
-{
-    throw std::logic_error("conv1d is an encoder op; the decoder backend does not run it");
-}
-
-Tensor HipNet::add(const Tensor&, const Tensor&)
-{
-    throw std::logic_error("add is an encoder op; the decoder folds its residuals into linearAdd");
+    const std::size_t skip = floatBytes((long long) first * width);
+    const BufferRange range {const_cast<void*>(table.data()), skip, table.storage->size() - table.byteOffset - skip};
+    return handleTo(newValue(Home::fixed, range, Shape {count, width}, count * width));
 }
 
 Tensor HipNet::cached(const Cache& cache)
 {
-    flush();
-    const auto& storage = caches.at((std::size_t) cache.id);
-    Record record;
-    record.storage = BufferRange::of(storage.buffer);
-    record.shape = {cache.rows, storage.width};
-    record.capacity = {storage.capacity, storage.width};
-    return view(record);
+    requireRecording("cached");
+    const CacheBlock& block = caches.at((std::size_t) cache.id);
+    return handleTo(newValue(Home::fixed, BufferRange::of(block.buffer), Shape {cache.rows, block.width},
+                             block.capacity * block.width));
+}
+
+Tensor HipNet::transpose(const Tensor&)
+{
+    throw std::logic_error("HipNet::transpose: an encoder op; this backend runs the decoder");
+}
+
+Tensor HipNet::conv1d(const Tensor&, const Weight&, const Weight&, int, int, Activation)
+{
+    throw std::logic_error("HipNet::conv1d: an encoder op; this backend runs the decoder");
+}
+
+Tensor HipNet::add(const Tensor&, const Tensor&)
+{
+    throw std::logic_error("HipNet::add: an encoder op; the decoder's residuals go through linearAdd");
 }
 
 Tensor HipNet::linear(const Tensor& input, const Weight& weight, const Weight* bias, Activation activation)
 {
-    flush();
-    const auto source = recordOf(input);
+    const int source = valueOf(input, "linear");
+    const Value& in = values[(std::size_t) source];
     const int outputs = weight.dimension(0);
-    Tensor result = fresh({source.shape.rows(), outputs}, {source.capacity.rows(), outputs});
-    PendingOp op;
-    op.kind = OpKind::linear;
-    op.result = result.index();
-    op.first = input.index();
+    const int capacityRows = in.elements / in.shape.columns();
+    const int dst = newValue(Home::scratch, {}, Shape {in.shape.rows(), outputs}, capacityRows * outputs);
+    Instruction op;
+    op.code = Opcode::project;
+    op.dst = dst;
+    op.in[0] = source;
     op.weight = &weight;
     op.bias = bias;
-    op.activation = activation;
-    pending = op;
-    return result;
+    op.gelu = activation == Activation::gelu;
+    emit(op);
+    return handleTo(dst);
 }
 
 Tensor HipNet::linearAdd(const Tensor& input, const Weight& weight, const Weight* bias, const Tensor& stream)
 {
-    flush();
-    PendingOp op;
-    op.kind = OpKind::linearAdd;
-    op.result = stream.index();
-    op.first = input.index();
+    const int source = valueOf(input, "linearAdd");
+    const int into = valueOf(stream, "linearAdd");
+    Instruction op;
+    op.code = Opcode::accumulate;
+    op.dst = into;
+    op.in[0] = source;
+    op.in[1] = into;
     op.weight = &weight;
     op.bias = bias;
-    pending = op;
-    return stream;
+    emit(op);
+    return handleTo(into);
 }
 
 Tensor HipNet::layerNorm(const Tensor& input, const Weight& weight, const Weight& bias)
 {
-    flush();
-    const auto source = recordOf(input);
-    Tensor result = fresh(source.shape, source.capacity);
-    PendingOp op;
-    op.kind = OpKind::layerNorm;
-    op.result = result.index();
-    op.first = input.index();
+    const int source = valueOf(input, "layerNorm");
+    const Value& in = values[(std::size_t) source];
+    const int dst = newValue(Home::scratch, {}, in.shape, in.elements);
+    Instruction op;
+    op.code = Opcode::normalize;
+    op.dst = dst;
+    op.in[0] = source;
     op.weight = &weight;
     op.bias = &bias;
-    pending = op;
-    return result;
+    emit(op);
+    return handleTo(dst);
 }
 
-Tensor HipNet::attention(const Tensor& queries, const Tensor& keys, const Tensor& values, int heads, bool causal)
+Tensor HipNet::attention(const Tensor& queries, const Tensor& keys, const Tensor& values_, int heads, bool causal)
 {
-    flush();
-    const auto source = recordOf(queries);
-    Tensor result = fresh(source.shape, source.capacity);
-    PendingOp op;
-    op.kind = OpKind::attention;
-    op.result = result.index();
-    op.first = queries.index();
-    op.second = keys.index();
-    op.third = values.index();
+    const int q = valueOf(queries, "attention");
+    const int k = valueOf(keys, "attention");
+    const int v = valueOf(values_, "attention");
+    const Value& in = values[(std::size_t) q];
+    const int dst = newValue(Home::scratch, {}, in.shape, in.elements);
+    Instruction op;
+    op.code = Opcode::attend;
+    op.dst = dst;
+    op.in[0] = q;
+    op.in[1] = k;
+    op.in[2] = v;
     op.heads = heads;
     op.causal = causal;
-    pending = op;
-    return result;
+    emit(op);
+    return handleTo(dst);
 }
 
 Tensor HipNet::embed(const Tensor& tokens, const Weight& tokenTable, const Weight& positionTable, int firstPosition)
 {
-    flush();
-    const auto source = recordOf(tokens);
+    const int ids = valueOf(tokens, "embed");
+    const Value& in = values[(std::size_t) ids];
     const int width = tokenTable.dimension(1);
-    Tensor result = fresh({source.shape[0], width}, {source.capacity[0], width});
-    PendingOp op;
-    op.kind = OpKind::embed;
-    op.result = result.index();
-    op.first = tokens.index();
+    const int dst = newValue(Home::scratch, {}, Shape {in.shape[0], width}, in.elements * width);
+    Instruction op;
+    op.code = Opcode::embedRows;
+    op.dst = dst;
+    op.in[0] = ids;
     op.weight = &tokenTable;
-    op.positionTable = &positionTable;
-    op.position = firstPosition;
-    pending = op;
-    return result;
+    op.positions = &positionTable;
+    op.firstPosition = firstPosition;
+    emit(op);
+    return handleTo(dst);
 }
 
-// Net/KernelNet.cpp:724-758: the projection writes straight into the rows the
-// cache holds next.
+// The projection lands in the rows the cache holds next (Net/KernelNet.cpp
+// :724-758 gives appendLinear that meaning); the value returned is the whole
+// cache as it stands after them.
 Tensor HipNet::appendLinear(Cache& cache, const Tensor& input, const Weight& weight, const Weight* bias)
 {
-    flush();
-    const auto& storage = caches.at((std::size_t) cache.id);
-    const int width = storage.width;
-    const int count = recordOf(input).shape.rows();
-    if (cache.rows + count > storage.capacity)
-        throw std::logic_error("a cache was appended to past its capacity");
-    PendingOp op;
-    op.kind = OpKind::append;
-    op.first = input.index();
+    const int source = valueOf(input, "appendLinear");
+    const CacheBlock& block = caches.at((std::size_t) cache.id);
+    const int count = values[(std::size_t) source].shape.rows();
+    if (cache.rows + count > block.capacity)
+        throw std::logic_error("HipNet::appendLinear: " + std::to_string(count) + " more rows would overflow a cache of "
+                               + std::to_string(block.capacity) + " rows holding " + std::to_string(cache.rows));
+    const int dst = newValue(Home::fixed, BufferRange::of(block.buffer), Shape {cache.rows + count, block.width},
+                             block.capacity * block.width);
+    Instruction op;
+    op.code = Opcode::project;
+    op.dst = dst;
+    op.dstRow = cache.rows;
+    op.in[0] = source;
     op.weight = &weight;
     op.bias = bias;
-    op.target = {storage.buffer.data(), floatBytes(cache.rows * width), floatBytes(count * width)};
+    emit(op);
     cache.rows += count;
-    Tensor result = cached(cache);
-    op.result = result.index();
-    pending = op;
-    return result;
+    return handleTo(dst);
 }
 
-void HipNet::runProjection(const PendingOp& op)
+void HipNet::output(const Tensor& handle, const Binding& target)
 {
-    const auto& input = records[(std::size_t) op.first];
-    const BufferRange target = op.kind == OpKind::append ? op.target : records[(std::size_t) op.result].storage;
-    int flags = 0;
-    if (op.activation == Activation::gelu)
-        flags |= WSP_LINEAR_GELU;
-    if (op.kind == OpKind::linearAdd)
-        flags |= WSP_LINEAR_RESIDUAL;
-    const float* bias = op.bias != nullptr ? static_cast<const float*>(op.bias->data()) : nullptr;
-    check(wsp_hip_linear(ctx, static_cast<const float*>(input.storage.data()), input.shape.rows(),
-                         input.shape.columns(), op.weight->data(), wsp_dtype_of(op.weight->type), bias,
-                         static_cast<float*>(target.data()), op.weight->dimension(0), flags));
+    const int index = valueOf(handle, "output");
+    Value& v = values[(std::size_t) index];
+    switch (v.home)
+    {
+        case Home::scratch:
+            if (target.range.size != 0 && target.range.size < floatBytes((long long) v.shape.elementCount()))
+                throw std::logic_error("HipNet::output: the binding '" + target.name + "' holds "
+                                       + std::to_string(target.range.size) + " bytes, less than the value's "
+                                       + std::to_string(floatBytes((long long) v.shape.elementCount())));
+            v.home = Home::bound;
+            v.range = target.range;
+            return;
+        case Home::bound:
+        case Home::fixed:
+            if (v.range.sameStart(target.range))
+                return; // already there
+            throw std::logic_error(v.home == Home::bound
+                                       ? "HipNet::output: the value is already bound to other storage"
+                                       : "HipNet::output: the value is a view of storage the recording was given; "
+                                         "output() binds values the recording computes");
+    }
 }
 
-void HipNet::runAdd(const PendingOp&)
+// ---------------------------------------------------------------------------
+// end(): placement, then issue
+// ---------------------------------------------------------------------------
+void HipNet::end()
 {
-    throw std::logic_error("add is an encoder op");
+    requireRecording("end");
+    try
+    {
+        place();
+        for (const Instruction& instruction : program)
+            issue(instruction);
+    }
+    catch (...)
+    {
+        closeRecording();
+        throw;
+    }
+    closeRecording();
 }
 
-void HipNet::runLayerNorm(const PendingOp& op)
+// Walks the program once. At instruction i, first every scratch value whose
+// span starts at i takes the lowest free buffer of its class, then every one
+// whose span ends at i gives its buffer back: an instruction never writes a
+// buffer it reads, and a buffer returns to use at the first instruction after
+// its value's last touch. The spans are threaded into per-instruction lists
+// through the values themselves, so nothing is allocated.
+void HipNet::place()
 {
-    const auto& input = records[(std::size_t) op.first];
-    const auto& output = records[(std::size_t) op.result];
-    check(wsp_hip_layernorm(ctx, static_cast<const float*>(input.storage.data()),
-                            static_cast<const float*>(op.weight->data()),
-                            static_cast<const float*>(op.bias->data()), static_cast<float*>(output.storage.data()),
-                            input.shape.rows(), input.shape.columns(), 1e-5f));
+    const int instructions = (int) program.size();
+    std::fill(starting.begin(), starting.begin() + instructions, -1);
+    std::fill(ending.begin(), ending.begin() + instructions, -1);
+    for (int n = (int) values.size() - 1; n >= 0; --n)
+    {
+        Value& v = values[(std::size_t) n];
+        if (v.home != Home::scratch)
+            continue;
+        if (v.cls < 0)
+            throw std::logic_error("HipNet: instruction " + std::to_string(v.writer) + " writes a value of "
+                                   + floats(v.elements)
+                                   + " capacity; no scratch buffers of that capacity were reserved and output() "
+                                     "did not bind it");
+        v.nextStarting = starting[(std::size_t) v.writer];
+        starting[(std::size_t) v.writer] = n;
+        v.nextEnding = ending[(std::size_t) v.lastTouch];
+        ending[(std::size_t) v.lastTouch] = n;
+    }
+
+    std::fill(held.begin(), held.end(), 0);
+    std::fill(highWater.begin(), highWater.end(), 0);
+    for (int i = 0; i < instructions; ++i)
+    {
+        for (int n = starting[(std::size_t) i]; n >= 0; n = values[(std::size_t) n].nextStarting)
+        {
+            Value& v = values[(std::size_t) n];
+            ScratchClass& cls = scratchClasses[(std::size_t) v.cls];
+            const int count = (int) cls.buffers.size();
+            int b = 0;
+            while (b < count && held[(std::size_t) (cls.first + b)])
+                ++b;
+            if (b == count)
+                throw std::logic_error("HipNet: at instruction " + std::to_string(i) + " more values of "
+                                       + floats(cls.elements) + " capacity are live than the "
+                                       + std::to_string(count) + " scratch buffers reserved for it");
+            held[(std::size_t) (cls.first + b)] = 1;
+            v.buffer = b;
+            v.range = BufferRange::of(cls.buffers[(std::size_t) b]);
+            if (b + 1 > highWater[(std::size_t) v.cls])
+                highWater[(std::size_t) v.cls] = b + 1;
+        }
+        for (int n = ending[(std::size_t) i]; n >= 0; n = values[(std::size_t) n].nextEnding)
+        {
+            const Value& v = values[(std::size_t) n];
+            held[(std::size_t) (scratchClasses[(std::size_t) v.cls].first + v.buffer)] = 0;
+        }
+    }
 }
 
-void HipNet::runAttention(const PendingOp& op)
+void HipNet::issue(const Instruction& op)
 {
-    const auto& queries = records[(std::size_t) op.first];
-    const auto& keys = records[(std::size_t) op.second];
-    const auto& values = records[(std::size_t) op.third];
-    const auto& output = records[(std::size_t) op.result];
-    const int width = queries.shape.columns();
-    const float scale = 1.f / std::sqrt((float) (width / op.heads));
-    check(wsp_hip_attention(ctx, static_cast<const float*>(queries.storage.data()), queries.shape.rows(),
-                            static_cast<const float*>(keys.storage.data()),
-                            static_cast<const float*>(values.storage.data()), keys.shape.rows(), width, op.heads,
-                            op.causal ? 1 : 0, scale, static_cast<float*>(output.storage.data())));
-}
-
-void HipNet::runEmbed(const PendingOp& op)
-{
-    const auto& tokens = records[(std::size_t) op.first];
-    const auto& output = records[(std::size_t) op.result];
-    check(wsp_hip_embed(ctx, static_cast<const uint32_t*>(tokens.storage.data()), tokens.shape[0],
-                        static_cast<const float*>(op.weight->data()),
-                        static_cast<const float*>(op.positionTable->data()), op.position,
-                        static_cast<float*>(output.storage.data()), output.shape.columns()));
+    auto at = [&](int value) { return values[(std::size_t) value].range.data(); };
+    const Value& dst = values[(std::size_t) op.dst];
+    switch (op.code)
+    {
+        case Opcode::project:
+        case Opcode::accumulate:
+        {
+            const Value& in = values[(std::size_t) op.in[0]];
+            const int outputs = op.weight->dimension(0);
+            int flags = op.gelu ? WSP_LINEAR_GELU : 0;
+            if (op.code == Opcode::accumulate)
+                flags |= WSP_LINEAR_RESIDUAL;
+            float* target = static_cast<float*>(at(op.dst)) + (std::size_t) op.dstRow * (std::size_t) outputs;
+            const float* bias = op.bias != nullptr ? static_cast<const float*>(op.bias->data()) : nullptr;
+            check(wsp_hip_linear(ctx, static_cast<const float*>(at(op.in[0])), in.shape.rows(), in.shape.columns(),
+                                 op.weight->data(), wsp_dtype_of(op.weight->type), bias, target, outputs, flags));
+            return;
+        }
+        case Opcode::normalize:
+        {
+            const Value& in = values[(std::size_t) op.in[0]];
+            check(wsp_hip_layernorm(ctx, static_cast<const float*>(at(op.in[0])),
+                                    static_cast<const float*>(op.weight->data()),
+                                    static_cast<const float*>(op.bias->data()), static_cast<float*>(at(op.dst)),
+                                    in.shape.rows(), in.shape.columns(), 1e-5f));
+            return;
+        }
+        case Opcode::attend:
+        {
+            const Value& q = values[(std::size_t) op.in[0]];
+            const Value& k = values[(std::size_t) op.in[1]];
+            const int width = q.shape.columns();
+            const float scale = 1.f / std::sqrt((float) (width / op.heads));
+            check(wsp_hip_attention(ctx, static_cast<const float*>(at(op.in[0])), q.shape.rows(),
+                                    static_cast<const float*>(at(op.in[1])), static_cast<const float*>(at(op.in[2])),
+                                    k.shape.rows(), width, op.heads, op.causal ? 1 : 0, scale,
+                                    static_cast<float*>(at(op.dst))));
+            return;
+        }
+        case Opcode::embedRows:
+        {
+            const Value& ids = values[(std::size_t) op.in[0]];
+            check(wsp_hip_embed(ctx, static_cast<const uint32_t*>(at(op.in[0])), ids.shape[0],
+                                static_cast<const float*>(op.weight->data()),
+                                static_cast<const float*>(op.positions->data()), op.firstPosition,
+                                static_cast<float*>(at(op.dst)), dst.shape.columns()));
+            return;
+        }
+    }
 }
 } // namespace WSP
