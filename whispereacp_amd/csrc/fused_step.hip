@@ -234,10 +234,8 @@ void plan_persistent(Context* ctx, FusedState* st)
     st->off_xpart = at, at += H * cross_split_max * (hd + 2);
     st->off_xattn = at, at += d;
     st->off_h3 = at, at += block_d;
-    at = (at + 1) & ~1; // 16-byte aligned: the feed-forward vector is polled two words per load
     st->off_ff = at, at += row_groups << st->log2_f;
     st->off_h4 = at, at += block_d;
-    at = (at + 1) & ~1; // every layer's regions keep their alignment
     st->layer_words = at;
     st->off_argmax = at * s.layers;
     st->exchange_words = (size_t) at * s.layers + 16 * G;

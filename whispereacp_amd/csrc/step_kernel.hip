@@ -318,30 +318,36 @@ __device__ __forceinline__ bool gather_blocked(const uint64_t* base, int rows, i
     return true;
 }
 
-// The same for the long feed-forward vector, two slots per 16-byte
-// device-scope load (half the load instructions of a poll round). Each 8-byte
-// word of the pair was stored whole, so each is old or new on its own. The
-// vector starts 16-byte aligned (every exchange region has an even size).
-//
-// A poll round is one inline-assembly statement: four global_load_dwordx4
-// with the device-scope (sc1) cache policy, then s_waitcnt vmcnt(0), so no
-// use of a loaded register can be scheduled between the loads and the wait
-// (the compiler's own wait insertion does not see loads written in assembly).
-// Every thread loads all four of its pairs each round, a pair past the vector
-// re-reading pair 0, so every address stays inside the vector. Measured
-// against the alternatives at the small shape: compiler-tracked buffer loads
-// of the same policy 272 us a step, loads skipped for finished pairs with a
-// separate wait statement (which does not order the uses) 266, this form 269.
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// The same for the long feed-forward vector, eight slots per polling thread
+// (slot first + t + 448 k, so each load instruction of a wave reads 64
+// consecutive words). A poll round is one inline-assembly statement: eight
+// global_load_dwordx2 with the device-scope (sc1) cache policy, then
+// s_waitcnt vmcnt(0), so no use of a loaded register can be scheduled between
+// the loads and the wait (the compiler's own wait insertion does not see loads
+// written in assembly). Each word is read whole: a naturally aligned
+// global_load_dwordx2 with sc1 is the instruction LLVM's AMDGPU memory model
+// emits on gfx942/gfx950 for a relaxed agent-scope atomic load of 64 bits
+// (llvm/docs/AMDGPUUsage.rst, "Memory Model GFX942": load atomic monotonic,
+// agent scope, global -> global_load sc1=1), the same access peek() makes.
+// Addresses are one scalar base and eight 32-bit byte offsets, each clamped
+// into the vector: a slot past it re-reads word 0 and is ignored.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-template <int Q>
-__device__ __forceinline__ bool gather_pairs(const uint64_t* base, int rows, int log2_block, int stride, float* dst,
+template <int P>
+__device__ __forceinline__ bool gather_words(const uint64_t* base, int rows, int log2_block, int stride, float* dst,
                                              uint32_t epoch, int* status, Shared& sh)
 {
-    static_assert(Q == 4, "the wait below names four loaded registers");
-    const int pairs = (stride << log2_block) / 2;
+    static_assert(P == 8, "the poll statement below names eight loads");
+    // The base as a value the compiler knows to be uniform, so it lives in a
+    // scalar register pair (the loads' saddr operand). readfirstlane returns
+    // a signed int: each half goes through uint32_t so it is zero-extended.
+    const uint64_t at = reinterpret_cast<uint64_t>(base);
+    const uint32_t high = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (at >> 32));
+    const uint32_t low = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) at);
+    const uint64_t scalar_base = ((uint64_t) high << 32) | (uint64_t) low;
+    const int slots = stride << log2_block;
     const int mask = (1 << log2_block) - 1;
-    for (int first = 0; first < pairs; first += Q * kPollThreads)
+    for (int first = 0; first < slots; first += P * kPollThreads)
     {
         bool failed = false;
         if (threadIdx.x < kWave)
@@ -350,45 +356,41 @@ __device__ __forceinline__ bool gather_pairs(const uint64_t* base, int rows, int
         {
             const int t = threadIdx.x - kWave;
             uint32_t pending = 0;
+            uint32_t off[P];
 #pragma unroll
-            for (int q = 0; q < Q; ++q)
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-                {
-                    const int pair = first + t + q * kPollThreads;
-                    const int slot = 2 * pair + h;
-                    if (pair < pairs && (slot & mask) * stride + (slot >> log2_block) < rows)
-                        pending |= 1u << (2 * q + h);
-                }
-            const uint64_t* p[Q];
-#pragma unroll
-            for (int q = 0; q < Q; ++q)
+            for (int k = 0; k < P; ++k)
             {
-                const int pair = first + t + q * kPollThreads;
-                p[q] = base + 2 * (pair < pairs ? pair : 0);
+                const int slot = first + t + k * kPollThreads;
+                if (slot < slots && (slot & mask) * stride + (slot >> log2_block) < rows)
+                    pending |= 1u << k;
+                off[k] = (uint32_t) (slot < slots ? slot : 0) * (uint32_t) sizeof(uint64_t);
             }
             int spins = 0;
             while (pending != 0)
             {
-                u32x4 v[Q];
-                asm volatile("global_load_dwordx4 %0, %4, off sc1\n\t"
-                             "global_load_dwordx4 %1, %5, off sc1\n\t"
-                             "global_load_dwordx4 %2, %6, off sc1\n\t"
-                             "global_load_dwordx4 %3, %7, off sc1\n\t"
+                u32x2 v[P];
+                asm volatile("global_load_dwordx2 %0, %8, %16 sc1\n\t"
+                             "global_load_dwordx2 %1, %9, %16 sc1\n\t"
+                             "global_load_dwordx2 %2, %10, %16 sc1\n\t"
+                             "global_load_dwordx2 %3, %11, %16 sc1\n\t"
+                             "global_load_dwordx2 %4, %12, %16 sc1\n\t"
+                             "global_load_dwordx2 %5, %13, %16 sc1\n\t"
+                             "global_load_dwordx2 %6, %14, %16 sc1\n\t"
+                             "global_load_dwordx2 %7, %15, %16 sc1\n\t"
                              "s_waitcnt vmcnt(0)"
-                             : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
-                             : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3])
+                             : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+                               "=&v"(v[6]), "=&v"(v[7])
+                             : "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "v"(off[4]), "v"(off[5]),
+                               "v"(off[6]), "v"(off[7]), "s"(scalar_base)
                              : "memory");
 #pragma unroll
-                for (int q = 0; q < Q; ++q)
-#pragma unroll
-                    for (int h = 0; h < 2; ++h)
-                        if ((pending & (1u << (2 * q + h))) && v[q][2 * h + 1] == epoch)
-                        {
-                            const int slot = 2 * (first + t + q * kPollThreads) + h;
-                            dst[(slot & mask) * stride + (slot >> log2_block)] = __uint_as_float(v[q][2 * h]);
-                            pending &= ~(1u << (2 * q + h));
-                        }
+                for (int k = 0; k < P; ++k)
+                    if ((pending & (1u << k)) && v[k][1] == epoch)
+                    {
+                        const int slot = first + t + k * kPollThreads;
+                        dst[(slot & mask) * stride + (slot >> log2_block)] = __uint_as_float(v[k][0]);
+                        pending &= ~(1u << k);
+                    }
                 if (pending != 0 && (++spins & 63) == 0)
                 {
                     if (spins > kSpinLimit)
@@ -1383,7 +1385,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         STEP_STAMP(11, l);
 
         // ---- fc2 + residual (weights in pb) ------------------------------------------------
-        if (!gather_pairs<kPollBlockedFF / 2>(ex + a.off_ff, f, a.log2_f, stride, sh.x, epoch, a.status, sh))
+        if (!gather_words<kPollBlockedFF>(ex + a.off_ff, f, a.log2_f, stride, sh.x, epoch, a.status, sh))
             return false;
         STEP_STAMP(12, l);
         {
