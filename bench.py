@@ -9,12 +9,16 @@ device (Decoder::step followed by Argmax::encode, as Whisper::encodeStep
 records them). Inputs are resident in HBM; warm-up steps run in a sequence of
 their own first.
 
-Timing: with --steps equal to the workload's own step count (the default) the
+Timing follows the reference's benchmark protocol (Benchmark/README.md:62-106):
+one warm-up, then --runs timed runs (10 by default) of the whole sequence, and
+the median run is reported with the fastest and slowest beside it. Within a
+run, with --steps equal to the workload's own step count (the default) the
 whole sequence is one event-bracketed region, the self-attention KV growing
 5..228 keys. With fewer, the whole sequence still runs, and --steps steps
 spread evenly over it are each bracketed by HIP events on the decoder's stream
 (nothing synchronises between them, so the launch queue never drains); the
-bytes per step are averaged over the same positions.
+bytes per step are averaged over the same positions. Every run must decode the
+same tokens.
 
 The JSON line reports decode tokens/s, ms/step, the HBM roofline of the step
 (algorithmic bytes per step / measured step time against 8 TB/s) and the CPU
@@ -30,6 +34,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -252,6 +257,8 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=None, help="timed steps (default: the workload's own)")
     parser.add_argument("--warmup", type=int, default=16)
+    parser.add_argument("--runs", type=int, default=10,
+                        help="timed runs of the whole sequence; the median is reported (decoder workloads)")
     parser.add_argument("--workload", default="small",
                         choices=["tiny.en", "base.en", "small", "medium", "large-v3"]
                         + ["encoder-" + n for n in ENCODER_DTYPES] + ["transcribe-tiny.en"])
@@ -292,8 +299,8 @@ def main():
     w = S.WORKLOADS[args.workload]
     if args.steps is None:
         args.steps = w["steps"]
-    if args.steps <= 0 or args.warmup < 0:
-        print("--steps must be positive and --warmup not negative", file=sys.stderr)
+    if args.steps <= 0 or args.warmup < 0 or args.runs <= 0:
+        print("--steps and --runs must be positive and --warmup not negative", file=sys.stderr)
         sys.exit(2)
     if args.cpu_only:
         cpu_only(args, w)
@@ -359,38 +366,50 @@ def bench_single(args, w):
     torch.cuda.synchronize()
     check_watchdog(decoder, "warm-up")
 
-    print("[bench] timed region", file=sys.stderr, flush=True)
-    open_sequence()
-    torch.cuda.synchronize()
     contiguous = args.steps == total
     timed = list(range(total)) if contiguous else sampled_steps(total, args.steps)
-    host0 = time.perf_counter()
-    if contiguous:
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for j in range(1, total + 1):
-            one_step(j)
-        stop.record()
-        events = [(start, stop)]
-    else:
-        wanted = set(timed)
-        events = []
-        for j in range(1, total + 1):
-            if j - 1 in wanted:
-                pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                pair[0].record()
+
+    def timed_run():
+        """One whole sequence; returns (ms per timed step, tokens, host s, enqueue s)."""
+        open_sequence()
+        torch.cuda.synchronize()
+        host0 = time.perf_counter()
+        if contiguous:
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for j in range(1, total + 1):
                 one_step(j)
-                pair[1].record()
-                events.append(pair)
-            else:
-                one_step(j)
-    enqueue_s = time.perf_counter() - host0
-    torch.cuda.synchronize()
-    host_s = time.perf_counter() - host0
-    check_watchdog(decoder, "timed region")
-    gpu_ms = sum(a.elapsed_time(b) for a, b in events)
-    ms_per_step = gpu_ms / args.steps
-    gpu_tokens = slots[base:base + total + 1].cpu().numpy().tolist()
+            stop.record()
+            events = [(start, stop)]
+        else:
+            wanted = set(timed)
+            events = []
+            for j in range(1, total + 1):
+                if j - 1 in wanted:
+                    pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                    pair[0].record()
+                    one_step(j)
+                    pair[1].record()
+                    events.append(pair)
+                else:
+                    one_step(j)
+        enqueue = time.perf_counter() - host0
+        torch.cuda.synchronize()
+        host = time.perf_counter() - host0
+        check_watchdog(decoder, "timed region")
+        gpu_ms = sum(a.elapsed_time(b) for a, b in events)
+        return gpu_ms / args.steps, slots[base:base + total + 1].cpu().numpy().tolist(), host, enqueue
+
+    print(f"[bench] timed region: {args.runs} runs", file=sys.stderr, flush=True)
+    runs = [timed_run() for _ in range(args.runs)]
+    run_ms = [r[0] for r in runs]
+    ms_per_step = statistics.median(run_ms)
+    gpu_tokens = runs[0][1]
+    if any(r[1] != gpu_tokens for r in runs):
+        print("[bench] the timed runs decoded different tokens", file=sys.stderr)
+        sys.exit(3)
+    median_run = min(runs, key=lambda r: abs(r[0] - ms_per_step))
+    host_s, enqueue_s = median_run[2], median_run[3]
 
     positions = [base + j for j in timed]
     bytes_per_step = sum(step_bytes(shape, weight_bytes, p) for p in positions) / len(positions)
@@ -434,10 +453,19 @@ def bench_single(args, w):
                      "bytes_per_step": round(bytes_per_step)},
         "cpu_baseline": baseline,
         "parity": parity,
+        "runs": run_summary(run_ms),
         "host_seconds": round(host_s, 4),
         "host_enqueue_seconds": round(enqueue_s, 4),
     }
     print(json.dumps(line))
+
+
+def run_summary(run_ms):
+    """The timed runs' ms/step: how many, the median (the reported figure),
+    the fastest and the slowest, and each in order."""
+    return {"count": len(run_ms), "median_ms_per_step": round(statistics.median(run_ms), 5),
+            "min_ms_per_step": round(min(run_ms), 5), "max_ms_per_step": round(max(run_ms), 5),
+            "each_ms_per_step": [round(x, 5) for x in run_ms]}
 
 
 def bench_streams(args, w):
@@ -488,26 +516,37 @@ def bench_streams(args, w):
     run_steps(args.warmup)
     torch.cuda.synchronize()
 
-    print("[bench] timed region", file=sys.stderr, flush=True)
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    if begin_timed:
+    def timed_run():
+        """One whole sequence; returns (GPU ms, tokens [stream][step], host s, enqueue s)."""
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if begin_timed:
+            torch.cuda.synchronize()
+            host0 = time.perf_counter()
+            start.record()
+            open_sequence()
+        else:
+            open_sequence()
+            torch.cuda.synchronize()
+            host0 = time.perf_counter()
+            start.record()
+        run_steps(args.steps)
+        stop.record()
+        enqueue = time.perf_counter() - host0
         torch.cuda.synchronize()
-        host0 = time.perf_counter()
-        start.record()
-        open_sequence()
-    else:
-        open_sequence()
-        torch.cuda.synchronize()
-        host0 = time.perf_counter()
-        start.record()
-    run_steps(args.steps)
-    stop.record()
-    enqueue_s = time.perf_counter() - host0
-    torch.cuda.synchronize()
-    host_s = time.perf_counter() - host0
-    gpu_ms = start.elapsed_time(stop)
-    ms_per_step = gpu_ms / args.steps
-    tokens = ring[t:t + args.steps + 1].cpu().numpy().T
+        host = time.perf_counter() - host0
+        return start.elapsed_time(stop), ring[t:t + args.steps + 1].cpu().numpy().T, host, enqueue
+
+    print(f"[bench] timed region: {args.runs} runs", file=sys.stderr, flush=True)
+    runs = [timed_run() for _ in range(args.runs)]
+    run_ms = [r[0] / args.steps for r in runs]
+    ms_per_step = statistics.median(run_ms)
+    gpu_ms = ms_per_step * args.steps
+    tokens = runs[0][1]
+    if any(not np.array_equal(r[1], tokens) for r in runs):
+        print("[bench] the timed runs decoded different tokens", file=sys.stderr)
+        sys.exit(3)
+    median_run = min(runs, key=lambda r: abs(r[0] / args.steps - ms_per_step))
+    host_s, enqueue_s = median_run[2], median_run[3]
 
     weight_bytes = 4 if dtype == "F32" else 2
     positions = range(t, t + args.steps)
@@ -545,6 +584,7 @@ def bench_streams(args, w):
                      "kernel": "whole step (batched per-op kernels)", "bytes_per_step": round(bytes_per_step)},
         "cpu_baseline": baseline,
         "parity": parity,
+        "runs": run_summary(run_ms),
         "host_seconds": round(host_s, 4),
         "host_enqueue_seconds": round(enqueue_s, 4),
     }
