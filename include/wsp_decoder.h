@@ -190,11 +190,14 @@ int wsp_tokenizer_is_special(const wsp_tokenizer* tokenizer, int token);
  * (e.g. "\xc4\xa0the"), or -1. */
 int wsp_tokenizer_token_for_text(const wsp_tokenizer* tokenizer, const char* text, size_t length);
 /* Tokenizer::encode: UTF-8 (or any bytes) in, ids out; *count_out is the full
- * count even when it exceeds capacity. */
+ * count even when it exceeds capacity (then WSP_ERR_CAPACITY). A host
+ * allocation failure or a count past INT_MAX is WSP_ERR_CAPACITY, any other
+ * tokenizer exception WSP_ERR_ARGUMENT; nothing escapes the call. */
 int wsp_tokenizer_encode(const wsp_tokenizer* tokenizer, const char* text, size_t length, int* ids_out, int capacity,
                          int* count_out);
 /* Tokenizer::decode / decodeKeepingSpecialTokens: the bytes and a NUL in
- * text_out; *length_out is the byte count without the NUL. */
+ * text_out; *length_out is the byte count without the NUL. Errors as for
+ * wsp_tokenizer_encode. */
 int wsp_tokenizer_decode(const wsp_tokenizer* tokenizer, const int* ids, int count, int keep_special, char* text_out,
                          int capacity, int* length_out);
 

@@ -147,6 +147,28 @@ def test_widest_shape_bf16_matches_oracle(oracle):
     check_run(tokens, rows, ref_tokens, ref_rows, 2e-2)
 
 
+@pytest.mark.timeout(600)
+def test_large_v3_shape_persistent_steps_match_oracle(oracle):
+    # The whole large-v3 decoder (d 1280, 20 heads, 32 layers, ffn 5120, vocab
+    # 51866, bf16, 1500 cross rows) on the persistent step: the batched
+    # large-v3 streams are checked against this decoder over all 444 steps, so
+    # it is pinned to the oracle here at full depth, 24 steps after the prefix.
+    from whispereacp_amd.decoder import Decoder
+    shape = S.workload_shape("large-v3")
+    f = S.workload_decoder_file(shape, "BF16", 2000)
+    enc = S.normal_encoder_output(shape.cross_positions, shape.width, 331)
+    decoder = Decoder(shape, f, packing="ExactHalf")
+    assert decoder.uses_persistent_step
+    prompt = S.SOT_PREFIX[shape.vocabulary_size]
+    steps = 24
+    tokens, rows = greedy_on_gpu(decoder, shape, enc, prompt, steps)
+    assert decoder.device_status() == 0
+    ref_tokens, ref_rows = oracle_greedy(oracle, shape, f, enc, prompt, steps)
+    rel, worst = check_run(tokens, rows, ref_tokens, ref_rows, 2e-2)
+    print(f"large-v3 shape, {steps} persistent steps: max relative {rel:.2e}, worst {worst:.2e}, "
+          f"{len(set(tokens))} distinct tokens")
+
+
 @pytest.mark.parametrize("dtype", ["BF16", "F16"])
 def test_long_sequence_crosses_the_self_key_split(oracle, dtype):
     # Past 256 positions the self-attention of a head spans two workgroups

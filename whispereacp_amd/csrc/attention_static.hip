@@ -49,7 +49,10 @@ int report(char* error, int capacity, int code, const char* format, ...)
 }
 
 // This device's copy of the array, looked up once per device with that device
-// current (the caller's current device is the one the kernels run on).
+// current (the caller's current device is the one the kernels run on). The
+// address is kept for the life of the process: hipDeviceReset unloads the
+// code object that holds the array, so a process that resets a device must
+// not call this entry point on that device afterwards.
 hipError_t device_scratch(float** out)
 {
     int device = 0;

@@ -871,11 +871,14 @@ __global__ void __launch_bounds__(kTileThreads) tile_kernel(Tile a)
             __hip_atomic_store(mine + c / 2,
                                (uint64_t) __float_as_uint(v[c]) | ((uint64_t) __float_as_uint(v[c + 1]) << 32),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0); // the stores are performed before the block counts itself in
+        // The barrier orders every thread's partial stores before thread 0's
+        // count (workgroup scope); the count is an agent-scope release, so
+        // the partials are visible device-wide before it is, and an acquire,
+        // so the last block reads every other block's partials after it.
         __syncthreads();
         if (threadIdx.x == 0)
         {
-            const unsigned before = __hip_atomic_fetch_add(a.counters + cg, 1u, __ATOMIC_RELAXED,
+            const unsigned before = __hip_atomic_fetch_add(a.counters + cg, 1u, __ATOMIC_ACQ_REL,
                                                            __HIP_MEMORY_SCOPE_AGENT);
             const bool last = before == (unsigned) a.splits - 1;
             if (last)

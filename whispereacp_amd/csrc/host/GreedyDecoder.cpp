@@ -135,6 +135,15 @@ GreedyRun GreedyDecoder::decode(Pass& pass, const BufferRange& encoderRows, int 
     }
     run.decodeSeconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
     checkHip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    // Steps still in flight when end-of-text arrived have drained now; their
+    // tokens are dropped, but a trip among them is reported, and the word is
+    // left clear for the next run.
+    int drained = 0;
+    if (wsp_hip_device_status(context, &drained, 1) != WSP_OK)
+        throw std::runtime_error(std::string("read the watchdog word: ") + wsp_hip_last_error(context));
+    if (drained != 0)
+        throw std::runtime_error("greedy decode: a step in flight after end-of-text timed out on the device (its "
+                                 "hand-over watchdog tripped)");
     return run;
 }
 } // namespace WSP

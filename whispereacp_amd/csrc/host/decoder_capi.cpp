@@ -11,6 +11,7 @@
 #include "../../../include/whispereacp/Whisper.h"
 
 #include <algorithm>
+#include <climits>
 #include <cstring>
 #include <memory>
 #include <new>
@@ -730,12 +731,25 @@ int wsp_tokenizer_encode(const wsp_tokenizer* t, const char* text, size_t length
     if (t == nullptr || (text == nullptr && length > 0) || count_out == nullptr || capacity < 0
         || (ids_out == nullptr && capacity > 0))
         return WSP_ERR_ARGUMENT;
-    const std::vector<int> ids = t->tokenizer.encode(std::string_view(text == nullptr ? "" : text, length));
-    *count_out = (int) ids.size();
-    if ((int) ids.size() > capacity)
+    try
+    {
+        const std::vector<int> ids = t->tokenizer.encode(std::string_view(text == nullptr ? "" : text, length));
+        if (ids.size() > (size_t) INT_MAX)
+            return WSP_ERR_CAPACITY;
+        *count_out = (int) ids.size();
+        if ((int) ids.size() > capacity)
+            return WSP_ERR_CAPACITY;
+        std::copy(ids.begin(), ids.end(), ids_out);
+        return WSP_OK;
+    }
+    catch (const std::bad_alloc&)
+    {
         return WSP_ERR_CAPACITY;
-    std::copy(ids.begin(), ids.end(), ids_out);
-    return WSP_OK;
+    }
+    catch (const std::exception&)
+    {
+        return WSP_ERR_ARGUMENT;
+    }
 }
 
 int wsp_tokenizer_decode(const wsp_tokenizer* t, const int* ids, int count, int keep_special, char* text_out,
@@ -744,14 +758,27 @@ int wsp_tokenizer_decode(const wsp_tokenizer* t, const int* ids, int count, int 
     if (t == nullptr || (ids == nullptr && count > 0) || count < 0 || length_out == nullptr || text_out == nullptr
         || capacity <= 0)
         return WSP_ERR_ARGUMENT;
-    const std::string text = keep_special ? t->tokenizer.decodeKeepingSpecialTokens(ids, count)
-                                          : t->tokenizer.decode(ids, count);
-    *length_out = (int) text.size();
-    if ((int) text.size() >= capacity)
+    try
+    {
+        const std::string text = keep_special ? t->tokenizer.decodeKeepingSpecialTokens(ids, count)
+                                              : t->tokenizer.decode(ids, count);
+        if (text.size() >= (size_t) INT_MAX)
+            return WSP_ERR_CAPACITY;
+        *length_out = (int) text.size();
+        if ((int) text.size() >= capacity)
+            return WSP_ERR_CAPACITY;
+        std::memcpy(text_out, text.data(), text.size());
+        text_out[text.size()] = 0;
+        return WSP_OK;
+    }
+    catch (const std::bad_alloc&)
+    {
         return WSP_ERR_CAPACITY;
-    std::memcpy(text_out, text.data(), text.size());
-    text_out[text.size()] = 0;
-    return WSP_OK;
+    }
+    catch (const std::exception&)
+    {
+        return WSP_ERR_ARGUMENT;
+    }
 }
 
 } // extern "C"
