@@ -121,8 +121,96 @@ struct FusedState
     wsp_layer_tensors* table = nullptr; // device copy
     std::vector<wsp_layer_tensors> table_host;
     bool table_valid = false;
+    int table_wdtype = -1;
+    float* fold_terms = nullptr; // the folded LayerNorms' per-row terms, layers x FoldTermsLayout::stride
     uint32_t epoch = 0;
 };
+
+// Per-row terms of a LayerNorm folded into the projection that consumes it
+// (step_kernel.hip): gain_r = sum_i W_ri gamma_i and bias_r = b_r + sum_i
+// W_ri beta_i, accumulated in double over the stored weights widened to
+// float, and rounded once. One wave per row; a null bias counts as zero.
+template <int WT>
+__global__ void __launch_bounds__(256) fold_terms_kernel(const void* weight, const float* bias, const float* gamma,
+                                                        const float* beta, int rows, int inner, float* gain_out,
+                                                        float* bias_out)
+{
+    const int row = blockIdx.x * 4 + (int) (threadIdx.x / 64);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) // uniform over the wave
+        return;
+    double g = 0.0, c = 0.0;
+    for (int i = lane; i < inner; i += 64)
+    {
+        const size_t at = (size_t) row * inner + i;
+        float w;
+        if constexpr (WT == WSP_F32)
+            w = static_cast<const float*>(weight)[at];
+        else if constexpr (WT == WSP_F16)
+            w = (float) static_cast<const _Float16*>(weight)[at];
+        else
+            w = __uint_as_float((uint32_t) static_cast<const uint16_t*>(weight)[at] << 16);
+        g += (double) w * (double) gamma[i];
+        c += (double) w * (double) beta[i];
+    }
+    for (int offset = 32; offset > 0; offset >>= 1)
+    {
+        g += __shfl_xor(g, offset);
+        c += __shfl_xor(c, offset);
+    }
+    if (lane == 0)
+    {
+        gain_out[row] = (float) g;
+        bias_out[row] = (float) ((bias != nullptr ? (double) bias[row] : 0.0) + c);
+    }
+}
+
+// Every layer's folded terms for this table, on the context's stream.
+hipError_t compute_fold_terms(const wsp_decoder_shape& s, const wsp_layer_tensors* layers, int wdtype, float* terms,
+                              hipStream_t stream)
+{
+    const int d = s.width, f = s.feed_forward_width;
+    const step::FoldTermsLayout t = step::fold_terms_layout(d, f);
+    for (int l = 0; l < s.layers; ++l)
+    {
+        const wsp_layer_tensors& L = layers[l];
+        float* T = terms + (size_t) l * t.stride;
+        struct Job
+        {
+            const void* w;
+            const float* b;
+            const float* gamma;
+            const float* beta;
+            int rows;
+            int gain, bias;
+        } jobs[] = {{L.self_qkv_w, L.self_qkv_b, L.self_norm_w, L.self_norm_b, 3 * d, t.qkv_gain, t.qkv_bias},
+                    {L.cross_q_w, L.cross_q_b, L.cross_norm_w, L.cross_norm_b, d, t.xq_gain, t.xq_bias},
+                    {L.fc1_w, L.fc1_b, L.final_norm_w, L.final_norm_b, f, t.fc1_gain, t.fc1_bias}};
+        for (const Job& j : jobs)
+        {
+            const dim3 grid((unsigned) ((j.rows + 3) / 4));
+            switch (wdtype)
+            {
+                case WSP_F32:
+                    hipLaunchKernelGGL(fold_terms_kernel<WSP_F32>, grid, dim3(256), 0, stream, j.w, j.b, j.gamma,
+                                       j.beta, j.rows, d, T + j.gain, T + j.bias);
+                    break;
+                case WSP_F16:
+                    hipLaunchKernelGGL(fold_terms_kernel<WSP_F16>, grid, dim3(256), 0, stream, j.w, j.b, j.gamma,
+                                       j.beta, j.rows, d, T + j.gain, T + j.bias);
+                    break;
+                default:
+                    hipLaunchKernelGGL(fold_terms_kernel<WSP_BF16>, grid, dim3(256), 0, stream, j.w, j.b, j.gamma,
+                                       j.beta, j.rows, d, T + j.gain, T + j.bias);
+                    break;
+            }
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess)
+                return e;
+        }
+    }
+    return hipSuccess;
+}
 
 size_t element_bytes(int wdtype)
 {
@@ -192,6 +280,15 @@ void plan_persistent(Context* ctx, FusedState* st)
     }
     if (row_groups < H)
         return refuse("too few CUs for the head groups");
+    {
+        // A LayerNorm's input vector spans at most kFoldChunks poll chunks
+        // (the polling threads hold gamma at that many slots).
+        int block = 1;
+        while (block < ceil_div(d, row_groups))
+            block <<= 1;
+        if (row_groups * block > step::kFoldChunks * step::kPollBlocked * step::kPollThreads)
+            return refuse("width past the folded LayerNorm's poll capacity");
+    }
     if (self_split_max * H * (hd + 2) > step::kMaxCombine || 2 * G > step::kMaxCombine || G > 256)
         return refuse("attention partials past the combine capacity");
     const int cross_needed = ceil_div(s.cross_positions, step::kCrossKeys);
@@ -330,13 +427,20 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
 
     // The per-layer table lives on the device; it is uploaded when it changes.
     const size_t table_bytes = sizeof(wsp_layer_tensors) * (size_t) s.layers;
-    if (!st->table_valid || std::memcmp(st->table_host.data(), tensors->layers, table_bytes) != 0)
+    if (!st->table_valid || st->table_wdtype != tensors->wdtype
+        || std::memcmp(st->table_host.data(), tensors->layers, table_bytes) != 0)
     {
+        // A table with the same pointers is taken to hold the same weights, so
+        // the folded LayerNorms' terms are computed when the table changes.
+        st->table_valid = false;
         st->table_host.assign(tensors->layers, tensors->layers + s.layers);
-        const hipError_t e = hipMemcpyAsync(st->table, st->table_host.data(), table_bytes, hipMemcpyHostToDevice,
-                                            ctx->stream);
+        hipError_t e = hipMemcpyAsync(st->table, st->table_host.data(), table_bytes, hipMemcpyHostToDevice,
+                                      ctx->stream);
+        if (e == hipSuccess)
+            e = compute_fold_terms(s, st->table_host.data(), tensors->wdtype, st->fold_terms, ctx->stream);
         if (e != hipSuccess)
             return context_hip(ctx, e, "decoder step: layer table upload");
+        st->table_wdtype = tensors->wdtype;
         const hipError_t w = hipStreamSynchronize(ctx->stream);
         if (w != hipSuccess)
             return context_hip(ctx, w, "decoder step: layer table upload");
@@ -401,6 +505,15 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     a.log2_d = st->log2_d;
     a.log2_f = st->log2_f;
     a.timeline = step_timeline;
+    const step::FoldTermsLayout terms = step::fold_terms_layout(d, s.feed_forward_width);
+    a.fold_terms = st->fold_terms;
+    a.terms_stride = terms.stride;
+    a.terms_qkv_gain = terms.qkv_gain;
+    a.terms_qkv_bias = terms.qkv_bias;
+    a.terms_xq_gain = terms.xq_gain;
+    a.terms_xq_bias = terms.xq_bias;
+    a.terms_fc1_gain = terms.fc1_gain;
+    a.terms_fc1_bias = terms.fc1_bias;
 
     // A plain launch: the grid is one workgroup per CU, a CU holds only one of
     // these workgroups (registers), and the stream runs kernels one after
@@ -457,6 +570,14 @@ int fused_prepare(Context* ctx)
         status = context_hip(ctx,
                              hipMalloc(&state->table, sizeof(wsp_layer_tensors) * (size_t) ctx->shape.layers),
                              "step layer table");
+    if (status == WSP_OK)
+        status = context_hip(ctx,
+                             hipMalloc(&state->fold_terms,
+                                       sizeof(float) * (size_t) ctx->shape.layers
+                                           * (size_t) step::fold_terms_layout(ctx->shape.width,
+                                                                              ctx->shape.feed_forward_width)
+                                                 .stride),
+                             "step folded LayerNorm terms");
     // Epoch 0 is never used, so zeroed words never pass for a step's output
     // (a pooled area also holds a previous context's epochs until cleared).
     if (status == WSP_OK)
@@ -480,6 +601,7 @@ void fused_release(Context* ctx)
     release_area(ctx->device, state->exchange_held, state->exchange);
     hipFree(state->status);
     hipFree(state->table);
+    hipFree(state->fold_terms);
     delete state;
     ctx->fused = nullptr;
 }

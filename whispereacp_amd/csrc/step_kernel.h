@@ -22,6 +22,7 @@ constexpr int kMaxLayers = 32;         // layer table entries held in LDS
 constexpr int kPollThreads = kThreads - 64; // threads that poll exchange words (waves 1-7)
 constexpr int kPollBlocked = 2;        // slots per polling thread for a width-long vector, per chunk
 constexpr int kPollBlockedFF = 8;      // ... for the feed-forward vector
+constexpr int kFoldChunks = 2;         // chunks of kPollBlocked * kPollThreads slots a LayerNorm's input may span
 
 // Exchange words per layer, in this order (offsets in StepArgs):
 //   qkv [row_groups << log2_qkv] | self partials [self_split_max][heads][hd + 2]
@@ -63,7 +64,34 @@ struct StepArgs
     int layer_words, off_argmax;
     int log2_qkv, log2_d, log2_f; // producer block sizes of the row-group vectors
     uint64_t* timeline; // per-workgroup timestamps of a WSP_STEP_TIMELINE build (else unused)
+
+    // The folded LayerNorms' per-row terms (fold_terms_kernel): per layer
+    // terms_stride floats, holding for the q/k/v, cross-query and fc1 rows
+    // gain_r = sum_i W_ri gamma_i and bias_r = b_r + sum_i W_ri beta_i of the
+    // LayerNorm each consumes, at these offsets.
+    const float* fold_terms;
+    int terms_stride;
+    int terms_qkv_gain, terms_qkv_bias, terms_xq_gain, terms_xq_bias, terms_fc1_gain, terms_fc1_bias;
 };
+
+// The folded terms' layout for a shape (floats; see StepArgs::fold_terms).
+struct FoldTermsLayout
+{
+    int stride, qkv_gain, qkv_bias, xq_gain, xq_bias, fc1_gain, fc1_bias;
+};
+
+inline FoldTermsLayout fold_terms_layout(int width, int feed_forward)
+{
+    FoldTermsLayout t {};
+    t.qkv_gain = 0;
+    t.qkv_bias = 3 * width;
+    t.xq_gain = 6 * width;
+    t.xq_bias = 7 * width;
+    t.fc1_gain = 8 * width;
+    t.fc1_bias = 8 * width + feed_forward;
+    t.stride = 8 * width + 2 * feed_forward;
+    return t;
+}
 
 // Longest projection row, in 16-byte chunks: 16 slices of 3 chunks per lane.
 constexpr int kMaxRowChunks = 16 * 32 * 3;

@@ -61,7 +61,9 @@ static_assert(kKeySlots / kWaves == 4, "attend() folds four key slots per wave")
 // STEP_STAMP(event, layer) into LDS, and the kernel writes them to
 // StepArgs::timeline ([workgroup][kTimelineEvents][kTimelineLayers]) at its
 // end. Without it the marks compile to nothing.
-constexpr int kTimelineEvents = 24, kTimelineLayers = 33;
+// STEP_MARK(event) stamps inside a phase, at the layer the workgroup last
+// named with STEP_LAYER (events below 0 are not stamped).
+constexpr int kTimelineEvents = 40, kTimelineLayers = 33;
 #ifdef WSP_STEP_TIMELINE
 #define STEP_STAMP(e, l)                                      \
     do                                                        \
@@ -69,10 +71,30 @@ constexpr int kTimelineEvents = 24, kTimelineLayers = 33;
         if (threadIdx.x == 0)                                 \
             sh.timeline[(e)][(l)] = wall_clock64();           \
     } while (0)
+#define STEP_LAYER(l)                                         \
+    do                                                        \
+    {                                                         \
+        if (threadIdx.x == 0)                                 \
+            sh.mark_layer = (l);                              \
+    } while (0)
+#define STEP_MARK(e)                                          \
+    do                                                        \
+    {                                                         \
+        if (threadIdx.x == 0 && (e) >= 0)                     \
+            sh.timeline[(e)][sh.mark_layer] = wall_clock64(); \
+    } while (0)
 #else
 #define STEP_STAMP(e, l) \
     do                   \
     {                    \
+    } while (0)
+#define STEP_LAYER(l) \
+    do                \
+    {                 \
+    } while (0)
+#define STEP_MARK(e) \
+    do               \
+    {                \
     } while (0)
 #endif
 
@@ -182,12 +204,14 @@ struct Shared
     float red[kWaves][kMaxHeadWidth];    // per-wave value rows of an attention chunk
     float q[3 * kMaxHeadWidth];          // a head's query, then (self-attention) its new key and value
     float scratch[2][kWaves];            // per-wave maxima and sums of an attention chunk
+    float fold[kWaves][2];               // per-wave sums of (x - K) and (x - K)^2 of a folded LayerNorm
     alignas(16) float part[kRowGroups];  // per-row-group partial sums of a projection pass
     float best_v[kRowGroups];
     uint32_t best_i[kRowGroups];
     int abort;
 #ifdef WSP_STEP_TIMELINE
     uint64_t timeline[kTimelineEvents][kTimelineLayers];
+    int mark_layer;
 #endif
 };
 
@@ -470,7 +494,7 @@ __device__ __forceinline__ void load_norm(NormParams& p, const float* gamma, con
 // The statistics and this wave's run, with R runs per lane (R * 256 >= n).
 template <int R>
 __device__ __forceinline__ void norm_row(const NormParams& p, int n, float inv_n, float eps, Shared& sh, int lane,
-                                         int own)
+                                         int own, int mark)
 {
     // Every LDS read is issued before the first is used: the row's runs and
     // this thread's own run.
@@ -501,6 +525,7 @@ __device__ __forceinline__ void norm_row(const NormParams& p, int n, float inv_n
     for (int k = 0; k < R; k += 2)
         q += k + 1 < R ? t[k] + t[k + 1] : t[k];
     const float scale = rsqrtf(sum64(q) * inv_n + eps);
+    STEP_MARK(mark);
     if (own < n)
     {
         float4v y;
@@ -512,7 +537,8 @@ __device__ __forceinline__ void norm_row(const NormParams& p, int n, float inv_n
 }
 
 // inv_n = 1 / n (the row means are the sums times inv_n).
-__device__ __forceinline__ void layer_norm(const NormParams& p, int n, float inv_n, float eps, Shared& sh)
+__device__ __forceinline__ void layer_norm(const NormParams& p, int n, float inv_n, float eps, Shared& sh,
+                                           int mark = -1)
 {
     const int lane = threadIdx.x & (kWave - 1);
     const int own = 4 * (lane + kWave * (int) (threadIdx.x / kWave)); // the run this wave writes
@@ -523,13 +549,193 @@ __device__ __forceinline__ void layer_norm(const NormParams& p, int n, float inv
         switch ((n + 4 * kWave - 1) / (4 * kWave))
         {
             case 1:
-            case 2: norm_row<2>(p, n, inv_n, eps, sh, lane, own); break;
-            case 3: norm_row<3>(p, n, inv_n, eps, sh, lane, own); break;
-            case 4: norm_row<4>(p, n, inv_n, eps, sh, lane, own); break;
-            default: norm_row<kNormRuns>(p, n, inv_n, eps, sh, lane, own); break;
+            case 2: norm_row<2>(p, n, inv_n, eps, sh, lane, own, mark); break;
+            case 3: norm_row<3>(p, n, inv_n, eps, sh, lane, own, mark); break;
+            case 4: norm_row<4>(p, n, inv_n, eps, sh, lane, own, mark); break;
+            default: norm_row<kNormRuns>(p, n, inv_n, eps, sh, lane, own, mark); break;
         }
     }
     __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// A LayerNorm folded into the projection that consumes it. With
+// LN(x)_i = (x_i - mean) rstd gamma_i + beta_i, row r of that projection is
+//   (W LN(x))_r + b_r = rstd (sum_i W_ri gamma_i (x_i - K) - (mean - K) g_r) + b'_r
+// for any shift K, with g_r = sum_i W_ri gamma_i and b'_r = b_r + sum_i W_ri
+// beta_i computed once per weight set (fold_terms_kernel, fused_step.hip). So
+// the polling threads write gamma_i (x_i - K) into the dot products' input as
+// the words arrive, keep x_i for the residual, and sum their slots' (x_i - K)
+// and (x_i - K)^2 in slot order; one reduction of the two sums gives
+// mean = K + E[x - K] and var = E[(x - K)^2] - E[x - K]^2, and nothing
+// normalises the row before the dot products start. K is the workgroup's
+// previous LayerNorm mean (zero before the first), so (mean - K) stays small
+// next to the row's spread: neither the variance nor the correction
+// (mean - K) g_r loses precision to cancellation while the residual stream's
+// mean moves little from one sublayer to the next.
+// ---------------------------------------------------------------------------
+static_assert(kFoldChunks * kPollBlocked * kPollThreads >= 2 * 768, "two chunks hold d 768 at any row-group count");
+constexpr int kFoldSlots = kPollBlocked * kFoldChunks; // a polling thread's slots of a folded row
+
+struct FoldParams
+{
+    float gamma[kFoldSlots]; // gamma at this thread's slots (zero where a slot holds nothing)
+};
+
+// A folded LayerNorm's statistics (fold_stats): rstd, and the mean less the
+// shift K the input was written against.
+struct FoldStats
+{
+    float rstd;
+    float dmean;
+};
+
+// One thread's sums of (x_i - K) and (x_i - K)^2 over the entries it wrote.
+struct FoldSums
+{
+    float s1;
+    float s2;
+};
+
+// The slot of a blocked vector that polling thread t reads as its k-th
+// (chunk k / kPollBlocked, the same order gather_blocked polls in).
+__device__ __forceinline__ int fold_slot(int t, int k)
+{
+    return (k / kPollBlocked) * (kPollBlocked * kPollThreads) + t + (k % kPollBlocked) * kPollThreads;
+}
+
+// Loads gamma at this thread's slots of a `rows`-long blocked vector (2^log2
+// words per producer, `stride` producers). Every load is issued on every path,
+// at a clamped index; wave 0, which does not poll, holds zeros.
+__device__ __forceinline__ void load_fold(FoldParams& fp, const float* gamma, int rows, int log2_block, int stride)
+{
+    const int t = (int) threadIdx.x - kWave;
+    const int slots = stride << log2_block;
+    const int mask = (1 << log2_block) - 1;
+#pragma unroll
+    for (int k = 0; k < kFoldSlots; ++k)
+    {
+        const int slot = fold_slot(t, k);
+        const bool valid = t >= 0 && slot < slots && (slot & mask) * stride + (slot >> log2_block) < rows;
+        const float g = global(gamma)[valid ? (slot & mask) * stride + (slot >> log2_block) : 0];
+        fp.gamma[k] = valid ? g : 0.f;
+    }
+}
+
+// Each wave's totals of the threads' sums into sh.fold (every lane of the
+// wave active); read after the next barrier.
+__device__ __forceinline__ void fold_reduce(const FoldSums& sums, Shared& sh)
+{
+    const float s1 = sum64(sums.s1);
+    const float s2 = sum64(sums.s2);
+    if ((threadIdx.x & (kWave - 1)) == 0)
+    {
+        sh.fold[threadIdx.x / kWave][0] = s1;
+        sh.fold[threadIdx.x / kWave][1] = s2;
+    }
+}
+
+// gather_blocked for a LayerNorm's input, the whole vector in chunks of
+// kPollBlocked * 448 slots: sh.raw[i] = x_i, sh.x[i] = gamma_i (x_i - shift),
+// and each wave's sums of (x_i - shift) and (x_i - shift)^2 over its slots (in
+// slot order, then a fixed tree) in sh.fold. Returns false, uniformly, when
+// the watchdog tripped.
+__device__ __forceinline__ bool gather_fold(const uint64_t* base, int rows, int log2_block, int stride,
+                                            const FoldParams& fp, float shift, uint32_t epoch, int* status,
+                                            Shared& sh)
+{
+    const int slots = stride << log2_block;
+    const int mask = (1 << log2_block) - 1;
+    float s1 = 0.f, s2 = 0.f;
+    bool failed = false;
+    if (threadIdx.x < kWave)
+        __builtin_amdgcn_s_waitcnt(0); // wave 0 stored the last phase's outputs: it only waits for them
+    else
+    {
+        const int t = threadIdx.x - kWave;
+#pragma unroll
+        for (int c = 0; c < kFoldChunks; ++c)
+        {
+            if (c * kPollBlocked * kPollThreads >= slots || failed) // uniform over the workgroup but for failed
+                break;
+            uint32_t pending = 0;
+            int index[kPollBlocked];
+#pragma unroll
+            for (int k = 0; k < kPollBlocked; ++k)
+            {
+                const int slot = fold_slot(t, c * kPollBlocked + k);
+                index[k] = (slot & mask) * stride + (slot >> log2_block);
+                if (slot < slots && index[k] < rows)
+                    pending |= 1u << k;
+            }
+            const uint32_t valid = pending;
+            float got[kPollBlocked] = {};
+            int spins = 0;
+            while (pending != 0)
+            {
+                uint64_t w[kPollBlocked];
+#pragma unroll
+                for (int k = 0; k < kPollBlocked; ++k)
+                    if (pending & (1u << k))
+                        w[k] = peek(base + fold_slot(t, c * kPollBlocked + k));
+#pragma unroll
+                for (int k = 0; k < kPollBlocked; ++k)
+                    if ((pending & (1u << k)) && (uint32_t) (w[k] >> 32) == epoch)
+                    {
+                        got[k] = __uint_as_float((uint32_t) w[k]);
+                        pending &= ~(1u << k);
+                    }
+                if (pending != 0 && (++spins & 63) == 0)
+                {
+                    if (spins > kSpinLimit)
+                    {
+                        __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        failed = true;
+                        break;
+                    }
+                    if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
+                    {
+                        failed = true;
+                        break;
+                    }
+                }
+            }
+            // In slot order: the stores into the row and the two sums.
+#pragma unroll
+            for (int k = 0; k < kPollBlocked; ++k)
+                if (valid & (1u << k))
+                {
+                    const float dx = got[k] - shift;
+                    sh.raw[index[k]] = got[k];
+                    sh.x[index[k]] = fp.gamma[c * kPollBlocked + k] * dx;
+                    s1 += dx;
+                    s2 += dx * dx;
+                }
+        }
+    }
+    fold_reduce({s1, s2}, sh);
+    if (failed)
+        sh.abort = 1;
+    __syncthreads();
+    return sh.abort == 0;
+}
+
+
+// The statistics from the waves' sums (in wave order): rstd, and the mean
+// less the shift. Every thread computes the same values.
+__device__ __forceinline__ FoldStats fold_stats(const Shared& sh, float inv_n, float eps)
+{
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+    {
+        s1 += sh.fold[w][0];
+        s2 += sh.fold[w][1];
+    }
+    FoldStats fs;
+    fs.dmean = s1 * inv_n;
+    fs.rstd = rsqrtf(fmaxf(s2 * inv_n - fs.dmean * fs.dmean, 0.f) + eps);
+    return fs;
 }
 
 // ---------------------------------------------------------------------------
@@ -701,12 +907,14 @@ struct Prefetch
 {
     RowLoad r;
     float bias; // the bias of the row this thread finishes in pass 0
+    float gain; // a folded LayerNorm's sum_i W_ri gamma_i of that row (FOLD phases)
 };
 
 // Issues this row group's pass-0 weights and, for the finishing threads, the
-// bias of their pass-0 row.
-__device__ __forceinline__ void prefetch(Prefetch& p, const void* weight, const float* bias, const PhaseShape& ps,
-                                         int group, int stride)
+// bias of their pass-0 row (and with FOLD its gain).
+template <bool FOLD>
+__device__ __forceinline__ void prefetch(Prefetch& p, const void* weight, const float* bias, const float* gain,
+                                         const PhaseShape& ps, int group, int stride)
 {
     int row, first, last;
     phase_task(ps, group, stride, 0, row, first, last);
@@ -720,6 +928,8 @@ __device__ __forceinline__ void prefetch(Prefetch& p, const void* weight, const 
     const float* source = bias != nullptr ? bias : static_cast<const float*>(weight);
     const float b = global(source)[finisher_row];
     p.bias = bias != nullptr ? b : 0.f;
+    if constexpr (FOLD)
+        p.gain = global(gain)[finisher_row];
 }
 
 // The slices of finisher t's row (slots [t << log2, (t + 1) << log2) of
@@ -756,11 +966,12 @@ __device__ __forceinline__ float slice_total(const Shared& sh, int t, int log2)
 static_assert(kRowGroups == 16, "slice_total covers up to 16 slices");
 
 // Sums a pass's partials, then the finishing threads add the slices of their
-// row, the bias, and hand the value to epi; two barriers bracket the shared
-// partial slots.
-template <class Epilogue, class Bias>
+// row, turn the dot product into the row's value (value_of: the bias, or a
+// folded LayerNorm's correction and bias) and hand it to epi; two barriers
+// bracket the shared partial slots.
+template <class Epilogue, class Value>
 __device__ __forceinline__ void finish_pass(float acc, bool has_task, int pass, const PhaseShape& ps, int group,
-                                            int stride, Shared& sh, Epilogue& epi, Bias bias_of)
+                                            int stride, Shared& sh, Epilogue& epi, Value value_of)
 {
     acc = sum32(acc);
     if (has_task && (threadIdx.x & (kRowLanes - 1)) == 0)
@@ -771,7 +982,7 @@ __device__ __forceinline__ void finish_pass(float acc, bool has_task, int pass, 
     {
         const float v = slice_total(sh, (int) threadIdx.x, ps.slice_log2);
         const int r = phase_row(ps, group, stride, local);
-        epi(r, local, v + bias_of(r));
+        epi(r, local, value_of(r, v));
     }
     // Also keeps the other waves from issuing loads (polls, prefetches)
     // ahead of the finishers' stores.
@@ -779,24 +990,31 @@ __device__ __forceinline__ void finish_pass(float acc, bool has_task, int pass, 
 }
 
 // Runs every task of the phase against sh.x. epi(row, value) receives the dot
-// product plus bias, on thread (local row) % rows_per_pass (all in wave 0).
-// Pass 0 is straight-line code whose weights and bias were loaded a phase
-// earlier; further passes, which only long rows or narrow grids need, load on
-// the spot. after() issues the loads of a later phase (its prefetch): every
-// thread calls it once, after pass 0's stores, so they are not held up behind
-// the issue.
-template <int WT, class Epilogue, class After>
-__device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight, const float* bias,
-                                          const PhaseShape& ps, int group, int stride, Shared& sh, Epilogue epi,
-                                          After after)
+// product plus bias, on thread (local row) % rows_per_pass (all in wave 0);
+// with FOLD, sh.x holds gamma (x - K) of a LayerNorm's input and the value is
+// rstd (dot - (mean - K) gain) + bias, where bias and gain are the row's folded
+// terms. Pass 0 is straight-line code whose weights, bias and gain were loaded
+// a phase earlier; further passes, which only long rows or narrow grids need,
+// load on the spot. after() issues the loads of a later phase (its prefetch):
+// every thread calls it once, after pass 0's stores, so they are not held up
+// behind the issue.
+template <int WT, bool FOLD, class Epilogue, class After>
+__device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight, const float* bias, const float* gain,
+                                          const FoldStats& fs, const PhaseShape& ps, int group, int stride,
+                                          Shared& sh, Epilogue epi, After after, int mark = -1)
 {
     const int lane = threadIdx.x & (kRowLanes - 1);
     int row, first, last;
     const bool has_task = phase_task(ps, group, stride, 0, row, first, last);
     const float acc = run_dot<WT>(p.r, sh.x, first, last, lane);
     const float bias0 = p.bias;
+    const float gain0 = FOLD ? p.gain : 0.f;
+    auto value = [&](float v, float b, float g) { return FOLD ? fs.rstd * (v - fs.dmean * g) + b : v + b; };
+    STEP_MARK(mark);
     if (ps.passes > 0)
-        finish_pass(acc, has_task, 0, ps, group, stride, sh, epi, [&](int) { return bias0; });
+        finish_pass(acc, has_task, 0, ps, group, stride, sh, epi,
+                    [&](int, float v) { return value(v, bias0, gain0); });
+    STEP_MARK(mark < 0 ? -1 : mark + 1);
     after();
     for (int pass = 1; pass < ps.passes; ++pass)
     {
@@ -804,7 +1022,9 @@ __device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight,
         RowLoad r;
         load_run(r, weight, row, ps.row_bytes, first, last);
         finish_pass(run_dot<WT>(r, sh.x, first, last, lane), task, pass, ps, group, stride, sh, epi,
-                    [&](int rr) { return bias != nullptr ? global(bias)[rr] : 0.f; });
+                    [&](int rr, float v) {
+                        return value(v, bias != nullptr ? global(bias)[rr] : 0.f, FOLD ? global(gain)[rr] : 0.f);
+                    });
     }
 }
 
@@ -861,7 +1081,7 @@ __device__ __forceinline__ void load_keys(KeyRows<NP>& kr, const float* keys, co
 // writes sh.red and sh.scratch again only after a barrier of its own.
 template <int NP>
 __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int head_width, float scale2, uint64_t* out,
-                                       uint32_t epoch, Shared& sh, bool normalized = false)
+                                       uint32_t epoch, Shared& sh, bool normalized = false, int mark = -1)
 {
     const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
@@ -885,6 +1105,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
         }
     }
     const float m = max64(local_max); // this wave's keys; -inf when it holds none
+    STEP_MARK(mark);
     float local_sum = 0.f;
     float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -908,6 +1129,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
     for (int i = 0; i < 4; ++i)
         acc[i] = add32(add16(acc[i]));
     local_sum = add32(add16(local_sum));
+    STEP_MARK(mark < 0 ? -1 : mark + 1);
     if (lane < kKeyLanes && live)
         *reinterpret_cast<float4v*>(&sh.red[wave][4 * kl]) = acc;
     if (lane == 0)
@@ -916,6 +1138,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
         sh.scratch[1][wave] = local_sum;
     }
     __syncthreads();
+    STEP_MARK(mark < 0 ? -1 : mark + 2);
     if ((int) threadIdx.x < head_width)
     {
         float mw[kWaves], lw[kWaves], rw[kWaves];
@@ -1224,20 +1447,44 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
     const int task_count = task < tasks ? min(a.cross_chunk, a.cross_rows - task_first) : 0;
 
     Prefetch pa, pb;
-    NormParams norm;
+    FoldParams fold;
+    FoldStats fs;
+    float shift = 0.f; // the previous LayerNorm's mean (the next one's K)
     KeyRows<kCrossPasses> cross;
+    const FoldStats none {};
+    // After a folded gather every thread reads the statistics (the waves'
+    // sums are in sh.fold past its barrier) and moves the shift to this
+    // LayerNorm's mean, the next one's K.
+    auto statistics = [&] {
+        fs = fold_stats(sh, a.inv_width, a.eps);
+        shift += fs.dmean;
+    };
 
     {
+        // The layer-0 input, folded into LN1 the way gather_fold folds the
+        // later layers' (all eight waves hold embedding entries; K = 0).
         const wsp_layer_tensors& L0 = sh.table[0];
-        prefetch(pa, L0.self_qkv_w, L0.self_qkv_b, qkv_shape, group, stride);
-        load_norm(norm, L0.self_norm_w, L0.self_norm_b, d);
+        const float* T0 = a.fold_terms;
+        prefetch<true>(pa, L0.self_qkv_w, T0 + a.terms_qkv_bias, T0 + a.terms_qkv_gain, qkv_shape, group, stride);
+        float gamma[kEmbedSlots];
+#pragma unroll
+        for (int k = 0; k < kEmbedSlots; ++k)
+            gamma[k] = global(L0.self_norm_w)[min((int) threadIdx.x + kThreads * k, d - 1)];
+        float s1 = 0.f, s2 = 0.f;
 #pragma unroll
         for (int k = 0; k < kEmbedSlots; ++k)
         {
             const int c = (int) threadIdx.x + kThreads * k;
             if (c < d)
-                sh.raw[c] = embed.known ? embed.token[k] + embed.position[k] : __builtin_nanf("");
+            {
+                const float x = embed.known ? embed.token[k] + embed.position[k] : __builtin_nanf("");
+                sh.raw[c] = x;
+                sh.x[c] = gamma[k] * x;
+                s1 += x;
+                s2 += x * x;
+            }
         }
+        fold_reduce({s1, s2}, sh);
         __syncthreads();
     }
     STEP_STAMP(0, 0);
@@ -1245,27 +1492,30 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
     for (int l = 0; l < a.layer_count; ++l)
     {
         const wsp_layer_tensors& L = sh.table[l];
+        const float* T = a.fold_terms + (size_t) l * a.terms_stride;
         uint64_t* ex = a.exchange + (size_t) l * a.layer_words;
+        STEP_LAYER(l);
 
-        // ---- LN1 + fused q/k/v (weights in pa) ---------------------------------
+        // ---- LN1 folded into the fused q/k/v (weights in pa) --------------------
         if (l > 0
-            && !gather_blocked<kPollBlocked>(a.exchange + (size_t) (l - 1) * a.layer_words + a.off_h4, d, a.log2_d,
-                                             stride, sh.raw, epoch, a.status, sh))
+            && !gather_fold(a.exchange + (size_t) (l - 1) * a.layer_words + a.off_h4, d, a.log2_d, stride, fold,
+                            shift, epoch, a.status, sh))
             return false;
         if (l > 0)
             STEP_STAMP(0, l);
-        layer_norm(norm, d, a.inv_width, a.eps, sh);
+        statistics();
         {
             uint64_t* qkv = ex + a.off_qkv;
             float* krow = L.self_keys + (size_t) pos * d;
             float* vrow = L.self_values + (size_t) pos * d;
-            run_phase<WT>(pa, L.self_qkv_w, L.self_qkv_b, qkv_shape, group, stride, sh, [&](int r, int j, float v) {
+            run_phase<WT, true>(pa, L.self_qkv_w, T + a.terms_qkv_bias, T + a.terms_qkv_gain, fs, qkv_shape, group,
+                                stride, sh, [&](int r, int j, float v) {
                 put(qkv + (group << a.log2_qkv) + j, v, epoch);
                 if (r >= 2 * d)
                     global_mut(vrow)[r - 2 * d] = v;
                 else if (r >= d)
                     global_mut(krow)[r - d] = v;
-            }, [&] { prefetch(pb, L.self_out_w, L.self_out_b, square_shape, group, stride); });
+            }, [&] { prefetch<false>(pb, L.self_out_w, L.self_out_b, nullptr, square_shape, group, stride); }, 25);
         }
         STEP_STAMP(1, l);
 
@@ -1283,9 +1533,9 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
             // One partial per head, written normalized: its rows are the
             // attention output, gathered straight into sh.x (two poll slots
             // per thread cover 896 words, three the widest row).
-            const int shift = 31 - __builtin_clz(hd);
+            const int shift_hd = 31 - __builtin_clz(hd);
             auto map = [&](int i, int& offset, int& index) {
-                offset = (i >> shift) * (hd + 2) + 2 + (i & (hd - 1));
+                offset = (i >> shift_hd) * (hd + 2) + 2 + (i & (hd - 1));
                 index = i;
                 return true;
             };
@@ -1306,27 +1556,30 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         }
         {
             uint64_t* out = ex + a.off_h2;
-            run_phase<WT>(
-                pb, L.self_out_w, L.self_out_b, square_shape, group, stride, sh,
+            run_phase<WT, false>(
+                pb, L.self_out_w, L.self_out_b, nullptr, none, square_shape, group, stride, sh,
                 [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); },
                 [&] {
-                    prefetch(pa, L.cross_q_w, L.cross_q_b, xq_shape, group, stride);
-                    load_norm(norm, L.cross_norm_w, L.cross_norm_b, d);
-                });
+                    prefetch<true>(pa, L.cross_q_w, T + a.terms_xq_bias, T + a.terms_xq_gain, xq_shape, group,
+                                   stride);
+                    load_fold(fold, L.cross_norm_w, d, a.log2_d, stride);
+                },
+                27);
         }
         STEP_STAMP(3, l);
 
-        // ---- LN2 + cross q (weights in pa) ----------------------------------------
-        if (!gather_blocked<kPollBlocked>(ex + a.off_h2, d, a.log2_d, stride, sh.raw, epoch, a.status, sh))
+        // ---- LN2 folded into the cross q (weights in pa) --------------------------
+        if (!gather_fold(ex + a.off_h2, d, a.log2_d, stride, fold, shift, epoch, a.status, sh))
             return false;
         STEP_STAMP(4, l);
-        layer_norm(norm, d, a.inv_width, a.eps, sh);
+        statistics();
         {
             uint64_t* out = ex + a.off_xq;
-            run_phase<WT>(
-                pa, L.cross_q_w, L.cross_q_b, xq_shape, group, stride, sh,
+            run_phase<WT, true>(
+                pa, L.cross_q_w, T + a.terms_xq_bias, T + a.terms_xq_gain, fs, xq_shape, group, stride, sh,
                 [&](int, int j, float v) { put(out + (group << a.log2_d) + j, v, epoch); },
-                [&] { prefetch(pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride); });
+                [&] { prefetch<false>(pb, L.cross_out_w, L.cross_out_b, nullptr, square_shape, group, stride); },
+                29);
         }
         STEP_STAMP(5, l);
 
@@ -1350,7 +1603,8 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
             if (t == task)
                 STEP_STAMP(6, l);
             attend<kCrossPasses>(cross, count, hd, a.scale * kLog2e,
-                                 ex + a.off_xpart + (size_t) (h * a.cross_splits + s) * (hd + 2), epoch, sh);
+                                 ex + a.off_xpart + (size_t) (h * a.cross_splits + s) * (hd + 2), epoch, sh, false,
+                                 t == task ? 22 : -1);
         }
         STEP_STAMP(7, l);
 
@@ -1360,27 +1614,28 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         STEP_STAMP(8, l);
         {
             uint64_t* out = ex + a.off_h3;
-            run_phase<WT>(
-                pb, L.cross_out_w, L.cross_out_b, square_shape, group, stride, sh,
+            run_phase<WT, false>(
+                pb, L.cross_out_w, L.cross_out_b, nullptr, none, square_shape, group, stride, sh,
                 [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); },
                 [&] {
-                    prefetch(pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride);
-                    load_norm(norm, L.final_norm_w, L.final_norm_b, d);
-                });
+                    prefetch<true>(pa, L.fc1_w, T + a.terms_fc1_bias, T + a.terms_fc1_gain, fc1_shape, group, stride);
+                    load_fold(fold, L.final_norm_w, d, a.log2_d, stride);
+                },
+                31);
         }
         STEP_STAMP(9, l);
 
-        // ---- LN3 + fc1 + GELU (weights in pa) ------------------------------------------
-        if (!gather_blocked<kPollBlocked>(ex + a.off_h3, d, a.log2_d, stride, sh.raw, epoch, a.status, sh))
+        // ---- LN3 folded into fc1 + GELU (weights in pa) ----------------------------------
+        if (!gather_fold(ex + a.off_h3, d, a.log2_d, stride, fold, shift, epoch, a.status, sh))
             return false;
         STEP_STAMP(10, l);
-        layer_norm(norm, d, a.inv_width, a.eps, sh);
+        statistics();
         {
             uint64_t* out = ex + a.off_ff;
-            run_phase<WT>(
-                pa, L.fc1_w, L.fc1_b, fc1_shape, group, stride, sh,
+            run_phase<WT, true>(
+                pa, L.fc1_w, T + a.terms_fc1_bias, T + a.terms_fc1_gain, fs, fc1_shape, group, stride, sh,
                 [&](int, int j, float v) { put(out + (group << a.log2_f) + j, exact_gelu(v), epoch); },
-                [&] { prefetch(pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride); });
+                [&] { prefetch<false>(pb, L.fc2_w, L.fc2_b, nullptr, fc2_shape, group, stride); }, 33);
         }
         STEP_STAMP(11, l);
 
@@ -1389,18 +1644,22 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
             return false;
         STEP_STAMP(12, l);
         {
-            // After the dot products: the next layer's q/k/v slice and LN1
-            // parameters (the last layer loads its own again, unused, so these
-            // loads are issued on every path).
-            const wsp_layer_tensors& next = sh.table[min(l + 1, a.layer_count - 1)];
+            // After the dot products: the next layer's q/k/v slice, its folded
+            // terms and LN1's gamma (the last layer loads its own again, unused,
+            // so these loads are issued on every path).
+            const int next_layer = min(l + 1, a.layer_count - 1);
+            const wsp_layer_tensors& next = sh.table[next_layer];
+            const float* TN = a.fold_terms + (size_t) next_layer * a.terms_stride;
             uint64_t* out = ex + a.off_h4;
-            run_phase<WT>(
-                pb, L.fc2_w, L.fc2_b, fc2_shape, group, stride, sh,
+            run_phase<WT, false>(
+                pb, L.fc2_w, L.fc2_b, nullptr, none, fc2_shape, group, stride, sh,
                 [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); },
                 [&] {
-                    prefetch(pa, next.self_qkv_w, next.self_qkv_b, qkv_shape, group, stride);
-                    load_norm(norm, next.self_norm_w, next.self_norm_b, d);
-                });
+                    prefetch<true>(pa, next.self_qkv_w, TN + a.terms_qkv_bias, TN + a.terms_qkv_gain, qkv_shape,
+                                   group, stride);
+                    load_fold(fold, next.self_norm_w, d, a.log2_d, stride);
+                },
+                35);
         }
         STEP_STAMP(13, l);
     }
@@ -1428,6 +1687,7 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
     {
         uint64_t* ex = a.exchange + (size_t) l * a.layer_words;
         const bool last_layer = l + 1 == a.layer_count;
+        STEP_LAYER(l);
         if (attends)
         {
             // q, and the new key/value rows, of this head, in one wait.
@@ -1457,7 +1717,7 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
                     }
             }
             attend<kSelfPasses>(self, count, hd, a.scale * kLog2e, ex + a.off_self + (size_t) (split * H + head) * (hd + 2),
-                                epoch, sh, a.self_splits == 1);
+                                epoch, sh, a.self_splits == 1, 22);
             STEP_STAMP(15, l);
         }
         // Cross-attention combine of one head; the next layer's keys are
