@@ -79,6 +79,44 @@ def build(verbose: bool = True) -> str:
     return LIBRARY
 
 
+# The timeline variant: the persistent step built with WSP_STEP_TIMELINE, which
+# stamps the real-time clock at every phase boundary of every workgroup. Only
+# the two translation units that see the macro are recompiled; the rest are the
+# main build's objects.
+TIMELINE_SOURCES = ["step_kernel.hip", "fused_step.hip"]
+TIMELINE_BUILD = os.path.join(BUILD, "timeline")
+TIMELINE_LIBRARY = os.path.join(TIMELINE_BUILD, "libwhispereacp_hip.so")
+
+
+def build_timeline(verbose: bool = True) -> str:
+    """The timeline variant of the library (after build()); returns its path."""
+    if not all(os.path.exists(_object_path(s)) for s in DEVICE_SOURCES + HOST_SOURCES):
+        build(verbose)
+    os.makedirs(TIMELINE_BUILD, exist_ok=True)
+    objects = []
+    for source in DEVICE_SOURCES + HOST_SOURCES:
+        if source not in TIMELINE_SOURCES:
+            objects.append(_object_path(source))
+            continue
+        out = os.path.join(TIMELINE_BUILD, source.replace("/", "_") + ".o")
+        cmd = [hipcc()] + COMMON + DEVICE_FLAGS + ["-DWSP_STEP_TIMELINE", "-c", os.path.join(CSRC, source), "-o", out]
+        result = subprocess.run(cmd, capture_output=True, text=True)
+        if result.returncode != 0:
+            raise RuntimeError(f"compiling {source} (timeline) failed:\n{result.stderr[-6000:]}")
+        objects.append(out)
+        if verbose:
+            print(f"  compiled {source} (timeline)", flush=True)
+    tmp = TIMELINE_LIBRARY + ".tmp"
+    result = subprocess.run([hipcc(), "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", tmp] + sorted(objects),
+                            capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"linking the timeline variant failed:\n{result.stderr[-6000:]}")
+    os.replace(tmp, TIMELINE_LIBRARY)
+    if verbose:
+        print(f"  linked {TIMELINE_LIBRARY}", flush=True)
+    return TIMELINE_LIBRARY
+
+
 if __name__ == "__main__":
     try:
         build()
