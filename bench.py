@@ -14,11 +14,11 @@ one warm-up, then --runs timed runs (10 by default) of the whole sequence, and
 the median run is reported with the fastest and slowest beside it. Within a
 run, with --steps equal to the workload's own step count (the default) the
 whole sequence is one event-bracketed region, the self-attention KV growing
-5..228 keys. With fewer, the whole sequence still runs, and --steps steps
-spread evenly over it are each bracketed by HIP events on the decoder's stream
-(nothing synchronises between them, so the launch queue never drains); the
-bytes per step are averaged over the same positions. Every run must decode the
-same tokens.
+5..228 keys. With fewer, the whole sequence still runs, and --steps consecutive
+steps from its middle are bracketed by one pair of HIP events on the decoder's
+stream (nothing synchronises inside the sequence, so the launch queue never
+drains); the bytes per step are averaged over the same positions. Every run
+must decode the same tokens.
 
 The JSON line reports decode tokens/s, ms/step, the HBM roofline of the step
 (algorithmic bytes per step / measured step time against 8 TB/s) and the CPU
@@ -77,12 +77,6 @@ def measured_traffic(workload: str, unfused: bool):
     with open(path) as f:
         data = json.load(f)
     return data.get("bytes_per_launch"), data.get("positions")
-
-
-def sampled_steps(total: int, count: int):
-    """`count` step indices (0-based, of `total`) spread evenly, each the
-    middle of its share."""
-    return sorted({int((i + 0.5) * total / count) for i in range(count)})
 
 
 def host_description():
@@ -367,37 +361,29 @@ def bench_single(args, w):
     check_watchdog(decoder, "warm-up")
 
     contiguous = args.steps == total
-    timed = list(range(total)) if contiguous else sampled_steps(total, args.steps)
+    # The timed steps: the whole sequence, or --steps consecutive steps from
+    # its middle, one event pair around them (an event pair around each of a
+    # few scattered steps would add the events' own cost to every step).
+    first_timed = (total - args.steps) // 2
+    timed = list(range(first_timed, first_timed + args.steps))
 
     def timed_run():
         """One whole sequence; returns (ms per timed step, tokens, host s, enqueue s)."""
         open_sequence()
         torch.cuda.synchronize()
         host0 = time.perf_counter()
-        if contiguous:
-            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record()
-            for j in range(1, total + 1):
-                one_step(j)
-            stop.record()
-            events = [(start, stop)]
-        else:
-            wanted = set(timed)
-            events = []
-            for j in range(1, total + 1):
-                if j - 1 in wanted:
-                    pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                    pair[0].record()
-                    one_step(j)
-                    pair[1].record()
-                    events.append(pair)
-                else:
-                    one_step(j)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for j in range(1, total + 1):
+            if j - 1 == timed[0]:
+                start.record()
+            one_step(j)
+            if j - 1 == timed[-1]:
+                stop.record()
         enqueue = time.perf_counter() - host0
         torch.cuda.synchronize()
         host = time.perf_counter() - host0
         check_watchdog(decoder, "timed region")
-        gpu_ms = sum(a.elapsed_time(b) for a, b in events)
+        gpu_ms = start.elapsed_time(stop)
         return gpu_ms / args.steps, slots[base:base + total + 1].cpu().numpy().tolist(), host, enqueue
 
     print(f"[bench] timed region: {args.runs} runs", file=sys.stderr, flush=True)
@@ -423,7 +409,7 @@ def bench_single(args, w):
         baseline, parity = cpu_baseline(shape, decoder_file, encoder, prompt, gpu_tokens, args.cpu_budget)
 
     sampling = ("every step" if contiguous else
-                f"{args.steps} steps spread evenly over the {total}, each bracketed by HIP events")
+                f"{args.steps} consecutive steps from the middle of the {total}, one HIP event pair around them")
     line = {
         "metric": METRIC,
         "value": round(1e3 / ms_per_step, 2),
@@ -443,8 +429,7 @@ def bench_single(args, w):
                                f"(timed: {sampling})",
                    "path": "per-op kernel sequence" if args.unfused else "fused single-token step",
                    "global_batch": 1, "seq_len": base + total, "parallelism": "none (one GPU)",
-                   "timed_positions": f"{positions[0]}..{positions[-1]}" if contiguous
-                   else positions},
+                   "timed_positions": f"{positions[0]}..{positions[-1]}"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_positions": traffic_positions,
