@@ -1814,6 +1814,8 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
         sh.best_i[rg] = best_i;
     }
     __syncthreads();
+    STEP_LAYER(0);
+    STEP_MARK(37); // every row group of this workgroup done with the logits
     if (threadIdx.x < kKeyLanes)
     {
         // The row groups' candidates (at most 16: rows of 32 or 64 lanes) in
@@ -1844,6 +1846,7 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
             },
             sh.comb, epoch, a.status, sh))
         return;
+    STEP_MARK(38); // every workgroup's candidate arrived
     if (threadIdx.x < kWave)
     {
         float bv = 0.f;

@@ -36,6 +36,7 @@ FINAL_IN, LOGITS_DONE, ARGMAX_DONE, TABLE_DONE = 18, 19, 20, 21
 # weighted sums' folds, after the barrier) and each projection (after the dot
 # products, after the partial sums' barrier and the stores).
 ATT_MAX, ATT_FOLDED, ATT_BARRIER = 22, 23, 24
+LOGITS_ALL, CANDIDATES_IN = 37, 38 # every row group of a workgroup done; the fold's poll done
 QKV_DOT, OUT_DOT, XQ_DOT, XOUT_DOT, FC1_DOT, FC2_DOT = 25, 27, 29, 31, 33, 35
 EVENTS, LAYER_SLOTS = 40, 33
 TICK_US = 0.01  # 100 MHz
@@ -129,6 +130,11 @@ def step_table(stamps, layers):
         "final h -> every workgroup": np.median(t[everyone, FINAL_IN, 0]) - np.max(t[r["row"], FC2_DONE, layers - 1]),
         "final LayerNorm + tied logits": np.median(t[everyone, LOGITS_DONE, 0] - t[everyone, FINAL_IN, 0]),
         "slowest logits workgroup": np.max(t[everyone, LOGITS_DONE, 0] - t[everyone, FINAL_IN, 0]),
+        "row groups' imbalance (last row group of a workgroup, median)": np.median(
+            t[everyone, LOGITS_ALL, 0] - t[everyone, LOGITS_DONE, 0]),
+        "last workgroup done -> fold sees every candidate": float(np.max(t[:, CANDIDATES_IN, 0]))
+        - np.max(t[everyone, LOGITS_ALL, 0]),
+        "fold -> token written": float(np.max(t[:, ARGMAX_DONE, 0])) - float(np.max(t[:, CANDIDATES_IN, 0])),
         "argmax fold (last candidate -> token)": float(np.max(t[:, ARGMAX_DONE, 0]))
         - np.max(t[everyone, LOGITS_DONE, 0]),
     }
