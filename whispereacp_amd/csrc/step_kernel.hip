@@ -98,6 +98,19 @@ constexpr int kTimelineEvents = 40, kTimelineLayers = 33;
     } while (0)
 #endif
 
+// A workgroup-uniform pointer as a value the compiler knows to be uniform, so
+// it lives in a scalar register pair (a load's saddr operand, with a 32-bit
+// per-lane offset beside it). readfirstlane returns a signed int: each half
+// goes through uint32_t so it is zero-extended.
+template <class T>
+__device__ __forceinline__ T* uniform(T* p)
+{
+    const uint64_t at = reinterpret_cast<uint64_t>(p);
+    const uint32_t high = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (at >> 32));
+    const uint32_t low = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) at);
+    return reinterpret_cast<T*>(((uint64_t) high << 32) | (uint64_t) low);
+}
+
 // ---------------------------------------------------------------------------
 // Exchange words
 // ---------------------------------------------------------------------------
@@ -227,6 +240,105 @@ struct Shared
 // anywhere else.
 static_assert(kPollThreads == kThreads - kWave, "wave 0 does not poll");
 
+// One polling thread's wait for P exchange words (word k at base +
+// offset_of(k), a valid offset for every k; the set bits of `pending` name the
+// words it waits for) to carry `epoch`; deliver(k, value) receives each
+// awaited word's float once. The first round of loads is examined alone: a
+// word that was there before the consumer asked costs one trip. After a miss
+// two rounds are in flight at once, the second issued kPollStagger sleep units
+// (64 clocks each) after the first, and each is issued again as soon as it has
+// been examined, so a word is seen about half a trip after it lands instead of
+// up to a whole trip. Every round loads all P words, so the number of loads in
+// flight is fixed and the compiler's wait for the older round is exact.
+// Returns false when the watchdog tripped here or anywhere else.
+#ifndef WSP_POLL_STAGGER
+#define WSP_POLL_STAGGER 3
+#endif
+#ifndef WSP_POLL_TWO_MAX
+#define WSP_POLL_TWO_MAX 1
+#endif
+constexpr int kPollStagger = WSP_POLL_STAGGER;
+constexpr int kPollTwoMax = WSP_POLL_TWO_MAX; // the most words per thread polled with two rounds in flight
+
+template <int P, class Offset>
+__device__ __forceinline__ void issue_round(uint64_t (&w)[P], const uint64_t* base, const Offset& offset_of)
+{
+#pragma unroll
+    for (int k = 0; k < P; ++k)
+        w[k] = peek(base + offset_of(k));
+}
+
+template <int P, class Deliver>
+__device__ __forceinline__ bool take_round(const uint64_t (&w)[P], uint32_t& pending, uint32_t epoch,
+                                           const Deliver& deliver)
+{
+#pragma unroll
+    for (int k = 0; k < P; ++k)
+        if ((pending & (1u << k)) && (uint32_t) (w[k] >> 32) == epoch)
+        {
+            deliver(k, __uint_as_float((uint32_t) w[k]));
+            pending &= ~(1u << k);
+        }
+    return pending == 0;
+}
+
+// The watchdog, every 32 turns of a poll loop: false when this poll gave up
+// or another one did.
+__device__ __forceinline__ bool watchdog_ok(int spins, int limit, int* status)
+{
+    if ((spins & 31) != 0)
+        return true;
+    if (spins > limit)
+    {
+        __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+    }
+    return __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
+}
+
+template <int P, bool TWO, class Offset, class Deliver>
+__device__ __forceinline__ bool poll_words(const uint64_t* base, const Offset& offset_of, uint32_t pending,
+                                           uint32_t epoch, int* status, const Deliver& deliver)
+{
+    if (pending == 0)
+        return true;
+    uint64_t first[P];
+    issue_round(first, base, offset_of);
+    if (take_round(first, pending, epoch, deliver))
+        return true;
+    if constexpr (!TWO)
+    {
+        // One round in flight where two would not fit in registers.
+        for (int spins = 1;; ++spins)
+        {
+            issue_round(first, base, offset_of);
+            if (take_round(first, pending, epoch, deliver))
+                return true;
+            if (!watchdog_ok(spins, kSpinLimit, status))
+                return false;
+        }
+    }
+    else
+    {
+        uint64_t second[P];
+        issue_round(first, base, offset_of);
+        if constexpr (kPollStagger > 0)
+            asm volatile("s_sleep %0" ::"n"(kPollStagger) : "memory");
+        issue_round(second, base, offset_of);
+        for (int spins = 1;; ++spins)
+        {
+            if (take_round(first, pending, epoch, deliver))
+                return true;
+            issue_round(first, base, offset_of);
+            if (take_round(second, pending, epoch, deliver))
+                return true;
+            issue_round(second, base, offset_of);
+            if (!watchdog_ok(spins, kSpinLimit / 2, status))
+                return false;
+        }
+    }
+}
+
 template <int P, class Map>
 __device__ __forceinline__ bool poll(const uint64_t* base, int n, Map map, float* dst, uint32_t epoch, int* status,
                                      Shared& sh)
@@ -234,8 +346,11 @@ __device__ __forceinline__ bool poll(const uint64_t* base, int n, Map map, float
     bool failed = false;
     if (threadIdx.x < kWave)
         __builtin_amdgcn_s_waitcnt(0); // every counter at zero: this wave's stores and loads are done
-    else
+    else if constexpr (P > kPollTwoMax)
     {
+        // Wide gathers (attention partials, the argmax candidates): each round
+        // loads only the words still awaited and stores each as it arrives
+        // (fewer registers than the fixed rounds below).
         const int t = threadIdx.x - kWave;
         uint32_t pending = 0;
 #pragma unroll
@@ -245,8 +360,7 @@ __device__ __forceinline__ bool poll(const uint64_t* base, int n, Map map, float
             if (t + k * kPollThreads < n && map(t + k * kPollThreads, offset, index))
                 pending |= 1u << k;
         }
-        int spins = 0;
-        while (pending != 0)
+        for (int spins = 1; pending != 0; ++spins)
         {
             uint64_t w[P];
 #pragma unroll
@@ -266,21 +380,36 @@ __device__ __forceinline__ bool poll(const uint64_t* base, int n, Map map, float
                     dst[index] = __uint_as_float((uint32_t) w[k]);
                     pending &= ~(1u << k);
                 }
-            if (pending != 0 && (++spins & 63) == 0)
+            if (pending != 0 && !watchdog_ok(spins, kSpinLimit, status))
             {
-                if (spins > kSpinLimit)
-                {
-                    __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    failed = true;
-                    break;
-                }
-                if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
-                {
-                    failed = true;
-                    break;
-                }
+                failed = true;
+                break;
             }
         }
+    }
+    else
+    {
+        const int t = threadIdx.x - kWave;
+        uint32_t pending = 0;
+#pragma unroll
+        for (int k = 0; k < P; ++k)
+        {
+            int offset, index;
+            if (t + k * kPollThreads < n && map(t + k * kPollThreads, offset, index))
+                pending |= 1u << k;
+        }
+        failed = !poll_words<P, true>(
+            base,
+            [&](int k) {
+                int offset, index;
+                return t + k * kPollThreads < n && map(t + k * kPollThreads, offset, index) ? offset : 0;
+            },
+            pending, epoch, status,
+            [&](int k, float v) {
+                int offset, index;
+                map(t + k * kPollThreads, offset, index);
+                dst[index] = v;
+            });
     }
     if (failed)
         sh.abort = 1;
@@ -362,13 +491,7 @@ __device__ __forceinline__ bool gather_words(const uint64_t* base, int rows, int
                                              uint32_t epoch, int* status, Shared& sh)
 {
     static_assert(P == 8, "the poll statement below names eight loads");
-    // The base as a value the compiler knows to be uniform, so it lives in a
-    // scalar register pair (the loads' saddr operand). readfirstlane returns
-    // a signed int: each half goes through uint32_t so it is zero-extended.
-    const uint64_t at = reinterpret_cast<uint64_t>(base);
-    const uint32_t high = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (at >> 32));
-    const uint32_t low = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) at);
-    const uint64_t scalar_base = ((uint64_t) high << 32) | (uint64_t) low;
+    const uint64_t scalar_base = reinterpret_cast<uint64_t>(uniform(base));
     const int slots = stride << log2_block;
     const int mask = (1 << log2_block) - 1;
     for (int first = 0; first < slots; first += P * kPollThreads)
@@ -670,35 +793,16 @@ __device__ __forceinline__ bool gather_fold(const uint64_t* base, int rows, int 
             }
             const uint32_t valid = pending;
             float got[kPollBlocked] = {};
-            int spins = 0;
-            while (pending != 0)
+            if (!poll_words<kPollBlocked, true>(
+                    base,
+                    [&](int k) {
+                        const int slot = fold_slot(t, c * kPollBlocked + k);
+                        return slot < slots ? slot : 0;
+                    },
+                    pending, epoch, status, [&](int k, float v) { got[k] = v; }))
             {
-                uint64_t w[kPollBlocked];
-#pragma unroll
-                for (int k = 0; k < kPollBlocked; ++k)
-                    if (pending & (1u << k))
-                        w[k] = peek(base + fold_slot(t, c * kPollBlocked + k));
-#pragma unroll
-                for (int k = 0; k < kPollBlocked; ++k)
-                    if ((pending & (1u << k)) && (uint32_t) (w[k] >> 32) == epoch)
-                    {
-                        got[k] = __uint_as_float((uint32_t) w[k]);
-                        pending &= ~(1u << k);
-                    }
-                if (pending != 0 && (++spins & 63) == 0)
-                {
-                    if (spins > kSpinLimit)
-                    {
-                        __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        failed = true;
-                        break;
-                    }
-                    if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
-                    {
-                        failed = true;
-                        break;
-                    }
-                }
+                failed = true;
+                break;
             }
             // In slot order: the stores into the row and the two sums.
 #pragma unroll
@@ -828,16 +932,19 @@ __device__ __forceinline__ bool phase_task(const PhaseShape& ps, int group, int 
 }
 
 // Loads chunks [first, last) of `row` (lane l taking first + l + 32 i); lanes
-// past `last` load the run's first chunk again.
+// past `last` load the run's first chunk again. The matrix base is uniform
+// and every byte offset fits 32 bits (a matrix is far below 4 GiB), so each
+// load takes a scalar base and one 32-bit offset register.
 __device__ __forceinline__ void load_run(RowLoad& r, const void* weight, int row, int row_bytes, int first, int last)
 {
     const int lane = threadIdx.x & (kRowLanes - 1);
-    const char* base = static_cast<const char*>(weight) + (size_t) row * row_bytes;
+    const char* base = uniform(static_cast<const char*>(weight));
+    const uint32_t row_offset = (uint32_t) row * (uint32_t) row_bytes;
 #pragma unroll
     for (int i = 0; i < kChunks; ++i)
     {
         const int c = first + lane + kRowLanes * i;
-        r.w[i] = load_global16(base + (size_t) (c < last ? c : first) * 16);
+        r.w[i] = load_global16(base + (row_offset + (uint32_t) (c < last ? c : first) * 16u));
     }
 }
 
@@ -1061,13 +1168,16 @@ __device__ __forceinline__ void load_keys(KeyRows<NP>& kr, const float* keys, co
 {
     const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
     const int channel = 4 * kl < head_width ? 4 * kl : 0;
+    // Uniform bases and 32-bit element offsets (a cache is far below 4 GiB).
+    const float* kb = uniform(keys);
+    const float* vb = uniform(values);
 #pragma unroll
     for (int p = 0; p < NP; ++p)
     {
         const int key = ks + kKeySlots * p;
-        const size_t at = (size_t) (first + (key < count ? key : 0)) * width + column + channel;
-        kr.k[p] = *global(reinterpret_cast<const float4v*>(keys + at));
-        kr.v[p] = *global(reinterpret_cast<const float4v*>(values + at));
+        const uint32_t at = (uint32_t) (first + (key < count ? key : 0)) * (uint32_t) width + (uint32_t) (column + channel);
+        kr.k[p] = *global(reinterpret_cast<const float4v*>(kb + at));
+        kr.v[p] = *global(reinterpret_cast<const float4v*>(vb + at));
     }
 }
 
@@ -1324,13 +1434,14 @@ __device__ __forceinline__ void load_logit_row(RowLoad& r, float& mask, const St
     const int row = logit_row(s, j);
     const bool valid = row < a.vocabulary;
     const int lane = threadIdx.x & ((1 << s.lanes_log2) - 1);
-    const char* base = static_cast<const char*>(a.logits_weight) + (size_t) (valid ? row : 0) * s.row_bytes;
+    const char* base = uniform(static_cast<const char*>(a.logits_weight));
+    const uint32_t row_offset = (uint32_t) (valid ? row : 0) * (uint32_t) s.row_bytes;
     const int last = valid ? s.chunks : 1;
 #pragma unroll
     for (int i = 0; i < kChunks; ++i)
     {
         const int c = lane + (i << s.lanes_log2);
-        r.w[i] = load_global16(base + (size_t) (c < last ? c : 0) * 16);
+        r.w[i] = load_global16(base + (row_offset + (uint32_t) (c < last ? c : 0) * 16u));
     }
     // Issued with or without a mask (then a weight word, dropped), so every
     // path has the same number of loads in flight.
