@@ -251,14 +251,13 @@ static_assert(kPollThreads == kThreads - kWave, "wave 0 does not poll");
 // up to a whole trip. Every round loads all P words, so the number of loads in
 // flight is fixed and the compiler's wait for the older round is exact.
 // Returns false when the watchdog tripped here or anywhere else.
-#ifndef WSP_POLL_STAGGER
-#define WSP_POLL_STAGGER 3
-#endif
-#ifndef WSP_POLL_TWO_MAX
-#define WSP_POLL_TWO_MAX 1
-#endif
-constexpr int kPollStagger = WSP_POLL_STAGGER;
-constexpr int kPollTwoMax = WSP_POLL_TWO_MAX; // the most words per thread polled with two rounds in flight
+// Two rounds pay where few workgroups wait for a few words (a head group for
+// its q/k/v rows, a cross task for its query, a combining workgroup for its
+// head's partials); where every row group polls a whole vector the second
+// round's loads slow the hand-over more than they shorten it, so those gathers
+// keep one round in flight.
+constexpr int kPollStagger = 3;  // sleep units between the two rounds
+constexpr int kPollTwoMax = 1;   // poll<P> with P at most this takes two rounds by default
 
 template <int P, class Offset>
 __device__ __forceinline__ void issue_round(uint64_t (&w)[P], const uint64_t* base, const Offset& offset_of)
@@ -339,14 +338,14 @@ __device__ __forceinline__ bool poll_words(const uint64_t* base, const Offset& o
     }
 }
 
-template <int P, class Map>
+template <int P, class Map, bool TWO = (P <= kPollTwoMax)>
 __device__ __forceinline__ bool poll(const uint64_t* base, int n, Map map, float* dst, uint32_t epoch, int* status,
                                      Shared& sh)
 {
     bool failed = false;
     if (threadIdx.x < kWave)
         __builtin_amdgcn_s_waitcnt(0); // every counter at zero: this wave's stores and loads are done
-    else if constexpr (P > kPollTwoMax)
+    else if constexpr (!TWO)
     {
         // Wide gathers (attention partials, the argmax candidates): each round
         // loads only the words still awaited and stores each as it arrives
@@ -418,12 +417,15 @@ __device__ __forceinline__ bool poll(const uint64_t* base, int n, Map map, float
 }
 
 // n contiguous words.
-template <int P>
+template <int P, bool TWO = (P <= kPollTwoMax)>
 __device__ __forceinline__ bool gather(const uint64_t* src, int n, float* dst, uint32_t epoch, int* status,
                                        Shared& sh)
 {
-    return poll<P>(src, n, [](int i, int& offset, int& index) { offset = index = i; return true; }, dst, epoch,
-                   status, sh);
+    auto map = [](int i, int& offset, int& index) {
+        offset = index = i;
+        return true;
+    };
+    return poll<P, decltype(map), TWO>(src, n, map, dst, epoch, status, sh);
 }
 
 // n <= kMaxCombine contiguous words, polled with as few slots per thread as
@@ -793,7 +795,7 @@ __device__ __forceinline__ bool gather_fold(const uint64_t* base, int rows, int 
             }
             const uint32_t valid = pending;
             float got[kPollBlocked] = {};
-            if (!poll_words<kPollBlocked, true>(
+            if (!poll_words<kPollBlocked, false>(
                     base,
                     [&](int k) {
                         const int slot = fold_slot(t, c * kPollBlocked + k);
@@ -1836,8 +1838,10 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
         if (index < H)
         {
             const int parts = a.cross_splits;
-            if (!gather_any(ex + a.off_xpart + (size_t) head * parts * (hd + 2), parts * (hd + 2), sh.comb,
-                                      epoch, a.status, sh))
+            const uint64_t* src = ex + a.off_xpart + (size_t) head * parts * (hd + 2);
+            const int n = parts * (hd + 2);
+            if (!(n <= 2 * kPollThreads ? gather<2, true>(src, n, sh.comb, epoch, a.status, sh)
+                                        : gather_any(src, n, sh.comb, epoch, a.status, sh)))
                 return false;
             STEP_STAMP(16, l);
             combine_parts(sh.comb, parts, hd, ex + a.off_xattn + head * hd, epoch, sh);
@@ -1948,14 +1952,7 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
     // its polls would wait for those stores' acknowledgements.
     if (blockIdx.x != gridDim.x - 1 || a.argmax_out == nullptr)
         return;
-    if (!poll<kPollArgmax>(
-            a.exchange + a.off_argmax, 2 * G,
-            [](int i, int& offset, int& index) {
-                offset = i;
-                index = i;
-                return true;
-            },
-            sh.comb, epoch, a.status, sh))
+    if (!gather<kPollArgmax, false>(a.exchange + a.off_argmax, 2 * G, sh.comb, epoch, a.status, sh))
         return;
     STEP_MARK(38); // every workgroup's candidate arrived
     if (threadIdx.x < kWave)
