@@ -58,12 +58,11 @@ public:
     void step(Pass& pass, const BufferRange& tokens, int tokenCount, const DecoderWeights& weights,
               const BufferRange& logits);
 
-    // The fused single-token path: on by default when the weights allow it.
-    // A step of up to fusedPromptTokens tokens (the transcript prompt) runs as
-    // that many fused launches, one token each: on MI355X two tokens take 188
-    // us that way at the tiny.en shape against 402 us for the recorded
-    // sequence, four 376 against 531 (small: 560 / 1258, 1120 / 1568).
-    static constexpr int fusedPromptTokens = 4;
+    // The fused path: on by default when the weights allow it. A step of up
+    // to fusedPromptTokens tokens runs as persistent launches of up to four
+    // tokens each (wsp_hip_decoder_step_tokens), whose rows share every
+    // weight read; longer steps run the recorded sequence.
+    static constexpr int fusedPromptTokens = 16;
     void setFusedSteps(bool enabled) { fusedSteps = enabled; }
     bool usesFusedStep(const DecoderWeights& weights, int tokenCount) const;
 
@@ -83,9 +82,10 @@ public:
 private:
     void requireMatchingWeights(const DecoderWeights& weights) const;
     void requireRoomFor(int tokenCount) const;
-    // One fused token: tokens[row] in, logits row `row` and hidden row `row` out.
-    void fusedStep(Pass& pass, const BufferRange& tokens, const DecoderWeights& weights,
-                   const BufferRange& logits, const float* mask, const BufferRange* argmaxSlot, int row = 0);
+    // tokenCount fused tokens: their logits and hidden rows out, the argmax of
+    // the last row into argmaxSlot when given.
+    void fusedStep(Pass& pass, const BufferRange& tokens, int tokenCount, const DecoderWeights& weights,
+                   const BufferRange& logits, const float* mask, const BufferRange* argmaxSlot);
 
     DecoderShape decoderShape;
     int decodedPositions = 0;

@@ -198,6 +198,19 @@ int wsp_hip_decoder_step(wsp_hip_ctx* ctx, const wsp_decoder_tensors* tensors,
                          const uint32_t* tokens, int position, int cross_rows, float* hidden,
                          float* logits, const float* mask, uint32_t* argmax_out);
 
+/* A step of token_count tokens at position .. position + token_count - 1
+ * (Decoder::step, Decoder/Decoder.cpp:270-308 with tokenCount tokens, and
+ * the causal self attention of Kernels/Attention.h:34-47): token i sees the
+ * keys of every token before it. hidden receives [token_count, width] and
+ * logits [token_count, vocab]; with argmax_out non-null the masked argmax of
+ * the last row lands there. On the persistent path a launch carries up to
+ * four tokens (fewer where the shape leaves fewer head groups per token), so
+ * their rows share each weight read; a step is as many launches as that
+ * takes. Otherwise each token runs the per-op sequence. */
+int wsp_hip_decoder_step_tokens(wsp_hip_ctx* ctx, const wsp_decoder_tensors* tensors,
+                                const uint32_t* tokens, int token_count, int position, int cross_rows,
+                                float* hidden, float* logits, const float* mask, uint32_t* argmax_out);
+
 /* Whether wsp_hip_decoder_step runs as the one persistent launch on this
  * context (1) or falls back to the per-op sequence (0) because the shape or
  * device is outside the persistent kernel's capacities. No reference

@@ -106,6 +106,8 @@ SIGNATURES = {
                                          c_void_p, c_void_p]),
     "wsp_hip_decoder_step": (c_int, [c_void_p, ctypes.POINTER(wsp_decoder_tensors), c_void_p, c_int, c_int,
                                      c_void_p, c_void_p, c_void_p, c_void_p]),
+    "wsp_hip_decoder_step_tokens": (c_int, [c_void_p, ctypes.POINTER(wsp_decoder_tensors), c_void_p, c_int, c_int,
+                                            c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
     "wsp_hip_step_persistent": (c_int, [c_void_p]),
     "wsp_hip_device_status": (c_int, [c_void_p, ctypes.POINTER(c_int), c_int]),
     "wsp_hip_device_status_copy": (c_int, [c_void_p, ctypes.POINTER(c_int)]),

@@ -110,7 +110,8 @@ struct FusedState
     int row_groups = 0;
     int self_split_max = 0;
     int cross_split_max = 0;
-    int layer_words = 0;
+    int max_tokens = 1; // tokens one launch may carry (head groups for every (token, head) pair)
+    int token_words = 0, layer_words = 0;
     int off_qkv = 0, off_self = 0, off_h2 = 0, off_xq = 0, off_xpart = 0, off_xattn = 0, off_h3 = 0, off_ff = 0,
         off_h4 = 0, off_argmax = 0;
     int log2_qkv = 0, log2_d = 0, log2_f = 0;
@@ -299,13 +300,15 @@ void plan_persistent(Context* ctx, FusedState* st)
 
     // Every kernel variant must fit one workgroup per CU.
     for (int wt : {WSP_F32, WSP_F16, WSP_BF16})
-    {
-        int blocks = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, step::kernel_for(wt), step::kThreads, 0)
-                != hipSuccess
-            || blocks < 1)
-            return refuse("the persistent kernel does not fit a CU");
-    }
+        for (bool multi : {false, true})
+        {
+            int blocks = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, step::kernel_for(wt, multi), step::kThreads,
+                                                             0)
+                    != hipSuccess
+                || blocks < 1)
+                return refuse("the persistent kernel does not fit a CU");
+        }
 
     // Producer blocks: a row group's rows of a phase, rounded up to a power of two.
     auto block_log2 = [&](int rows) {
@@ -333,9 +336,13 @@ void plan_persistent(Context* ctx, FusedState* st)
     st->off_h3 = at, at += block_d;
     st->off_ff = at, at += row_groups << st->log2_f;
     st->off_h4 = at, at += block_d;
-    st->layer_words = at;
-    st->off_argmax = at * s.layers;
-    st->exchange_words = (size_t) at * s.layers + 16 * G;
+    // Every layer holds kMaxTokens token blocks, so a multi-token launch
+    // writes each token's words where a single-token launch writes token 0's.
+    st->token_words = at;
+    st->layer_words = step::kMaxTokens * at;
+    st->off_argmax = st->layer_words * s.layers;
+    st->exchange_words = (size_t) st->layer_words * s.layers + 16 * G;
+    st->max_tokens = std::max(1, std::min(step::kMaxTokens, (G - row_groups) / H));
     st->persistent = true;
 }
 
@@ -405,8 +412,10 @@ bool aligned16(const void* p)
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
 }
 
+// `count` tokens (1, or up to st->max_tokens with the multi-token kernel) at
+// position .. position + count - 1.
 int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* tensors, const uint32_t* tokens,
-                    int position, int cross_rows, float* hidden, float* logits, const float* mask,
+                    int count, int position, int cross_rows, float* hidden, float* logits, const float* mask,
                     uint32_t* argmax_out)
 {
     const wsp_decoder_shape& s = ctx->shape;
@@ -458,6 +467,10 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     cross_splits = ceil_div(cross_rows, cross_chunk);
     if (cross_chunk > step::kCrossKeys || self_splits > st->self_split_max)
         return context_fail(ctx, WSP_ERR_CAPACITY, "decoder step: attention split past the planned capacity");
+    if (count > 1
+        && (count > st->max_tokens || position + count > step::kSelfKeys
+            || count * cross_splits * (hd + 2) > step::kMaxCombine))
+        return context_fail(ctx, WSP_ERR_LOGIC, "decoder step: tokens past the multi-token kernel's capacity");
 
     step::StepArgs a {};
     a.layers = st->table;
@@ -482,6 +495,7 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     a.logits_wdtype = tensors->logits_wdtype;
     a.position = position;
     a.cross_rows = cross_rows;
+    a.token_count = count;
     a.row_groups = st->row_groups;
     a.self_splits = self_splits;
     a.cross_splits = cross_splits;
@@ -499,6 +513,7 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     a.off_h3 = st->off_h3;
     a.off_ff = st->off_ff;
     a.off_h4 = st->off_h4;
+    a.token_words = st->token_words;
     a.layer_words = st->layer_words;
     a.off_argmax = st->off_argmax;
     a.log2_qkv = st->log2_qkv;
@@ -525,9 +540,10 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     static const bool cooperative =
         getenv("WSP_STEP_LAUNCH") != nullptr && strcmp(getenv("WSP_STEP_LAUNCH"), "cooperative") == 0;
     const hipError_t e = cooperative
-                             ? hipLaunchCooperativeKernel(step::kernel_for(tensors->wdtype), dim3(st->workgroups),
-                                                          dim3(step::kThreads), args, 0, ctx->stream)
-                             : hipLaunchKernel(step::kernel_for(tensors->wdtype), dim3(st->workgroups),
+                             ? hipLaunchCooperativeKernel(step::kernel_for(tensors->wdtype, count > 1),
+                                                          dim3(st->workgroups), dim3(step::kThreads), args, 0,
+                                                          ctx->stream)
+                             : hipLaunchKernel(step::kernel_for(tensors->wdtype, count > 1), dim3(st->workgroups),
                                                dim3(step::kThreads), args, 0, ctx->stream);
     if (e == hipSuccess && a.host_pair != nullptr)
     {
@@ -697,8 +713,62 @@ extern "C" int wsp_hip_decoder_step(wsp_hip_ctx* ctx, const wsp_decoder_tensors*
 
     auto* st = static_cast<FusedState*>(ctx->fused);
     if (st->persistent)
-        return persistent_step(ctx, st, tensors, tokens, position, cross_rows, hidden, logits, mask, argmax_out);
+        return persistent_step(ctx, st, tensors, tokens, 1, position, cross_rows, hidden, logits, mask, argmax_out);
     return per_op_step(ctx, st, tensors, tokens, position, cross_rows, hidden, logits, mask, argmax_out);
+}
+
+extern "C" int wsp_hip_decoder_step_tokens(wsp_hip_ctx* ctx, const wsp_decoder_tensors* tensors,
+                                           const uint32_t* tokens, int token_count, int position, int cross_rows,
+                                           float* hidden, float* logits, const float* mask, uint32_t* argmax_out)
+{
+    using namespace wsp;
+    if (ctx == nullptr)
+        return WSP_ERR_ARGUMENT;
+    if (tensors == nullptr || tensors->layers == nullptr || tokens == nullptr || hidden == nullptr
+        || logits == nullptr || token_count <= 0)
+        return context_fail(ctx, WSP_ERR_ARGUMENT, "decoder step: null pointer or no tokens");
+    const wsp_decoder_shape& s = ctx->shape;
+    if (position < 0 || position + token_count > s.max_positions)
+        return context_fail(ctx, WSP_ERR_CAPACITY, "decoder step: position past the window");
+    if (cross_rows <= 0 || cross_rows > s.cross_positions)
+        return context_fail(ctx, WSP_ERR_CAPACITY, "decoder step: cross rows outside the encoder output");
+    const int head_width = s.width / s.heads;
+    if (head_width % 4 != 0 || head_width > ops::kMaxHeadWidth)
+        return context_fail(ctx, WSP_ERR_LOGIC, "decoder step: unsupported head width");
+
+    // Launches of as many tokens as the multi-token kernel takes at their
+    // position (one where the self keys would leave its key block, or the
+    // cross partials its combine capacity); each sees the keys the ones
+    // before it appended. Only the last launch writes the argmax.
+    auto* st = static_cast<FusedState*>(ctx->fused);
+    const size_t d = (size_t) s.width, V = (size_t) s.vocabulary_size;
+    int cross_splits = std::max(1, ceil_div(cross_rows, step::kCrossKeys));
+    if (st->persistent)
+        cross_splits = std::min(cross_splits, st->cross_split_max);
+    for (int done = 0; done < token_count;)
+    {
+        const int at = position + done;
+        int n = 1;
+        if (st->persistent)
+        {
+            n = std::min(token_count - done, st->max_tokens);
+            n = std::min(n, step::kMaxCombine / (cross_splits * (head_width + 2)));
+            if (at + n > step::kSelfKeys || (head_width & (head_width - 1)) != 0)
+                n = 1;
+            n = std::max(n, 1);
+        }
+        const bool last = done + n == token_count;
+        const int status =
+            st->persistent
+                ? persistent_step(ctx, st, tensors, tokens + done, n, at, cross_rows, hidden + done * d,
+                                  logits + done * V, last ? mask : nullptr, last ? argmax_out : nullptr)
+                : per_op_step(ctx, st, tensors, tokens + done, at, cross_rows, hidden + done * d, logits + done * V,
+                              last ? mask : nullptr, last ? argmax_out : nullptr);
+        if (status != WSP_OK)
+            return status;
+        done += n;
+    }
+    return WSP_OK;
 }
 
 extern "C" int wsp_hip_step_persistent(const wsp_hip_ctx* ctx)

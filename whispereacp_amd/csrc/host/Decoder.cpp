@@ -104,8 +104,7 @@ void Decoder::step(Pass& pass, const BufferRange& tokens, int tokenCount, const 
     {
         // Token i at position + i sees the keys of every token before it, as
         // the causal recorded step would (Kernels/Attention.h:34-47).
-        for (int i = 0; i < tokenCount; ++i)
-            fusedStep(pass, tokens, weights, logits, nullptr, nullptr, i);
+        fusedStep(pass, tokens, tokenCount, weights, logits, nullptr, nullptr);
         return;
     }
 
@@ -125,7 +124,7 @@ void Decoder::stepAndSample(Pass& pass, const BufferRange& tokens, const Decoder
     requireRoomFor(1);
     if (usesFusedStep(weights, 1))
     {
-        fusedStep(pass, tokens, weights, logits, mask, &argmaxSlot);
+        fusedStep(pass, tokens, 1, weights, logits, mask, &argmaxSlot);
         return;
     }
     step(pass, tokens, 1, weights, logits);
@@ -135,8 +134,8 @@ void Decoder::stepAndSample(Pass& pass, const BufferRange& tokens, const Decoder
         throwForStatus(status, wsp_hip_last_error(hipNet.context()));
 }
 
-void Decoder::fusedStep(Pass& pass, const BufferRange& tokens, const DecoderWeights& weights,
-                        const BufferRange& logits, const float* mask, const BufferRange* argmaxSlot, int row)
+void Decoder::fusedStep(Pass& pass, const BufferRange& tokens, int tokenCount, const DecoderWeights& weights,
+                        const BufferRange& logits, const float* mask, const BufferRange* argmaxSlot)
 {
     if (pass.hipStream() != wsp_hip_stream(hipNet.context()))
         throw std::logic_error("a decoder records into the stream it was prepared with");
@@ -154,21 +153,19 @@ void Decoder::fusedStep(Pass& pass, const BufferRange& tokens, const DecoderWeig
     }
     const wsp_decoder_tensors tensors = decoderTable(weights, fusedLayers);
 
-    const auto r = (std::size_t) row;
-    const int status = wsp_hip_decoder_step(
-        hipNet.context(), &tensors, static_cast<const uint32_t*>(tokens.data()) + r, decodedPositions,
-        activeCrossPositions, static_cast<float*>(normalisedRows->data()) + r * (std::size_t) decoderShape.width,
-        static_cast<float*>(logits.data()) + r * (std::size_t) decoderShape.vocabularySize, mask,
+    const int status = wsp_hip_decoder_step_tokens(
+        hipNet.context(), &tensors, static_cast<const uint32_t*>(tokens.data()), tokenCount, decodedPositions,
+        activeCrossPositions, static_cast<float*>(normalisedRows->data()), static_cast<float*>(logits.data()), mask,
         argmaxSlot != nullptr ? static_cast<uint32_t*>(argmaxSlot->data()) : nullptr);
     if (status != WSP_OK)
         throwForStatus(status, wsp_hip_last_error(hipNet.context()));
 
-    // The self caches now hold one more row; their Cache records follow.
+    // The self caches now hold the new rows; their Cache records follow.
     for (int l = 0; l < decoderShape.layers; ++l)
     {
-        caches.selfKeys[(std::size_t) l].rows = decodedPositions + 1;
-        caches.selfValues[(std::size_t) l].rows = decodedPositions + 1;
+        caches.selfKeys[(std::size_t) l].rows = decodedPositions + tokenCount;
+        caches.selfValues[(std::size_t) l].rows = decodedPositions + tokenCount;
     }
-    decodedPositions += 1;
+    decodedPositions += tokenCount;
 }
 } // namespace WSP

@@ -23,8 +23,10 @@ constexpr int kPollThreads = kThreads - 64; // threads that poll exchange words 
 constexpr int kPollBlocked = 2;        // slots per polling thread for a width-long vector, per chunk
 constexpr int kPollBlockedFF = 8;      // ... for the feed-forward vector
 constexpr int kFoldChunks = 2;         // chunks of kPollBlocked * kPollThreads slots a LayerNorm's input may span
+constexpr int kMaxTokens = 4;          // tokens one multi-token launch carries (their rows share each weight load)
 
-// Exchange words per layer, in this order (offsets in StepArgs):
+// Exchange words per token and layer, in this order (offsets in StepArgs; a
+// layer holds kMaxTokens such blocks, token_words apart):
 //   qkv [row_groups << log2_qkv] | self partials [self_split_max][heads][hd + 2]
 //   | h2 [row_groups << log2_d] | xq [row_groups << log2_d]
 //   | cross partials [heads][cross_split_max][hd + 2] | xattn [d]
@@ -52,6 +54,7 @@ struct StepArgs
 
     int width, heads, layer_count, feed_forward, vocabulary, logits_wdtype;
     int position, cross_rows;
+    int token_count;    // tokens of this launch (1 for the single-token kernel, else 1..kMaxTokens)
     int row_groups;     // workgroups [0, row_groups) run projections and cross chunks
     int self_splits;    // key splits per head for this position (<= self_split_max)
     int cross_splits;   // key chunks per head
@@ -61,7 +64,7 @@ struct StepArgs
     float inv_width; // 1 / width, the LayerNorm mean factor
 
     int off_qkv, off_self, off_h2, off_xq, off_xpart, off_xattn, off_h3, off_ff, off_h4;
-    int layer_words, off_argmax;
+    int token_words, layer_words, off_argmax;
     int log2_qkv, log2_d, log2_f; // producer block sizes of the row-group vectors
     uint64_t* timeline; // per-workgroup timestamps of a WSP_STEP_TIMELINE build (else unused)
 
@@ -96,6 +99,7 @@ inline FoldTermsLayout fold_terms_layout(int width, int feed_forward)
 // Longest projection row, in 16-byte chunks: 16 slices of 3 chunks per lane.
 constexpr int kMaxRowChunks = 16 * 32 * 3;
 
-// The kernel for this projection storage (the logits storage is an argument).
-const void* kernel_for(int wdtype);
+// The kernel for this projection storage (the logits storage is an argument),
+// carrying one token or up to kMaxTokens.
+const void* kernel_for(int wdtype, bool multi_token);
 } // namespace wsp::step

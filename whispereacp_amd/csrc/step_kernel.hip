@@ -208,20 +208,46 @@ __device__ __forceinline__ float max64(float v)
     return fmaxf(a, b);
 }
 
+// Per-token rows in LDS: token k's residual row at raw + k * kRawStride, its
+// head block (query, new key, new value) at q + k * kQStride, and element i
+// of its phase input at x + x_at<T>(k, i). The single-token kernel keeps that
+// input contiguous. With T tokens the inputs interleave in blocks of eight
+// floats, token k's block c at c * kXBlock<T> + 8 k: a lane's chunk then has
+// one address for every token (the tokens sit at immediate offsets of the LDS
+// instructions), and a pad of four floats per block spreads the lanes' reads
+// over the banks.
+constexpr int kRawStride = kMaxWidth;
+constexpr int kQStride = 3 * kMaxHeadWidth;
+template <int T>
+constexpr int kXBlock = T == 1 ? 8 : 8 * T + 4;
+constexpr int kXFloats = kMaxFeedForward / 8 * kXBlock<kMaxTokens>;
+static_assert(kMaxFeedForward % 8 == 0, "whole blocks");
+
+template <int T>
+__device__ __forceinline__ int x_at(int k, int i)
+{
+    if constexpr (T == 1)
+        return i;
+    else
+        return (i >> 3) * kXBlock<T> + 8 * k + (i & 7);
+}
+
+// The large per-token rows come last: every array's base then stays below
+// 64 KB, within the 16-bit offset of an LDS instruction, for token 0.
 struct Shared
 {
     wsp_layer_tensors table[kMaxLayers]; // the layer table, read once per launch
-    alignas(16) float raw[kMaxWidth];    // the residual stream as gathered (un-normalised)
-    alignas(16) float x[kMaxFeedForward]; // the current phase's input vector
     float comb[kMaxCombine];             // attention partials being combined
     float red[kWaves][kMaxHeadWidth];    // per-wave value rows of an attention chunk
-    float q[3 * kMaxHeadWidth];          // a head's query, then (self-attention) its new key and value
+    float q[kMaxTokens * kQStride];      // a head's query, then (self-attention) its new key and value
     float scratch[2][kWaves];            // per-wave maxima and sums of an attention chunk
-    float fold[kWaves][2];               // per-wave sums of (x - K) and (x - K)^2 of a folded LayerNorm
-    alignas(16) float part[kRowGroups];  // per-row-group partial sums of a projection pass
+    float fold[kWaves][kMaxTokens][2];   // per-wave sums of (x - K) and (x - K)^2 of a folded LayerNorm
+    alignas(16) float part[kMaxTokens * kRowGroups]; // per-row-group partial sums of a projection pass
     float best_v[kRowGroups];
     uint32_t best_i[kRowGroups];
     int abort;
+    alignas(16) float raw[kMaxTokens * kRawStride]; // the residual stream as gathered (un-normalised)
+    alignas(16) float x[kXFloats];                  // the current phase's input vectors
 #ifdef WSP_STEP_TIMELINE
     uint64_t timeline[kTimelineEvents][kTimelineLayers];
     int mark_layer;
@@ -488,9 +514,11 @@ __device__ __forceinline__ bool gather_blocked(const uint64_t* base, int rows, i
 // into the vector: a slot past it re-reads word 0 and is ignored.
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-template <int P>
+// place(index) is where element `index` goes in dst (the identity for one
+// token's contiguous row).
+template <int P, class Place>
 __device__ __forceinline__ bool gather_words(const uint64_t* base, int rows, int log2_block, int stride, float* dst,
-                                             uint32_t epoch, int* status, Shared& sh)
+                                             uint32_t epoch, int* status, Shared& sh, Place place)
 {
     static_assert(P == 8, "the poll statement below names eight loads");
     const uint64_t scalar_base = reinterpret_cast<uint64_t>(uniform(base));
@@ -537,7 +565,7 @@ __device__ __forceinline__ bool gather_words(const uint64_t* base, int rows, int
                     if ((pending & (1u << k)) && v[k][1] == epoch)
                     {
                         const int slot = first + t + k * kPollThreads;
-                        dst[(slot & mask) * stride + (slot >> log2_block)] = __uint_as_float(v[k][0]);
+                        dst[place((slot & mask) * stride + (slot >> log2_block))] = __uint_as_float(v[k][0]);
                         pending &= ~(1u << k);
                     }
                 if (pending != 0 && (++spins & 63) == 0)
@@ -617,17 +645,17 @@ __device__ __forceinline__ void load_norm(NormParams& p, const float* gamma, con
 }
 
 // The statistics and this wave's run, with R runs per lane (R * 256 >= n).
-template <int R>
-__device__ __forceinline__ void norm_row(const NormParams& p, int n, float inv_n, float eps, Shared& sh, int lane,
-                                         int own, int mark)
+template <int R, int XB>
+__device__ __forceinline__ void norm_row(const NormParams& p, int n, float inv_n, float eps, const float* raw,
+                                         float* out, int lane, int own, int mark, Shared& sh)
 {
     // Every LDS read is issued before the first is used: the row's runs and
     // this thread's own run.
     float4v v[R];
 #pragma unroll
     for (int k = 0; k < R; ++k)
-        v[k] = *reinterpret_cast<const float4v*>(&sh.raw[min(4 * (lane + kWave * k), n - 4)]);
-    const float4v x = *reinterpret_cast<const float4v*>(&sh.raw[min(own, n - 4)]);
+        v[k] = *reinterpret_cast<const float4v*>(&raw[min(4 * (lane + kWave * k), n - 4)]);
+    const float4v x = *reinterpret_cast<const float4v*>(&raw[min(own, n - 4)]);
     // Pairwise sums (a fixed order, shallow dependency chains; runs past the
     // row add zeros, so the order does not depend on R).
     float t[R];
@@ -657,14 +685,19 @@ __device__ __forceinline__ void norm_row(const NormParams& p, int n, float inv_n
 #pragma unroll
         for (int c = 0; c < 4; ++c)
             y[c] = (x[c] - mean) * scale * p.g[c] + p.b[c];
-        *reinterpret_cast<float4v*>(&sh.x[own]) = y;
+        // (own is a multiple of 4: its run sits inside one block of eight.)
+        *reinterpret_cast<float4v*>(&out[XB == 8 ? own : (own >> 3) * XB + (own & 7)]) = y;
     }
 }
 
-// inv_n = 1 / n (the row means are the sums times inv_n).
+// inv_n = 1 / n (the row means are the sums times inv_n); token k's row of
+// a T-token launch.
+template <int T = 1>
 __device__ __forceinline__ void layer_norm(const NormParams& p, int n, float inv_n, float eps, Shared& sh,
-                                           int mark = -1)
+                                           int mark = -1, int token = 0)
 {
+    const float* raw = sh.raw + token * kRawStride;
+    float* out = sh.x + x_at<T>(token, 0);
     const int lane = threadIdx.x & (kWave - 1);
     const int own = 4 * (lane + kWave * (int) (threadIdx.x / kWave)); // the run this wave writes
     // Only the waves that write a run compute the statistics; the others go
@@ -674,10 +707,10 @@ __device__ __forceinline__ void layer_norm(const NormParams& p, int n, float inv
         switch ((n + 4 * kWave - 1) / (4 * kWave))
         {
             case 1:
-            case 2: norm_row<2>(p, n, inv_n, eps, sh, lane, own, mark); break;
-            case 3: norm_row<3>(p, n, inv_n, eps, sh, lane, own, mark); break;
-            case 4: norm_row<4>(p, n, inv_n, eps, sh, lane, own, mark); break;
-            default: norm_row<kNormRuns>(p, n, inv_n, eps, sh, lane, own, mark); break;
+            case 2: norm_row<2, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
+            case 3: norm_row<3, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
+            case 4: norm_row<4, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
+            default: norm_row<kNormRuns, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
         }
     }
     __syncthreads();
@@ -748,36 +781,52 @@ __device__ __forceinline__ void load_fold(FoldParams& fp, const float* gamma, in
 }
 
 // Each wave's totals of the threads' sums into sh.fold (every lane of the
-// wave active); read after the next barrier.
-__device__ __forceinline__ void fold_reduce(const FoldSums& sums, Shared& sh)
+// wave active), per token; read after the next barrier.
+template <int T>
+__device__ __forceinline__ void fold_reduce(const FoldSums (&sums)[T], Shared& sh)
 {
-    const float s1 = sum64(sums.s1);
-    const float s2 = sum64(sums.s2);
-    if ((threadIdx.x & (kWave - 1)) == 0)
+#pragma unroll
+    for (int k = 0; k < T; ++k)
     {
-        sh.fold[threadIdx.x / kWave][0] = s1;
-        sh.fold[threadIdx.x / kWave][1] = s2;
+        const float s1 = sum64(sums[k].s1);
+        const float s2 = sum64(sums[k].s2);
+        if ((threadIdx.x & (kWave - 1)) == 0)
+        {
+            sh.fold[threadIdx.x / kWave][k][0] = s1;
+            sh.fold[threadIdx.x / kWave][k][1] = s2;
+        }
     }
 }
 
 // gather_blocked for a LayerNorm's input, the whole vector in chunks of
 // kPollBlocked * 448 slots: sh.raw[i] = x_i, sh.x[i] = gamma_i (x_i - shift),
 // and each wave's sums of (x_i - shift) and (x_i - shift)^2 over its slots (in
-// slot order, then a fixed tree) in sh.fold. Returns false, uniformly, when
-// the watchdog tripped.
-__device__ __forceinline__ bool gather_fold(const uint64_t* base, int rows, int log2_block, int stride,
-                                            const FoldParams& fp, float shift, uint32_t epoch, int* status,
-                                            Shared& sh)
+// slot order, then a fixed tree) in sh.fold. With T tokens the first `count`
+// tokens' vectors (token_words apart) are polled in the same rounds, each
+// against its own shift, into its own rows. Returns false, uniformly, when the
+// watchdog tripped.
+template <int T>
+__device__ __forceinline__ bool gather_fold(const uint64_t* base, int token_words, int count, int rows,
+                                            int log2_block, int stride, const FoldParams& fp, const float (&shift)[T],
+                                            uint32_t epoch, int* status, Shared& sh)
 {
     const int slots = stride << log2_block;
     const int mask = (1 << log2_block) - 1;
-    float s1 = 0.f, s2 = 0.f;
+    FoldSums sums[T];
+#pragma unroll
+    for (int k = 0; k < T; ++k)
+        sums[k] = {0.f, 0.f};
     bool failed = false;
     if (threadIdx.x < kWave)
         __builtin_amdgcn_s_waitcnt(0); // wave 0 stored the last phase's outputs: it only waits for them
     else
     {
-        const int t = threadIdx.x - kWave;
+        int t = threadIdx.x - kWave;
+        // With several tokens the slots' offsets and LDS addresses are
+        // recomputed at each call (a few VALU operations) rather than held
+        // across the layer loop, where they would not fit in registers.
+        if constexpr (T > 1)
+            asm volatile("" : "+v"(t));
 #pragma unroll
         for (int c = 0; c < kFoldChunks; ++c)
         {
@@ -791,52 +840,57 @@ __device__ __forceinline__ bool gather_fold(const uint64_t* base, int rows, int 
                 const int slot = fold_slot(t, c * kPollBlocked + k);
                 index[k] = (slot & mask) * stride + (slot >> log2_block);
                 if (slot < slots && index[k] < rows)
-                    pending |= 1u << k;
+#pragma unroll
+                    for (int tok = 0; tok < T; ++tok)
+                        if (T == 1 || tok < count)
+                            pending |= 1u << (tok * kPollBlocked + k);
             }
             const uint32_t valid = pending;
-            float got[kPollBlocked] = {};
-            if (!poll_words<kPollBlocked, false>(
+            float got[T * kPollBlocked] = {};
+            if (!poll_words<T * kPollBlocked, false>(
                     base,
-                    [&](int k) {
-                        const int slot = fold_slot(t, c * kPollBlocked + k);
-                        return slot < slots ? slot : 0;
+                    [&](int w) {
+                        const int slot = fold_slot(t, c * kPollBlocked + w % kPollBlocked);
+                        return (w / kPollBlocked) * token_words + (slot < slots ? slot : 0);
                     },
-                    pending, epoch, status, [&](int k, float v) { got[k] = v; }))
+                    pending, epoch, status, [&](int w, float v) { got[w] = v; }))
             {
                 failed = true;
                 break;
             }
             // In slot order: the stores into the row and the two sums.
 #pragma unroll
-            for (int k = 0; k < kPollBlocked; ++k)
-                if (valid & (1u << k))
-                {
-                    const float dx = got[k] - shift;
-                    sh.raw[index[k]] = got[k];
-                    sh.x[index[k]] = fp.gamma[c * kPollBlocked + k] * dx;
-                    s1 += dx;
-                    s2 += dx * dx;
-                }
+            for (int tok = 0; tok < T; ++tok)
+#pragma unroll
+                for (int k = 0; k < kPollBlocked; ++k)
+                    if (valid & (1u << (tok * kPollBlocked + k)))
+                    {
+                        const float value = got[tok * kPollBlocked + k];
+                        const float dx = value - shift[tok];
+                        sh.raw[tok * kRawStride + index[k]] = value;
+                        sh.x[x_at<T>(tok, index[k])] = fp.gamma[c * kPollBlocked + k] * dx;
+                        sums[tok].s1 += dx;
+                        sums[tok].s2 += dx * dx;
+                    }
         }
     }
-    fold_reduce({s1, s2}, sh);
+    fold_reduce<T>(sums, sh);
     if (failed)
         sh.abort = 1;
     __syncthreads();
     return sh.abort == 0;
 }
 
-
 // The statistics from the waves' sums (in wave order): rstd, and the mean
-// less the shift. Every thread computes the same values.
-__device__ __forceinline__ FoldStats fold_stats(const Shared& sh, float inv_n, float eps)
+// less the shift, of token k. Every thread computes the same values.
+__device__ __forceinline__ FoldStats fold_stats(const Shared& sh, int k, float inv_n, float eps)
 {
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w)
     {
-        s1 += sh.fold[w][0];
-        s2 += sh.fold[w][1];
+        s1 += sh.fold[w][k][0];
+        s2 += sh.fold[w][k][1];
     }
     FoldStats fs;
     fs.dmean = s1 * inv_n;
@@ -950,66 +1004,105 @@ __device__ __forceinline__ void load_run(RowLoad& r, const void* weight, int row
     }
 }
 
+// A chunk's weights as floats (4 for fp32 storage, 8 for fp16/bf16).
 template <int WT>
-__device__ __forceinline__ float chunk_dot(const uint4& u, const float* x)
+struct ChunkWeights
 {
-    float acc = 0.f;
+    float w[Storage<WT>::kPerChunk];
+};
+
+template <int WT>
+__device__ __forceinline__ ChunkWeights<WT> chunk_weights(const uint4& u)
+{
+    ChunkWeights<WT> c;
     if constexpr (WT == kF32)
     {
-        const float4v xv = *reinterpret_cast<const float4v*>(x);
-        acc += xv[0] * __uint_as_float(u.x);
-        acc += xv[1] * __uint_as_float(u.y);
-        acc += xv[2] * __uint_as_float(u.z);
-        acc += xv[3] * __uint_as_float(u.w);
+        c.w[0] = __uint_as_float(u.x);
+        c.w[1] = __uint_as_float(u.y);
+        c.w[2] = __uint_as_float(u.z);
+        c.w[3] = __uint_as_float(u.w);
     }
     else
     {
-        const float4v xa = *reinterpret_cast<const float4v*>(x);
-        const float4v xb = *reinterpret_cast<const float4v*>(x + 4);
         const uint32_t v[4] = {u.x, u.y, u.z, u.w};
-        float w[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
         {
             if constexpr (WT == kF16)
             {
                 const _Float16* h = reinterpret_cast<const _Float16*>(&v[i]);
-                w[2 * i] = (float) h[0];
-                w[2 * i + 1] = (float) h[1];
+                c.w[2 * i] = (float) h[0];
+                c.w[2 * i + 1] = (float) h[1];
             }
             else
             {
-                w[2 * i] = __uint_as_float(v[i] << 16);
-                w[2 * i + 1] = __uint_as_float(v[i] & 0xFFFF0000u);
+                c.w[2 * i] = __uint_as_float(v[i] << 16);
+                c.w[2 * i + 1] = __uint_as_float(v[i] & 0xFFFF0000u);
             }
         }
+    }
+    return c;
+}
+
+// The chunk's dot product with x (the same order for every token).
+template <int WT>
+__device__ __forceinline__ float chunk_dot(const ChunkWeights<WT>& c, const float* x)
+{
+    float acc = 0.f;
+    if constexpr (WT == kF32)
+    {
+        const float4v xv = *reinterpret_cast<const float4v*>(x);
+        acc += xv[0] * c.w[0];
+        acc += xv[1] * c.w[1];
+        acc += xv[2] * c.w[2];
+        acc += xv[3] * c.w[3];
+    }
+    else
+    {
+        const float4v xa = *reinterpret_cast<const float4v*>(x);
+        const float4v xb = *reinterpret_cast<const float4v*>(x + 4);
         // Two chains of four (even and odd weights), added at the end.
         float odd = 0.f;
-        acc += xa[0] * w[0];
-        odd += xa[1] * w[1];
-        acc += xa[2] * w[2];
-        odd += xa[3] * w[3];
-        acc += xb[0] * w[4];
-        odd += xb[1] * w[5];
-        acc += xb[2] * w[6];
-        odd += xb[3] * w[7];
+        acc += xa[0] * c.w[0];
+        odd += xa[1] * c.w[1];
+        acc += xa[2] * c.w[2];
+        odd += xa[3] * c.w[3];
+        acc += xb[0] * c.w[4];
+        odd += xb[1] * c.w[5];
+        acc += xb[2] * c.w[6];
+        odd += xb[3] * c.w[7];
         acc += odd;
     }
     return acc;
 }
 
 template <int WT>
-__device__ __forceinline__ float run_dot(const RowLoad& r, const float* x, int first, int last, int lane)
+__device__ __forceinline__ float chunk_dot(const uint4& u, const float* x)
 {
-    float acc = 0.f;
+    return chunk_dot<WT>(chunk_weights<WT>(u), x);
+}
+
+// The row slice's dot products with T tokens' inputs (x + x_at<T>(k, .)):
+// each chunk is unpacked once and used for every token.
+template <int WT, int T>
+__device__ __forceinline__ void run_dot(const RowLoad& r, const float* x, int first, int last, int lane,
+                                        float (&acc)[T])
+{
+#pragma unroll
+    for (int k = 0; k < T; ++k)
+        acc[k] = 0.f;
 #pragma unroll
     for (int i = 0; i < kChunks; ++i)
     {
         const int c = first + lane + kRowLanes * i;
         if (c < last)
-            acc += chunk_dot<WT>(r.w[i], x + c * Storage<WT>::kPerChunk);
+        {
+            const ChunkWeights<WT> w = chunk_weights<WT>(r.w[i]);
+#pragma unroll
+            for (int k = 0; k < T; ++k)
+                acc[k] += chunk_dot<WT>(w, x + x_at<T>(k, c * Storage<WT>::kPerChunk));
+        }
     }
-    return acc;
 }
 
 struct Prefetch
@@ -1021,14 +1114,26 @@ struct Prefetch
 
 // Issues this row group's pass-0 weights and, for the finishing threads, the
 // bias of their pass-0 row (and with FOLD its gain).
-template <bool FOLD>
+// A finishing thread's local row: thread t finishes row t % rows_per_pass of
+// its pass for token t / rows_per_pass (rows_per_pass is a power of two).
+template <int T>
+__device__ __forceinline__ int finisher_local(const PhaseShape& ps)
+{
+    return T == 1 ? (int) threadIdx.x : (int) threadIdx.x & (ps.rows_per_pass - 1);
+}
+
+template <bool FOLD, int T = 1>
 __device__ __forceinline__ void prefetch(Prefetch& p, const void* weight, const float* bias, const float* gain,
                                          const PhaseShape& ps, int group, int stride)
 {
     int row, first, last;
     phase_task(ps, group, stride, 0, row, first, last);
+    // With several tokens the chunk offsets are recomputed at each phase
+    // rather than held across the layer loop (registers are short there).
+    if constexpr (T > 1)
+        asm volatile("" : "+v"(row), "+v"(first));
     load_run(p.r, weight, row, ps.row_bytes, first, last);
-    const int finisher_row = min(phase_row(ps, group, stride, (int) threadIdx.x), ps.rows - 1);
+    const int finisher_row = min(phase_row(ps, group, stride, finisher_local<T>(ps)), ps.rows - 1);
     // The load is issued whether or not the phase has a bias (a phase without
     // one reads a weight word and drops it): the compiler counts outstanding
     // loads per program point, and a load skipped on some path makes every
@@ -1043,15 +1148,16 @@ __device__ __forceinline__ void prefetch(Prefetch& p, const void* weight, const 
 
 // The slices of finisher t's row (slots [t << log2, (t + 1) << log2) of
 // sh.part), read in one or a few vector reads and added pairwise.
-__device__ __forceinline__ float slice_total(const Shared& sh, int t, int log2)
+__device__ __forceinline__ float slice_total(const Shared& sh, int token, int t, int log2)
 {
-    const float4v* run = reinterpret_cast<const float4v*>(sh.part);
+    const float* part = sh.part + token * kRowGroups;
+    const float4v* run = reinterpret_cast<const float4v*>(part);
     switch (log2)
     {
-        case 0: return sh.part[t];
+        case 0: return part[t];
         case 1:
         {
-            const float2 v = reinterpret_cast<const float2*>(sh.part)[t];
+            const float2 v = reinterpret_cast<const float2*>(part)[t];
             return v.x + v.y;
         }
         case 2:
@@ -1077,52 +1183,77 @@ static_assert(kRowGroups == 16, "slice_total covers up to 16 slices");
 // Sums a pass's partials, then the finishing threads add the slices of their
 // row, turn the dot product into the row's value (value_of: the bias, or a
 // folded LayerNorm's correction and bias) and hand it to epi; two barriers
-// bracket the shared partial slots.
-template <class Epilogue, class Value>
-__device__ __forceinline__ void finish_pass(float acc, bool has_task, int pass, const PhaseShape& ps, int group,
-                                            int stride, Shared& sh, Epilogue& epi, Value value_of)
+// bracket the shared partial slots. With T tokens thread t finishes token
+// t / rows_per_pass (the first `count` tokens only).
+template <int T, class Epilogue, class Value>
+__device__ __forceinline__ void finish_pass(const float (&acc)[T], bool has_task, int pass, const PhaseShape& ps,
+                                            int group, int stride, int count, Shared& sh, Epilogue& epi,
+                                            Value value_of)
 {
-    acc = sum32(acc);
-    if (has_task && (threadIdx.x & (kRowLanes - 1)) == 0)
-        sh.part[threadIdx.x / kRowLanes] = acc;
-    __syncthreads();
-    const int local = pass * ps.rows_per_pass + (int) threadIdx.x;
-    if ((int) threadIdx.x < ps.rows_per_pass && local < ps.local_rows)
+#pragma unroll
+    for (int k = 0; k < T; ++k)
     {
-        const float v = slice_total(sh, (int) threadIdx.x, ps.slice_log2);
+        const float total = sum32(acc[k]);
+        if (has_task && (threadIdx.x & (kRowLanes - 1)) == 0)
+            sh.part[k * kRowGroups + threadIdx.x / kRowLanes] = total;
+    }
+    __syncthreads();
+    const int lr = finisher_local<T>(ps);
+    const int token = T == 1 ? 0 : (int) threadIdx.x / ps.rows_per_pass;
+    const int local = pass * ps.rows_per_pass + lr;
+    if ((T == 1 ? (int) threadIdx.x < ps.rows_per_pass : token < count) && local < ps.local_rows)
+    {
+        const float v = slice_total(sh, token, lr, ps.slice_log2);
         const int r = phase_row(ps, group, stride, local);
-        epi(r, local, value_of(r, v));
+        epi(r, local, token, value_of(token, r, v));
     }
     // Also keeps the other waves from issuing loads (polls, prefetches)
     // ahead of the finishers' stores.
     __syncthreads();
 }
 
-// Runs every task of the phase against sh.x. epi(row, value) receives the dot
-// product plus bias, on thread (local row) % rows_per_pass (all in wave 0);
-// with FOLD, sh.x holds gamma (x - K) of a LayerNorm's input and the value is
-// rstd (dot - (mean - K) gain) + bias, where bias and gain are the row's folded
-// terms. Pass 0 is straight-line code whose weights, bias and gain were loaded
-// a phase earlier; further passes, which only long rows or narrow grids need,
-// load on the spot. after() issues the loads of a later phase (its prefetch):
-// every thread calls it once, after pass 0's stores, so they are not held up
-// behind the issue.
-template <int WT, bool FOLD, class Epilogue, class After>
+// Runs every task of the phase against sh.x. epi(row, local row, token,
+// value) receives the dot product plus bias, on thread (local row) %
+// rows_per_pass (+ token * rows_per_pass; all in wave 0); with FOLD, sh.x
+// holds gamma (x - K) of a LayerNorm's input and the value is
+// rstd (dot - (mean - K) gain) + bias, where bias and gain are the row's
+// folded terms. Pass 0 is straight-line code whose weights, bias and gain were
+// loaded a phase earlier; further passes, which only long rows or narrow grids
+// need, load on the spot. after() issues the loads of a later phase (its
+// prefetch): every thread calls it once, after pass 0's stores, so they are
+// not held up behind the issue. With T tokens every weight chunk is used for
+// the first `count` tokens' inputs.
+template <int WT, bool FOLD, int T = 1, class Epilogue, class After>
 __device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight, const float* bias, const float* gain,
-                                          const FoldStats& fs, const PhaseShape& ps, int group, int stride,
-                                          Shared& sh, Epilogue epi, After after, int mark = -1)
+                                          const FoldStats (&fs)[T], const PhaseShape& ps, int group, int stride,
+                                          int count, Shared& sh, Epilogue epi, After after, int mark = -1)
 {
     const int lane = threadIdx.x & (kRowLanes - 1);
     int row, first, last;
     const bool has_task = phase_task(ps, group, stride, 0, row, first, last);
-    const float acc = run_dot<WT>(p.r, sh.x, first, last, lane);
+    float acc[T];
+    run_dot<WT, T>(p.r, sh.x, first, last, lane, acc);
     const float bias0 = p.bias;
     const float gain0 = FOLD ? p.gain : 0.f;
-    auto value = [&](float v, float b, float g) { return FOLD ? fs.rstd * (v - fs.dmean * g) + b : v + b; };
+    auto value = [&](int k, float v, float b, float g) {
+        // Token k's statistics by selects on values: an indexed register
+        // array would be placed in memory (the empty asm keeps the compiler
+        // from turning the selects back into an indexed load).
+        float rstd = fs[0].rstd, dmean = fs[0].dmean;
+#pragma unroll
+        for (int i = 1; i < T; ++i)
+        {
+            float r = fs[i].rstd, m = fs[i].dmean;
+            asm volatile("" : "+v"(r), "+v"(m));
+            rstd = k == i ? r : rstd;
+            dmean = k == i ? m : dmean;
+        }
+        return FOLD ? rstd * (v - dmean * g) + b : v + b;
+    };
     STEP_MARK(mark);
     if (ps.passes > 0)
-        finish_pass(acc, has_task, 0, ps, group, stride, sh, epi,
-                    [&](int, float v) { return value(v, bias0, gain0); });
+        finish_pass<T>(acc, has_task, 0, ps, group, stride, count, sh, epi,
+                       [&](int k, int, float v) { return value(k, v, bias0, gain0); });
     STEP_MARK(mark < 0 ? -1 : mark + 1);
     after();
     for (int pass = 1; pass < ps.passes; ++pass)
@@ -1130,10 +1261,10 @@ __device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight,
         const bool task = phase_task(ps, group, stride, pass, row, first, last);
         RowLoad r;
         load_run(r, weight, row, ps.row_bytes, first, last);
-        finish_pass(run_dot<WT>(r, sh.x, first, last, lane), task, pass, ps, group, stride, sh, epi,
-                    [&](int rr, float v) {
-                        return value(v, bias != nullptr ? global(bias)[rr] : 0.f, FOLD ? global(gain)[rr] : 0.f);
-                    });
+        run_dot<WT, T>(r, sh.x, first, last, lane, acc);
+        finish_pass<T>(acc, task, pass, ps, group, stride, count, sh, epi, [&](int k, int rr, float v) {
+            return value(k, v, bias != nullptr ? global(bias)[rr] : 0.f, FOLD ? global(gain)[rr] : 0.f);
+        });
     }
 }
 
@@ -1193,14 +1324,15 @@ __device__ __forceinline__ void load_keys(KeyRows<NP>& kr, const float* keys, co
 // writes sh.red and sh.scratch again only after a barrier of its own.
 template <int NP>
 __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int head_width, float scale2, uint64_t* out,
-                                       uint32_t epoch, Shared& sh, bool normalized = false, int mark = -1)
+                                       uint32_t epoch, Shared& sh, bool normalized = false, int mark = -1,
+                                       const float* query = nullptr)
 {
     const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const bool live = 4 * kl < head_width;
     float4v qv = {0.f, 0.f, 0.f, 0.f};
     if (live)
-        qv = *reinterpret_cast<const float4v*>(sh.q + 4 * kl);
+        qv = *reinterpret_cast<const float4v*>((query != nullptr ? query : sh.q) + 4 * kl);
     float s[NP];
     float local_max = -INFINITY;
 #pragma unroll
@@ -1458,31 +1590,49 @@ __device__ __forceinline__ void issue_ring(Ring& ring, const StepArgs& a, const 
         load_logit_row(ring.r[k], ring.mask[k], a, s, k);
 }
 
-template <int LWT>
-__device__ __forceinline__ float logit_dot(const RowLoad& r, const StepArgs& a, const LogitShape& s, int row,
-                                           const float* x)
+// The row's dot products with T tokens' normalised rows (x + x_at<T>(k, .)),
+// each chunk unpacked once.
+template <int LWT, int T>
+__device__ __forceinline__ void logit_dot(const RowLoad& r, const StepArgs& a, const LogitShape& s, int row,
+                                          const float* x, float (&v)[T])
 {
     const int lanes = 1 << s.lanes_log2;
     const int lane = threadIdx.x & (lanes - 1);
-    float acc = 0.f;
+    float acc[T];
+#pragma unroll
+    for (int k = 0; k < T; ++k)
+        acc[k] = 0.f;
 #pragma unroll
     for (int i = 0; i < kChunks; ++i)
     {
         const int c = lane + i * lanes;
         if (c < s.chunks)
-            acc += chunk_dot<LWT>(r.w[i], x + c * Storage<LWT>::kPerChunk);
+        {
+            const ChunkWeights<LWT> w = chunk_weights<LWT>(r.w[i]);
+#pragma unroll
+            for (int k = 0; k < T; ++k)
+                acc[k] += chunk_dot<LWT>(w, x + x_at<T>(k, c * Storage<LWT>::kPerChunk));
+        }
     }
     // Rows longer than the ring's share load the rest here.
     for (int c = lane + kChunks * lanes; c < s.chunks; c += lanes)
-        acc += chunk_dot<LWT>(*reinterpret_cast<const uint4*>(static_cast<const char*>(a.logits_weight)
-                                                              + (size_t) row * s.row_bytes + (size_t) c * 16),
-                              x + c * Storage<LWT>::kPerChunk);
-    return s.lanes_log2 == 5 ? sum32(acc) : sum64(acc);
+    {
+        const ChunkWeights<LWT> w = chunk_weights<LWT>(*reinterpret_cast<const uint4*>(
+            static_cast<const char*>(a.logits_weight) + (size_t) row * s.row_bytes + (size_t) c * 16));
+#pragma unroll
+        for (int k = 0; k < T; ++k)
+            acc[k] += chunk_dot<LWT>(w, x + x_at<T>(k, c * Storage<LWT>::kPerChunk));
+    }
+#pragma unroll
+    for (int k = 0; k < T; ++k)
+        v[k] = s.lanes_log2 == 5 ? sum32(acc[k]) : sum64(acc[k]);
 }
 
-template <int LWT>
+// The logits of the first `count` tokens; the top-1 under the mask of the
+// last of them.
+template <int LWT, int T>
 __device__ __forceinline__ void logits_loop(Ring& ring, const StepArgs& a, const LogitShape& s, const Shared& sh,
-                                            float& best_v, uint32_t& best_i)
+                                            int count, float& best_v, uint32_t& best_i)
 {
     const int lane = threadIdx.x & ((1 << s.lanes_log2) - 1);
     for (int j = 0;; j += kRing)
@@ -1493,15 +1643,23 @@ __device__ __forceinline__ void logits_loop(Ring& ring, const StepArgs& a, const
             const int row = logit_row(s, j + k);
             if (row >= a.vocabulary)
                 return;
-            const float v = logit_dot<LWT>(ring.r[k], a, s, row, sh.x);
+            float v[T];
+            logit_dot<LWT, T>(ring.r[k], a, s, row, sh.x, v);
             const float m = ring.mask[k];
             load_logit_row(ring.r[k], ring.mask[k], a, s, j + k + kRing);
             if (lane == 0)
             {
-                a.logits[row] = v;
-                if (m == 0.f && (best_i == kUnchosen || v > best_v))
+                float last = v[0];
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+                    if (T == 1 || t < count)
+                    {
+                        a.logits[(size_t) t * a.vocabulary + row] = v[t];
+                        last = v[t];
+                    }
+                if (m == 0.f && (best_i == kUnchosen || last > best_v))
                 {
-                    best_v = v;
+                    best_v = last;
                     best_i = (uint32_t) row;
                 }
             }
@@ -1518,34 +1676,74 @@ __device__ __forceinline__ void logits_loop(Ring& ring, const StepArgs& a, const
 // two parts are added where the row is written.
 constexpr int kEmbedSlots = (kMaxWidth + kThreads - 1) / kThreads;
 
+template <int T>
 struct Embedding
 {
-    float token[kEmbedSlots];
-    float position[kEmbedSlots];
-    bool known;
+    float token[T][kEmbedSlots];
+    float position[T][kEmbedSlots];
+    bool known[T];
 };
 
-__device__ __forceinline__ void issue_embedding(Embedding& e, const StepArgs& a)
+// Token k (of the first `count`; later slots repeat the last) at position
+// position + k.
+template <int T>
+__device__ __forceinline__ void issue_embedding(Embedding<T>& e, const StepArgs& a)
 {
     const int d = a.width;
-    const uint32_t token = a.tokens[0];
-    e.known = token < (uint32_t) a.vocabulary;
-    const size_t row = e.known ? (size_t) token * d : 0;
 #pragma unroll
-    for (int k = 0; k < kEmbedSlots; ++k)
+    for (int t = 0; t < T; ++t)
     {
-        const int c = min((int) threadIdx.x + kThreads * k, d - 1);
-        e.position[k] = global(a.position_embedding)[(size_t) a.position * d + c];
-        e.token[k] = global(a.token_embedding)[row + c];
+        const int k = T == 1 ? 0 : min(t, a.token_count - 1);
+        const uint32_t token = a.tokens[k];
+        e.known[t] = token < (uint32_t) a.vocabulary;
+        const size_t row = e.known[t] ? (size_t) token * d : 0;
+#pragma unroll
+        for (int s = 0; s < kEmbedSlots; ++s)
+        {
+            const int c = min((int) threadIdx.x + kThreads * s, d - 1);
+            e.position[t][s] = global(a.position_embedding)[(size_t) (a.position + k) * d + c];
+            e.token[t][s] = global(a.token_embedding)[row + c];
+        }
     }
 }
 
-template <int WT>
-__device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, const Embedding& embed)
+// The first `count` tokens' n-word vectors (token_words apart from base):
+// word j of token k is read at base + k * token_words + offset and written to
+// dst[place(k, index)], with map(j, offset, index) as in poll(). The tokens'
+// words are polled in order, P * 448 slots a round.
+template <int P, class Map, class Place>
+__device__ __forceinline__ bool gather_tokens(const uint64_t* base, int token_words, int count, int n, Map map,
+                                              float* dst, Place place, uint32_t epoch, int* status, Shared& sh)
+{
+    const int total = count * n;
+    for (int first = 0; first < total; first += P * kPollThreads)
+    {
+        const bool ok = poll<P>(
+            base, min(P * kPollThreads, total - first),
+            [&](int i, int& offset, int& index) {
+                const int w = first + i;
+                const int k = w / n, j = w - k * n;
+                int o, x;
+                const bool used = map(j, o, x);
+                offset = k * token_words + o;
+                index = place(k, x);
+                return used;
+            },
+            dst, epoch, status, sh);
+        if (!ok)
+            return false;
+    }
+    return true;
+}
+
+template <int WT, int T>
+__device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, const Embedding<T>& embed)
 {
     const int d = a.width, f = a.feed_forward, H = a.heads, hd = d / H;
     const int group = blockIdx.x, stride = a.row_groups;
     const int pos = a.position;
+    const int count = T == 1 ? 1 : a.token_count;
+    const int tw = a.token_words;
     const uint32_t epoch = a.epoch;
     const PhaseShape qkv_shape = phase_shape<WT>(3 * d, d, group, stride, true); // read per head
     const PhaseShape square_shape = phase_shape<WT>(d, d, group, stride);
@@ -1561,16 +1759,26 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
 
     Prefetch pa, pb;
     FoldParams fold;
-    FoldStats fs;
-    float shift = 0.f; // the previous LayerNorm's mean (the next one's K)
+    FoldStats fs[T];
+    float shift[T]; // per token: the previous LayerNorm's mean (the next one's K)
+#pragma unroll
+    for (int k = 0; k < T; ++k)
+        shift[k] = 0.f;
     KeyRows<kCrossPasses> cross;
-    const FoldStats none {};
+    FoldStats none[T];
+#pragma unroll
+    for (int k = 0; k < T; ++k)
+        none[k] = {};
     // After a folded gather every thread reads the statistics (the waves'
     // sums are in sh.fold past its barrier) and moves the shift to this
     // LayerNorm's mean, the next one's K.
     auto statistics = [&] {
-        fs = fold_stats(sh, a.inv_width, a.eps);
-        shift += fs.dmean;
+#pragma unroll
+        for (int k = 0; k < T; ++k)
+        {
+            fs[k] = fold_stats(sh, k, a.inv_width, a.eps);
+            shift[k] += fs[k].dmean;
+        }
     };
 
     {
@@ -1578,26 +1786,31 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         // later layers' (all eight waves hold embedding entries; K = 0).
         const wsp_layer_tensors& L0 = sh.table[0];
         const float* T0 = a.fold_terms;
-        prefetch<true>(pa, L0.self_qkv_w, T0 + a.terms_qkv_bias, T0 + a.terms_qkv_gain, qkv_shape, group, stride);
+        prefetch<true, T>(pa, L0.self_qkv_w, T0 + a.terms_qkv_bias, T0 + a.terms_qkv_gain, qkv_shape, group, stride);
         float gamma[kEmbedSlots];
 #pragma unroll
         for (int k = 0; k < kEmbedSlots; ++k)
             gamma[k] = global(L0.self_norm_w)[min((int) threadIdx.x + kThreads * k, d - 1)];
-        float s1 = 0.f, s2 = 0.f;
+        FoldSums sums[T];
 #pragma unroll
-        for (int k = 0; k < kEmbedSlots; ++k)
+        for (int t = 0; t < T; ++t)
         {
-            const int c = (int) threadIdx.x + kThreads * k;
-            if (c < d)
+            sums[t] = {0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < kEmbedSlots; ++k)
             {
-                const float x = embed.known ? embed.token[k] + embed.position[k] : __builtin_nanf("");
-                sh.raw[c] = x;
-                sh.x[c] = gamma[k] * x;
-                s1 += x;
-                s2 += x * x;
+                const int c = (int) threadIdx.x + kThreads * k;
+                if (c < d)
+                {
+                    const float x = embed.known[t] ? embed.token[t][k] + embed.position[t][k] : __builtin_nanf("");
+                    sh.raw[t * kRawStride + c] = x;
+                    sh.x[x_at<T>(t, c)] = gamma[k] * x;
+                    sums[t].s1 += x;
+                    sums[t].s2 += x * x;
+                }
             }
         }
-        fold_reduce({s1, s2}, sh);
+        fold_reduce<T>(sums, sh);
         __syncthreads();
     }
     STEP_STAMP(0, 0);
@@ -1605,30 +1818,30 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
     for (int l = 0; l < a.layer_count; ++l)
     {
         const wsp_layer_tensors& L = sh.table[l];
-        const float* T = a.fold_terms + (size_t) l * a.terms_stride;
+        const float* TL = a.fold_terms + (size_t) l * a.terms_stride;
         uint64_t* ex = a.exchange + (size_t) l * a.layer_words;
         STEP_LAYER(l);
 
         // ---- LN1 folded into the fused q/k/v (weights in pa) --------------------
         if (l > 0
-            && !gather_fold(a.exchange + (size_t) (l - 1) * a.layer_words + a.off_h4, d, a.log2_d, stride, fold,
-                            shift, epoch, a.status, sh))
+            && !gather_fold<T>(a.exchange + (size_t) (l - 1) * a.layer_words + a.off_h4, tw, count, d, a.log2_d,
+                               stride, fold, shift, epoch, a.status, sh))
             return false;
         if (l > 0)
             STEP_STAMP(0, l);
         statistics();
         {
             uint64_t* qkv = ex + a.off_qkv;
-            float* krow = L.self_keys + (size_t) pos * d;
-            float* vrow = L.self_values + (size_t) pos * d;
-            run_phase<WT, true>(pa, L.self_qkv_w, T + a.terms_qkv_bias, T + a.terms_qkv_gain, fs, qkv_shape, group,
-                                stride, sh, [&](int r, int j, float v) {
-                put(qkv + (group << a.log2_qkv) + j, v, epoch);
+            run_phase<WT, true, T>(pa, L.self_qkv_w, TL + a.terms_qkv_bias, TL + a.terms_qkv_gain, fs, qkv_shape,
+                                   group, stride, count, sh, [&](int r, int j, int k, float v) {
+                put(qkv + k * tw + (group << a.log2_qkv) + j, v, epoch);
+                // The new key and value rows of token k, at position pos + k.
+                const size_t at = (size_t) (pos + k) * d;
                 if (r >= 2 * d)
-                    global_mut(vrow)[r - 2 * d] = v;
+                    global_mut(L.self_values + at)[r - 2 * d] = v;
                 else if (r >= d)
-                    global_mut(krow)[r - d] = v;
-            }, [&] { prefetch<false>(pb, L.self_out_w, L.self_out_b, nullptr, square_shape, group, stride); }, 25);
+                    global_mut(L.self_keys + at)[r - d] = v;
+            }, [&] { prefetch<false, T>(pb, L.self_out_w, L.self_out_b, nullptr, square_shape, group, stride); }, 25);
         }
         STEP_STAMP(1, l);
 
@@ -1653,13 +1866,20 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
                 return true;
             };
             static_assert(3 * kPollThreads >= kMaxWidth, "three slots cover the widest row");
-            if (!(d <= 2 * kPollThreads ? poll<2>(ex + a.off_self, d, map, sh.x, epoch, a.status, sh)
-                                        : poll<3>(ex + a.off_self, d, map, sh.x, epoch, a.status, sh)))
+            if constexpr (T == 1)
+            {
+                if (!(d <= 2 * kPollThreads ? poll<2>(ex + a.off_self, d, map, sh.x, epoch, a.status, sh)
+                                            : poll<3>(ex + a.off_self, d, map, sh.x, epoch, a.status, sh)))
+                    return false;
+            }
+            else if (!gather_tokens<kPollCombine>(ex + a.off_self, tw, count, d, map, sh.x, x_at<T>, epoch,
+                                                  a.status, sh))
                 return false;
             STEP_STAMP(2, l);
         }
         else
         {
+            // (Key splits: the single-token kernel only.)
             if (!gather_any(ex + a.off_self, a.self_splits * H * (hd + 2), sh.comb, epoch, a.status, sh))
                 return false;
             STEP_STAMP(2, l);
@@ -1669,12 +1889,14 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         }
         {
             uint64_t* out = ex + a.off_h2;
-            run_phase<WT, false>(
-                pb, L.self_out_w, L.self_out_b, nullptr, none, square_shape, group, stride, sh,
-                [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); },
+            run_phase<WT, false, T>(
+                pb, L.self_out_w, L.self_out_b, nullptr, none, square_shape, group, stride, count, sh,
+                [&](int r, int j, int k, float v) {
+                    put(out + k * tw + (group << a.log2_d) + j, sh.raw[k * kRawStride + r] + v, epoch);
+                },
                 [&] {
-                    prefetch<true>(pa, L.cross_q_w, T + a.terms_xq_bias, T + a.terms_xq_gain, xq_shape, group,
-                                   stride);
+                    prefetch<true, T>(pa, L.cross_q_w, TL + a.terms_xq_bias, TL + a.terms_xq_gain, xq_shape, group,
+                                      stride);
                     load_fold(fold, L.cross_norm_w, d, a.log2_d, stride);
                 },
                 27);
@@ -1682,16 +1904,16 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         STEP_STAMP(3, l);
 
         // ---- LN2 folded into the cross q (weights in pa) --------------------------
-        if (!gather_fold(ex + a.off_h2, d, a.log2_d, stride, fold, shift, epoch, a.status, sh))
+        if (!gather_fold<T>(ex + a.off_h2, tw, count, d, a.log2_d, stride, fold, shift, epoch, a.status, sh))
             return false;
         STEP_STAMP(4, l);
         statistics();
         {
             uint64_t* out = ex + a.off_xq;
-            run_phase<WT, true>(
-                pa, L.cross_q_w, T + a.terms_xq_bias, T + a.terms_xq_gain, fs, xq_shape, group, stride, sh,
-                [&](int, int j, float v) { put(out + (group << a.log2_d) + j, v, epoch); },
-                [&] { prefetch<false>(pb, L.cross_out_w, L.cross_out_b, nullptr, square_shape, group, stride); },
+            run_phase<WT, true, T>(
+                pa, L.cross_q_w, TL + a.terms_xq_bias, TL + a.terms_xq_gain, fs, xq_shape, group, stride, count, sh,
+                [&](int, int j, int k, float v) { put(out + k * tw + (group << a.log2_d) + j, v, epoch); },
+                [&] { prefetch<false, T>(pb, L.cross_out_w, L.cross_out_b, nullptr, square_shape, group, stride); },
                 29);
         }
         STEP_STAMP(5, l);
@@ -1701,37 +1923,62 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         {
             const int h = t % H, s = t / H;
             const int first = s * a.cross_chunk;
-            const int count = min(a.cross_chunk, a.cross_rows - first);
+            const int keys = min(a.cross_chunk, a.cross_rows - first);
             if (t != task)
-                load_keys<kCrossPasses>(cross, L.cross_keys, L.cross_values, first, count, d, h * hd, hd);
-            if (!poll<1>(
-                    ex + a.off_xq, hd,
-                    [&](int i, int& offset, int& index) {
-                        offset = blocked_slot(h * hd + i, xq_shape.block, a.log2_d);
-                        index = i;
-                        return true;
-                    },
-                    sh.q, epoch, a.status, sh))
+                load_keys<kCrossPasses>(cross, L.cross_keys, L.cross_values, first, keys, d, h * hd, hd);
+            auto map = [&](int i, int& offset, int& index) {
+                offset = blocked_slot(h * hd + i, xq_shape.block, a.log2_d);
+                index = i;
+                return true;
+            };
+            if constexpr (T == 1)
+            {
+                if (!poll<1>(ex + a.off_xq, hd, map, sh.q, epoch, a.status, sh))
+                    return false;
+            }
+            else if (!gather_tokens<1>(ex + a.off_xq, tw, count, hd, map, sh.q,
+                                       [](int k, int i) { return k * kQStride + i; }, epoch, a.status, sh))
                 return false;
             if (t == task)
                 STEP_STAMP(6, l);
-            attend<kCrossPasses>(cross, count, hd, a.scale * kLog2e,
-                                 ex + a.off_xpart + (size_t) (h * a.cross_splits + s) * (hd + 2), epoch, sh, false,
-                                 t == task ? 22 : -1);
+#pragma unroll
+            for (int k = 0; k < T; ++k)
+                if (T == 1 || k < count)
+                {
+                    if (k > 0)
+                        __syncthreads(); // the previous token's rows are read out of sh.red
+                    attend<kCrossPasses>(cross, keys, hd, a.scale * kLog2e,
+                                         ex + k * tw + a.off_xpart + (size_t) (h * a.cross_splits + s) * (hd + 2),
+                                         epoch, sh, false, t == task && k == 0 ? 22 : -1, sh.q + k * kQStride);
+                }
         }
         STEP_STAMP(7, l);
 
         // ---- cross out-proj + residual (weights in pb) --------------------------------
-        if (!gather_any(ex + a.off_xattn, d, sh.x, epoch, a.status, sh))
+        if constexpr (T == 1)
+        {
+            if (!gather_any(ex + a.off_xattn, d, sh.x, epoch, a.status, sh))
+                return false;
+        }
+        else if (!gather_tokens<kPollCombine>(
+                     ex + a.off_xattn, tw, count, d,
+                     [](int i, int& offset, int& index) {
+                         offset = index = i;
+                         return true;
+                     },
+                     sh.x, x_at<T>, epoch, a.status, sh))
             return false;
         STEP_STAMP(8, l);
         {
             uint64_t* out = ex + a.off_h3;
-            run_phase<WT, false>(
-                pb, L.cross_out_w, L.cross_out_b, nullptr, none, square_shape, group, stride, sh,
-                [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); },
+            run_phase<WT, false, T>(
+                pb, L.cross_out_w, L.cross_out_b, nullptr, none, square_shape, group, stride, count, sh,
+                [&](int r, int j, int k, float v) {
+                    put(out + k * tw + (group << a.log2_d) + j, sh.raw[k * kRawStride + r] + v, epoch);
+                },
                 [&] {
-                    prefetch<true>(pa, L.fc1_w, T + a.terms_fc1_bias, T + a.terms_fc1_gain, fc1_shape, group, stride);
+                    prefetch<true, T>(pa, L.fc1_w, TL + a.terms_fc1_bias, TL + a.terms_fc1_gain, fc1_shape, group,
+                                      stride);
                     load_fold(fold, L.final_norm_w, d, a.log2_d, stride);
                 },
                 31);
@@ -1739,22 +1986,35 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         STEP_STAMP(9, l);
 
         // ---- LN3 folded into fc1 + GELU (weights in pa) ----------------------------------
-        if (!gather_fold(ex + a.off_h3, d, a.log2_d, stride, fold, shift, epoch, a.status, sh))
+        if (!gather_fold<T>(ex + a.off_h3, tw, count, d, a.log2_d, stride, fold, shift, epoch, a.status, sh))
             return false;
         STEP_STAMP(10, l);
         statistics();
         {
             uint64_t* out = ex + a.off_ff;
-            run_phase<WT, true>(
-                pa, L.fc1_w, T + a.terms_fc1_bias, T + a.terms_fc1_gain, fs, fc1_shape, group, stride, sh,
-                [&](int, int j, float v) { put(out + (group << a.log2_f) + j, exact_gelu(v), epoch); },
-                [&] { prefetch<false>(pb, L.fc2_w, L.fc2_b, nullptr, fc2_shape, group, stride); }, 33);
+            run_phase<WT, true, T>(
+                pa, L.fc1_w, TL + a.terms_fc1_bias, TL + a.terms_fc1_gain, fs, fc1_shape, group, stride, count, sh,
+                [&](int, int j, int k, float v) { put(out + k * tw + (group << a.log2_f) + j, exact_gelu(v), epoch); },
+                [&] { prefetch<false, T>(pb, L.fc2_w, L.fc2_b, nullptr, fc2_shape, group, stride); }, 33);
         }
         STEP_STAMP(11, l);
 
         // ---- fc2 + residual (weights in pb) ------------------------------------------------
-        if (!gather_words<kPollBlockedFF>(ex + a.off_ff, f, a.log2_f, stride, sh.x, epoch, a.status, sh))
-            return false;
+        if constexpr (T == 1)
+        {
+            if (!gather_words<kPollBlockedFF>(ex + a.off_ff, f, a.log2_f, stride, sh.x, epoch, a.status, sh,
+                                              [](int i) { return i; }))
+                return false;
+        }
+        else
+        {
+            // Token after token: each token's vector is one round of eight
+            // loads per thread, which arrive together once the first has.
+            for (int k = 0; k < count; ++k)
+                if (!gather_words<kPollBlockedFF>(ex + k * tw + a.off_ff, f, a.log2_f, stride, sh.x, epoch, a.status,
+                                                  sh, [k](int i) { return x_at<T>(k, i); }))
+                    return false;
+        }
         STEP_STAMP(12, l);
         {
             // After the dot products: the next layer's q/k/v slice, its folded
@@ -1764,12 +2024,14 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
             const wsp_layer_tensors& next = sh.table[next_layer];
             const float* TN = a.fold_terms + (size_t) next_layer * a.terms_stride;
             uint64_t* out = ex + a.off_h4;
-            run_phase<WT, false>(
-                pb, L.fc2_w, L.fc2_b, nullptr, none, fc2_shape, group, stride, sh,
-                [&](int r, int j, float v) { put(out + (group << a.log2_d) + j, sh.raw[r] + v, epoch); },
+            run_phase<WT, false, T>(
+                pb, L.fc2_w, L.fc2_b, nullptr, none, fc2_shape, group, stride, count, sh,
+                [&](int r, int j, int k, float v) {
+                    put(out + k * tw + (group << a.log2_d) + j, sh.raw[k * kRawStride + r] + v, epoch);
+                },
                 [&] {
-                    prefetch<true>(pa, next.self_qkv_w, TN + a.terms_qkv_bias, TN + a.terms_qkv_gain, qkv_shape,
-                                   group, stride);
+                    prefetch<true, T>(pa, next.self_qkv_w, TN + a.terms_qkv_bias, TN + a.terms_qkv_gain, qkv_shape,
+                                      group, stride);
                     load_fold(fold, next.self_norm_w, d, a.log2_d, stride);
                 },
                 35);
@@ -1855,38 +2117,147 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
     return true;
 }
 
+// The head groups of a multi-token launch: workgroup (query k, head h) —
+// index k * H + h past the row groups — attends token k's query of head h
+// over the cached keys and the new keys of tokens 0..k (the causal mask of
+// Kernels/Attention.h:34-47); its row goes to token k's self slot, normalized.
+// The positions stay within one key block (position + count <= kSelfKeys), so
+// no key split is combined. The first H of them also combine every token's
+// cross-attention partials of their head.
+template <int T>
+__device__ __forceinline__ bool head_group_tokens(const StepArgs& a, Shared& sh)
+{
+    const int d = a.width, H = a.heads, hd = d / H;
+    const int index = blockIdx.x - a.row_groups;
+    const int qkv_block = (3 * d + a.row_groups - 1) / a.row_groups; // the q/k/v phase's rows per workgroup
+    const int head = index % H, query = index / H;
+    const int count = a.token_count, tw = a.token_words;
+    const int cached = a.position;                // keys read from the cache
+    const bool attends = query < count;
+    const int keys = cached + query + 1;          // keys attended by this query
+    const uint32_t epoch = a.epoch;
+
+    KeyRows<kSelfPasses> self;
+    if (attends && cached > 0)
+        load_keys<kSelfPasses>(self, sh.table[0].self_keys, sh.table[0].self_values, 0, cached, d, head * hd, hd);
+
+    for (int l = 0; l < a.layer_count; ++l)
+    {
+        uint64_t* ex = a.exchange + (size_t) l * a.layer_words;
+        const bool last_layer = l + 1 == a.layer_count;
+        STEP_LAYER(l);
+        if (attends)
+        {
+            // q, new key and new value of this head for tokens 0..query, in
+            // one wait: token k's block at sh.q + k * kQStride.
+            if (!gather_tokens<2>(
+                    ex + a.off_qkv, tw, query + 1, 3 * hd,
+                    [&](int i, int& offset, int& at) {
+                        offset = blocked_slot((i / hd) * d + head * hd + i % hd, qkv_block, a.log2_qkv);
+                        at = i;
+                        return true;
+                    },
+                    sh.q, [](int k, int i) { return k * kQStride + i; }, epoch, a.status, sh))
+                return false;
+            STEP_STAMP(14, l);
+            // The new keys sit at local indices cached .. cached + query.
+            const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
+            const int c = 4 * min(kl, hd / 4 - 1);
+#pragma unroll
+            for (int p = 0; p < kSelfPasses; ++p)
+            {
+                const int j = ks + kKeySlots * p - cached; // the new token this slot holds
+                if (j >= 0 && j <= query && 4 * kl < hd)
+                {
+                    self.k[p] = *reinterpret_cast<const float4v*>(&sh.q[j * kQStride + hd + c]);
+                    self.v[p] = *reinterpret_cast<const float4v*>(&sh.q[j * kQStride + 2 * hd + c]);
+                }
+            }
+            attend<kSelfPasses>(self, keys, hd, a.scale * kLog2e, ex + query * tw + a.off_self + (size_t) head * (hd + 2),
+                                epoch, sh, true, 22, sh.q + query * kQStride);
+            STEP_STAMP(15, l);
+        }
+        // Cross-attention combine of one head for every token.
+        if (index < H)
+        {
+            const int parts = a.cross_splits;
+            const int n = parts * (hd + 2);
+            if (!gather_tokens<kPollCombine>(
+                    ex + a.off_xpart + (size_t) head * n, tw, count, n,
+                    [](int i, int& offset, int& at) {
+                        offset = at = i;
+                        return true;
+                    },
+                    sh.comb, [n](int k, int i) { return k * n + i; }, epoch, a.status, sh))
+                return false;
+            STEP_STAMP(16, l);
+            for (int k = 0; k < count; ++k)
+            {
+                if (k > 0)
+                    __syncthreads(); // the previous token's rows are read out of sh.red
+                combine_parts(sh.comb + k * n, parts, hd, ex + k * tw + a.off_xattn + head * hd, epoch, sh);
+            }
+            STEP_STAMP(17, l);
+        }
+        if (!last_layer && attends && cached > 0)
+            load_keys<kSelfPasses>(self, sh.table[l + 1].self_keys, sh.table[l + 1].self_values, 0, cached, d,
+                                   head * hd, hd);
+        __syncthreads();
+    }
+    return true;
+}
+
 // Final LN of the last layer's output, the tied logits (Decoder/Decoder.cpp
 // :174-176) and this workgroup's top-1 under the mask.
-template <int LWT>
+template <int LWT, int T>
 __device__ __forceinline__ bool final_phase(const StepArgs& a, Shared& sh, Ring& ring, const NormParams& norm,
                                             float& best_v, uint32_t& best_i)
 {
     const int d = a.width;
-    if (!gather_blocked<kPollBlocked>(a.exchange + (size_t) (a.layer_count - 1) * a.layer_words + a.off_h4, d, a.log2_d,
-                                      a.row_groups, sh.raw, a.epoch, a.status, sh))
-        return false;
+    const int count = T == 1 ? 1 : a.token_count;
+    const uint64_t* h4 = a.exchange + (size_t) (a.layer_count - 1) * a.layer_words + a.off_h4;
+    if constexpr (T == 1)
+    {
+        if (!gather_blocked<kPollBlocked>(h4, d, a.log2_d, a.row_groups, sh.raw, a.epoch, a.status, sh))
+            return false;
+    }
+    else
+    {
+        const int stride = a.row_groups, mask = (1 << a.log2_d) - 1;
+        if (!gather_tokens<kPollCombine>(
+                h4, a.token_words, count, stride << a.log2_d,
+                [&](int i, int& offset, int& index) {
+                    offset = i;
+                    index = (i & mask) * stride + (i >> a.log2_d);
+                    return index < d;
+                },
+                sh.raw, [](int k, int i) { return k * kRawStride + i; }, a.epoch, a.status, sh))
+            return false;
+    }
     STEP_STAMP(18, 0);
     // The first logits rows are issued once the last layer's output is in:
     // issued before, they would share the memory pipeline with its polls.
     issue_ring(ring, a, logit_shape(a));
-    layer_norm(norm, d, a.inv_width, a.eps, sh);
+    for (int k = 0; k < count; ++k)
+        layer_norm<T>(norm, d, a.inv_width, a.eps, sh, -1, k);
     if (blockIdx.x == 0)
-        for (int c = threadIdx.x; c < d; c += kThreads)
-            a.hidden[c] = sh.x[c];
-    logits_loop<LWT>(ring, a, logit_shape(a), sh, best_v, best_i);
+        for (int k = 0; k < count; ++k)
+            for (int c = threadIdx.x; c < d; c += kThreads)
+                a.hidden[(size_t) k * d + c] = sh.x[x_at<T>(k, c)];
+    logits_loop<LWT, T>(ring, a, logit_shape(a), sh, count, best_v, best_i);
     STEP_STAMP(19, 0);
     return true;
 }
 
-template <int WT>
+template <int WT, int T>
 __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
 {
     if (threadIdx.x == 0)
         sh.abort = 0;
     const bool row_group = (int) blockIdx.x < a.row_groups;
-    Embedding embed;
+    Embedding<T> embed;
     if (row_group)
-        issue_embedding(embed, a);
+        issue_embedding<T>(embed, a);
     {
         // The layer table, once.
         const int words = a.layer_count * (int) (sizeof(wsp_layer_tensors) / sizeof(uint64_t));
@@ -1898,7 +2269,11 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
     __syncthreads();
     STEP_STAMP(21, 0);
 
-    const bool ok = row_group ? row_group_layers<WT>(a, sh, embed) : head_group_layers(a, sh);
+    bool ok;
+    if constexpr (T == 1)
+        ok = row_group ? row_group_layers<WT, 1>(a, sh, embed) : head_group_layers(a, sh);
+    else
+        ok = row_group ? row_group_layers<WT, T>(a, sh, embed) : head_group_tokens<T>(a, sh);
     if (!ok)
         return;
     // The final norm's parameters are in flight before the last layer's output
@@ -1915,9 +2290,9 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
     bool done;
     switch (a.logits_wdtype)
     {
-        case kF32: done = final_phase<kF32>(a, sh, ring, norm, best_v, best_i); break;
-        case kF16: done = final_phase<kF16>(a, sh, ring, norm, best_v, best_i); break;
-        default: done = final_phase<kBF16>(a, sh, ring, norm, best_v, best_i); break;
+        case kF32: done = final_phase<kF32, T>(a, sh, ring, norm, best_v, best_i); break;
+        case kF16: done = final_phase<kF16, T>(a, sh, ring, norm, best_v, best_i); break;
+        default: done = final_phase<kBF16, T>(a, sh, ring, norm, best_v, best_i); break;
     }
     if (!done)
         return;
@@ -1988,7 +2363,7 @@ __device__ __forceinline__ void step_body(const StepArgs& a, Shared& sh)
     }
 }
 
-template <int WT>
+template <int WT, int T>
 __global__ void __launch_bounds__(kThreads) step_kernel(StepArgs a)
 {
     __shared__ Shared sh;
@@ -1997,7 +2372,7 @@ __global__ void __launch_bounds__(kThreads) step_kernel(StepArgs a)
         (&sh.timeline[0][0])[i] = 0;
     __syncthreads();
 #endif
-    step_body<WT>(a, sh);
+    step_body<WT, T>(a, sh);
 #ifdef WSP_STEP_TIMELINE
     __syncthreads();
     if (a.timeline != nullptr)
@@ -2007,13 +2382,19 @@ __global__ void __launch_bounds__(kThreads) step_kernel(StepArgs a)
 }
 } // namespace
 
-const void* kernel_for(int wdtype)
+const void* kernel_for(int wdtype, bool multi_token)
 {
     switch (wdtype)
     {
-        case kF32: return reinterpret_cast<const void*>(&step_kernel<kF32>);
-        case kF16: return reinterpret_cast<const void*>(&step_kernel<kF16>);
-        default: return reinterpret_cast<const void*>(&step_kernel<kBF16>);
+        case kF32:
+            return multi_token ? reinterpret_cast<const void*>(&step_kernel<kF32, kMaxTokens>)
+                               : reinterpret_cast<const void*>(&step_kernel<kF32, 1>);
+        case kF16:
+            return multi_token ? reinterpret_cast<const void*>(&step_kernel<kF16, kMaxTokens>)
+                               : reinterpret_cast<const void*>(&step_kernel<kF16, 1>);
+        default:
+            return multi_token ? reinterpret_cast<const void*>(&step_kernel<kBF16, kMaxTokens>)
+                               : reinterpret_cast<const void*>(&step_kernel<kBF16, 1>);
     }
 }
 } // namespace wsp::step

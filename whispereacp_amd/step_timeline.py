@@ -155,6 +155,8 @@ def main():
     parser.add_argument("--build", action="store_true", help="build the timeline variant of the library and exit")
     parser.add_argument("--samples", type=int, default=16, help="steps of the sequence whose stamps are recorded")
     parser.add_argument("--steps", type=int, default=224, help="single-token steps in the sequence")
+    parser.add_argument("--tokens", type=int, default=0,
+                        help="record instead one multi-token step of this many tokens (at most 4) at position 0")
     args = parser.parse_args()
 
     sys.path.insert(0, ROOT)
@@ -195,22 +197,40 @@ def main():
     prompt_logits = torch.empty((base, V), dtype=torch.float32, device="cuda")
     logits = torch.empty((1, V), dtype=torch.float32, device="cuda")
 
-    decoder.begin_sequence(to_device(encoder))
-    decoder.step(slots[:base], base, prompt_logits)
-    decoder.argmax(prompt_logits[-1:], 1, V, None, slots[base:base + 1])
-    sampled = sorted({int((i + 0.5) * args.steps / args.samples) for i in range(args.samples)})
     results = []
-    for j in range(1, args.steps + 1):
-        take = (j - 1) in sampled
-        if take:
+    if args.tokens:
+        # Launches of args.tokens tokens at position 0, each recorded alone.
+        n = args.tokens
+        ids = torch.arange(1, n + 1, dtype=torch.int32, device="cuda")
+        out = torch.empty((n, V), dtype=torch.float32, device="cuda")
+        for _ in range(args.samples):
+            decoder.begin_sequence(to_device(encoder))
             torch.cuda.synchronize()
             stamps.zero_()
             set_timeline(stamps.data_ptr())
-        decoder.step_and_sample(slots[base + j - 1:base + j], logits, None, slots[base + j:base + j + 1])
-        if take:
+            decoder.step(ids, n, out)
             torch.cuda.synchronize()
             set_timeline(None)
             results.append(step_table(stamps.cpu().numpy(), shape.layers))
+        what = f"{n}-token launches at position 0, {len(results)} sampled"
+    else:
+        decoder.begin_sequence(to_device(encoder))
+        decoder.step(slots[:base], base, prompt_logits)
+        decoder.argmax(prompt_logits[-1:], 1, V, None, slots[base:base + 1])
+        sampled = sorted({int((i + 0.5) * args.steps / args.samples) for i in range(args.samples)})
+        for j in range(1, args.steps + 1):
+            take = (j - 1) in sampled
+            if take:
+                torch.cuda.synchronize()
+                stamps.zero_()
+                set_timeline(stamps.data_ptr())
+            decoder.step_and_sample(slots[base + j - 1:base + j], logits, None, slots[base + j:base + j + 1])
+            if take:
+                torch.cuda.synchronize()
+                set_timeline(None)
+                results.append(step_table(stamps.cpu().numpy(), shape.layers))
+        positions = [base + j for j in sampled]
+        what = f"{len(results)} steps sampled at positions {positions[0]}..{positions[-1]}"
     assert decoder.device_status() == 0, "the step's watchdog tripped"
 
     hand = {k: float(np.mean([r[0][k] for r in results])) for k in results[0][0]}
@@ -219,10 +239,8 @@ def main():
     tail = {k: float(np.mean([r[3][k] for r in results])) for k in results[0][3]}
     whole = float(np.mean([r[4] for r in results]))
     counts = results[0][5]
-    positions = [base + j for j in sampled]
 
-    print(f"Small decoder step on the timeline build, {len(results)} steps sampled at positions "
-          f"{positions[0]}..{positions[-1]}; {workgroups} workgroups: {counts['row']} row groups "
+    print(f"Small decoder step on the timeline build, {what}; {workgroups} workgroups: {counts['row']} row groups "
           f"({counts['task']} with a cross-attention task), {counts['attend']} attending head groups, "
           f"{counts['combine']} combining. Times in microseconds, averaged over the layers and the sampled "
           f"steps.\n")
