@@ -240,7 +240,7 @@ struct Shared
     float comb[kMaxCombine];             // attention partials being combined
     float red[kWaves][kMaxHeadWidth];    // per-wave value rows of an attention chunk
     float q[kMaxTokens * kQStride];      // a head's query, then (self-attention) its new key and value
-    float scratch[2][kWaves];            // per-wave maxima and sums of an attention chunk
+    float scratch[kMaxTokens][2][kWaves]; // per-wave maxima and sums of an attention chunk, per query
     float fold[kWaves][kMaxTokens][2];   // per-wave sums of (x - K) and (x - K)^2 of a folded LayerNorm
     alignas(16) float part[kMaxTokens * kRowGroups]; // per-row-group partial sums of a projection pass
     float best_v[kRowGroups];
@@ -248,6 +248,7 @@ struct Shared
     int abort;
     alignas(16) float raw[kMaxTokens * kRawStride]; // the residual stream as gathered (un-normalised)
     alignas(16) float x[kXFloats];                  // the current phase's input vectors
+    float red_more[kMaxTokens - 1][kWaves][kMaxHeadWidth]; // red for the queries of tokens 1.. (multi-token)
 #ifdef WSP_STEP_TIMELINE
     uint64_t timeline[kTimelineEvents][kTimelineLayers];
     int mark_layer;
@@ -684,7 +685,7 @@ __device__ __forceinline__ void norm_row(const NormParams& p, int n, float inv_n
         float4v y;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-            y[c] = (x[c] - mean) * scale * p.g[c] + p.b[c];
+            y[c] = __builtin_fmaf((x[c] - mean) * scale, p.g[c], p.b[c]);
         // (own is a multiple of 4: its run sits inside one block of eight.)
         *reinterpret_cast<float4v*>(&out[XB == 8 ? own : (own >> 3) * XB + (own & 7)]) = y;
     }
@@ -870,7 +871,7 @@ __device__ __forceinline__ bool gather_fold(const uint64_t* base, int token_word
                         sh.raw[tok * kRawStride + index[k]] = value;
                         sh.x[x_at<T>(tok, index[k])] = fp.gamma[c * kPollBlocked + k] * dx;
                         sums[tok].s1 += dx;
-                        sums[tok].s2 += dx * dx;
+                        sums[tok].s2 = __builtin_fmaf(dx, dx, sums[tok].s2);
                     }
         }
     }
@@ -971,9 +972,9 @@ __device__ __forceinline__ int phase_row(const PhaseShape& ps, int group, int st
 // This row group's (row, first chunk, end chunk) in `pass`; false when it has
 // no task (then the dummy row 0, chunks [0, 0)).
 __device__ __forceinline__ bool phase_task(const PhaseShape& ps, int group, int stride, int pass, int& row,
-                                           int& first, int& last)
+                                           int& first, int& last, int tid = threadIdx.x)
 {
-    const int task = pass * kRowGroups + (int) (threadIdx.x / kRowLanes);
+    const int task = pass * kRowGroups + tid / kRowLanes;
     if (task >= (ps.local_rows << ps.slice_log2))
     {
         row = 0;
@@ -991,9 +992,10 @@ __device__ __forceinline__ bool phase_task(const PhaseShape& ps, int group, int 
 // past `last` load the run's first chunk again. The matrix base is uniform
 // and every byte offset fits 32 bits (a matrix is far below 4 GiB), so each
 // load takes a scalar base and one 32-bit offset register.
-__device__ __forceinline__ void load_run(RowLoad& r, const void* weight, int row, int row_bytes, int first, int last)
+__device__ __forceinline__ void load_run(RowLoad& r, const void* weight, int row, int row_bytes, int first, int last,
+                                         int tid = threadIdx.x)
 {
-    const int lane = threadIdx.x & (kRowLanes - 1);
+    const int lane = tid & (kRowLanes - 1);
     const char* base = uniform(static_cast<const char*>(weight));
     const uint32_t row_offset = (uint32_t) row * (uint32_t) row_bytes;
 #pragma unroll
@@ -1049,13 +1051,15 @@ template <int WT>
 __device__ __forceinline__ float chunk_dot(const ChunkWeights<WT>& c, const float* x)
 {
     float acc = 0.f;
+    // Fused multiply-adds written out, so every kernel that inlines this
+    // rounds alike.
     if constexpr (WT == kF32)
     {
         const float4v xv = *reinterpret_cast<const float4v*>(x);
-        acc += xv[0] * c.w[0];
-        acc += xv[1] * c.w[1];
-        acc += xv[2] * c.w[2];
-        acc += xv[3] * c.w[3];
+        acc = __builtin_fmaf(xv[0], c.w[0], acc);
+        acc = __builtin_fmaf(xv[1], c.w[1], acc);
+        acc = __builtin_fmaf(xv[2], c.w[2], acc);
+        acc = __builtin_fmaf(xv[3], c.w[3], acc);
     }
     else
     {
@@ -1063,14 +1067,14 @@ __device__ __forceinline__ float chunk_dot(const ChunkWeights<WT>& c, const floa
         const float4v xb = *reinterpret_cast<const float4v*>(x + 4);
         // Two chains of four (even and odd weights), added at the end.
         float odd = 0.f;
-        acc += xa[0] * c.w[0];
-        odd += xa[1] * c.w[1];
-        acc += xa[2] * c.w[2];
-        odd += xa[3] * c.w[3];
-        acc += xb[0] * c.w[4];
-        odd += xb[1] * c.w[5];
-        acc += xb[2] * c.w[6];
-        odd += xb[3] * c.w[7];
+        acc = __builtin_fmaf(xa[0], c.w[0], acc);
+        odd = __builtin_fmaf(xa[1], c.w[1], odd);
+        acc = __builtin_fmaf(xa[2], c.w[2], acc);
+        odd = __builtin_fmaf(xa[3], c.w[3], odd);
+        acc = __builtin_fmaf(xb[0], c.w[4], acc);
+        odd = __builtin_fmaf(xb[1], c.w[5], odd);
+        acc = __builtin_fmaf(xb[2], c.w[6], acc);
+        odd = __builtin_fmaf(xb[3], c.w[7], odd);
         acc += odd;
     }
     return acc;
@@ -1117,23 +1121,25 @@ struct Prefetch
 // A finishing thread's local row: thread t finishes row t % rows_per_pass of
 // its pass for token t / rows_per_pass (rows_per_pass is a power of two).
 template <int T>
-__device__ __forceinline__ int finisher_local(const PhaseShape& ps)
+__device__ __forceinline__ int finisher_local(const PhaseShape& ps, int tid = threadIdx.x)
 {
-    return T == 1 ? (int) threadIdx.x : (int) threadIdx.x & (ps.rows_per_pass - 1);
+    return T == 1 ? tid : tid & (ps.rows_per_pass - 1);
 }
 
 template <bool FOLD, int T = 1>
 __device__ __forceinline__ void prefetch(Prefetch& p, const void* weight, const float* bias, const float* gain,
                                          const PhaseShape& ps, int group, int stride)
 {
-    int row, first, last;
-    phase_task(ps, group, stride, 0, row, first, last);
-    // With several tokens the chunk offsets are recomputed at each phase
-    // rather than held across the layer loop (registers are short there).
+    // With several tokens the task's offsets are recomputed at each phase
+    // (from an opaque copy of the thread index) rather than held across the
+    // layer loop, where registers are short.
+    int tid = threadIdx.x;
     if constexpr (T > 1)
-        asm volatile("" : "+v"(row), "+v"(first));
-    load_run(p.r, weight, row, ps.row_bytes, first, last);
-    const int finisher_row = min(phase_row(ps, group, stride, finisher_local<T>(ps)), ps.rows - 1);
+        asm volatile("" : "+v"(tid));
+    int row, first, last;
+    phase_task(ps, group, stride, 0, row, first, last, tid);
+    load_run(p.r, weight, row, ps.row_bytes, first, last, tid);
+    const int finisher_row = min(phase_row(ps, group, stride, finisher_local<T>(ps, tid)), ps.rows - 1);
     // The load is issued whether or not the phase has a bias (a phase without
     // one reads a weight word and drops it): the compiler counts outstanding
     // loads per program point, and a load skipped on some path makes every
@@ -1198,10 +1204,13 @@ __device__ __forceinline__ void finish_pass(const float (&acc)[T], bool has_task
             sh.part[k * kRowGroups + threadIdx.x / kRowLanes] = total;
     }
     __syncthreads();
-    const int lr = finisher_local<T>(ps);
-    const int token = T == 1 ? 0 : (int) threadIdx.x / ps.rows_per_pass;
+    int tid = threadIdx.x;
+    if constexpr (T > 1)
+        asm volatile("" : "+v"(tid)); // recomputed here, not held across the layer loop
+    const int lr = finisher_local<T>(ps, tid);
+    const int token = T == 1 ? 0 : tid / ps.rows_per_pass;
     const int local = pass * ps.rows_per_pass + lr;
-    if ((T == 1 ? (int) threadIdx.x < ps.rows_per_pass : token < count) && local < ps.local_rows)
+    if ((T == 1 ? tid < ps.rows_per_pass : token < count) && local < ps.local_rows)
     {
         const float v = slice_total(sh, token, lr, ps.slice_log2);
         const int r = phase_row(ps, group, stride, local);
@@ -1248,7 +1257,7 @@ __device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight,
             rstd = k == i ? r : rstd;
             dmean = k == i ? m : dmean;
         }
-        return FOLD ? rstd * (v - dmean * g) + b : v + b;
+        return FOLD ? __builtin_fmaf(rstd, __builtin_fmaf(-dmean, g, v), b) : v + b;
     };
     STEP_MARK(mark);
     if (ps.passes > 0)
@@ -1285,6 +1294,23 @@ constexpr float kLog2e = 1.44269504088896340736f;
 __device__ __forceinline__ float exp2_weight(float x)
 {
     return __builtin_amdgcn_exp2f(x);
+}
+
+// q . k over a lane's four channels, and acc += e * v, with the fused
+// multiply-adds written out: the single- and multi-token kernels then round
+// alike (the compiler's own contraction could pair the products differently
+// in each).
+__device__ __forceinline__ float dot4(const float4v& q, const float4v& k)
+{
+    return __builtin_fmaf(q[0], k[0], q[1] * k[1]) + __builtin_fmaf(q[2], k[2], q[3] * k[3]);
+}
+
+__device__ __forceinline__ void add_scaled(float4v& acc, float e, const float4v& v)
+{
+    acc[0] = __builtin_fmaf(e, v[0], acc[0]);
+    acc[1] = __builtin_fmaf(e, v[1], acc[1]);
+    acc[2] = __builtin_fmaf(e, v[2], acc[2]);
+    acc[3] = __builtin_fmaf(e, v[3], acc[3]);
 }
 
 template <int NP>
@@ -1327,6 +1353,9 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
                                        uint32_t epoch, Shared& sh, bool normalized = false, int mark = -1,
                                        const float* query = nullptr)
 {
+    // No contraction beyond the fused multiply-adds written out: the single-
+    // and multi-token kernels must round every token alike.
+#pragma clang fp contract(off)
     const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const bool live = 4 * kl < head_width;
@@ -1341,8 +1370,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
         s[p] = -INFINITY;
         if (kKeySlots * p < count) // uniform: passes past the keys are skipped
         {
-            const float part =
-                live ? (qv[0] * kr.k[p][0] + qv[1] * kr.k[p][1]) + (qv[2] * kr.k[p][2] + qv[3] * kr.k[p][3]) : 0.f;
+            const float part = live ? dot4(qv, kr.k[p]) : 0.f;
             s[p] = scale2 * sum16(part);
             if (ks + kKeySlots * p < count)
                 local_max = fmaxf(local_max, s[p]);
@@ -1360,10 +1388,7 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
             const float e = exp2_weight(s[p] - m);
             if (kl == 0)
                 local_sum += e;
-            acc[0] += e * kr.v[p][0];
-            acc[1] += e * kr.v[p][1];
-            acc[2] += e * kr.v[p][2];
-            acc[3] += e * kr.v[p][3];
+            add_scaled(acc, e, kr.v[p]);
         }
     }
     // Fold the wave's four key slots (lanes 16 apart) with the neighbouring
@@ -1378,8 +1403,8 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
         *reinterpret_cast<float4v*>(&sh.red[wave][4 * kl]) = acc;
     if (lane == 0)
     {
-        sh.scratch[0][wave] = m;
-        sh.scratch[1][wave] = local_sum;
+        sh.scratch[0][0][wave] = m;
+        sh.scratch[0][1][wave] = local_sum;
     }
     __syncthreads();
     STEP_MARK(mark < 0 ? -1 : mark + 2);
@@ -1389,8 +1414,8 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
         {
-            mw[w] = sh.scratch[0][w];
-            lw[w] = sh.scratch[1][w];
+            mw[w] = sh.scratch[0][0][w];
+            lw[w] = sh.scratch[0][1][w];
             rw[w] = sh.red[w][threadIdx.x];
         }
         static_assert(kWaves == 8, "three-level trees over the waves");
@@ -1410,6 +1435,125 @@ __device__ __forceinline__ void attend(const KeyRows<NP>& kr, int count, int hea
         {
             put(out, count > 0 ? top : -INFINITY, epoch);
             put(out + 1, l, epoch);
+        }
+    }
+}
+
+// Token k's per-wave rows of an attention chunk.
+__device__ __forceinline__ float (*red_of(Shared& sh, int k))[kMaxHeadWidth]
+{
+    return k == 0 ? sh.red : sh.red_more[k - 1];
+}
+
+// attend() for the queries of Q tokens over the same keys (a cross-attention
+// chunk of a multi-token launch): token k's query at query + k * kQStride,
+// its (max, sum, row) at out + k * out_stride, for the first `tokens` tokens.
+// Every key register is used for all Q queries, and the Q chains of
+// reductions run side by side; each token's arithmetic is attend()'s.
+template <int NP, int Q>
+__device__ __forceinline__ void attend_tokens(const KeyRows<NP>& kr, int count, int tokens, int head_width,
+                                              float scale2, uint64_t* out, int out_stride, uint32_t epoch, Shared& sh,
+                                              const float* query)
+{
+    // No contraction beyond the fused multiply-adds written out: the single-
+    // and multi-token kernels must round every token alike.
+#pragma clang fp contract(off)
+    const int kl = threadIdx.x % kKeyLanes, ks = threadIdx.x / kKeyLanes;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const bool live = 4 * kl < head_width;
+    float4v qv[Q];
+#pragma unroll
+    for (int k = 0; k < Q; ++k)
+    {
+        qv[k] = float4v {0.f, 0.f, 0.f, 0.f};
+        if (live)
+            qv[k] = *reinterpret_cast<const float4v*>(query + k * kQStride + 4 * kl);
+    }
+    float s[NP][Q];
+    float local_max[Q];
+#pragma unroll
+    for (int k = 0; k < Q; ++k)
+        local_max[k] = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int k = 0; k < Q; ++k)
+        {
+            s[p][k] = -INFINITY;
+            if (kKeySlots * p < count) // uniform: passes past the keys are skipped
+            {
+                const float part = live ? dot4(qv[k], kr.k[p]) : 0.f;
+                s[p][k] = scale2 * sum16(part);
+                if (ks + kKeySlots * p < count)
+                    local_max[k] = fmaxf(local_max[k], s[p][k]);
+            }
+        }
+    float m[Q], local_sum[Q];
+    float4v acc[Q];
+#pragma unroll
+    for (int k = 0; k < Q; ++k)
+    {
+        m[k] = max64(local_max[k]);
+        local_sum[k] = 0.f;
+        acc[k] = float4v {0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+        if (kKeySlots * p < count && ks + kKeySlots * p < count)
+#pragma unroll
+            for (int k = 0; k < Q; ++k)
+            {
+                const float e = exp2_weight(s[p][k] - m[k]);
+                if (kl == 0)
+                    local_sum[k] += e;
+                add_scaled(acc[k], e, kr.v[p]);
+            }
+#pragma unroll
+    for (int k = 0; k < Q; ++k)
+    {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            acc[k][i] = add32(add16(acc[k][i]));
+        local_sum[k] = add32(add16(local_sum[k]));
+        if (lane < kKeyLanes && live)
+            *reinterpret_cast<float4v*>(&red_of(sh, k)[wave][4 * kl]) = acc[k];
+        if (lane == 0)
+        {
+            sh.scratch[k][0][wave] = m[k];
+            sh.scratch[k][1][wave] = local_sum[k];
+        }
+    }
+    __syncthreads();
+    // Thread k * head_width + c folds channel c of token k (head_width is a
+    // power of two here).
+    const int k = (int) threadIdx.x / head_width, c = (int) threadIdx.x & (head_width - 1);
+    if (k < tokens)
+    {
+        float mw[kWaves], lw[kWaves], rw[kWaves];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+        {
+            mw[w] = sh.scratch[k][0][w];
+            lw[w] = sh.scratch[k][1][w];
+            rw[w] = red_of(sh, k)[w][c];
+        }
+        const float top = fmaxf(fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3])),
+                                fmaxf(fmaxf(mw[4], mw[5]), fmaxf(mw[6], mw[7])));
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+        {
+            const float f = lw[w] == 0.f ? 0.f : exp2_weight(mw[w] - top); // a wave without keys adds nothing
+            lw[w] *= f;
+            rw[w] *= f;
+        }
+        const float l = ((lw[0] + lw[1]) + (lw[2] + lw[3])) + ((lw[4] + lw[5]) + (lw[6] + lw[7]));
+        const float row = ((rw[0] + rw[1]) + (rw[2] + rw[3])) + ((rw[4] + rw[5]) + (rw[6] + rw[7]));
+        uint64_t* o = out + k * out_stride;
+        put(o + 2 + c, row, epoch);
+        if (c == 0)
+        {
+            put(o, count > 0 ? top : -INFINITY, epoch);
+            put(o + 1, l, epoch);
         }
     }
 }
@@ -1444,6 +1588,9 @@ __device__ __forceinline__ float combine(const float* part, int parts, int strid
 __device__ __forceinline__ void combine_parts(const float* part, int parts, int head_width, uint64_t* out,
                                               uint32_t epoch, Shared& sh)
 {
+    // No contraction beyond the fused multiply-adds written out: the single-
+    // and multi-token kernels must round every token alike.
+#pragma clang fp contract(off)
     const int stride = head_width + 2;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const float m = lane < parts ? part[lane * stride] : -INFINITY;
@@ -1455,7 +1602,8 @@ __device__ __forceinline__ void combine_parts(const float* part, int parts, int 
     {
         float acc = 0.f;
         for (int i = wave; i < parts; i += kWaves) // i is uniform over the wave
-            acc += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(factor), i)) * part[i * stride + 2 + lane];
+            acc = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(factor), i)),
+                                 part[i * stride + 2 + lane], acc);
         sh.red[wave][lane] = acc;
     }
     __syncthreads();
@@ -1467,6 +1615,59 @@ __device__ __forceinline__ void combine_parts(const float* part, int parts, int 
             r[w] = sh.red[w][threadIdx.x];
         const float numerator = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
         put(out + threadIdx.x, numerator * __builtin_amdgcn_rcpf(denominator), epoch);
+    }
+}
+
+// combine_parts for the first `count` tokens of a T-token launch at once:
+// token k's partials at comb + k * n, its row to out + k * out_stride. The
+// waves split over the tokens (kWaves / T each); each wave folds the partials
+// of the "virtual waves" v = its index within the token + (kWaves / T) j,
+// partial i going to virtual wave i % kWaves as in combine_parts, so every
+// token's sums run in combine_parts' order.
+template <int T>
+__device__ __forceinline__ void combine_tokens(const float* comb, int n, int parts, int head_width, uint64_t* out,
+                                               int out_stride, int count, uint32_t epoch, Shared& sh)
+{
+    // No contraction beyond the fused multiply-adds written out: the single-
+    // and multi-token kernels must round every token alike.
+#pragma clang fp contract(off)
+    static_assert(kWaves % T == 0, "whole waves per token");
+    constexpr int kPer = kWaves / T;
+    const int stride = head_width + 2;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int k = wave / kPer, sub = wave % kPer;
+    const bool active = k < count; // a token past the launch's reads nothing
+    const float* part = comb + (active ? k : 0) * n;
+    const float m = active && lane < parts ? part[lane * stride] : -INFINITY;
+    const float l = active && lane < parts ? part[lane * stride + 1] : 0.f;
+    const float largest = max64(m);
+    const float factor = l == 0.f ? 0.f : exp2_weight(m - largest);
+    const float denominator = sum64(factor * l);
+    if (active && lane < head_width)
+    {
+#pragma unroll
+        for (int j = 0; j < T; ++j)
+        {
+            const int v = sub + kPer * j; // kPer * T = kWaves virtual waves per token
+            float acc = 0.f;
+            for (int i = v; i < parts; i += kWaves) // i is uniform over the wave
+                acc = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(factor), i)),
+                                 part[i * stride + 2 + lane], acc);
+            red_of(sh, k)[v][lane] = acc;
+        }
+    }
+    if (lane == 0 && sub == 0)
+        sh.scratch[k][0][0] = denominator;
+    __syncthreads();
+    const int kk = (int) threadIdx.x / head_width, c = (int) threadIdx.x & (head_width - 1);
+    if (kk < count && kk < T)
+    {
+        float r[kWaves];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+            r[w] = red_of(sh, kk)[w][c];
+        const float numerator = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        put(out + kk * out_stride + c, numerator * __builtin_amdgcn_rcpf(sh.scratch[kk][0][0]), epoch);
     }
 }
 
@@ -1736,6 +1937,54 @@ __device__ __forceinline__ bool gather_tokens(const uint64_t* base, int token_wo
     return true;
 }
 
+// Tokens [k0, k0 + TT) (those below `count`) of an n-slot vector each,
+// slots [first, first + PT * 448) of it, polled in one round of TT * PT words
+// per thread: slot j of a token is word map(j, offset, index) of that token's
+// vector (token_words apart from base) and lands in dst[place(token, index)].
+template <int PT, int TT, class Map, class Place>
+__device__ __forceinline__ bool gather_token_block(const uint64_t* base, int token_words, int k0, int count, int n,
+                                                   Map map, float* dst, Place place, uint32_t epoch, int* status,
+                                                   Shared& sh, int first = 0)
+{
+    bool failed = false;
+    if (threadIdx.x < kWave)
+        __builtin_amdgcn_s_waitcnt(0); // wave 0 stored the last phase's outputs: it only waits for them
+    else
+    {
+        int t = threadIdx.x - kWave;
+        asm volatile("" : "+v"(t)); // offsets recomputed per call, not held across the layer loop
+        uint32_t pending = 0;
+#pragma unroll
+        for (int k = 0; k < TT; ++k)
+#pragma unroll
+            for (int j = 0; j < PT; ++j)
+            {
+                const int slot = first + t + j * kPollThreads;
+                int offset, index;
+                if (k0 + k < count && slot < n && map(slot, offset, index))
+                    pending |= 1u << (k * PT + j);
+            }
+        failed = !poll_words<TT * PT, false>(
+            base,
+            [&](int w) {
+                const int slot = first + t + (w % PT) * kPollThreads;
+                int offset = 0, index;
+                const bool used = slot < n && map(slot, offset, index);
+                return (k0 + w / PT) * token_words + (used ? offset : 0);
+            },
+            pending, epoch, status,
+            [&](int w, float v) {
+                int offset, index;
+                map(first + t + (w % PT) * kPollThreads, offset, index);
+                dst[place(k0 + w / PT, index)] = v;
+            });
+    }
+    if (failed)
+        sh.abort = 1;
+    __syncthreads();
+    return sh.abort == 0;
+}
+
 template <int WT, int T>
 __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, const Embedding<T>& embed)
 {
@@ -1806,7 +2055,7 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
                     sh.raw[t * kRawStride + c] = x;
                     sh.x[x_at<T>(t, c)] = gamma[k] * x;
                     sums[t].s1 += x;
-                    sums[t].s2 += x * x;
+                    sums[t].s2 = __builtin_fmaf(x, x, sums[t].s2);
                 }
             }
         }
@@ -1872,8 +2121,11 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
                                             : poll<3>(ex + a.off_self, d, map, sh.x, epoch, a.status, sh)))
                     return false;
             }
-            else if (!gather_tokens<kPollCombine>(ex + a.off_self, tw, count, d, map, sh.x, x_at<T>, epoch,
-                                                  a.status, sh))
+            else if (!(d <= 2 * kPollThreads
+                           ? gather_token_block<2, T>(ex + a.off_self, tw, 0, count, d, map, sh.x, x_at<T>, epoch,
+                                                      a.status, sh)
+                           : gather_token_block<3, T>(ex + a.off_self, tw, 0, count, d, map, sh.x, x_at<T>, epoch,
+                                                      a.status, sh)))
                 return false;
             STEP_STAMP(2, l);
         }
@@ -1941,16 +2193,11 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
                 return false;
             if (t == task)
                 STEP_STAMP(6, l);
-#pragma unroll
-            for (int k = 0; k < T; ++k)
-                if (T == 1 || k < count)
-                {
-                    if (k > 0)
-                        __syncthreads(); // the previous token's rows are read out of sh.red
-                    attend<kCrossPasses>(cross, keys, hd, a.scale * kLog2e,
-                                         ex + k * tw + a.off_xpart + (size_t) (h * a.cross_splits + s) * (hd + 2),
-                                         epoch, sh, false, t == task && k == 0 ? 22 : -1, sh.q + k * kQStride);
-                }
+            uint64_t* part = ex + a.off_xpart + (size_t) (h * a.cross_splits + s) * (hd + 2);
+            if constexpr (T == 1)
+                attend<kCrossPasses>(cross, keys, hd, a.scale * kLog2e, part, epoch, sh, false, t == task ? 22 : -1);
+            else
+                attend_tokens<kCrossPasses, T>(cross, keys, count, hd, a.scale * kLog2e, part, tw, epoch, sh, sh.q);
         }
         STEP_STAMP(7, l);
 
@@ -1960,14 +2207,19 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
             if (!gather_any(ex + a.off_xattn, d, sh.x, epoch, a.status, sh))
                 return false;
         }
-        else if (!gather_tokens<kPollCombine>(
-                     ex + a.off_xattn, tw, count, d,
-                     [](int i, int& offset, int& index) {
-                         offset = index = i;
-                         return true;
-                     },
-                     sh.x, x_at<T>, epoch, a.status, sh))
-            return false;
+        else
+        {
+            auto map = [](int i, int& offset, int& index) {
+                offset = index = i;
+                return true;
+            };
+            if (!(d <= 2 * kPollThreads
+                      ? gather_token_block<2, T>(ex + a.off_xattn, tw, 0, count, d, map, sh.x, x_at<T>, epoch,
+                                                 a.status, sh)
+                      : gather_token_block<3, T>(ex + a.off_xattn, tw, 0, count, d, map, sh.x, x_at<T>, epoch,
+                                                 a.status, sh)))
+                return false;
+        }
         STEP_STAMP(8, l);
         {
             uint64_t* out = ex + a.off_h3;
@@ -2008,12 +2260,18 @@ __device__ __forceinline__ bool row_group_layers(const StepArgs& a, Shared& sh, 
         }
         else
         {
-            // Token after token: each token's vector is one round of eight
-            // loads per thread, which arrive together once the first has.
-            for (int k = 0; k < count; ++k)
-                if (!gather_words<kPollBlockedFF>(ex + k * tw + a.off_ff, f, a.log2_f, stride, sh.x, epoch, a.status,
-                                                  sh, [k](int i) { return x_at<T>(k, i); }))
-                    return false;
+            // Two tokens a round of sixteen words per thread.
+            const int mask = (1 << a.log2_f) - 1, slots = stride << a.log2_f;
+            auto map = [&](int i, int& offset, int& index) {
+                offset = i;
+                index = (i & mask) * stride + (i >> a.log2_f);
+                return index < f;
+            };
+            for (int k = 0; k < count; k += 2)
+                for (int first = 0; first < slots; first += kPollBlockedFF * kPollThreads)
+                    if (!gather_token_block<kPollBlockedFF, 2>(ex + a.off_ff, tw, k, count, slots, map, sh.x,
+                                                               x_at<T>, epoch, a.status, sh, first))
+                        return false;
         }
         STEP_STAMP(12, l);
         {
@@ -2191,12 +2449,7 @@ __device__ __forceinline__ bool head_group_tokens(const StepArgs& a, Shared& sh)
                     sh.comb, [n](int k, int i) { return k * n + i; }, epoch, a.status, sh))
                 return false;
             STEP_STAMP(16, l);
-            for (int k = 0; k < count; ++k)
-            {
-                if (k > 0)
-                    __syncthreads(); // the previous token's rows are read out of sh.red
-                combine_parts(sh.comb + k * n, parts, hd, ex + k * tw + a.off_xattn + head * hd, epoch, sh);
-            }
+            combine_tokens<T>(sh.comb, n, parts, hd, ex + a.off_xattn + head * hd, tw, count, epoch, sh);
             STEP_STAMP(17, l);
         }
         if (!last_layer && attends && cached > 0)
@@ -2224,14 +2477,18 @@ __device__ __forceinline__ bool final_phase(const StepArgs& a, Shared& sh, Ring&
     else
     {
         const int stride = a.row_groups, mask = (1 << a.log2_d) - 1;
-        if (!gather_tokens<kPollCombine>(
-                h4, a.token_words, count, stride << a.log2_d,
-                [&](int i, int& offset, int& index) {
-                    offset = i;
-                    index = (i & mask) * stride + (i >> a.log2_d);
-                    return index < d;
-                },
-                sh.raw, [](int k, int i) { return k * kRawStride + i; }, a.epoch, a.status, sh))
+        auto map = [&](int i, int& offset, int& index) {
+            offset = i;
+            index = (i & mask) * stride + (i >> a.log2_d);
+            return index < d;
+        };
+        auto place = [](int k, int i) { return k * kRawStride + i; };
+        const int slots = stride << a.log2_d;
+        if (!(slots <= 2 * kPollThreads
+                  ? gather_token_block<2, T>(h4, a.token_words, 0, count, slots, map, sh.raw, place, a.epoch,
+                                             a.status, sh)
+                  : gather_token_block<4, T>(h4, a.token_words, 0, count, slots, map, sh.raw, place, a.epoch,
+                                             a.status, sh)))
             return false;
     }
     STEP_STAMP(18, 0);
