@@ -344,10 +344,16 @@ def bench_single(args, w):
     base = len(prompt)
 
     def open_sequence():
+        """begin_sequence and the prefix in one step; returns the event pair
+        around the prefix step."""
         slots[:base] = torch.tensor(prompt, dtype=torch.int32, device="cuda")
         decoder.begin_sequence(enc)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
         decoder.step(slots[:base], base, prompt_logits)
+        stop.record()
         decoder.argmax(prompt_logits[-1:], 1, V, None, slots[base:base + 1])
+        return start, stop
 
     def one_step(j):
         # step j (1-based) reads the token at position base + j - 1
@@ -368,9 +374,11 @@ def bench_single(args, w):
     timed = list(range(first_timed, first_timed + args.steps))
 
     def timed_run():
-        """One whole sequence; returns (ms per timed step, tokens, host s, enqueue s)."""
-        open_sequence()
+        """One whole sequence; returns (ms per timed step, tokens, host s,
+        enqueue s, prefix step ms)."""
+        prefix = open_sequence()
         torch.cuda.synchronize()
+        prefix_ms = prefix[0].elapsed_time(prefix[1])
         host0 = time.perf_counter()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         for j in range(1, total + 1):
@@ -384,7 +392,7 @@ def bench_single(args, w):
         host = time.perf_counter() - host0
         check_watchdog(decoder, "timed region")
         gpu_ms = start.elapsed_time(stop)
-        return gpu_ms / args.steps, slots[base:base + total + 1].cpu().numpy().tolist(), host, enqueue
+        return gpu_ms / args.steps, slots[base:base + total + 1].cpu().numpy().tolist(), host, enqueue, prefix_ms
 
     print(f"[bench] timed region: {args.runs} runs", file=sys.stderr, flush=True)
     runs = [timed_run() for _ in range(args.runs)]
@@ -438,6 +446,8 @@ def bench_single(args, w):
                      "bytes_per_step": round(bytes_per_step)},
         "cpu_baseline": baseline,
         "parity": parity,
+        "prefix_step": {"tokens": base, "ms": round(statistics.median(r[4] for r in runs), 4),
+                        "note": "the 4-token prefix as one decoder step (one multi-token launch), median of the runs"},
         "runs": run_summary(run_ms),
         "host_seconds": round(host_s, 4),
         "host_enqueue_seconds": round(enqueue_s, 4),

@@ -13,6 +13,10 @@ issue, averaged over the layers and the sampled steps.
 
     python -m whispereacp_amd.step_timeline --build     # on the build host
     python -m whispereacp_amd.step_timeline             # on the GPU
+    python -m whispereacp_amd.step_timeline --tokens 4  # one 4-token launch instead
+
+With --tokens N the tool records launches of the multi-token kernel (N tokens
+at position 0, without the fused argmax) instead of single-token steps.
 
 The stamps cost a few instructions each, so the step runs a little slower
 under this variant than in the product build; the table is for the shape of
@@ -132,19 +136,26 @@ def step_table(stamps, layers):
         "slowest logits workgroup": np.max(t[everyone, LOGITS_DONE, 0] - t[everyone, FINAL_IN, 0]),
         "row groups' imbalance (last row group of a workgroup, median)": np.median(
             t[everyone, LOGITS_ALL, 0] - t[everyone, LOGITS_DONE, 0]),
-        "last workgroup done -> fold sees every candidate": float(np.max(t[:, CANDIDATES_IN, 0]))
-        - np.max(t[everyone, LOGITS_ALL, 0]),
-        "fold -> token written": float(np.max(t[:, ARGMAX_DONE, 0])) - float(np.max(t[:, CANDIDATES_IN, 0])),
-        "argmax fold (last candidate -> token)": float(np.max(t[:, ARGMAX_DONE, 0]))
-        - np.max(t[everyone, LOGITS_DONE, 0]),
     }
     start = np.median(t[r["row"], TABLE_DONE, 0])
-    whole = float(np.max(t[:, ARGMAX_DONE, 0])) - start
+    if np.max(stamps[:, ARGMAX_DONE, 0]) != 0:
+        tail["last workgroup done -> fold sees every candidate"] = (float(np.max(t[:, CANDIDATES_IN, 0]))
+                                                                   - np.max(t[everyone, LOGITS_ALL, 0]))
+        tail["fold -> token written"] = float(np.max(t[:, ARGMAX_DONE, 0])) - float(np.max(t[:, CANDIDATES_IN, 0]))
+        tail["argmax fold (last candidate -> token)"] = (float(np.max(t[:, ARGMAX_DONE, 0]))
+                                                         - np.max(t[everyone, LOGITS_DONE, 0]))
+        whole = float(np.max(t[:, ARGMAX_DONE, 0])) - start
+    else:
+        # A step without the fused argmax (a multi-token step) ends with its logits.
+        whole = float(np.max(t[everyone, LOGITS_ALL, 0])) - start
     inside = {}
     for label, role, parts in INSIDE:
         for part, se, ee in parts:
-            inside[(label, part)] = float(np.mean([np.median(t[r[role], ee, l] - t[r[role], se, l])
-                                                   for l in range(layers)]))
+            # (a part the kernel does not mark, e.g. inside a multi-token
+            # cross-attention chunk, is left out)
+            if np.all(stamps[r[role], se, :layers] != 0) and np.all(stamps[r[role], ee, :layers] != 0):
+                inside[(label, part)] = float(np.mean([np.median(t[r[role], ee, l] - t[r[role], se, l])
+                                                       for l in range(layers)]))
     return ({k: float(np.mean(v)) for k, v in hand.items()}, {k: float(np.mean(v)) for k, v in phase.items()},
             float(np.mean(layer_time)), {k: float(v) for k, v in tail.items()}, whole,
             {k: len(v) for k, v in r.items()}, inside)
@@ -258,7 +269,8 @@ def main():
     print("|---|---|")
     for k, v in tail.items():
         print(f"| {k} | {v:.2f} |")
-    print(f"\nWhole step (layer table loaded -> token written), timeline build: {whole:.1f} us.")
+    end = "token written" if not args.tokens else "last logits row written"
+    print(f"\nWhole step (layer table loaded -> {end}), timeline build: {whole:.1f} us.")
     inside = {k: float(np.mean([r[6][k] for r in results])) for k in results[0][6]}
     print("\nInside the phases (median workgroup of the phase's role, us):\n")
     print("| Phase | Part | us |")
