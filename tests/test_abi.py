@@ -147,6 +147,20 @@ def test_net_refusals_without_a_device():
     assert result.stdout.count("ok ") == 7, result.stdout
 
 
+def test_batch_split_sizing_and_refusals_on_the_host():
+    # The batched step's split products refuse a launch whose partials or
+    # counters would overflow the buffers reserved at create; the sizing rule
+    # and the refusal are host code (csrc/batch_plan.h), checked here on the
+    # CPU under ASan/UBSan: every planned launch fits, one column group, row
+    # tile or split more does not.
+    import subprocess
+    path = os.path.join(ROOT, "tests", "native", "_build", "batch_plan_check")
+    subprocess.run(["make", "-s", "_build/batch_plan_check"], cwd=os.path.join(ROOT, "tests", "native"), check=True)
+    result = subprocess.run([path], capture_output=True, text=True, timeout=60)
+    assert result.returncode == 0, result.stdout + result.stderr
+    assert "FAIL" not in result.stdout and result.stdout.count("ok ") == 32, result.stdout
+
+
 def test_headers_compile_as_c99(tmp_path):
     # The C ABI is meant for C callers (cgo, ctypes, plain C): both headers
     # must stand alone as C99, with no C++ in their C view.

@@ -16,6 +16,7 @@
 // with its residual, and the same for cross attention and the feed-forward
 // pair. Every reduction runs in a fixed order.
 #include "../../include/wsp_hip.h"
+#include "batch_plan.h"
 #include "device_common.h"
 #include "ops.h"
 
@@ -662,9 +663,7 @@ __global__ void __launch_bounds__(kNormThreads) hidden_kernel(const float* h, co
 // order (so the result does not depend on which block finishes last), runs
 // the epilogue and sets the counter back to zero for the next launch.
 // ---------------------------------------------------------------------------
-constexpr int kTileColumns = 64;
-constexpr int kTileThreads = 256;
-constexpr int kMaxSplits = 8;
+constexpr int kTileThreads = 256; // (kTileColumns and kMaxSplits: batch_plan.h)
 constexpr int kStageBytes = 64 * 1024; // LDS for a block's split activations
 
 struct Tile
@@ -1328,14 +1327,6 @@ __global__ void __launch_bounds__(128) advance_kernel(int* state, uint32_t* ring
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
-int row_tiles(int rows)
-{
-    const int tiles = (rows + 15) / 16;
-    int t = 1;
-    while (t < tiles)
-        t *= 2;
-    return t;
-}
 
 template <int WT, int MT>
 void launch_product_tiles(hipStream_t stream, const Product& a)
@@ -1415,10 +1406,7 @@ hipError_t launch_norm(hipStream_t stream, const Norm& a, int rows, bool embed)
 // best for fc2 at the medium and large-v3 shapes), whole k-blocks each.
 void plan_splits(Tile& a, bool can_split)
 {
-    const int kblocks = a.inner / 32;
-    const int splits = can_split ? std::min(kMaxSplits, kblocks) : 1;
-    a.kb_per_split = (kblocks + splits - 1) / splits;
-    a.splits = (kblocks + a.kb_per_split - 1) / a.kb_per_split;
+    plan_split_runs(a.inner, can_split, a.kb_per_split, a.splits);
 }
 
 template <int WT, int MT>
@@ -1437,13 +1425,8 @@ hipError_t launch_tile(hipStream_t stream, const Tile& a)
     // A split launch writes 64 x (16 row tiles) partial floats per block and
     // counts on one counter per column group: refuse it when the buffers are
     // smaller than that.
-    if (a.splits > 1)
-    {
-        const size_t groups = (size_t) (a.out + kTileColumns - 1) / kTileColumns;
-        const size_t floats = groups * a.splits * kTileColumns * 16 * (size_t) row_tiles(a.rows);
-        if (floats > a.partials_capacity || groups > a.counters_capacity)
-            return hipErrorInvalidValue;
-    }
+    if (!split_launch_fits(a.out, a.rows, a.splits, a.partials_capacity, a.counters_capacity))
+        return hipErrorInvalidValue;
     switch (row_tiles(a.rows))
     {
         case 1: launch_tile_rows<WT, 1>(stream, a); break;
@@ -2090,8 +2073,7 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
         e = allocate(b, &b->packed, packed_capacity(s));
     if (e == hipSuccess)
         e = allocate(b, &b->stats, (size_t) b->rows_padded * stat_groups * 2);
-    b->tile_partials_capacity = (size_t) wsp::batch::kMaxSplits * split_groups * b->rows_padded
-                                * wsp::batch::kTileColumns;
+    b->tile_partials_capacity = wsp::batch::split_partials_capacity(split_groups, b->rows_padded);
     b->counters_capacity = split_groups;
     if (e == hipSuccess)
         e = allocate(b, &b->tile_partials, b->tile_partials_capacity);
