@@ -257,8 +257,8 @@ void plan_persistent(Context* ctx, FusedState* st)
     if (!cooperative)
         return refuse("device has no cooperative launch");
     const int G = prop.multiProcessorCount;
-    const int self_split_max = ceil_div(s.max_positions, step::kSelfKeys);
-    const int head_groups = H * self_split_max;
+    const int key_blocks = ceil_div(s.max_positions, step::kSelfKeys); // splits the longest sequence needs
+    const int head_groups = H * key_blocks;
     // Row groups: the fewest in the top eighth of the CUs not holding a head
     // group whose width-long vectors' producer blocks fit two words per
     // polling thread (each poll round tests every slot a thread holds, so
@@ -290,6 +290,10 @@ void plan_persistent(Context* ctx, FusedState* st)
         if (row_groups * block > step::kFoldChunks * step::kPollBlocked * step::kPollThreads)
             return refuse("width past the folded LayerNorm's poll capacity");
     }
+    // The spare workgroups past the row groups split each head's keys further
+    // when a position's keys allow (splits of at least kSelfSplitKeys keys).
+    const int self_split_max =
+        std::max(key_blocks, std::min((G - row_groups) / H, step::kMaxCombine / (H * (hd + 2))));
     if (self_split_max * H * (hd + 2) > step::kMaxCombine || 2 * G > step::kMaxCombine || G > 256)
         return refuse("attention partials past the combine capacity");
     const int cross_needed = ceil_div(s.cross_positions, step::kCrossKeys);
@@ -412,6 +416,12 @@ bool aligned16(const void* p)
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
 }
 
+// The fewest keys a self-attention split takes when spare head groups could
+// split a head's keys further. One full block: at the small shape, splits of
+// 128 keys ran 269 us/step and of 64 keys 276, against 261 unsplit (the row
+// groups' combine of the partials costs more than the shorter chains save).
+constexpr int kSelfSplitKeys = step::kSelfKeys;
+
 // `count` tokens (1, or up to st->max_tokens with the multi-token kernel) at
 // position .. position + count - 1.
 int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* tensors, const uint32_t* tokens,
@@ -457,7 +467,13 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     }
 
     // The work split of this call.
-    const int self_splits = ceil_div(position + 1, step::kSelfKeys);
+    // Self-attention key splits: as many blocks of kSelfKeys as the keys
+    // need, more (down to kSelfSplitKeys keys each) where head groups allow;
+    // a multi-token launch keeps one.
+    int self_splits = ceil_div(position + 1, step::kSelfKeys);
+    if (count == 1)
+        self_splits = std::min(st->self_split_max, std::max(self_splits, ceil_div(position + 1, kSelfSplitKeys)));
+    const int self_chunk = ceil_div(position + 1, self_splits);
     // As few cross-attention chunks as the per-task key capacity allows: the
     // head's combine then polls the fewest partials (at 1500 keys, 12 chunks of
     // 125 ran 269 us/step against 273 for 18 chunks of 84).
@@ -498,6 +514,7 @@ int persistent_step(Context* ctx, FusedState* st, const wsp_decoder_tensors* ten
     a.token_count = count;
     a.row_groups = st->row_groups;
     a.self_splits = self_splits;
+    a.self_chunk = self_chunk;
     a.cross_splits = cross_splits;
     a.cross_chunk = cross_chunk;
     a.epoch = ++st->epoch;

@@ -57,6 +57,7 @@ struct StepArgs
     int token_count;    // tokens of this launch (1 for the single-token kernel, else 1..kMaxTokens)
     int row_groups;     // workgroups [0, row_groups) run projections and cross chunks
     int self_splits;    // key splits per head for this position (<= self_split_max)
+    int self_chunk;     // keys per split (<= kSelfKeys); split s holds keys [s * self_chunk, ...)
     int cross_splits;   // key chunks per head
     int cross_chunk;    // keys per chunk (<= kCrossKeys)
     uint32_t epoch;

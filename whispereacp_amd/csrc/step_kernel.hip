@@ -48,7 +48,7 @@ constexpr int kCrossPasses = kCrossKeys / kKeySlots;
 constexpr int kRowLanes = 32;                      // lanes per projection row
 constexpr int kRowGroups = kThreads / kRowLanes;   // rows in flight per workgroup
 constexpr int kChunks = 3;                         // 16-byte chunks per lane per row slice
-constexpr int kRing = 5;                           // logits rows in flight per row group
+constexpr int kRing = 5;                           // logits rows in flight per row group (6, 7, 8: slower)
 constexpr int kWaves = kThreads / kWave;
 constexpr int kSpinLimit = 1 << 21;                // poll rounds before the watchdog trips
 constexpr uint32_t kUnchosen = 0xFFFFFFFFu;
@@ -2306,8 +2306,8 @@ __device__ __forceinline__ bool head_group_layers(const StepArgs& a, Shared& sh)
     const int qkv_block = (3 * d + a.row_groups - 1) / a.row_groups; // the q/k/v phase's rows per workgroup
     const int head = index % H, split = index / H;
     const int n = a.position + 1; // keys attended, the new one included
-    const int first = split * kSelfKeys;
-    const int count = min(kSelfKeys, n - first);               // <= 0 for an idle split
+    const int first = split * a.self_chunk;
+    const int count = min(a.self_chunk, n - first);            // <= 0 for an idle split
     const int cached = max(0, min(count, a.position - first)); // keys read from the cache
     const bool attends = split < a.self_splits;
     const uint32_t epoch = a.epoch;
