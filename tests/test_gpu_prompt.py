@@ -117,3 +117,45 @@ def test_small_shape_prompt_matches_single_steps_and_the_oracle(oracle):
     h, l = session.step(tokens)
     assert worst_error(l1, l) <= 1e-4
     assert [int(np.argmax(r)) for r in l1] == [int(np.argmax(r)) for r in l]
+
+
+def test_widest_shape_bf16_two_tokens_a_launch(oracle):
+    # The large-v3 layer shape (d 1280, 20 heads, ffn 5120, bf16) with two
+    # layers: its 20 heads leave head groups for two tokens a launch, so a
+    # 5-token step is three launches (2 + 2 + 1).
+    from whispereacp_amd.decoder import Decoder
+    shape = S.DecoderShape(1280, 20, 2, 5120, 5003, 448, 1500)
+    f = S.workload_decoder_file(shape, "BF16", 5000)
+    enc = S.normal_encoder_output(shape.cross_positions, shape.width, 11)
+    tokens = [1, 2, 3, 4, 77]
+    together = Decoder(shape, f, packing="ExactHalf")
+    h1, l1 = run_steps(together, shape, enc, [tokens])
+    single = Decoder(shape, f, packing="ExactHalf")
+    h2, l2 = run_steps(single, shape, enc, [[t] for t in tokens])
+    assert np.array_equal(h1, h2) and np.array_equal(l1, l2)
+    session = oracle.session(shape, oracle_tensors(f, shape))
+    session.begin(enc, 0)
+    h, l = session.step(tokens)
+    assert worst_error(l1, l) <= 1e-4
+
+
+def test_a_step_across_the_self_key_block(oracle):
+    # Launches carry several tokens only while the self keys stay inside one
+    # 256-key block: a step over positions 250..259 runs 250..253 in one
+    # launch and 254 on one token a launch (past 256 the keys split over two
+    # head groups), and still equals the single-token steps.
+    from whispereacp_amd.decoder import Decoder
+    shape = S.DecoderShape(256, 4, 2, 1024, 4099, 448, 300)
+    f = S.workload_decoder_file(shape, "F16", 3000)
+    enc = S.normal_encoder_output(shape.cross_positions, shape.width, 5)
+    tokens = [(37 * i + 11) % shape.vocabulary_size for i in range(260)]
+    prefix = [tokens[i:i + 16] for i in range(0, 240, 16)] + [tokens[240:250]]
+    together = Decoder(shape, f, packing="ExactHalf")
+    h1, l1 = run_steps(together, shape, enc, prefix + [tokens[250:]])
+    single = Decoder(shape, f, packing="ExactHalf")
+    h2, l2 = run_steps(single, shape, enc, [[t] for t in tokens])
+    assert np.array_equal(h1, h2) and np.array_equal(l1, l2)
+    session = oracle.session(shape, oracle_tensors(f, shape))
+    session.begin(enc, 0)
+    h, l = session.step(tokens)
+    assert worst_error(l1[-10:], l[-10:]) <= 1e-4
