@@ -1238,25 +1238,32 @@ __device__ __forceinline__ void run_phase(const Prefetch& p, const void* weight,
                                           int count, Shared& sh, Epilogue epi, After after, int mark = -1)
 {
     const int lane = threadIdx.x & (kRowLanes - 1);
+    // The statistics of the token this thread finishes (thread t finishes
+    // token t / rows_per_pass), picked before the dot products, off the
+    // chain that follows them. By selects on values: an indexed register
+    // array would be placed in memory (the empty asm keeps the compiler from
+    // turning the selects back into an indexed load).
+    float rstd = fs[0].rstd, dmean = fs[0].dmean;
+    if constexpr (FOLD && T > 1)
+    {
+        const int mine = (int) threadIdx.x / ps.rows_per_pass;
+#pragma unroll
+        for (int i = 1; i < T; ++i)
+        {
+            float r = fs[i].rstd, m = fs[i].dmean;
+            asm volatile("" : "+v"(r), "+v"(m));
+            rstd = mine == i ? r : rstd;
+            dmean = mine == i ? m : dmean;
+        }
+    }
     int row, first, last;
     const bool has_task = phase_task(ps, group, stride, 0, row, first, last);
     float acc[T];
     run_dot<WT, T>(p.r, sh.x, first, last, lane, acc);
     const float bias0 = p.bias;
     const float gain0 = FOLD ? p.gain : 0.f;
-    auto value = [&](int k, float v, float b, float g) {
-        // Token k's statistics by selects on values: an indexed register
-        // array would be placed in memory (the empty asm keeps the compiler
-        // from turning the selects back into an indexed load).
-        float rstd = fs[0].rstd, dmean = fs[0].dmean;
-#pragma unroll
-        for (int i = 1; i < T; ++i)
-        {
-            float r = fs[i].rstd, m = fs[i].dmean;
-            asm volatile("" : "+v"(r), "+v"(m));
-            rstd = k == i ? r : rstd;
-            dmean = k == i ? m : dmean;
-        }
+    // k is always the finishing thread's own token.
+    auto value = [&](int, float v, float b, float g) {
         return FOLD ? __builtin_fmaf(rstd, __builtin_fmaf(-dmean, g, v), b) : v + b;
     };
     STEP_MARK(mark);
