@@ -691,27 +691,30 @@ __device__ __forceinline__ void norm_row(const NormParams& p, int n, float inv_n
     }
 }
 
-// inv_n = 1 / n (the row means are the sums times inv_n); token k's row of
-// a T-token launch.
+// inv_n = 1 / n (the row means are the sums times inv_n); the rows of tokens
+// [0, count) of a T-token launch, one barrier for all of them.
 template <int T = 1>
 __device__ __forceinline__ void layer_norm(const NormParams& p, int n, float inv_n, float eps, Shared& sh,
-                                           int mark = -1, int token = 0)
+                                           int mark = -1, int count = 1)
 {
-    const float* raw = sh.raw + token * kRawStride;
-    float* out = sh.x + x_at<T>(token, 0);
     const int lane = threadIdx.x & (kWave - 1);
     const int own = 4 * (lane + kWave * (int) (threadIdx.x / kWave)); // the run this wave writes
     // Only the waves that write a run compute the statistics; the others go
     // straight to the barrier and leave their SIMDs' issue slots to them.
     if (own - 4 * lane < n)
     {
-        switch ((n + 4 * kWave - 1) / (4 * kWave))
+        for (int k = 0; k < (T == 1 ? 1 : count); ++k)
         {
-            case 1:
-            case 2: norm_row<2, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
-            case 3: norm_row<3, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
-            case 4: norm_row<4, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
-            default: norm_row<kNormRuns, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
+            const float* raw = sh.raw + k * kRawStride;
+            float* out = sh.x + x_at<T>(k, 0);
+            switch ((n + 4 * kWave - 1) / (4 * kWave))
+            {
+                case 1:
+                case 2: norm_row<2, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
+                case 3: norm_row<3, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
+                case 4: norm_row<4, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
+                default: norm_row<kNormRuns, kXBlock<T>>(p, n, inv_n, eps, raw, out, lane, own, mark, sh); break;
+            }
         }
     }
     __syncthreads();
@@ -2502,8 +2505,7 @@ __device__ __forceinline__ bool final_phase(const StepArgs& a, Shared& sh, Ring&
     // The first logits rows are issued once the last layer's output is in:
     // issued before, they would share the memory pipeline with its polls.
     issue_ring(ring, a, logit_shape(a));
-    for (int k = 0; k < count; ++k)
-        layer_norm<T>(norm, d, a.inv_width, a.eps, sh, -1, k);
+    layer_norm<T>(norm, d, a.inv_width, a.eps, sh, -1, count);
     if (blockIdx.x == 0)
         for (int k = 0; k < count; ++k)
             for (int c = threadIdx.x; c < d; c += kThreads)
