@@ -21,7 +21,7 @@ LIBRARY = os.path.join(BUILD, "libwhispereacp_hip.so")
 ARCH = "gfx950"
 
 DEVICE_SOURCES = ["ops.hip", "capi.hip", "cross_kv.hip", "fused_step.hip", "step_kernel.hip", "batch.hip",
-                  "mfma_product.hip", "attention_static.hip", "encoder.hip", "mel.hip"]
+                  "mfma_product.hip", "split_product.hip", "attention_static.hip", "encoder.hip", "mel.hip"]
 HOST_SOURCES = ["host/Gpu.cpp", "host/Net.cpp", "host/Half.cpp", "host/HipNet.cpp", "host/DecoderWeights.cpp",
                 "host/Decoder.cpp", "host/DecoderRecording.cpp", "host/Argmax.cpp", "host/GreedyDecoder.cpp", "host/BatchedDecoder.cpp",
                 "host/SafeTensors.cpp", "host/Tokenizer.cpp", "host/Encoder.cpp", "host/Whisper.cpp",
@@ -31,6 +31,9 @@ COMMON = ["-std=c++20", "-fPIC", "-Wall", "-Wno-unused-result", "-I" + os.path.j
 DEVICE_FLAGS = ["-O3", "--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HOST_FLAGS = ["-O2", "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROCM, "include")]
+# Per-source device flags: the pre-split products keep their matrix-core
+# accumulators in VGPRs (in AGPRs the compiler shuffles them between steps).
+SOURCE_FLAGS = {"split_product.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def hipcc() -> str:
@@ -46,8 +49,8 @@ def _object_path(source: str) -> str:
 
 def _compile(source: str, device: bool) -> str:
     out = _object_path(source)
-    cmd = [hipcc()] + COMMON + (DEVICE_FLAGS if device else HOST_FLAGS) + ["-c", os.path.join(CSRC, source),
-                                                                             "-o", out]
+    flags = DEVICE_FLAGS + SOURCE_FLAGS.get(source, []) if device else HOST_FLAGS
+    cmd = [hipcc()] + COMMON + flags + ["-c", os.path.join(CSRC, source), "-o", out]
     if not device:
         cmd[1:1] = ["-x", "c++"]
     result = subprocess.run(cmd, capture_output=True, text=True)

@@ -172,6 +172,33 @@ __device__ __forceinline__ float block_max(float v, float* scratch)
     return best;
 }
 
+// x as exact 16-bit parts for products with 16-bit weights of type WT
+// (kF16: fp16 hi + lo, for |x| < 65504; kBF16: three bf16 parts); part p in
+// the low 16 bits of bits[p], and x equals the sum of the parts.
+template <int WT>
+__device__ __forceinline__ void exact_parts(float x, uint32_t (&bits)[3])
+{
+    if constexpr (WT == kF16)
+    {
+        const _Float16 hi = (_Float16) x;
+        const _Float16 lo = (_Float16) (x - (float) hi);
+        bits[0] = __builtin_bit_cast(uint16_t, hi);
+        bits[1] = __builtin_bit_cast(uint16_t, lo);
+        bits[2] = 0;
+    }
+    else
+    {
+        float rest = x;
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+        {
+            const __bf16 b = (__bf16) rest;
+            bits[p] = __builtin_bit_cast(uint16_t, b);
+            rest -= (float) b;
+        }
+    }
+}
+
 // x * 0.5 * (1 + erf(x / sqrt(2))), the exact form (Kernels/Gelu.h:16-21),
 // with the device library's erff.
 __device__ __forceinline__ float exact_gelu(float x)

@@ -354,6 +354,10 @@ struct wsp_encoder
     float* v = nullptr;
     float* att = nullptr;
     float* ff = nullptr;      // [positions, feed_forward_width]
+    // 16-bit weights: a product's input as exact 16-bit parts (split_product):
+    // up to three [positions, width] parts, and fc2's [positions, feed_forward_width].
+    void* parts = nullptr;
+    void* ff_parts = nullptr;
     float* workspace = nullptr;
     float* flash_partials = nullptr; // [kMaxFlashSplits][heads][positions][66], split-key attention
     std::vector<void*> owned;
@@ -424,6 +428,12 @@ int wsp_encoder_create(const wsp_encoder_shape* shape, int device, void* stream,
             status = encoder_allocate(e, r, positions * d);
     if (status == hipSuccess)
         status = encoder_allocate(e, &e->ff, positions * s.feed_forward_width);
+    // Three 16-bit parts take 1.5 floats a value.
+    if (status == hipSuccess)
+        status = encoder_allocate(e, reinterpret_cast<float**>(&e->parts), (positions * d * 3 + 1) / 2);
+    if (status == hipSuccess)
+        status = encoder_allocate(e, reinterpret_cast<float**>(&e->ff_parts),
+                                  (positions * s.feed_forward_width * 3 + 1) / 2);
     if (status == hipSuccess && s.heads > 0 && s.width == s.heads * wsp::encoder::kFlashWidth)
         status = encoder_allocate(e, &e->flash_partials,
                                   (size_t) wsp::encoder::kMaxFlashSplits * s.heads * positions
@@ -511,13 +521,62 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
         return encoder_hip(e, status, "conv2");
 
     const int wt = T->wdtype;
+    // 16-bit weights take the products over pre-split inputs: each product's
+    // input is stored once as exact 16-bit parts (fc1 writes fc2's itself).
+    const size_t part_stride = (size_t) positions * d, ff_part_stride = (size_t) positions * f;
+    const bool split = positions > 16 && part_stride % 8 == 0 && ops::split_product_fits(wt, d, 3 * d, d, 2 * d)
+                       && ops::split_product_fits(wt, d, f, f, f) && ops::split_product_fits(wt, f, d, d, d);
+    auto split_product = [&](const void* parts, size_t stride, int inner, const void* w, const float* bias, float* y,
+                             int out, int flags, void* out_parts) {
+        ops::SplitProduct p {};
+        p.parts = parts;
+        p.part_stride = stride;
+        p.rows = positions;
+        p.inner = inner;
+        p.w0 = w;
+        p.out = out;
+        p.bias0 = bias;
+        p.y0 = y;
+        p.ldy = out;
+        p.flags = flags;
+        p.out_parts = out_parts;
+        p.out_part_stride = ff_part_stride;
+        p.wdtype = wt;
+        return ops::split_product(st, p);
+    };
     for (int l = 0; l < s.layers; ++l)
     {
         const wsp_encoder_layer_tensors& L = T->layers[l];
-        if ((status = ops::layernorm(st, e->hidden, L.attention_norm_w, L.attention_norm_b, e->normed, positions, d,
-                                     eps)) != hipSuccess)
+        status = split ? ops::layernorm_parts(st, e->hidden, L.attention_norm_w, L.attention_norm_b, e->parts,
+                                              part_stride, positions, d, eps, wt)
+                       : ops::layernorm(st, e->hidden, L.attention_norm_w, L.attention_norm_b, e->normed, positions,
+                                        d, eps);
+        if (status != hipSuccess)
             return encoder_hip(e, status, "self-attention norm");
-        if (positions > 16 && ops::tile_product_fits(wt, d, 3 * d, d, e->normed) && d % 128 == 0)
+        if (split)
+        {
+            // q, k and v side by side in one launch.
+            ops::SplitProduct p {};
+            p.parts = e->parts;
+            p.part_stride = part_stride;
+            p.rows = positions;
+            p.inner = d;
+            p.w0 = L.q_w;
+            p.w1 = L.k_w;
+            p.w2 = L.v_w;
+            p.split = d;
+            p.split2 = 2 * d;
+            p.out = 3 * d;
+            p.bias0 = L.q_b;
+            p.bias2 = L.v_b;
+            p.y0 = e->q;
+            p.y1 = e->k;
+            p.y2 = e->v;
+            p.ldy = d;
+            p.wdtype = wt;
+            status = ops::split_product(st, p);
+        }
+        else if (positions > 16 && ops::tile_product_fits(wt, d, 3 * d, d, e->normed) && d % 128 == 0)
         {
             // q, k and v side by side in one launch: three times the blocks of one.
             ops::TileProduct p {};
@@ -586,12 +645,32 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
                                     e->workspace);
         if (status != hipSuccess)
             return encoder_hip(e, status, "self attention");
-        if ((status = ops::linear(st, e->att, positions, d, L.out_w, wt, L.out_b, e->hidden, d, 2)) != hipSuccess)
+        if (split)
+        {
+            if ((status = ops::split_rows(st, e->att, part_stride, wt, e->parts, part_stride)) == hipSuccess)
+                status = split_product(e->parts, part_stride, d, L.out_w, L.out_b, e->hidden, d,
+                                       ops::kProductResidual, nullptr);
+        }
+        else
+            status = ops::linear(st, e->att, positions, d, L.out_w, wt, L.out_b, e->hidden, d, 2);
+        if (status != hipSuccess)
             return encoder_hip(e, status, "attention output");
-        if ((status = ops::layernorm(st, e->hidden, L.final_norm_w, L.final_norm_b, e->normed, positions, d, eps))
-                != hipSuccess
-            || (status = ops::linear(st, e->normed, positions, d, L.fc1_w, wt, L.fc1_b, e->ff, f, 1)) != hipSuccess
-            || (status = ops::linear(st, e->ff, positions, f, L.fc2_w, wt, L.fc2_b, e->hidden, d, 2)) != hipSuccess)
+        status = split ? ops::layernorm_parts(st, e->hidden, L.final_norm_w, L.final_norm_b, e->parts, part_stride,
+                                              positions, d, eps, wt)
+                       : ops::layernorm(st, e->hidden, L.final_norm_w, L.final_norm_b, e->normed, positions, d, eps);
+        if (status != hipSuccess)
+            return encoder_hip(e, status, "feed-forward norm");
+        if (split)
+        {
+            if ((status = split_product(e->parts, part_stride, d, L.fc1_w, L.fc1_b, nullptr, f, ops::kProductGelu,
+                                        e->ff_parts))
+                == hipSuccess)
+                status = split_product(e->ff_parts, ff_part_stride, f, L.fc2_w, L.fc2_b, e->hidden, d,
+                                       ops::kProductResidual, nullptr);
+        }
+        else if ((status = ops::linear(st, e->normed, positions, d, L.fc1_w, wt, L.fc1_b, e->ff, f, 1)) == hipSuccess)
+            status = ops::linear(st, e->ff, positions, f, L.fc2_w, wt, L.fc2_b, e->hidden, d, 2);
+        if (status != hipSuccess)
             return encoder_hip(e, status, "feed-forward");
     }
     if ((status = ops::layernorm(st, e->hidden, T->final_norm_w, T->final_norm_b, output, positions, d, eps))

@@ -55,6 +55,48 @@ hipError_t tile_product(hipStream_t stream, const TileProduct& product);
 hipError_t layernorm(hipStream_t stream, const float* x, const float* gamma, const float* beta,
                      float* y, int rows, int width, float eps);
 
+// The encoder's products over pre-split activations (split_product.hip):
+// y = X·Wᵀ where X [rows, inner] is held as exact 16-bit parts (three bf16
+// parts for bf16 W, fp16 hi + lo for fp16 W), part p at
+// parts + p·part_stride + r·inner. Columns [0, split) read w0 (bias0, y0),
+// [split, split2) w1 and [split2, out) w2, each matrix's own column index c;
+// row r of a column lands at y·[r·ldy + c] (+= with kProductResidual, after
+// GELU with kProductGelu), or, with out_parts set, as the parts of the value
+// (one matrix only, rows of `out` values, part p at out_parts + p·out_part_stride).
+constexpr int kProductGelu = 1;
+constexpr int kProductResidual = 2;
+struct SplitProduct
+{
+    const void* parts;
+    size_t part_stride;
+    int rows, inner;
+    const void* w0;
+    const void* w1;
+    const void* w2;
+    int split, split2, out;
+    const float* bias0;
+    const float* bias1;
+    const float* bias2;
+    float* y0;
+    float* y1;
+    float* y2;
+    int ldy;
+    int flags;
+    void* out_parts;
+    size_t out_part_stride;
+    int wdtype;
+};
+
+// 16-bit weights, inner % 32 == 0, out, split and split2 multiples of 128.
+bool split_product_fits(int wdtype, int inner, int out, int split, int split2);
+hipError_t split_product(hipStream_t stream, const SplitProduct& product);
+// LayerNorm rows (as layernorm) written as the parts of split_product's input.
+hipError_t layernorm_parts(hipStream_t stream, const float* x, const float* gamma, const float* beta, void* parts,
+                           size_t part_stride, int rows, int width, float eps, int wdtype);
+// count fp32 values (a multiple of 8) as parts for 16-bit weights of wdtype.
+hipError_t split_rows(hipStream_t stream, const float* x, size_t count, int wdtype, void* parts,
+                      size_t part_stride);
+
 // Token ids at or past `vocabulary` poison their row with NaN.
 hipError_t embed(hipStream_t stream, const uint32_t* tokens, int count, const float* token_table,
                  const float* position_table, int first_position, float* y, int width,
