@@ -683,7 +683,9 @@ def bench_encoder(args):
                    "window_achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1)},
         "roofline": {"bound": "mfma", "achieved": round(fc1_tflops, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(fc1_tflops / peak, 4), "traffic": None,
-                     "kernel": f"tile_product_kernel, fc1 ({T} x {d} -> {f}, GELU), {fc1_us:.1f} us per launch",
+                     "kernel": f"tile_product_kernel through wsp_hip_linear (fp32 rows in), fc1 shape ({T} x {d} -> "
+                               f"{f}, GELU), {fc1_us:.1f} us per launch; the encoder itself runs its products "
+                               f"over pre-split rows (split_product_kernel), timed in its kernel trace",
                      "flops_per_launch": 2.0 * T * d * f,
                      "note": "algorithmic flops; the matrix cores do 2x (fp16) or 3x (bf16) of them, one "
                              "product per exact 16-bit part of the fp32 activations"},

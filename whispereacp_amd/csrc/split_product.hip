@@ -45,6 +45,7 @@ constexpr int kStep = 32;       // k per step: four 16-byte chunks of 16-bit val
 template <int TN>
 constexpr int kStages = TN == 128 ? 2 : 4;
 constexpr int kSplitThreads = 256;
+constexpr int kWaveRows = 4; // waves along the tile's rows (the rest along its columns)
 
 template <int WT>
 constexpr int parts_of()
@@ -149,13 +150,15 @@ __global__ void __launch_bounds__(kThreads) split_product_kernel(SplitProduct a)
 {
     using L = Layout<WT, TN>;
     constexpr int P = L::P;
-    constexpr int NT = TN / 32; // 16-column tiles per wave
+    constexpr int WM = kWaveRows, WN = 4 / WM;   // the waves' grid over the tile
+    constexpr int MT = kTileRows / 16 / WM;     // 16-row tiles per wave
+    constexpr int NT = TN / 16 / WN;            // 16-column tiles per wave
     extern __shared__ __attribute__((aligned(16))) unsigned char stage_mem[];
 
     const int tid = threadIdx.x, lane = tid % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave); // uniform, so the load bases are scalar
     const int li = lane % 16, g = lane / 16;
-    const int wm = wave / 2, wn = wave % 2;
+    const int wm = wave / WN, wn = wave % WN;
     const int n_block = blockIdx.x * TN, m_block = blockIdx.y * kTileRows;
     const int steps = a.inner / kStep;
     // The block's columns lie in one of the (up to three) matrices.
@@ -204,9 +207,9 @@ __global__ void __launch_bounds__(kThreads) split_product_kernel(SplitProduct a)
                        __builtin_amdgcn_readfirstlane(stage0 + buf * L::kStageBytes + dst[t]));
     };
 
-    float4v acc[4][NT];
+    float4v acc[MT][NT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int j = 0; j < NT; ++j)
             acc[i][j] = float4v {0.f, 0.f, 0.f, 0.f};
@@ -224,17 +227,17 @@ __global__ void __launch_bounds__(kThreads) split_product_kernel(SplitProduct a)
         __syncthreads();
         issue(s + L::kStages - 1, buf == 0 ? L::kStages - 1 : buf - 1);
         const unsigned char* st = stage_mem + buf * L::kStageBytes;
-        u32x4 af[4][P], bf[NT];
+        u32x4 af[MT][P], bf[NT];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int p = 0; p < P; ++p)
-                af[mt][p] = reinterpret_cast<const u32x4*>(st + p * L::kABytes)[slot(64 * wm + 16 * mt + li, g)];
+                af[mt][p] = reinterpret_cast<const u32x4*>(st + p * L::kABytes)[slot(16 * (MT * wm + mt) + li, g)];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-            bf[nt] = reinterpret_cast<const u32x4*>(st + P * L::kABytes)[slot(TN / 2 * wn + 16 * nt + li, g)];
+            bf[nt] = reinterpret_cast<const u32x4*>(st + P * L::kABytes)[slot(16 * (NT * wn + nt) + li, g)];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -251,14 +254,14 @@ __global__ void __launch_bounds__(kThreads) split_product_kernel(SplitProduct a)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
     {
-        const int c = n_block - seg_first + TN / 2 * wn + 16 * nt + li;
+        const int c = n_block - seg_first + 16 * (NT * wn + nt) + li;
         const float b = bias != nullptr ? bias[c] : 0.f;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
             {
-                const int row = m_block + 64 * wm + 16 * mt + 4 * g + r;
+                const int row = m_block + 16 * (MT * wm + mt) + 4 * g + r;
                 if (row >= a.rows)
                     continue;
                 float v = acc[mt][nt][r] + b;
