@@ -162,24 +162,27 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
     for (int t = 0; t < 4; ++t)
         o[t] = f32x4 {0.f, 0.f, 0.f, 0.f};
 
-    // The next tile's K and V runs, loaded while the current one is used.
-    f32x4 kn[kPerThread], vn[kPerThread];
-    auto load_tile = [&](int first) {
+    // K and V runs of a tile, loaded two tiles ahead of its use into one of
+    // two register stages (a tile past the end reloads the last keys, unused).
+    struct Stage
+    {
+        f32x4 k[kPerThread], v[kPerThread];
+    };
+    auto load_tile = [&](Stage& st, int first) {
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i)
         {
             const int unit = (int) threadIdx.x + i * kThreadsHere;
             const int key = first + (unit % kUnits) / 16, d4 = 4 * (unit % 16);
             const size_t at = (size_t) min(key, k_end - 1) * width + column + d4;
-            kn[i] = *reinterpret_cast<const f32x4*>(k + at);
-            vn[i] = *reinterpret_cast<const f32x4*>(v + at);
+            st.k[i] = *reinterpret_cast<const f32x4*>(k + at);
+            st.v[i] = *reinterpret_cast<const f32x4*>(v + at);
         }
     };
-    if (k_begin < k_end)
-        load_tile(k_begin);
 
-    for (int first = k_begin; first < k_end; first += kFlashKeys)
-    {
+    // One tile: its stage into LDS (as fp16 parts), the stage refilled with
+    // the tile two ahead, then the scores, the online softmax and P·V.
+    auto tile = [&](int first, Stage& st) {
         __syncthreads(); // the previous tile has been read
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i)
@@ -193,7 +196,7 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                 {
-                    const float kv = in ? kn[i][e] : 0.f, vv = in ? vn[i][e] : 0.f;
+                    const float kv = in ? st.k[i][e] : 0.f, vv = in ? st.v[i][e] : 0.f;
                     kh[e] = half_hi(kv);
                     kl[e] = half_lo(kv);
                     vt[0][d4 + e][row] = half_hi(vv);
@@ -204,21 +207,21 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
             }
         }
         __syncthreads();
-        if (first + kFlashKeys < k_end)
-            load_tile(first + kFlashKeys);
+        if (k_begin < k_end)
+            load_tile(st, first + 2 * kFlashKeys);
 
         // S^T for keys 16 mt + 4 g + r of the tile, query li.
-        f32x4 st[2];
+        f32x4 st_[2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
         {
-            st[mt] = f32x4 {0.f, 0.f, 0.f, 0.f};
+            st_[mt] = f32x4 {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < 2; ++s)
             {
                 const f16x8 kh = *reinterpret_cast<const f16x8*>(&ks[0][16 * mt + li][32 * s + 8 * g]);
                 const f16x8 kl = *reinterpret_cast<const f16x8*>(&ks[1][16 * mt + li][32 * s + 8 * g]);
-                st[mt] = mfma3(kh, kl, qh[s], ql[s], st[mt]);
+                st_[mt] = mfma3(kh, kl, qh[s], ql[s], st_[mt]);
             }
         }
         float x[8];
@@ -229,7 +232,7 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
             for (int r = 0; r < 4; ++r)
             {
                 const int key = first + 16 * mt + 4 * g + r;
-                x[4 * mt + r] = key < k_end ? st[mt][r] * scale2 : -INFINITY;
+                x[4 * mt + r] = key < k_end ? st_[mt][r] * scale2 : -INFINITY;
                 tile_max = fmaxf(tile_max, x[4 * mt + r]);
             }
         tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
@@ -264,7 +267,24 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
             const f16x8 vl = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
             o[t] = mfma3(vh, vl, ph, pl, o[t]);
         }
+    };
+
+    // Pairs of tiles, then an odd last one outside the loop, so the loop's
+    // back edge always follows the second tile of a pair.
+    Stage s0, s1;
+    if (k_begin < k_end)
+    {
+        load_tile(s0, k_begin);
+        load_tile(s1, k_begin + kFlashKeys);
     }
+    int first = k_begin;
+    for (; first + kFlashKeys < k_end; first += 2 * kFlashKeys)
+    {
+        tile(first, s0);
+        tile(first + kFlashKeys, s1);
+    }
+    if (first < k_end)
+        tile(first, s0);
     // The row sum over the four lanes of query li, then O = O^T / l.
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
