@@ -84,6 +84,7 @@ constexpr int kFlashWidth = 64;
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ _Float16 half_hi(float x)
 {
@@ -115,19 +116,31 @@ int compute_units()
 }
 
 // Key splits: blockIdx.z takes keys [z·span, min((z + 1)·span, count)); with
-// one split the block writes the normalised rows to out, with several it
-// writes (max, sum, row) partials [split][head][query][66] for
-// flash_combine_kernel.
-template <int WAVES>
+// one split the block writes the normalised rows to out (OUT = kF32) or as
+// the exact 16-bit parts of the output product's input (OUT = kF16, kBF16:
+// part p at out_parts + p·out_part_stride), with several it writes (max, sum,
+// row) partials [split][head][query][66] for flash_combine_kernel.
+// With PRESPLIT, K and V arrive already cut into fp16 hi and lo by the q/k/v
+// product (k_halves [2][pitch][width], vt_halves transposed [2][width][pitch],
+// pitch a multiple of the key tile and zero past count), so a tile's staging
+// is a copy; otherwise the fp32 k and v are cut here.
+template <int WAVES, bool PRESPLIT = false, int OUT = kF32>
 __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float* __restrict__ q,
                                                                     const float* __restrict__ k,
                                                                     const float* __restrict__ v, int count,
                                                                     int width, float scale2, float* __restrict__ out,
-                                                                    int span, float* __restrict__ partials)
+                                                                    int span, float* __restrict__ partials,
+                                                                    const uint16_t* __restrict__ k_halves,
+                                                                    const uint16_t* __restrict__ vt_halves, int pitch,
+                                                                    uint16_t* __restrict__ out_parts,
+                                                                    size_t out_part_stride)
 {
     constexpr int kThreadsHere = WAVES * 64;
     constexpr int kUnits = kFlashKeys * kFlashWidth / 4; // float4 runs of a K (or V) tile
     constexpr int kPerThread = (kUnits + kThreadsHere - 1) / kThreadsHere;
+    constexpr int kHalfChunks = 2 * kFlashKeys * kFlashWidth / 8; // 16-byte runs of a tile's K (or V) halves
+    constexpr int kHalfPerThread = kHalfChunks / kThreadsHere;
+    static_assert(kHalfChunks % kThreadsHere == 0, "whole half runs per thread");
     __shared__ __attribute__((aligned(16))) _Float16 ks[2][kFlashKeys][kFlashWidth + 8];
     __shared__ __attribute__((aligned(16))) _Float16 vt[2][kFlashWidth][kFlashKeys + 8];
 
@@ -167,8 +180,37 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
     struct Stage
     {
         f32x4 k[kPerThread], v[kPerThread];
+        u32x4 kh[kHalfPerThread], vh[kHalfPerThread];
     };
+    // Run i of this thread in a tile of halves: part, then K row and 8-column
+    // block, or V^T row (channel) and 8-key block.
+    auto half_run = [&](int i, int& part, int& a, int& b, int& c, int& kb) {
+        const int unit = (int) threadIdx.x + i * kThreadsHere;
+        const int rest = unit % (kHalfChunks / 2);
+        part = unit / (kHalfChunks / 2);
+        a = rest / 8;
+        b = rest % 8;
+        c = rest / 4;
+        kb = rest % 4;
+    };
+    const int last_first = k_begin + (max(k_end - k_begin, 1) - 1) / kFlashKeys * kFlashKeys;
+    const size_t halves_part = (size_t) pitch * width;
     auto load_tile = [&](Stage& st, int first) {
+        if constexpr (PRESPLIT)
+        {
+            const int f = min(first, last_first);
+#pragma unroll
+            for (int i = 0; i < kHalfPerThread; ++i)
+            {
+                int part, row, cb, c, kb;
+                half_run(i, part, row, cb, c, kb);
+                st.kh[i] = *reinterpret_cast<const u32x4*>(k_halves + part * halves_part + (size_t) (f + row) * width
+                                                           + column + 8 * cb);
+                st.vh[i] = *reinterpret_cast<const u32x4*>(vt_halves + part * halves_part
+                                                           + (size_t) (column + c) * pitch + f + 8 * kb);
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i)
         {
@@ -184,26 +226,40 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
     // the tile two ahead, then the scores, the online softmax and P·V.
     auto tile = [&](int first, Stage& st) {
         __syncthreads(); // the previous tile has been read
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i)
+        if constexpr (PRESPLIT)
         {
-            const int unit = (int) threadIdx.x + i * kThreadsHere;
-            if (unit < kUnits)
-            {
-                const int row = unit / 16, d4 = 4 * (unit % 16);
-                const bool in = first + row < k_end;
-                f16x4 kh, kl;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
+            for (int i = 0; i < kHalfPerThread; ++i)
+            {
+                int part, row, cb, c, kb;
+                half_run(i, part, row, cb, c, kb);
+                *reinterpret_cast<u32x4*>(&ks[part][row][8 * cb]) = st.kh[i];
+                *reinterpret_cast<u32x4*>(&vt[part][c][8 * kb]) = st.vh[i];
+            }
+        }
+        else
+        {
+#pragma unroll
+            for (int i = 0; i < kPerThread; ++i)
+            {
+                const int unit = (int) threadIdx.x + i * kThreadsHere;
+                if (unit < kUnits)
                 {
-                    const float kv = in ? st.k[i][e] : 0.f, vv = in ? st.v[i][e] : 0.f;
-                    kh[e] = half_hi(kv);
-                    kl[e] = half_lo(kv);
-                    vt[0][d4 + e][row] = half_hi(vv);
-                    vt[1][d4 + e][row] = half_lo(vv);
+                    const int row = unit / 16, d4 = 4 * (unit % 16);
+                    const bool in = first + row < k_end;
+                    f16x4 kh, kl;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                    {
+                        const float kv = in ? st.k[i][e] : 0.f, vv = in ? st.v[i][e] : 0.f;
+                        kh[e] = half_hi(kv);
+                        kl[e] = half_lo(kv);
+                        vt[0][d4 + e][row] = half_hi(vv);
+                        vt[1][d4 + e][row] = half_lo(vv);
+                    }
+                    *reinterpret_cast<f16x4*>(&ks[0][row][d4]) = kh;
+                    *reinterpret_cast<f16x4*>(&ks[1][row][d4]) = kl;
                 }
-                *reinterpret_cast<f16x4*>(&ks[0][row][d4]) = kh;
-                *reinterpret_cast<f16x4*>(&ks[1][row][d4]) = kl;
             }
         }
         __syncthreads();
@@ -314,7 +370,19 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                out[(size_t) query * width + column + 16 * t + 4 * g + r] = o[t][r] * inv;
+            {
+                const size_t at = (size_t) query * width + column + 16 * t + 4 * g + r;
+                if constexpr (OUT == kF32)
+                    out[at] = o[t][r] * inv;
+                else
+                {
+                    uint32_t bits[3];
+                    exact_parts<OUT>(o[t][r] * inv, bits);
+#pragma unroll
+                    for (int p = 0; p < (OUT == kF16 ? 2 : 3); ++p)
+                        out_parts[p * out_part_stride + at] = (uint16_t) bits[p];
+                }
+            }
     }
 }
 
@@ -378,6 +446,12 @@ struct wsp_encoder
     // up to three [positions, width] parts, and fc2's [positions, feed_forward_width].
     void* parts = nullptr;
     void* ff_parts = nullptr;
+    // The attention's keys and values as fp16 hi and lo halves, written by the
+    // q/k/v product: [2][pitch][width] and transposed [2][width][pitch], pitch
+    // the positions rounded up to the key tile, zero past the positions.
+    uint16_t* k_halves = nullptr;
+    uint16_t* vt_halves = nullptr;
+    int pitch = 0;
     float* workspace = nullptr;
     float* flash_partials = nullptr; // [kMaxFlashSplits][heads][positions][66], split-key attention
     std::vector<void*> owned;
@@ -454,6 +528,17 @@ int wsp_encoder_create(const wsp_encoder_shape* shape, int device, void* stream,
     if (status == hipSuccess)
         status = encoder_allocate(e, reinterpret_cast<float**>(&e->ff_parts),
                                   (positions * s.feed_forward_width * 3 + 1) / 2);
+    e->pitch = (int) ((positions + wsp::encoder::kFlashKeys - 1) / wsp::encoder::kFlashKeys
+                      * wsp::encoder::kFlashKeys);
+    const size_t halves = (size_t) 2 * e->pitch * d; // two parts of 16 bits
+    if (status == hipSuccess)
+        status = encoder_allocate(e, reinterpret_cast<float**>(&e->k_halves), halves / 2);
+    if (status == hipSuccess)
+        status = encoder_allocate(e, reinterpret_cast<float**>(&e->vt_halves), halves / 2);
+    if (status == hipSuccess)
+        status = hipMemsetAsync(e->k_halves, 0, halves * sizeof(uint16_t), e->stream);
+    if (status == hipSuccess)
+        status = hipMemsetAsync(e->vt_halves, 0, halves * sizeof(uint16_t), e->stream);
     if (status == hipSuccess && s.heads > 0 && s.width == s.heads * wsp::encoder::kFlashWidth)
         status = encoder_allocate(e, &e->flash_partials,
                                   (size_t) wsp::encoder::kMaxFlashSplits * s.heads * positions
@@ -567,6 +652,7 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
     for (int l = 0; l < s.layers; ++l)
     {
         const wsp_encoder_layer_tensors& L = T->layers[l];
+        bool att_parts = false; // the attention wrote its rows as the output product's parts
         status = split ? ops::layernorm_parts(st, e->hidden, L.attention_norm_w, L.attention_norm_b, e->parts,
                                               part_stride, positions, d, eps, wt)
                        : ops::layernorm(st, e->hidden, L.attention_norm_w, L.attention_norm_b, e->normed, positions,
@@ -594,6 +680,13 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
             p.y2 = e->v;
             p.ldy = d;
             p.wdtype = wt;
+            if (d / heads == kFlashWidth)
+            {
+                // The attention takes k and v as fp16 halves.
+                p.y1_halves = e->k_halves;
+                p.y2_halves_t = e->vt_halves;
+                p.halves_pitch = e->pitch;
+            }
             status = ops::split_product(st, p);
         }
         else if (positions > 16 && ops::tile_product_fits(wt, d, 3 * d, d, e->normed) && d % 128 == 0)
@@ -642,16 +735,39 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
                                                positions / 64}));
             const int span = ((positions + splits - 1) / splits + kFlashKeys - 1) / kFlashKeys * kFlashKeys;
             float* partials = splits > 1 ? e->flash_partials : nullptr;
-            if (8 * wide_blocks >= 7 * compute_units())
-                hipLaunchKernelGGL(flash_attention_kernel<kFlashWideWaves>,
-                                   dim3((positions + 16 * kFlashWideWaves - 1) / (16 * kFlashWideWaves), heads),
-                                   dim3(64 * kFlashWideWaves), 0, st, e->q, e->k, e->v, positions, d, scale2, e->att,
-                                   positions, nullptr);
+            const bool wide = 8 * wide_blocks >= 7 * compute_units();
+            // With the pre-split products, one split writes its rows straight
+            // as the output product's input parts.
+            att_parts = split && (wide || splits == 1);
+            const dim3 grid = wide ? dim3((positions + 16 * kFlashWideWaves - 1) / (16 * kFlashWideWaves), heads)
+                                   : dim3((positions + 16 * kFlashWaves - 1) / (16 * kFlashWaves), heads, splits);
+            const int key_span = wide ? positions : span;
+            uint16_t* const out_parts = static_cast<uint16_t*>(e->parts);
+            auto launch = [&](auto kernel, int waves) {
+                hipLaunchKernelGGL(kernel, grid, dim3(64 * waves), 0, st, e->q, e->k, e->v, positions, d, scale2,
+                                   e->att, key_span, wide ? nullptr : partials, e->k_halves, e->vt_halves, e->pitch,
+                                   out_parts, part_stride);
+            };
+            if (!split)
+            {
+                if (wide)
+                    launch(flash_attention_kernel<kFlashWideWaves>, kFlashWideWaves);
+                else
+                    launch(flash_attention_kernel<kFlashWaves>, kFlashWaves);
+            }
+            else if (!att_parts)
+                launch(flash_attention_kernel<kFlashWaves, true>, kFlashWaves);
+            else if (wt == WSP_F16)
+            {
+                if (wide)
+                    launch(flash_attention_kernel<kFlashWideWaves, true, wsp::kF16>, kFlashWideWaves);
+                else
+                    launch(flash_attention_kernel<kFlashWaves, true, wsp::kF16>, kFlashWaves);
+            }
+            else if (wide)
+                launch(flash_attention_kernel<kFlashWideWaves, true, wsp::kBF16>, kFlashWideWaves);
             else
-                hipLaunchKernelGGL(flash_attention_kernel<kFlashWaves>,
-                                   dim3((positions + 16 * kFlashWaves - 1) / (16 * kFlashWaves), heads, splits),
-                                   dim3(64 * kFlashWaves), 0, st, e->q, e->k, e->v, positions, d, scale2, e->att,
-                                   span, partials);
+                launch(flash_attention_kernel<kFlashWaves, true, wsp::kBF16>, kFlashWaves);
             status = hipGetLastError();
             if (status == hipSuccess && splits > 1)
             {
@@ -667,7 +783,8 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
             return encoder_hip(e, status, "self attention");
         if (split)
         {
-            if ((status = ops::split_rows(st, e->att, part_stride, wt, e->parts, part_stride)) == hipSuccess)
+            if (att_parts || (status = ops::split_rows(st, e->att, part_stride, wt, e->parts, part_stride))
+                                 == hipSuccess)
                 status = split_product(e->parts, part_stride, d, L.out_w, L.out_b, e->hidden, d,
                                        ops::kProductResidual, nullptr);
         }

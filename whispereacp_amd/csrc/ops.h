@@ -85,6 +85,14 @@ struct SplitProduct
     void* out_parts;
     size_t out_part_stride;
     int wdtype;
+    // Columns [split, split2) (y1_halves) and [split2, out) (y2_halves_t), when
+    // set, go out as fp16 hi = fp16(v) and lo = fp16(v - hi) instead of fp32:
+    // hi of row r, column c at y1_halves[r·width + c], lo halves_pitch·width
+    // further; y2_halves_t transposed, hi at [c·halves_pitch + r]. (The
+    // encoder's keys and values for its attention.)
+    void* y1_halves;
+    void* y2_halves_t;
+    int halves_pitch;
 };
 
 // 16-bit weights, inner % 32 == 0, out, split and split2 multiples of 128.

@@ -276,6 +276,15 @@ __global__ void __launch_bounds__(kThreads) split_product_kernel(SplitProduct a)
                     for (int p = 0; p < P; ++p)
                         o[p * a.out_part_stride] = (u16) bits[p];
                 }
+                else if ((seg == 1 && a.y1_halves != nullptr) || (seg == 2 && a.y2_halves_t != nullptr))
+                {
+                    const _Float16 hi = (_Float16) v;
+                    const _Float16 lo = (_Float16) (v - (float) hi);
+                    u16* o = seg == 1 ? static_cast<u16*>(a.y1_halves) + (size_t) row * width + c
+                                      : static_cast<u16*>(a.y2_halves_t) + (size_t) c * a.halves_pitch + row;
+                    o[0] = __builtin_bit_cast(u16, hi);
+                    o[(size_t) a.halves_pitch * width] = __builtin_bit_cast(u16, lo);
+                }
                 else if (a.flags & kProductResidual)
                     y[(size_t) row * a.ldy + c] += v;
                 else
