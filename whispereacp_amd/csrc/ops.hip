@@ -287,15 +287,11 @@ __global__ void __launch_bounds__(kBlock) gemm_kernel(const float* __restrict__ 
 // LayerNorm: one block per row; mean, then the centred variance, then
 // (x - mean) * rsqrt(var + eps) * gamma + beta (Kernels/LayerNorm.h:44-89).
 // ---------------------------------------------------------------------------
-// PARTS (kF16 or kBF16): the row goes out as exact 16-bit parts for a
-// product with such weights, part p at parts + p·part_stride (split_product).
-template <int PARTS>
 __global__ void __launch_bounds__(kBlock) layernorm_kernel(const float* __restrict__ x,
                                                            const float* __restrict__ gamma,
                                                            const float* __restrict__ beta,
                                                            float* __restrict__ y, int width,
-                                                           float eps, uint16_t* __restrict__ parts,
-                                                           size_t part_stride)
+                                                           float eps)
 {
     __shared__ float scratch[kWavesPerBlock];
     const float* row = x + (size_t) blockIdx.x * width;
@@ -315,20 +311,7 @@ __global__ void __launch_bounds__(kBlock) layernorm_kernel(const float* __restri
     const float scale = rsqrtf(block_sum(squares, scratch) / (float) width + eps);
 
     for (int c = threadIdx.x; c < width; c += kBlock)
-    {
-        const float v = (row[c] - mean) * scale * gamma[c] + beta[c];
-        if constexpr (PARTS == kF32)
-            dst[c] = v;
-        else
-        {
-            uint32_t bits[3];
-            exact_parts<PARTS>(v, bits);
-            uint16_t* out = parts + (size_t) blockIdx.x * width + c;
-#pragma unroll
-            for (int p = 0; p < (PARTS == kF16 ? 2 : 3); ++p)
-                out[p * part_stride] = (uint16_t) bits[p];
-        }
-    }
+        dst[c] = (row[c] - mean) * scale * gamma[c] + beta[c];
 }
 
 // ---------------------------------------------------------------------------
@@ -845,23 +828,7 @@ hipError_t linear(hipStream_t stream, const float* x, int rows, int inner, const
 hipError_t layernorm(hipStream_t stream, const float* x, const float* gamma, const float* beta,
                      float* y, int rows, int width, float eps)
 {
-    hipLaunchKernelGGL(layernorm_kernel<kF32>, dim3(rows), dim3(kBlock), 0, stream, x, gamma, beta, y, width, eps,
-                       nullptr, 0);
-    return hipGetLastError();
-}
-
-hipError_t layernorm_parts(hipStream_t stream, const float* x, const float* gamma, const float* beta, void* parts,
-                           size_t part_stride, int rows, int width, float eps, int wdtype)
-{
-    uint16_t* out = static_cast<uint16_t*>(parts);
-    if (wdtype == kF16)
-        hipLaunchKernelGGL(layernorm_kernel<kF16>, dim3(rows), dim3(kBlock), 0, stream, x, gamma, beta, nullptr,
-                           width, eps, out, part_stride);
-    else if (wdtype == kBF16)
-        hipLaunchKernelGGL(layernorm_kernel<kBF16>, dim3(rows), dim3(kBlock), 0, stream, x, gamma, beta, nullptr,
-                           width, eps, out, part_stride);
-    else
-        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(layernorm_kernel, dim3(rows), dim3(kBlock), 0, stream, x, gamma, beta, y, width, eps);
     return hipGetLastError();
 }
 

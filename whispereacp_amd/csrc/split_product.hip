@@ -106,6 +106,63 @@ __global__ void __launch_bounds__(kSplitThreads) split_rows_kernel(const float* 
         *reinterpret_cast<u32x4*>(parts + p * part_stride + i) = out[p];
 }
 
+// LayerNorm of one row per wave (ops::layernorm's arithmetic: the mean, the
+// centred squares' mean, then (x - mean)·rstd·gamma + beta), written as the
+// parts of split_product's input. A lane holds float4 runs lane, lane + 64,
+// ... of the row in registers (at most kNormRuns of them), so the row is read
+// once; each part's four values of a run go out as one 8-byte store.
+constexpr int kNormRowsPerBlock = 4;
+constexpr int kNormRuns = 8; // widths up to 2048
+
+template <int WT>
+__global__ void __launch_bounds__(kNormRowsPerBlock * kWave) layernorm_parts_kernel(
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta, int rows,
+    int width, float eps, u16* __restrict__ parts, size_t part_stride)
+{
+    constexpr int P = parts_of<WT>();
+    const int row = blockIdx.x * kNormRowsPerBlock + (int) threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    if (row >= rows)
+        return;
+    const int runs = width / 4;
+    const float* src = x + (size_t) row * width;
+    float4v v[kNormRuns];
+    float total = 0.f;
+#pragma unroll
+    for (int i = 0; i < kNormRuns; ++i)
+    {
+        const int r = lane + kWave * i;
+        v[i] = r < runs ? *reinterpret_cast<const float4v*>(src + 4 * r) : float4v {0.f, 0.f, 0.f, 0.f};
+        total += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+    }
+    const float mean = wave_sum(total) / (float) width;
+    float squares = 0.f;
+#pragma unroll
+    for (int i = 0; i < kNormRuns; ++i)
+        if (lane + kWave * i < runs)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                const float c = v[i][e] - mean;
+                squares += c * c;
+            }
+    const float scale = rsqrtf(wave_sum(squares) / (float) width + eps);
+#pragma unroll
+    for (int i = 0; i < kNormRuns; ++i)
+    {
+        const int r = lane + kWave * i;
+        if (r >= runs)
+            continue;
+        uint32_t bits[4][3];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            split<WT>((v[i][e] - mean) * scale * gamma[4 * r + e] + beta[4 * r + e], bits[e]);
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+            *reinterpret_cast<uint2*>(parts + p * part_stride + (size_t) row * width + 4 * r)
+                = uint2 {bits[0][p] | (bits[1][p] << 16), bits[2][p] | (bits[3][p] << 16)};
+    }
+}
+
 // The LDS byte address of a shared-memory pointer.
 __device__ __forceinline__ uint32_t lds_address(const void* p)
 {
@@ -343,6 +400,21 @@ hipError_t split_rows(hipStream_t stream, const float* x, size_t count, int wdty
     else
         hipLaunchKernelGGL(split_rows_kernel<kBF16>, grid, dim3(kSplitThreads), 0, stream, x, count,
                            static_cast<u16*>(parts), part_stride);
+    return hipGetLastError();
+}
+
+hipError_t layernorm_parts(hipStream_t stream, const float* x, const float* gamma, const float* beta, void* parts,
+                           size_t part_stride, int rows, int width, float eps, int wdtype)
+{
+    if (width % 4 != 0 || width > 4 * kWave * kNormRuns || (wdtype != kF16 && wdtype != kBF16))
+        return hipErrorInvalidValue;
+    const dim3 grid((rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
+    if (wdtype == kF16)
+        hipLaunchKernelGGL(layernorm_parts_kernel<kF16>, grid, dim3(kNormRowsPerBlock * kWave), 0, stream, x, gamma,
+                           beta, rows, width, eps, static_cast<u16*>(parts), part_stride);
+    else
+        hipLaunchKernelGGL(layernorm_parts_kernel<kBF16>, grid, dim3(kNormRowsPerBlock * kWave), 0, stream, x,
+                           gamma, beta, rows, width, eps, static_cast<u16*>(parts), part_stride);
     return hipGetLastError();
 }
 
