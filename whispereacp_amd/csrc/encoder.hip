@@ -629,7 +629,8 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
     // 16-bit weights take the products over pre-split inputs: each product's
     // input is stored once as exact 16-bit parts (fc1 writes fc2's itself).
     const size_t part_stride = (size_t) positions * d, ff_part_stride = (size_t) positions * f;
-    const bool split = positions > 16 && part_stride % 8 == 0 && ops::split_product_fits(wt, d, 3 * d, d, 2 * d)
+    const bool split = positions > 16 && part_stride % 8 == 0 && ops::layernorm_parts_fits(d)
+                       && ops::split_product_fits(wt, d, 3 * d, d, 2 * d)
                        && ops::split_product_fits(wt, d, f, f, f) && ops::split_product_fits(wt, f, d, d, d);
     auto split_product = [&](const void* parts, size_t stride, int inner, const void* w, const float* bias, float* y,
                              int out, int flags, void* out_parts) {

@@ -98,7 +98,9 @@ struct SplitProduct
 // 16-bit weights, inner % 32 == 0, out, split and split2 multiples of 128.
 bool split_product_fits(int wdtype, int inner, int out, int split, int split2);
 hipError_t split_product(hipStream_t stream, const SplitProduct& product);
-// LayerNorm rows (as layernorm) written as the parts of split_product's input.
+// LayerNorm rows (as layernorm) written as the parts of split_product's input;
+// widths that are multiples of 4 up to 2048 (layernorm_parts_fits).
+bool layernorm_parts_fits(int width);
 hipError_t layernorm_parts(hipStream_t stream, const float* x, const float* gamma, const float* beta, void* parts,
                            size_t part_stride, int rows, int width, float eps, int wdtype);
 // count fp32 values (a multiple of 8) as parts for 16-bit weights of wdtype.

@@ -403,10 +403,15 @@ hipError_t split_rows(hipStream_t stream, const float* x, size_t count, int wdty
     return hipGetLastError();
 }
 
+bool layernorm_parts_fits(int width)
+{
+    return width > 0 && width % 4 == 0 && width <= 4 * kWave * kNormRuns;
+}
+
 hipError_t layernorm_parts(hipStream_t stream, const float* x, const float* gamma, const float* beta, void* parts,
                            size_t part_stride, int rows, int width, float eps, int wdtype)
 {
-    if (width % 4 != 0 || width > 4 * kWave * kNormRuns || (wdtype != kF16 && wdtype != kBF16))
+    if (!layernorm_parts_fits(width) || (wdtype != kF16 && wdtype != kBF16))
         return hipErrorInvalidValue;
     const dim3 grid((rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
     if (wdtype == kF16)
