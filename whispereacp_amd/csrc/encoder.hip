@@ -64,22 +64,25 @@ __global__ void __launch_bounds__(kColumnThreads) mel_columns_kernel(const float
 // sees every key, softmax(scale q.k) v per head) for head width 64, on the
 // matrix cores, one pass over the keys with an online softmax.
 //
-// A block takes 16 queries per wave of one head; key tiles of 32 rows of K
-// and V go through LDS once for all its waves. Every fp32 operand is cut
-// into fp16 parts, hi = fp16(x) and lo = fp16(x - hi), and a product takes
+// A block takes 16 queries per wave of one head; key tiles of 64 rows of K
+// and V go through LDS once for all its waves (64 measured 12.19 against
+// 12.33 ms a large-v3 window for 32: half the barriers and softmax passes).
+// Every fp32 operand is cut into fp16 parts, hi = fp16(x) and
+// lo = fp16(x - hi), and a product takes
 // the three terms hi·hi + hi·lo + lo·hi (v_mfma_f32_16x16x32_f16, fp32
 // accumulation): what is dropped, lo·lo, is about 2^-22 of the product, so
 // the sums stay at fp32 rather than fp16 accuracy.
 //
 // Layout: the wave computes S^T = K·Q^T, so lane (g, l) holds the scores of
-// keys 4g..4g+3 and 16+4g..16+4g+3 of the tile for query l — exactly the B
-// operand of O^T = V^T·P^T once the tile's key order inside the 32-key
-// k-block is taken as (4g..4g+3, 16+4g..16+4g+3) for both operands, so P
+// keys 4g..4g+3 and 16+4g..16+4g+3 of each 32-key block of the tile for
+// query l — exactly the B operand of O^T = V^T·P^T once the key order
+// inside each 32-key block is taken as (4g..4g+3, 16+4g..16+4g+3) for both
+// operands, so P
 // never leaves its registers. V is staged transposed for that A operand.
 // Scores are in base-2 units (scale·log2 e folded in); each new tile
 // rescales the running row by exp2(m_old - m_new) (exact online softmax).
 // ---------------------------------------------------------------------------
-constexpr int kFlashKeys = 32;
+constexpr int kFlashKeys = 64;
 constexpr int kFlashWidth = 64;
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -139,6 +142,7 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
     constexpr int kUnits = kFlashKeys * kFlashWidth / 4; // float4 runs of a K (or V) tile
     constexpr int kPerThread = (kUnits + kThreadsHere - 1) / kThreadsHere;
     constexpr int kHalfChunks = 2 * kFlashKeys * kFlashWidth / 8; // 16-byte runs of a tile's K (or V) halves
+    constexpr int KB = kFlashKeys / 32;                           // 32-key blocks of a tile (P·V k-steps)
     constexpr int kHalfPerThread = kHalfChunks / kThreadsHere;
     static_assert(kHalfChunks % kThreadsHere == 0, "whole half runs per thread");
     __shared__ __attribute__((aligned(16))) _Float16 ks[2][kFlashKeys][kFlashWidth + 8];
@@ -188,10 +192,10 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
         const int unit = (int) threadIdx.x + i * kThreadsHere;
         const int rest = unit % (kHalfChunks / 2);
         part = unit / (kHalfChunks / 2);
-        a = rest / 8;
-        b = rest % 8;
-        c = rest / 4;
-        kb = rest % 4;
+        a = rest / (kFlashWidth / 8);
+        b = rest % (kFlashWidth / 8);
+        c = rest / (kFlashKeys / 8);
+        kb = rest % (kFlashKeys / 8);
     };
     const int last_first = k_begin + (max(k_end - k_begin, 1) - 1) / kFlashKeys * kFlashKeys;
     const size_t halves_part = (size_t) pitch * width;
@@ -267,9 +271,9 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
             load_tile(st, first + 2 * kFlashKeys);
 
         // S^T for keys 16 mt + 4 g + r of the tile, query li.
-        f32x4 st_[2];
+        f32x4 st_[2 * KB];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < 2 * KB; ++mt)
         {
             st_[mt] = f32x4 {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -280,10 +284,10 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
                 st_[mt] = mfma3(kh, kl, qh[s], ql[s], st_[mt]);
             }
         }
-        float x[8];
+        float x[8 * KB];
         float tile_max = -INFINITY;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < 2 * KB; ++mt)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
             {
@@ -295,33 +299,40 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
         tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
         const float m_new = fmaxf(m, tile_max);
         const float alpha = exp2f(m - m_new);
-        float p[8], own = 0.f;
+        float p[8 * KB], own = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 8 * KB; ++j)
         {
             p[j] = exp2f(x[j] - m_new);
             own += p[j];
         }
         l = l * alpha + own;
         m = m_new;
-        f16x8 ph, pl;
+        // Key block b (keys 32 b .. 32 b + 31 of the tile) takes p[8 b .. 8 b + 7].
+        f16x8 ph[KB], pl[KB];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-        {
-            ph[j] = half_hi(p[j]);
-            pl[j] = half_lo(p[j]);
-        }
+        for (int b = 0; b < KB; ++b)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+            {
+                ph[b][j] = half_hi(p[8 * b + j]);
+                pl[b][j] = half_lo(p[8 * b + j]);
+            }
 #pragma unroll
         for (int t = 0; t < 4; ++t)
         {
             o[t] *= alpha;
-            const f16x4 a0 = *reinterpret_cast<const f16x4*>(&vt[0][16 * t + li][4 * g]);
-            const f16x4 a1 = *reinterpret_cast<const f16x4*>(&vt[0][16 * t + li][16 + 4 * g]);
-            const f16x4 b0 = *reinterpret_cast<const f16x4*>(&vt[1][16 * t + li][4 * g]);
-            const f16x4 b1 = *reinterpret_cast<const f16x4*>(&vt[1][16 * t + li][16 + 4 * g]);
-            const f16x8 vh = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-            const f16x8 vl = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-            o[t] = mfma3(vh, vl, ph, pl, o[t]);
+#pragma unroll
+            for (int b = 0; b < KB; ++b)
+            {
+                const f16x4 a0 = *reinterpret_cast<const f16x4*>(&vt[0][16 * t + li][32 * b + 4 * g]);
+                const f16x4 a1 = *reinterpret_cast<const f16x4*>(&vt[0][16 * t + li][32 * b + 16 + 4 * g]);
+                const f16x4 b0 = *reinterpret_cast<const f16x4*>(&vt[1][16 * t + li][32 * b + 4 * g]);
+                const f16x4 b1 = *reinterpret_cast<const f16x4*>(&vt[1][16 * t + li][32 * b + 16 + 4 * g]);
+                const f16x8 vh = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+                const f16x8 vl = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+                o[t] = mfma3(vh, vl, ph[b], pl[b], o[t]);
+            }
         }
     };
 
