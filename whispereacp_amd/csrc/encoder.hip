@@ -65,8 +65,9 @@ __global__ void __launch_bounds__(kColumnThreads) mel_columns_kernel(const float
 // matrix cores, one pass over the keys with an online softmax.
 //
 // A block takes 16 queries per wave of one head; key tiles of 64 rows of K
-// and V go through LDS once for all its waves (64 measured 12.19 against
-// 12.33 ms a large-v3 window for 32: half the barriers and softmax passes).
+// and V go through LDS once for all its waves (a large-v3 window took 12.19
+// ms with 64-key tiles, 12.33 with 32, 12.30 with 128: half the barriers and
+// softmax passes of 32, fewer registers than 128).
 // Every fp32 operand is cut into fp16 parts, hi = fp16(x) and
 // lo = fp16(x - hi), and a product takes
 // the three terms hi·hi + hi·lo + lo·hi (v_mfma_f32_16x16x32_f16, fp32
