@@ -2,8 +2,9 @@
 tests/test_encoder_oracle.py), in the manner of Tests/Encoder/EncoderTests.cpp:
 the reference test suite's small encoder over float, packed-half and all-half
 files, a reduced context against the shorter shape, a Whisper-width encoder
-with 16-bit projections on the matrix cores, and the tiny.en encoder over the
-full 30 s window. Bar: the reference's own 5e-6 worst error
+with 16-bit projections on the matrix cores, the tiny.en encoder over the
+full 30 s window, and one large-v3 layer over it (the product tile shapes
+the full model runs). Bar: the reference's own 5e-6 worst error
 (Tests/Encoder/EncoderTests.cpp:97-108) for the small encoder; 1e-4 for the
 larger ones (float32 sums over 1500-key softmaxes and 1536-wide products)."""
 
@@ -118,4 +119,20 @@ def test_tiny_en_encoder_full_window_matches_oracle(oracle):
     got = gpu_rows(shape, encoder_file, mel)
     err = worst_error(got, oracle_rows(oracle, shape, encoder_file, mel))
     print(f"tiny.en encoder, 1500 positions: worst error {err:.2e}")
+    assert err <= 1e-4
+
+
+@pytest.mark.parametrize("dtype", ["BF16", "F16"])
+@pytest.mark.timeout(300)
+def test_large_v3_layer_over_the_full_window_matches_oracle(oracle, dtype):
+    # One layer of the large-v3 encoder (d 1280, 20 heads, ffn 5120) over the
+    # whole window: the products take 128-column tiles (q/k/v: 360 blocks,
+    # fc1: 480) and 64-column ones (out, fc2), and the attention its 128-query
+    # blocks writing the out product's parts — the shapes the full model runs.
+    shape = S.EncoderShape(128, 1280, 20, 1, 5120, 3000)
+    encoder_file = S.workload_encoder_file(shape, dtype, 3000)
+    mel = S.normal_mel(shape, 3500)
+    got = gpu_rows(shape, encoder_file, mel)
+    err = worst_error(got, oracle_rows(oracle, shape, encoder_file, mel))
+    print(f"large-v3 layer, {dtype}, 1500 positions: worst error {err:.2e}")
     assert err <= 1e-4
