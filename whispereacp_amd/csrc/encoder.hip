@@ -147,7 +147,10 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
     constexpr int kHalfPerThread = kHalfChunks / kThreadsHere;
     static_assert(kHalfChunks % kThreadsHere == 0, "whole half runs per thread");
     __shared__ __attribute__((aligned(16))) _Float16 ks[2][kFlashKeys][kFlashWidth + 8];
-    __shared__ __attribute__((aligned(16))) _Float16 vt[2][kFlashWidth][kFlashKeys + 8];
+    // V^T rows padded by four halves (a pitch of 34 words): the 8-byte operand
+    // reads of 16 lanes (rows li) then land on 16 distinct bank pairs; K's
+    // 16-byte reads of 8 lanes need a pitch of 4 words mod 32 (72 halves).
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][kFlashWidth][kFlashKeys + 4];
 
     const int head = blockIdx.y;
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, li = lane % 16, g = lane / 16;
@@ -239,7 +242,10 @@ __global__ void __launch_bounds__(WAVES * 64) flash_attention_kernel(const float
                 int part, row, cb, c, kb;
                 half_run(i, part, row, cb, c, kb);
                 *reinterpret_cast<u32x4*>(&ks[part][row][8 * cb]) = st.kh[i];
-                *reinterpret_cast<u32x4*>(&vt[part][c][8 * kb]) = st.vh[i];
+                // (8-byte aligned rows: two 8-byte stores)
+                uint2* v2 = reinterpret_cast<uint2*>(&vt[part][c][8 * kb]);
+                v2[0] = uint2 {st.vh[i][0], st.vh[i][1]};
+                v2[1] = uint2 {st.vh[i][2], st.vh[i][3]};
             }
         }
         else
