@@ -673,7 +673,9 @@ def bench_encoder(args):
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("f16" if dtype == "F16" else "bf16") + "-weights/f32 (activations as exact 16-bit parts)",
+        "dtype": ("f16-weights/f32 (activations as fp16 hi/lo parts)" if dtype == "F16" else
+                  "bf16-weights held as exact scaled fp16/f32 (activations as fp16 hi/lo parts)"
+                  if weights.dtype == "F16" else "bf16-weights/f32 (activations as exact bf16 parts)"),
         "data": "synthetic: N(0,0.02) weights (LayerNorm gamma 1, beta 0), N(0,0.5) clipped mel",
         "config": {"workload": f"{name} encoder: {shape.mel_bins} mel bins x {shape.input_frames} frames, d_model "
                                f"{d}, {shape.heads} heads, {shape.layers} layers, ffn {f}, {T} positions, {dtype} "

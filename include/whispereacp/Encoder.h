@@ -7,6 +7,9 @@
 // Storage follows the reference's loader: every projection weight stays as
 // the file holds it (F16 or BF16) or is packed to fp16 where narrowing is
 // exact under WeightPacking::ExactHalf; everything else is widened to float.
+// BF16 projections are held as exact fp16 multiples w·2^k with their scales
+// (wsp_encoder_scaled_halves) when every one of them narrows exactly and the
+// shape's products run over pre-split inputs.
 // The gfx950 encoder reads one projection storage for the whole model, so a
 // file whose projections would end up in different storages is uploaded with
 // every projection widened to float.

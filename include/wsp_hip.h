@@ -349,7 +349,9 @@ typedef struct wsp_encoder_shape
 /* Encoder/EncoderWeights.h:19-36, HuggingFace's model.encoder.layers.<i>.*
  * tensors: projections in `wdtype` storage, everything else fp32 (the
  * reference widens every non-projection tensor, Encoder/EncoderWeights.h:44-52).
- * k_proj has no bias. */
+ * k_proj has no bias. The *_scale fields are the power of two each stored
+ * projection carries (wsp_encoder_scaled_halves: bf16 weights held as exact
+ * fp16 multiples); the products divide it out. 0 or 1: stored as they are. */
 typedef struct wsp_encoder_layer_tensors
 {
     const float* attention_norm_w;
@@ -367,6 +369,7 @@ typedef struct wsp_encoder_layer_tensors
     const float* fc1_b;
     const void* fc2_w;
     const float* fc2_b;
+    float q_scale, k_scale, v_scale, out_scale, fc1_scale, fc2_scale;
 } wsp_encoder_layer_tensors;
 
 /* Encoder/EncoderWeights.h:70-93: conv1 [width, mel_bins, 3], conv2 [width,
@@ -400,6 +403,20 @@ const char* wsp_encoder_last_error(const wsp_encoder* encoder);
  * window is WSP_ERR_SHAPE before anything is launched. No allocation. */
 int wsp_encoder_encode(wsp_encoder* encoder, const wsp_encoder_tensors* tensors, const float* mel, float* output,
                        int position_count);
+
+/* No reference counterpart: a storage choice of the loader, as the
+ * reference's exact fp16 packing of F32 projections is
+ * (Model/SafeTensors.cpp:554-592). A bf16 projection of `count` values
+ * (host memory) written to `halves` (host memory) as fp16 values w·2^k, k
+ * the largest shift that leaves every value finite, and *scale = 2^k. The
+ * products then read two fp16 parts of their fp32 input instead of three
+ * bf16 ones. WSP_OK when every value narrows exactly; WSP_ERR_LOGIC when one
+ * does not (or is not finite): keep the bf16 storage then; WSP_ERR_SHAPE when
+ * the shape's encoder does not take scaled projections (it needs its products
+ * over pre-split inputs: width and ffn width multiples of 128, width at most
+ * 2048). No GPU work. */
+int wsp_encoder_scaled_halves(const wsp_encoder_shape* shape, const void* bf16, size_t count, void* halves,
+                              float* scale);
 
 /* ---------------------------------------------------------------------------
  * The mel front end (Mel/MelSpectrogram.h:12-25, Mel/MelShape.h:16-30): 30 s

@@ -8,6 +8,7 @@ the full model runs). Bar: the reference's own 5e-6 worst error
 (Tests/Encoder/EncoderTests.cpp:97-108) for the small encoder; 1e-4 for the
 larger ones (float32 sums over 1500-key softmaxes and 1536-wide products)."""
 
+import ctypes
 import json
 import os
 
@@ -34,10 +35,10 @@ def oracle_rows(oracle, shape, encoder_file, mel, positions=0):
     return oracle.encode(run, tensors, np.ascontiguousarray(mel[:, :run.input_frames]))
 
 
-def gpu_rows(shape, encoder_file, mel, positions=0, fill=None):
+def gpu_rows(shape, encoder_file, mel, positions=0, fill=None, scaled_halves=True):
     from whispereacp_amd.encoder import Encoder, EncoderWeights
     encoder = Encoder(shape)
-    weights = EncoderWeights(shape, encoder_file)
+    weights = EncoderWeights(shape, encoder_file, scaled_halves)
     mel_d = torch.from_numpy(np.ascontiguousarray(mel, dtype=np.float32)).cuda()
     out = torch.full((shape.positions(), shape.width), float("nan") if fill is None else fill,
                      dtype=torch.float32, device="cuda")
@@ -86,19 +87,57 @@ def test_short_positional_table_is_a_model_error():
         EncoderWeights(shape.with_frames(40), encoder_file)
 
 
-@pytest.mark.parametrize("dtype,frames", [("F16", 64), ("BF16", 64), ("F32", 64), ("F16", 74), ("BF16", 27)])
-def test_whisper_width_encoder_matches_oracle(oracle, dtype, frames):
+@pytest.mark.parametrize("dtype,frames,scaled", [("F16", 64, True), ("BF16", 64, True), ("BF16", 64, False),
+                                                 ("F32", 64, True), ("F16", 74, True), ("BF16", 27, True),
+                                                 ("BF16", 27, False)])
+def test_whisper_width_encoder_matches_oracle(oracle, dtype, frames, scaled):
     # 80 mel bins and head width 64: the projections (more than 16 rows) take
     # the matrix-core product for 16-bit weights, and the attention the
     # matrix-core flash kernel — over 32 positions, and over 37 and 14, which
-    # leave part-filled query blocks and key tiles.
+    # leave part-filled query blocks and key tiles. BF16 runs both as exact
+    # scaled fp16 (the pre-split products at every position count, 14 too)
+    # and as stored (three bf16 parts).
     shape = S.EncoderShape(80, 128, 2, 2, 512, frames)
     encoder_file = S.workload_encoder_file(shape, dtype, 3000)
     mel = S.normal_mel(shape, 3500)
-    got = gpu_rows(shape, encoder_file, mel)
+    got = gpu_rows(shape, encoder_file, mel, scaled_halves=scaled)
     err = worst_error(got, oracle_rows(oracle, shape, encoder_file, mel))
-    print(f"width 128 encoder, {dtype}: worst error {err:.2e}")
+    print(f"width 128 encoder, {dtype}, scaled halves {scaled}: worst error {err:.2e}")
     assert err <= 1e-4
+
+
+def test_bf16_projections_are_held_as_scaled_halves():
+    from whispereacp_amd.encoder import EncoderWeights
+    shape = S.EncoderShape(80, 128, 2, 2, 512, 64)
+    encoder_file = S.workload_encoder_file(shape, "BF16", 3000)
+    weights = EncoderWeights(shape, encoder_file)
+    assert (weights.stored_dtype, weights.dtype) == ("BF16", "F16")
+    layer = weights._layers[1]
+    for field in ("q_scale", "k_scale", "v_scale", "out_scale", "fc1_scale", "fc2_scale"):
+        mantissa, exponent = np.frexp(getattr(layer, field))
+        assert mantissa == 0.5 and exponent > 1, field
+    stored = encoder_file[S.encoder_layer_name(1, "fc1.weight")]
+    held = weights._keep[S.encoder_layer_name(1, "fc1.weight")].cpu().numpy().astype(np.float64)
+    assert np.array_equal(held / layer.fc1_scale, stored.floats().astype(np.float64).reshape(held.shape))
+    assert EncoderWeights(shape, encoder_file, scaled_halves=False).dtype == "BF16"
+    # A narrow shape keeps its BF16 storage: its products take no scales.
+    narrow = S.EncoderShape(80, 64, 2, 1, 256, 64)
+    assert EncoderWeights(narrow, S.workload_encoder_file(narrow, "BF16", 3000)).dtype == "BF16"
+
+
+def test_a_scale_that_is_not_a_power_of_two_is_refused():
+    from whispereacp_amd import _native as N
+    from whispereacp_amd.encoder import Encoder, EncoderWeights
+    shape = S.EncoderShape(80, 128, 2, 1, 512, 64)
+    weights = EncoderWeights(shape, S.workload_encoder_file(shape, "BF16", 3000))
+    weights._layers[0].fc2_scale = 3.0
+    encoder = Encoder(shape)
+    mel = torch.zeros((shape.mel_bins, shape.input_frames), dtype=torch.float32, device="cuda")
+    out = torch.empty((shape.positions(), shape.width), dtype=torch.float32, device="cuda")
+    status = encoder.lib.wsp_encoder_encode(encoder.handle, ctypes.byref(weights.table), mel.data_ptr(),
+                                            out.data_ptr(), 0)
+    assert status == N.WSP_ERR_ARGUMENT
+    assert b"power of two" in encoder.lib.wsp_encoder_last_error(encoder.handle)
 
 
 def test_golden_fixture_through_the_gpu():
@@ -122,9 +161,9 @@ def test_tiny_en_encoder_full_window_matches_oracle(oracle):
     assert err <= 1e-4
 
 
-@pytest.mark.parametrize("dtype", ["BF16", "F16"])
+@pytest.mark.parametrize("dtype,scaled", [("BF16", True), ("BF16", False), ("F16", True)])
 @pytest.mark.timeout(300)
-def test_large_v3_layer_over_the_full_window_matches_oracle(oracle, dtype):
+def test_large_v3_layer_over_the_full_window_matches_oracle(oracle, dtype, scaled):
     # One layer of the large-v3 encoder (d 1280, 20 heads, ffn 5120) over the
     # whole window: the products take 128-column tiles (q/k/v: 360 blocks,
     # fc1: 480) and 64-column ones (out, fc2), and the attention its 128-query
@@ -132,7 +171,7 @@ def test_large_v3_layer_over_the_full_window_matches_oracle(oracle, dtype):
     shape = S.EncoderShape(128, 1280, 20, 1, 5120, 3000)
     encoder_file = S.workload_encoder_file(shape, dtype, 3000)
     mel = S.normal_mel(shape, 3500)
-    got = gpu_rows(shape, encoder_file, mel)
+    got = gpu_rows(shape, encoder_file, mel, scaled_halves=scaled)
     err = worst_error(got, oracle_rows(oracle, shape, encoder_file, mel))
-    print(f"large-v3 layer, {dtype}, 1500 positions: worst error {err:.2e}")
+    print(f"large-v3 layer, {dtype}, scaled halves {scaled}, 1500 positions: worst error {err:.2e}")
     assert err <= 1e-4

@@ -138,6 +138,28 @@ def test_packed_weights_transcribe_alike(tmp_path, tensors):
     assert len(set(plain)) >= 4
 
 
+def test_bf16_encoder_projections_transcribe_as_the_oracle(tmp_path, tensors):
+    # BF16 encoder projections: the C++ loader holds them as exact scaled fp16
+    # (wsp_encoder_scaled_halves), each with its own scale (q and fc2 are
+    # rescaled by powers of two so no two neighbours share one), and the
+    # transcript follows the oracle chain over the same bf16 values.
+    factors = {"self_attn.q_proj.weight": 0.25, "self_attn.k_proj.weight": 1.0, "self_attn.v_proj.weight": 0.5,
+               "self_attn.out_proj.weight": 1.0, "fc1.weight": 1.0, "fc2.weight": 2.0}
+    bf16 = dict(tensors)
+    for layer in range(H.WHISPER_ENCODER.layers):
+        for suffix, factor in factors.items():
+            name = S.encoder_layer_name(layer, suffix)
+            t = tensors[name]
+            bf16[name] = S.StoredTensor(t.name, "BF16", t.extents, S.store(t.floats().ravel() * factor, "BF16"))
+    directory = H.write_whisper(tmp_path / "bf16", bf16)
+    w = prepared(directory)
+    tokens = w.transcribe(SAMPLES)
+    expected, margins = oracle_run(bf16, w)
+    assert min(margins) > 1e-2, "the oracle's run has a near tie; pick other inputs"
+    assert tokens == expected
+    assert len(set(tokens)) >= 4
+
+
 def test_a_frequency_major_filterbank_transcribes_alike(tmp_path, model, tensors):
     directory = H.write_whisper(tmp_path / "transposed", tensors, filters=H.whisper_filters().T)
     assert prepared(directory).transcribe(SAMPLES) == prepared(model).transcribe(SAMPLES)

@@ -68,7 +68,8 @@ class wsp_encoder_shape(ctypes.Structure):
 class wsp_encoder_layer_tensors(ctypes.Structure):
     _fields_ = [(n, c_void_p) for n in (
         "attention_norm_w", "attention_norm_b", "q_w", "q_b", "k_w", "v_w", "v_b", "out_w", "out_b",
-        "final_norm_w", "final_norm_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b")]
+        "final_norm_w", "final_norm_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b")] + [
+        (n, c_float) for n in ("q_scale", "k_scale", "v_scale", "out_scale", "fc1_scale", "fc2_scale")]
 
 
 class wsp_encoder_tensors(ctypes.Structure):
@@ -180,6 +181,8 @@ SIGNATURES = {
     "wsp_encoder_destroy": (None, [c_void_p]),
     "wsp_encoder_last_error": (c_char_p, [c_void_p]),
     "wsp_encoder_encode": (c_int, [c_void_p, ctypes.POINTER(wsp_encoder_tensors), c_void_p, c_void_p, c_int]),
+    "wsp_encoder_scaled_halves": (c_int, [ctypes.POINTER(wsp_encoder_shape), c_void_p, ctypes.c_size_t, c_void_p,
+                                          ctypes.POINTER(c_float)]),
     "wsp_mel_create": (c_int, [ctypes.POINTER(wsp_mel_shape), c_int, c_void_p, ctypes.POINTER(c_void_p)]),
     "wsp_mel_destroy": (None, [c_void_p]),
     "wsp_mel_last_error": (c_char_p, [c_void_p]),

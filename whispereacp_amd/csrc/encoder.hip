@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <new>
@@ -492,6 +493,15 @@ int encoder_hip(wsp_encoder* e, hipError_t status, const char* what)
     return WSP_ERR_HIP;
 }
 
+// The products run over pre-split inputs (split_product) for 16-bit weights
+// when every product's extents and the LayerNorm's width fit them.
+bool pre_split_shape(int wdtype, int d, int f)
+{
+    namespace ops = wsp::ops;
+    return d % 8 == 0 && ops::layernorm_parts_fits(d) && ops::split_product_fits(wdtype, d, 3 * d, d, 2 * d)
+           && ops::split_product_fits(wdtype, d, f, f, f) && ops::split_product_fits(wdtype, f, d, d, d);
+}
+
 hipError_t encoder_allocate(wsp_encoder* e, float** out, size_t floats)
 {
     void* p = nullptr;
@@ -644,14 +654,32 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
         return encoder_hip(e, status, "conv2");
 
     const int wt = T->wdtype;
+    // Stored projection scales (powers of two; 0 reads as 1) and whether any
+    // projection carries one: those take the pre-split products at every
+    // position count, the only products that divide a scale out.
+    bool scaled = false;
+    for (int l = 0; l < s.layers; ++l)
+    {
+        const wsp_encoder_layer_tensors& L = T->layers[l];
+        for (const float c : {L.q_scale, L.k_scale, L.v_scale, L.out_scale, L.fc1_scale, L.fc2_scale})
+        {
+            int exponent = 0;
+            if (c != 0.f && !(std::isfinite(c) && c > 0.f && std::frexp(c, &exponent) == 0.5f))
+                return encoder_fail(e, WSP_ERR_ARGUMENT, "wsp_encoder_encode: a projection scale is not a power of two");
+            scaled = scaled || (c != 0.f && c != 1.f);
+        }
+    }
+    if (scaled && !pre_split_shape(wt, d, f))
+        return encoder_fail(e, WSP_ERR_SHAPE,
+                            "wsp_encoder_encode: scaled projections need 16-bit storage and the pre-split products' "
+                            "shapes");
+    auto unscale = [](float c) { return c == 0.f ? 1.f : 1.f / c; };
     // 16-bit weights take the products over pre-split inputs: each product's
     // input is stored once as exact 16-bit parts (fc1 writes fc2's itself).
     const size_t part_stride = (size_t) positions * d, ff_part_stride = (size_t) positions * f;
-    const bool split = positions > 16 && part_stride % 8 == 0 && ops::layernorm_parts_fits(d)
-                       && ops::split_product_fits(wt, d, 3 * d, d, 2 * d)
-                       && ops::split_product_fits(wt, d, f, f, f) && ops::split_product_fits(wt, f, d, d, d);
+    const bool split = (positions > 16 || scaled) && part_stride % 8 == 0 && pre_split_shape(wt, d, f);
     auto split_product = [&](const void* parts, size_t stride, int inner, const void* w, const float* bias, float* y,
-                             int out, int flags, void* out_parts) {
+                             int out, int flags, void* out_parts, float stored_scale) {
         ops::SplitProduct p {};
         p.parts = parts;
         p.part_stride = stride;
@@ -666,6 +694,7 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
         p.out_parts = out_parts;
         p.out_part_stride = ff_part_stride;
         p.wdtype = wt;
+        p.scale0 = unscale(stored_scale);
         return ops::split_product(st, p);
     };
     for (int l = 0; l < s.layers; ++l)
@@ -699,6 +728,9 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
             p.y2 = e->v;
             p.ldy = d;
             p.wdtype = wt;
+            p.scale0 = unscale(L.q_scale);
+            p.scale1 = unscale(L.k_scale);
+            p.scale2 = unscale(L.v_scale);
             if (d / heads == kFlashWidth)
             {
                 // The attention takes k and v as fp16 halves.
@@ -805,7 +837,7 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
             if (att_parts || (status = ops::split_rows(st, e->att, part_stride, wt, e->parts, part_stride))
                                  == hipSuccess)
                 status = split_product(e->parts, part_stride, d, L.out_w, L.out_b, e->hidden, d,
-                                       ops::kProductResidual, nullptr);
+                                       ops::kProductResidual, nullptr, L.out_scale);
         }
         else
             status = ops::linear(st, e->att, positions, d, L.out_w, wt, L.out_b, e->hidden, d, 2);
@@ -819,10 +851,10 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
         if (split)
         {
             if ((status = split_product(e->parts, part_stride, d, L.fc1_w, L.fc1_b, nullptr, f, ops::kProductGelu,
-                                        e->ff_parts))
+                                        e->ff_parts, L.fc1_scale))
                 == hipSuccess)
                 status = split_product(e->ff_parts, ff_part_stride, f, L.fc2_w, L.fc2_b, e->hidden, d,
-                                       ops::kProductResidual, nullptr);
+                                       ops::kProductResidual, nullptr, L.fc2_scale);
         }
         else if ((status = ops::linear(st, e->normed, positions, d, L.fc1_w, wt, L.fc1_b, e->ff, f, 1)) == hipSuccess)
             status = ops::linear(st, e->ff, positions, f, L.fc2_w, wt, L.fc2_b, e->hidden, d, 2);
@@ -832,6 +864,41 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
     if ((status = ops::layernorm(st, e->hidden, T->final_norm_w, T->final_norm_b, output, positions, d, eps))
         != hipSuccess)
         return encoder_hip(e, status, "final norm");
+    return WSP_OK;
+}
+
+int wsp_encoder_scaled_halves(const wsp_encoder_shape* shape, const void* bf16, size_t count, void* halves,
+                              float* scale)
+{
+    if (shape == nullptr || scale == nullptr || (count > 0 && (bf16 == nullptr || halves == nullptr)))
+        return WSP_ERR_ARGUMENT;
+    if (!pre_split_shape(WSP_F16, shape->width, shape->feed_forward_width))
+        return WSP_ERR_SHAPE;
+    const uint16_t* in = static_cast<const uint16_t*>(bf16);
+    uint16_t* out = static_cast<uint16_t*>(halves);
+    auto widen = [](uint16_t bits) { return __builtin_bit_cast(float, (uint32_t) bits << 16); };
+    // The shift puts the largest magnitude's binade at 2^15 (fp16's top one:
+    // an 8-bit significand there is at most 65280 < 65504).
+    int top = INT_MIN;
+    for (size_t i = 0; i < count; ++i)
+    {
+        const float v = widen(in[i]);
+        if (!std::isfinite(v))
+            return WSP_ERR_LOGIC;
+        if (v != 0.f)
+            top = std::max(top, std::ilogb(v));
+    }
+    // (At most 126, so the scale stays a finite float and its reciprocal a normal one.)
+    const int shift = top == INT_MIN ? 0 : std::min(15 - top, 126);
+    for (size_t i = 0; i < count; ++i)
+    {
+        const float v = widen(in[i]);
+        const _Float16 h = (_Float16) std::ldexp(v, shift);
+        if (__builtin_bit_cast(uint32_t, std::ldexp((float) h, -shift)) != __builtin_bit_cast(uint32_t, v))
+            return WSP_ERR_LOGIC;
+        out[i] = __builtin_bit_cast(uint16_t, h);
+    }
+    *scale = std::ldexp(1.f, shift);
     return WSP_OK;
 }
 

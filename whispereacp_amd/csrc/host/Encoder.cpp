@@ -204,13 +204,42 @@ EncoderWeights::EncoderWeights(const TensorSource& file, const EncoderShape& sha
         else
             packedHalves.clear();
     }
+    // BF16 projections as exact fp16 multiples w·2^k (wsp_encoder_scaled_halves),
+    // all or none: the products then read two fp16 parts of their input
+    // instead of three bf16 ones.
+    std::vector<float> scales;
+    if (storage == WSP_BF16 && shape.layers > 0)
+    {
+        const wsp_encoder_shape cs = shape.cShape();
+        for (const Entry& e : entries)
+            if (e.projection)
+            {
+                const std::size_t n = countOf(e.tensor->extents);
+                packedHalves.emplace_back(n);
+                float scale = 1.f;
+                const int status = wsp_encoder_scaled_halves(&cs, e.tensor->data, n, packedHalves.back().data(), &scale);
+                if (status == WSP_ERR_LOGIC || status == WSP_ERR_SHAPE)
+                {
+                    packedHalves.clear();
+                    scales.clear();
+                    break;
+                }
+                if (status != WSP_OK)
+                    throwForStatus(status, "wsp_encoder_scaled_halves failed");
+                scales.push_back(scale);
+            }
+        if (!packedHalves.empty())
+            storage = WSP_F16;
+    }
     projectionType = storage;
 
     buffers.reserve(entries.size());
     std::size_t packedIndex = 0;
     std::vector<const void*> pointers;
+    std::vector<float> entryScales; // per entry: its projection's scale (1 for the rest)
     for (const Entry& e : entries)
     {
+        entryScales.push_back(e.projection && !scales.empty() ? scales[packedIndex] : 1.f);
         if (e.projection && storage == WSP_F16 && !packedHalves.empty())
         {
             const auto& h = packedHalves[packedIndex++];
@@ -255,6 +284,12 @@ EncoderWeights::EncoderWeights(const TensorSource& file, const EncoderShape& sha
         L.fc1_b = f32(b + 12);
         L.fc2_w = pointers[b + 13];
         L.fc2_b = f32(b + 14);
+        L.q_scale = entryScales[b + 2];
+        L.k_scale = entryScales[b + 4];
+        L.v_scale = entryScales[b + 5];
+        L.out_scale = entryScales[b + 7];
+        L.fc1_scale = entryScales[b + 11];
+        L.fc2_scale = entryScales[b + 13];
     }
 }
 

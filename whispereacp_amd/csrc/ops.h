@@ -93,6 +93,10 @@ struct SplitProduct
     void* y1_halves;
     void* y2_halves_t;
     int halves_pitch;
+    // Each matrix's sums are multiplied by its factor before the bias: the
+    // reciprocal of the power of two its stored weights carry (exact), 1 for
+    // weights stored as they are.
+    float scale0 = 1.f, scale1 = 1.f, scale2 = 1.f;
 };
 
 // 16-bit weights, inner % 32 == 0, out, split and split2 multiples of 128.

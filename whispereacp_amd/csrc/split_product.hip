@@ -307,6 +307,7 @@ __global__ void __launch_bounds__(kThreads) split_product_kernel(SplitProduct a)
     // acc[mt][nt][r] of lane (g, li) is C[4g + r][li] of that 16 x 16 tile.
     float* y = seg == 0 ? a.y0 : seg == 1 ? a.y1 : a.y2;
     const float* bias = seg == 0 ? a.bias0 : seg == 1 ? a.bias1 : a.bias2;
+    const float scale = seg == 0 ? a.scale0 : seg == 1 ? a.scale1 : a.scale2;
     const int width = seg == 0 ? a.split : seg == 1 ? a.split2 - a.split : a.out - a.split2;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -321,7 +322,7 @@ __global__ void __launch_bounds__(kThreads) split_product_kernel(SplitProduct a)
                 const int row = m_block + 16 * (MT * wm + mt) + 4 * g + r;
                 if (row >= a.rows)
                     continue;
-                float v = acc[mt][nt][r] + b;
+                float v = acc[mt][nt][r] * scale + b;
                 if (a.flags & kProductGelu)
                     v = exact_gelu(v);
                 if (a.out_parts != nullptr)

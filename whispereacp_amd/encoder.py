@@ -5,7 +5,11 @@ layers and the final LayerNorm into [positions, width] rows.
 
 Weights stay on the device as the file stores them for the projections
 (F32, F16 or BF16) and widened to fp32 for everything else, as the
-reference's EncoderWeights does (Encoder/EncoderWeights.h:44-52).
+reference's EncoderWeights does (Encoder/EncoderWeights.h:44-52). BF16
+projections are held as exact fp16 multiples w·2^k with their scale
+(wsp_encoder_scaled_halves) when every value narrows exactly and the
+shape's products run over pre-split inputs: the products then read two
+fp16 parts of their input instead of three bf16 ones.
 """
 
 from __future__ import annotations
@@ -28,11 +32,32 @@ def _device_tensor(stored, widen: bool) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(data)).cuda()
 
 
+_SCALES = {"self_attn.q_proj.weight": "q_scale", "self_attn.k_proj.weight": "k_scale",
+           "self_attn.v_proj.weight": "v_scale", "self_attn.out_proj.weight": "out_scale",
+           "fc1.weight": "fc1_scale", "fc2.weight": "fc2_scale"}
+
+
+def _scaled_halves(lib, cshape, stored) -> Optional[tuple]:
+    """(fp16 array, scale) for a BF16 projection, or None when it does not
+    narrow exactly (or the shape takes no scaled projections)."""
+    bits = np.ascontiguousarray(stored.data, dtype=np.uint16)
+    halves = np.empty(bits.shape, dtype=np.float16)
+    scale = ctypes.c_float()
+    status = lib.wsp_encoder_scaled_halves(ctypes.byref(cshape), bits.ctypes.data, bits.size, halves.ctypes.data,
+                                           ctypes.byref(scale))
+    if status in (N.WSP_ERR_LOGIC, N.WSP_ERR_SHAPE):
+        return None
+    if status != N.WSP_OK:
+        _raise(N.WSP_KIND_NONE, f"wsp_encoder_scaled_halves failed with {status}", status)
+    return halves, scale.value
+
+
 class EncoderWeights:
     """Encoder/EncoderWeights.h:70-93 over a (synthetic or loaded) tensor
-    dictionary keyed by the HuggingFace names."""
+    dictionary keyed by the HuggingFace names. scaled_halves=False keeps BF16
+    projections as stored."""
 
-    def __init__(self, shape: EncoderShape, file: DecoderFile):
+    def __init__(self, shape: EncoderShape, file: DecoderFile, scaled_halves: bool = True):
         self.shape = shape
         projections = [file[encoder_layer_name(layer, s)] for layer in range(shape.layers)
                        for s in ENCODER_LAYER_SUFFIXES if s.endswith("proj.weight") or s.startswith("fc")
@@ -41,6 +66,21 @@ class EncoderWeights:
         if len(dtypes) > 1:
             raise ValueError(f"the encoder's projections mix storages {sorted(dtypes)}")
         self.dtype = dtypes.pop() if dtypes else "F32"
+        self.stored_dtype = self.dtype
+        # BF16 projections as exact fp16 multiples, all or none.
+        scaled: Dict[str, tuple] = {}
+        if self.dtype == "BF16" and scaled_halves and shape.layers > 0:
+            lib = N.load()
+            cshape = N.wsp_encoder_shape(shape.mel_bins, shape.width, shape.heads, shape.layers,
+                                         shape.feed_forward_width, shape.input_frames)
+            for name in [encoder_layer_name(layer, suffix) for layer in range(shape.layers) for suffix in _SCALES]:
+                converted = _scaled_halves(lib, cshape, file[name])
+                if converted is None:
+                    scaled = {}
+                    break
+                scaled[name] = converted
+            if scaled:
+                self.dtype = "F16"
         self._keep: Dict[str, torch.Tensor] = {}
         for name in ENCODER_MODEL_NAMES:
             self._keep[name] = _device_tensor(file[name], True)
@@ -48,13 +88,20 @@ class EncoderWeights:
             for suffix in ENCODER_LAYER_SUFFIXES:
                 name = encoder_layer_name(layer, suffix)
                 projection = suffix.endswith("proj.weight") or suffix in ("fc1.weight", "fc2.weight")
-                self._keep[name] = _device_tensor(file[name], not projection)
+                if name in scaled:
+                    self._keep[name] = torch.from_numpy(scaled[name][0]).cuda()
+                else:
+                    self._keep[name] = _device_tensor(file[name], not projection)
         self._layers = (N.wsp_encoder_layer_tensors * max(1, shape.layers))()
         fields = ["attention_norm_w", "attention_norm_b", "q_w", "q_b", "k_w", "v_w", "v_b", "out_w", "out_b",
                   "final_norm_w", "final_norm_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b"]
         for layer in range(shape.layers):
             values = [self._keep[encoder_layer_name(layer, s)].data_ptr() for s in ENCODER_LAYER_SUFFIXES]
-            self._layers[layer] = N.wsp_encoder_layer_tensors(**dict(zip(fields, values)))
+            entry = dict(zip(fields, values))
+            for suffix, field in _SCALES.items():
+                name = encoder_layer_name(layer, suffix)
+                entry[field] = scaled[name][1] if name in scaled else 1.0
+            self._layers[layer] = N.wsp_encoder_layer_tensors(**entry)
         k = self._keep
         self.table = N.wsp_encoder_tensors(
             _DTYPES[self.dtype], ptr(k[ENCODER_MODEL_NAMES[0]]), ptr(k[ENCODER_MODEL_NAMES[1]]),
