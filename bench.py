@@ -566,7 +566,9 @@ def bench_streams(args, w):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("f16" if dtype == "F16" else "bf16") + "-weights/f32",
+        "dtype": ("f16-weights/f32" if dtype == "F16" else
+                  "bf16-weights held as exact scaled fp16/f32" if decoder.product_storage == "F16" else
+                  "bf16-weights/f32"),
         "data": "synthetic: N(0,0.02) weights (LayerNorm gamma 1, beta 0), N(0,1) encoder states per stream",
         "config": {"workload": f"{args.workload} decoder: d_model {shape.width}, {shape.heads} heads, "
                                f"{shape.layers} layers, vocab {V}, {dtype} weights, 1500 cross positions, "

@@ -52,6 +52,8 @@ public:
     const DecoderShape& shape() const { return decoderShape; }
     int streams() const { return streamCount; }
     int position() const;
+    // The storage the step's products read the weights in (wsp_batch_product_storage).
+    int productStorage() const;
     int crossPositions() const;
     void* hipStream() const { return stream; }
 

@@ -235,6 +235,9 @@ int wsp_batch_decoder_step(wsp_batch_decoder* decoder, const uint32_t* tokens, i
 int wsp_batch_decoder_ring_step(wsp_batch_decoder* decoder, uint32_t* ring, float* logits, const float* mask);
 
 int wsp_batch_decoder_position(const wsp_batch_decoder* decoder);
+/* wsp_batch_product_storage (wsp_hip.h) of the decoder's batch; no reference
+ * counterpart. */
+int wsp_batch_decoder_product_storage(const wsp_batch_decoder* decoder);
 const float* wsp_batch_decoder_hidden_states(const wsp_batch_decoder* decoder);
 
 /* ---- Whisper end to end (Whisper/Whisper.h:144-560, the kernels backend) --

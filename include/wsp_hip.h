@@ -309,6 +309,15 @@ int wsp_batch_begin(wsp_batch* batch, const wsp_cross_tensors* layers, int wdtyp
 int wsp_batch_step(wsp_batch* batch, const wsp_decoder_tensors* tensors, const uint32_t* tokens, int count,
                    float* hidden, float* logits, const float* mask, uint32_t* argmax_out);
 
+/* No reference counterpart: the storage of the weight copy the products read,
+ * after the last packed table. A bf16 table is packed as exact fp16 multiples
+ * w·2^k per matrix (k puts the matrix's largest magnitude in fp16's top
+ * binade; the products divide 2^k out of each sum) when every value of every
+ * matrix narrows exactly, and the step then takes two fp16 parts of each
+ * input instead of three bf16 ones: WSP_F16 then and for fp16 tables,
+ * WSP_BF16 for a bf16 table that does not narrow, 0 before any table. */
+int wsp_batch_product_storage(const wsp_batch* batch);
+
 /* One single-token step for every stream driven by a token ring: ring is
  * device uint32 [max_positions + 1][streams], position-major. The step reads
  * each stream's token at the current position p from ring[p] and writes its

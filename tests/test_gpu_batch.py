@@ -14,8 +14,9 @@ checked three ways:
 Greedy tokens must be equal. Logits meet the configurations' bar (max relative
 error 2e-2 with 16-bit weights), and, tighter, the reference's worst-error
 measure within 1e-4. Projections run on the matrix cores with the
-activations split into exact 16-bit parts, so they differ from the fp32
-single-stream path only in summation order."""
+activations split into 16-bit parts: fp16 hi/lo (within 2^-22 relative) for
+fp16 weights and for bf16 weights the batch holds as exact scaled fp16, three
+exact bf16 parts for bf16 weights that do not narrow."""
 
 import ctypes
 
@@ -148,7 +149,10 @@ def large_batched(large):
     from whispereacp_amd.decoder import BatchedDecoder
     shape, f, encoders = large
     decoder = BatchedDecoder(shape, f, streams=32)
-    return batched_greedy(decoder, shape, encoders, S.SOT_PREFIX[shape.vocabulary_size], LARGE_STEPS)
+    run = batched_greedy(decoder, shape, encoders, S.SOT_PREFIX[shape.vocabulary_size], LARGE_STEPS)
+    # The bf16 weights narrow exactly, so the products read scaled fp16 copies.
+    assert decoder.product_storage == "F16"
+    return run
 
 
 @pytest.mark.timeout(600)
@@ -416,26 +420,51 @@ class DeviceTables:
             ctypes.cast(self.layers, ctypes.POINTER(N.wsp_layer_tensors)))
 
 
-def test_one_batch_switches_weight_sets_eagerly_and_in_the_ring(oracle):
+def inexact_bf16_file(f, shape):
+    """A bf16 file one of whose matrices cannot be held as exact fp16
+    multiples: layer 1's fc1 gets 1.0 (its largest magnitude, so the shift is
+    15) and (1 + 2^-7)·2^-40, whose last significand bit would fall below
+    fp16's smallest step 2^-24 after the shift."""
+    name = S.layer_name(1, "fc1.weight")
+    t = f[name]
+    values = t.floats().ravel().copy()
+    values[0], values[1] = 1.0, (1 + 2.0 ** -7) * 2.0 ** -40
+    out = dict(f)
+    out[name] = S.StoredTensor(t.name, "BF16", t.extents, S.store(values, "BF16"))
+    return out
+
+
+@pytest.mark.parametrize("dtype", ["F16", "BF16"])
+def test_one_batch_switches_weight_sets_eagerly_and_in_the_ring(oracle, dtype):
     # The batch keeps a fragment-major copy of the projection weights and
     # repacks it only when a step's table points elsewhere; the ring step's
     # graph is re-captured on the same change. Weight sets A, B, A on one batch
     # (separate buffers, different values), each sequence checked against the
     # oracle under that set, through wsp_batch_step and wsp_batch_ring_step.
+    # bf16 sets narrow to exact scaled fp16 (the products read fp16); set C,
+    # bf16 with one matrix that does not narrow, keeps bf16 products, and the
+    # batch switches between the two forms.
     import torch
     from whispereacp_amd import _native as N
     from whispereacp_amd.decoder import c_shape, current_stream, to_device
     lib = N.load()
     shape = S.DecoderShape(256, 4, 2, 1024, 4099, 448, 120)
-    files = {"A": S.workload_decoder_file(shape, "F16", 81), "B": S.workload_decoder_file(shape, "F16", 82)}
+    files = {"A": S.workload_decoder_file(shape, dtype, 81), "B": S.workload_decoder_file(shape, dtype, 82)}
+    order = ("A", "B", "A")
+    storage = {"A": N.WSP_F16, "B": N.WSP_F16}
+    if dtype == "BF16":
+        files["C"] = inexact_bf16_file(files["A"], shape)
+        order = ("A", "C", "B", "C", "A")
+        storage["C"] = N.WSP_BF16
     tables = {k: DeviceTables(shape, f) for k, f in files.items()}
     streams, prompt, steps, V, t = 2, [9, 8, 7, 6], 10, shape.vocabulary_size, 4
     encoders = [S.normal_encoder_output(120, shape.width, 40 + s) for s in range(streams)]
     enc = to_device(np.ascontiguousarray(np.stack(encoders)))
     cshape = c_shape(shape)
     handle = ctypes.c_void_p()
-    assert lib.wsp_batch_create(ctypes.byref(cshape), streams, 4, N.WSP_F16, 0, current_stream(),
+    assert lib.wsp_batch_create(ctypes.byref(cshape), streams, 4, getattr(N, "WSP_" + dtype), 0, current_stream(),
                                 ctypes.byref(handle)) == N.WSP_OK
+    assert lib.wsp_batch_product_storage(handle) == 0
     try:
         def ok(status):
             assert status == N.WSP_OK, lib.wsp_batch_last_error(handle).decode()
@@ -444,13 +473,14 @@ def test_one_batch_switches_weight_sets_eagerly_and_in_the_ring(oracle):
         tokens_in = torch.tensor([prompt] * streams, dtype=torch.int32, device="cuda")
         prompt_logits = torch.empty((streams * t, V), dtype=torch.float32, device="cuda")
         for ring_form in (False, True):
-            for k in ("A", "B", "A"):
+            for k in order:
                 T = tables[k]
                 ok(lib.wsp_batch_begin(handle, T.cross, T.wdtype, enc.data_ptr(), 0))
                 ring = torch.zeros((shape.max_positions + 1, streams), dtype=torch.int32, device="cuda")
                 ring[:t] = torch.tensor(prompt, dtype=torch.int32, device="cuda")[:, None].expand(t, streams)
                 ok(lib.wsp_batch_step(handle, ctypes.byref(T.tensors), tokens_in.data_ptr(), t, None,
                                       prompt_logits.data_ptr(), None, ring[t].data_ptr()))
+                assert lib.wsp_batch_product_storage(handle) == storage[k], k
                 rows = torch.empty((steps, streams, V), dtype=torch.float32, device="cuda")
                 logits = torch.empty((streams, V), dtype=torch.float32, device="cuda")
                 for j in range(steps):
@@ -467,8 +497,8 @@ def test_one_batch_switches_weight_sets_eagerly_and_in_the_ring(oracle):
                 for s in range(streams):
                     ref_tokens, ref_rows = expected[k][s]
                     rel, worst = check_run(got_tokens[s], got_rows[s], ref_tokens, ref_rows, 2e-2)
-                print(f"weights {k}, {'ring' if ring_form else 'eager'} steps: tokens match the oracle "
-                      f"(max relative {rel:.2e})")
+                print(f"{dtype} weights {k}, {'ring' if ring_form else 'eager'} steps: tokens match the oracle "
+                      f"(max relative {rel:.2e}, worst {worst:.2e})")
         # The two sets decode differently, so a stale copy would have shown.
         assert expected["A"][0][0] != expected["B"][0][0]
     finally:

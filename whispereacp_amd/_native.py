@@ -139,6 +139,7 @@ SIGNATURES = {
                                  ctypes.POINTER(c_void_p)]),
     "wsp_batch_destroy": (None, [c_void_p]),
     "wsp_batch_last_error": (c_char_p, [c_void_p]),
+    "wsp_batch_product_storage": (c_int, [c_void_p]),
     "wsp_batch_position": (c_int, [c_void_p]),
     "wsp_batch_cross_rows": (c_int, [c_void_p]),
     "wsp_batch_begin": (c_int, [c_void_p, ctypes.POINTER(wsp_cross_tensors), c_int, c_void_p, c_int]),
@@ -156,6 +157,7 @@ SIGNATURES = {
     "wsp_batch_decoder_step": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "wsp_batch_decoder_ring_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
     "wsp_batch_decoder_position": (c_int, [c_void_p]),
+    "wsp_batch_decoder_product_storage": (c_int, [c_void_p]),
     "wsp_batch_decoder_create_from_file": (c_int, [c_char_p, ctypes.POINTER(wsp_decoder_shape), c_int, c_int, c_int,
                                                    c_int, c_void_p, ctypes.POINTER(c_void_p)]),
     "wsp_decoder_create_from_file": (c_int, [c_char_p, ctypes.POINTER(wsp_decoder_shape), c_int, c_int, c_void_p,

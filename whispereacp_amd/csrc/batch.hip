@@ -123,6 +123,69 @@ __global__ void __launch_bounds__(256) pack_fragments_kernel(const u16* __restri
     *reinterpret_cast<u32x4*>(out + i * 8) = v;
 }
 
+// bf16 weights held as exact fp16 multiples w·2^shift (the products then
+// take two fp16 parts of their input instead of three bf16 ones, and divide
+// 2^shift out of each sum). bf16_range_kernel leaves the largest magnitude's
+// bits (sign dropped) of n values in range[0] and sets range[1] if a value is
+// not finite; pack_scaled_kernel is pack_fragments_kernel narrowing each
+// value, and sets *inexact if one does not come back bit for bit.
+__global__ void __launch_bounds__(256) bf16_range_kernel(const u16* __restrict__ w, size_t n,
+                                                         unsigned* __restrict__ range)
+{
+    unsigned top = 0, bad = 0;
+    for (size_t i = (size_t) blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t) gridDim.x * 256)
+    {
+        const unsigned m = w[i] & 0x7FFFu;
+        if (m >= 0x7F80u)
+            bad = 1u;
+        else
+            top = max(top, m);
+    }
+    for (int offset = 32; offset > 0; offset >>= 1)
+    {
+        top = max(top, (unsigned) __shfl_xor((int) top, offset));
+        bad |= (unsigned) __shfl_xor((int) bad, offset);
+    }
+    if (threadIdx.x % 64 == 0)
+    {
+        if (top != 0)
+            atomicMax(range, top);
+        if (bad != 0)
+            atomicOr(range + 1, 1u);
+    }
+}
+
+__global__ void __launch_bounds__(256) pack_scaled_kernel(const u16* __restrict__ w, int rows, int inner,
+                                                          u16* __restrict__ out, size_t chunks, int shift,
+                                                          unsigned* __restrict__ inexact)
+{
+    const size_t i = (size_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= chunks)
+        return;
+    const int lane = (int) (i % 64), kbs = inner / 32;
+    const size_t fragment = i / 64;
+    const int kb = (int) (fragment % kbs), tile = (int) (fragment / kbs);
+    const int n = tile * 16 + lane % 16, k = kb * 32 + 8 * (lane / 16);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (n < rows)
+    {
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(w + (size_t) n * inner + k);
+        bool exact = true;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+        {
+            const uint32_t bits = (raw[j / 2] >> (16 * (j % 2))) & 0xFFFFu;
+            const float x = __uint_as_float(bits << 16);
+            const _Float16 y = (_Float16) ldexpf(x, shift);
+            exact = exact && __float_as_uint(ldexpf((float) y, -shift)) == __float_as_uint(x);
+            v[j / 2] |= (uint32_t) __builtin_bit_cast(u16, y) << (16 * (j % 2));
+        }
+        if (!exact)
+            atomicOr(inexact, 1u);
+    }
+    *reinterpret_cast<u32x4*>(out + i * 8) = v;
+}
+
 // 16-bit values of the fragment-major copy of a [rows][inner] weight.
 size_t packed_size(int rows, int inner)
 {
@@ -265,13 +328,14 @@ struct Product
     const float* gamma;
     const float* beta;
     float eps;
+    float scale = 1.f; // each sum's factor before the bias: 2^-shift of weights held scaled
 };
 
 // `prior` is y[m][n] read before the product (kResidual; unused otherwise).
 template <int WT>
 __device__ __forceinline__ void finish(const Product& a, int m, int n, float acc, float prior = 0.f)
 {
-    const float v = acc + (a.bias != nullptr ? a.bias[n] : 0.f);
+    const float v = acc * a.scale + (a.bias != nullptr ? a.bias[n] : 0.f);
     switch (a.epilogue)
     {
         case kStore: a.y[(size_t) m * a.ldy + n] = v; break;
@@ -694,6 +758,7 @@ struct Tile
     float* partials;       // [blocks][kTileThreads][columns per thread]
     unsigned* counters;    // [column groups], zero between launches
     size_t partials_capacity, counters_capacity; // floats and counters the buffers hold
+    float scale = 1.f;     // each sum's factor before the bias (as Product::scale)
 };
 
 // k-blocks (32 inner values) a block stages per batch: what the LDS holds,
@@ -922,7 +987,7 @@ __global__ void __launch_bounds__(kTileThreads) tile_kernel(Tile a)
     {
         const int n = n0 + c0 + c;
         if (n < a.out)
-            v[c] += a.bias != nullptr ? a.bias[n] : 0.f;
+            v[c] = v[c] * a.scale + (a.bias != nullptr ? a.bias[n] : 0.f);
     }
     switch (a.epilogue)
     {
@@ -1548,6 +1613,14 @@ struct wsp_batch
     std::vector<char> packed_table;
     std::vector<wsp_layer_tensors> packed_layers;
     wsp_decoder_tensors packed_tensors {};
+    // bf16 tables: the copies hold exact fp16 multiples w·2^k when every
+    // matrix narrows exactly (compute WSP_F16, scales[i] = 2^-k of matrix i:
+    // per layer q/k/v, out, cross q, cross out, fc1, fc2, then the logits);
+    // else bf16 as given (compute WSP_BF16, scales 1). `range` is device
+    // scratch for the check, three words a matrix.
+    int compute = 0;
+    std::vector<float> scales;
+    unsigned* range = nullptr;
 
     // The single-token ring step, captured once as a HIP graph on a private
     // stream and replayed on `stream`; re-captured when anything it bakes in
@@ -1744,7 +1817,9 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         p.x_part = xs_part;
         p.inner = d;
         p.out = 3 * d;
+        const float* const scales = b->scales.data() + (size_t) 6 * l;
         p.w = L.self_qkv_w;
+        p.scale = scales[0];
         p.bias = L.self_qkv_b;
         p.epilogue = kQkv;
         p.q = b->q;
@@ -1768,6 +1843,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
 
         p.out = d;
         p.w = L.self_out_w;
+        p.scale = scales[1];
         p.bias = L.self_out_b;
         p.epilogue = kResidual;
         p.y = b->h;
@@ -1781,6 +1857,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         if (!normed && (e = launch_norm<WT>(st, n, rows, false)) != hipSuccess)
             return hip_fail(b, e, "cross-attention norm");
         p.w = L.cross_q_w;
+        p.scale = scales[2];
         p.bias = L.cross_q_b;
         p.epilogue = kStore;
         p.y = b->q;
@@ -1799,6 +1876,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
             return hip_fail(b, e, "cross attention");
 
         p.w = L.cross_out_w;
+        p.scale = scales[3];
         p.bias = L.cross_out_b;
         p.epilogue = kResidual;
         p.y = b->h;
@@ -1812,6 +1890,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
             return hip_fail(b, e, "feed-forward norm");
         p.out = f;
         p.w = L.fc1_w;
+        p.scale = scales[4];
         p.bias = L.fc1_b;
         p.epilogue = kGelu;
         p.y = b->ff;
@@ -1827,6 +1906,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         t.inner = f;
         t.out = d;
         t.w = L.fc2_w;
+        t.scale = scales[5];
         t.bias = L.fc2_b;
         t.epilogue = kResidual;
         t.y = b->h;
@@ -1854,6 +1934,7 @@ int run_step(wsp_batch* b, const wsp_decoder_tensors* T, const StepIo& io, hipSt
         t.inner = d;
         t.out = s.vocabulary_size;
         t.w = T->logits_weight;
+        t.scale = b->scales[(size_t) 6 * s.layers];
         t.gamma = T->final_norm_w;
         t.beta = T->final_norm_b;
         t.epilogue = kStore;
@@ -1932,11 +2013,96 @@ const wsp_decoder_tensors* packed_weights(wsp_batch* b, const wsp_decoder_tensor
         }
     }
     b->packed_table.clear();
-    uint16_t* at = b->packed;
     hipError_t e = hipSuccess;
+    // Every matrix in packing order: per layer q/k/v, out, cross q, cross
+    // out, fc1, fc2, then the logits weight.
+    struct Matrix
+    {
+        const void* w;
+        int rows, inner;
+    };
+    std::vector<Matrix> matrices;
+    for (int l = 0; l < s.layers; ++l)
+    {
+        const wsp_layer_tensors& L = T->layers[l];
+        matrices.push_back({L.self_qkv_w, 3 * d, d});
+        matrices.push_back({L.self_out_w, d, d});
+        matrices.push_back({L.cross_q_w, d, d});
+        matrices.push_back({L.cross_out_w, d, d});
+        matrices.push_back({L.fc1_w, f, d});
+        matrices.push_back({L.fc2_w, d, f});
+    }
+    matrices.push_back({T->logits_weight, s.vocabulary_size, d});
+    const size_t M = matrices.size();
+    b->compute = b->wdtype;
+    b->scales.assign(M, 1.f);
+    std::vector<int> shifts(M, 0);
+    if (b->wdtype == WSP_BF16 && b->range != nullptr)
+    {
+        // The shift puts each matrix's largest magnitude in fp16's top binade
+        // [2^15, 2^16) (an 8-bit significand there is at most 65280); at most
+        // 126, so 2^-shift stays a normal float.
+        std::vector<unsigned> words(3 * M);
+        e = hipMemsetAsync(b->range, 0, words.size() * sizeof(unsigned), b->stream);
+        for (size_t i = 0; i < M && e == hipSuccess; ++i)
+        {
+            const size_t n = (size_t) matrices[i].rows * matrices[i].inner;
+            const unsigned blocks = (unsigned) std::min<size_t>((n + 255) / 256, 1024);
+            hipLaunchKernelGGL(wsp::batch::bf16_range_kernel, dim3(blocks), dim3(256), 0, b->stream,
+                               static_cast<const uint16_t*>(matrices[i].w), n, b->range + 3 * i);
+            e = hipGetLastError();
+        }
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(words.data(), b->range, words.size() * sizeof(unsigned), hipMemcpyDeviceToHost,
+                               b->stream);
+        if (e == hipSuccess)
+            e = hipStreamSynchronize(b->stream);
+        bool finite = e == hipSuccess;
+        for (size_t i = 0; i < M && finite; ++i)
+        {
+            finite = words[3 * i + 1] == 0;
+            const unsigned top = words[3 * i];
+            const int exponent = top == 0 ? 0 : std::ilogb(__builtin_bit_cast(float, top << 16));
+            shifts[i] = top == 0 ? 0 : std::min(15 - exponent, 126);
+        }
+        if (finite)
+        {
+            uint16_t* at = b->packed;
+            for (size_t i = 0; i < M && e == hipSuccess; ++i)
+            {
+                const Matrix& m = matrices[i];
+                const size_t values = wsp::batch::packed_size(m.rows, m.inner), chunks = values / 8;
+                hipLaunchKernelGGL(wsp::batch::pack_scaled_kernel, dim3((unsigned) ((chunks + 255) / 256)), dim3(256),
+                                   0, b->stream, static_cast<const uint16_t*>(m.w), m.rows, m.inner, at, chunks,
+                                   shifts[i], b->range + 3 * i + 2);
+                e = hipGetLastError();
+                at += values;
+            }
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(words.data(), b->range, words.size() * sizeof(unsigned), hipMemcpyDeviceToHost,
+                                   b->stream);
+            if (e == hipSuccess)
+                e = hipStreamSynchronize(b->stream);
+            bool exact = e == hipSuccess;
+            for (size_t i = 0; i < M && exact; ++i)
+                exact = words[3 * i + 2] == 0;
+            if (exact)
+            {
+                b->compute = WSP_F16;
+                for (size_t i = 0; i < M; ++i)
+                    b->scales[i] = std::ldexp(1.f, -shifts[i]);
+            }
+        }
+        if (e != hipSuccess)
+        {
+            status = hip_fail(b, e, "weight range check");
+            return nullptr;
+        }
+    }
+    uint16_t* at = b->packed;
     auto pack = [&](const void* w, int rows, int inner) -> const void* {
         const size_t values = wsp::batch::packed_size(rows, inner), chunks = values / 8;
-        if (e == hipSuccess)
+        if (e == hipSuccess && b->compute == b->wdtype)
         {
             hipLaunchKernelGGL(wsp::batch::pack_fragments_kernel, dim3((unsigned) ((chunks + 255) / 256)), dim3(256),
                                0, b->stream, static_cast<const uint16_t*>(w), rows, inner, at, chunks);
@@ -2091,6 +2257,8 @@ int wsp_batch_create(const wsp_decoder_shape* shape, int streams, int max_step_t
         e = allocate(b, &b->state, 4);
     if (e == hipSuccess)
         e = allocate(b, &b->next, (size_t) streams);
+    if (e == hipSuccess && wdtype == WSP_BF16)
+        e = allocate(b, &b->range, (size_t) 3 * (6 * s.layers + 1));
     if (e == hipSuccess)
         e = hipMemsetAsync(b->state, 0, 4 * sizeof(int), b->stream);
     if (e == hipSuccess)
@@ -2143,6 +2311,11 @@ void wsp_batch_destroy(wsp_batch* b)
 const char* wsp_batch_last_error(const wsp_batch* b)
 {
     return b == nullptr ? "null batch" : b->error;
+}
+
+int wsp_batch_product_storage(const wsp_batch* b)
+{
+    return b == nullptr || b->packed_table.empty() ? 0 : b->compute;
 }
 
 int wsp_batch_position(const wsp_batch* b)
@@ -2252,8 +2425,8 @@ int wsp_batch_step(wsp_batch* b, const wsp_decoder_tensors* tensors, const uint3
     if (packed == nullptr)
         return status;
     const StepIo io {tokens, nullptr, count, hidden, logits, mask, argmax_out, false};
-    status = b->wdtype == WSP_F16 ? run_step<wsp::kF16>(b, packed, io, b->stream)
-                                  : run_step<wsp::kBF16>(b, packed, io, b->stream);
+    status = b->compute == WSP_F16 ? run_step<wsp::kF16>(b, packed, io, b->stream)
+                                   : run_step<wsp::kBF16>(b, packed, io, b->stream);
     if (status == WSP_OK)
         b->position += count;
     return status;
@@ -2281,8 +2454,8 @@ int wsp_batch_ring_step(wsp_batch* b, const wsp_decoder_tensors* tensors, uint32
     if (b->graph == nullptr || b->graph_ring != ring || b->graph_logits != logits || b->graph_mask != mask
         || b->graph_cross_rows != b->cross_rows || !same_table(b, table_bytes(packed, b->shape.layers)))
     {
-        const int status = b->wdtype == WSP_F16 ? capture_ring_step<wsp::kF16>(b, packed, ring, logits, mask)
-                                                : capture_ring_step<wsp::kBF16>(b, packed, ring, logits, mask);
+        const int status = b->compute == WSP_F16 ? capture_ring_step<wsp::kF16>(b, packed, ring, logits, mask)
+                                                 : capture_ring_step<wsp::kBF16>(b, packed, ring, logits, mask);
         if (status != WSP_OK)
             return status;
     }

@@ -62,6 +62,11 @@ int BatchedDecoder::position() const
     return batch == nullptr ? 0 : wsp_batch_position(batch);
 }
 
+int BatchedDecoder::productStorage() const
+{
+    return batch == nullptr ? 0 : wsp_batch_product_storage(batch);
+}
+
 int BatchedDecoder::crossPositions() const
 {
     return batch == nullptr ? 0 : wsp_batch_cross_rows(batch);

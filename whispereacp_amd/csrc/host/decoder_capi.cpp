@@ -439,6 +439,11 @@ int wsp_batch_decoder_position(const wsp_batch_decoder* d)
     return d == nullptr || !d->decoder ? -1 : d->decoder->position();
 }
 
+int wsp_batch_decoder_product_storage(const wsp_batch_decoder* d)
+{
+    return d == nullptr || !d->decoder ? 0 : d->decoder->productStorage();
+}
+
 const float* wsp_batch_decoder_hidden_states(const wsp_batch_decoder* d)
 {
     return d == nullptr || !d->decoder ? nullptr : static_cast<const float*>(d->decoder->hiddenStates().data());

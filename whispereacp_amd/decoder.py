@@ -295,6 +295,13 @@ class BatchedDecoder:
     def position(self) -> int:
         return self.lib.wsp_batch_decoder_position(self.handle)
 
+    @property
+    def product_storage(self) -> str:
+        """"F16" or "BF16": the weight storage the step's products read (bf16
+        weights are held as exact scaled fp16 when they narrow), "" before
+        the first step."""
+        return {N.WSP_F16: "F16", N.WSP_BF16: "BF16"}.get(self.lib.wsp_batch_decoder_product_storage(self.handle), "")
+
     def read_hidden(self, rows: int) -> np.ndarray:
         out = torch.empty((rows, self.shape.width), dtype=torch.float32, device="cuda")
         copy_device(out, self.lib.wsp_batch_decoder_hidden_states(self.handle), rows * self.shape.width * 4)
