@@ -360,7 +360,8 @@ typedef struct wsp_encoder_shape
  * reference widens every non-projection tensor, Encoder/EncoderWeights.h:44-52).
  * k_proj has no bias. The *_scale fields are the power of two each stored
  * projection carries (wsp_encoder_scaled_halves: bf16 weights held as exact
- * fp16 multiples); the products divide it out. 0 or 1: stored as they are. */
+ * fp16 multiples), in [2^-126, 2^126]; the products divide it out. 0 or 1:
+ * stored as they are. */
 typedef struct wsp_encoder_layer_tensors
 {
     const float* attention_norm_w;

@@ -130,14 +130,16 @@ def test_a_scale_that_is_not_a_power_of_two_is_refused():
     from whispereacp_amd.encoder import Encoder, EncoderWeights
     shape = S.EncoderShape(80, 128, 2, 1, 512, 64)
     weights = EncoderWeights(shape, S.workload_encoder_file(shape, "BF16", 3000))
-    weights._layers[0].fc2_scale = 3.0
     encoder = Encoder(shape)
     mel = torch.zeros((shape.mel_bins, shape.input_frames), dtype=torch.float32, device="cuda")
     out = torch.empty((shape.positions(), shape.width), dtype=torch.float32, device="cuda")
-    status = encoder.lib.wsp_encoder_encode(encoder.handle, ctypes.byref(weights.table), mel.data_ptr(),
-                                            out.data_ptr(), 0)
-    assert status == N.WSP_ERR_ARGUMENT
-    assert b"power of two" in encoder.lib.wsp_encoder_last_error(encoder.handle)
+    # Not a power of two; a power of two whose reciprocal is not a normal float; not finite.
+    for bad in (3.0, 2.0 ** -140, float("inf"), -4.0):
+        weights._layers[0].fc2_scale = bad
+        status = encoder.lib.wsp_encoder_encode(encoder.handle, ctypes.byref(weights.table), mel.data_ptr(),
+                                                out.data_ptr(), 0)
+        assert status == N.WSP_ERR_ARGUMENT, bad
+        assert b"power of two" in encoder.lib.wsp_encoder_last_error(encoder.handle)
 
 
 def test_golden_fixture_through_the_gpu():

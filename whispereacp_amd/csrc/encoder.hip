@@ -633,6 +633,28 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
     (void) hipSetDevice(e->device);
     hipError_t status;
 
+    // Stored projection scales (powers of two in [2^-126, 2^126], so their
+    // reciprocals are normal floats; 0 reads as 1) and whether any
+    // projection carries one: those take the pre-split products at every
+    // position count, the only products that divide a scale out.
+    bool scaled = false;
+    for (int l = 0; l < s.layers; ++l)
+    {
+        const wsp_encoder_layer_tensors& L = T->layers[l];
+        for (const float c : {L.q_scale, L.k_scale, L.v_scale, L.out_scale, L.fc1_scale, L.fc2_scale})
+        {
+            int exponent = 0;
+            if (c != 0.f && !(std::isfinite(c) && c > 0.f && std::frexp(c, &exponent) == 0.5f && exponent >= -125
+                               && exponent <= 127))
+                return encoder_fail(e, WSP_ERR_ARGUMENT,
+                                    "wsp_encoder_encode: a projection scale is not a power of two in [2^-126, 2^126]");
+            scaled = scaled || (c != 0.f && c != 1.f);
+        }
+    }
+    if (scaled && !pre_split_shape(T->wdtype, d, f))
+        return encoder_fail(e, WSP_ERR_SHAPE,
+                            "wsp_encoder_encode: scaled projections need 16-bit storage and the pre-split products' "
+                            "shapes");
     hipLaunchKernelGGL(mel_columns_kernel, dim3(conv_frames), dim3(kColumnThreads), 0, st, mel, s.mel_bins,
                        s.input_frames, frames, e->columns);
     if ((status = hipGetLastError()) != hipSuccess)
@@ -654,28 +676,10 @@ int wsp_encoder_encode(wsp_encoder* e, const wsp_encoder_tensors* T, const float
         return encoder_hip(e, status, "conv2");
 
     const int wt = T->wdtype;
-    // Stored projection scales (powers of two; 0 reads as 1) and whether any
-    // projection carries one: those take the pre-split products at every
-    // position count, the only products that divide a scale out.
-    bool scaled = false;
-    for (int l = 0; l < s.layers; ++l)
-    {
-        const wsp_encoder_layer_tensors& L = T->layers[l];
-        for (const float c : {L.q_scale, L.k_scale, L.v_scale, L.out_scale, L.fc1_scale, L.fc2_scale})
-        {
-            int exponent = 0;
-            if (c != 0.f && !(std::isfinite(c) && c > 0.f && std::frexp(c, &exponent) == 0.5f))
-                return encoder_fail(e, WSP_ERR_ARGUMENT, "wsp_encoder_encode: a projection scale is not a power of two");
-            scaled = scaled || (c != 0.f && c != 1.f);
-        }
-    }
-    if (scaled && !pre_split_shape(wt, d, f))
-        return encoder_fail(e, WSP_ERR_SHAPE,
-                            "wsp_encoder_encode: scaled projections need 16-bit storage and the pre-split products' "
-                            "shapes");
     auto unscale = [](float c) { return c == 0.f ? 1.f : 1.f / c; };
     // 16-bit weights take the products over pre-split inputs: each product's
-    // input is stored once as exact 16-bit parts (fc1 writes fc2's itself).
+    // input is stored once as its 16-bit parts (fc1 writes fc2's itself):
+    // three exact bf16 parts, or fp16 hi + lo for fp16 and scaled weights.
     const size_t part_stride = (size_t) positions * d, ff_part_stride = (size_t) positions * f;
     const bool split = (positions > 16 || scaled) && part_stride % 8 == 0 && pre_split_shape(wt, d, f);
     auto split_product = [&](const void* parts, size_t stride, int inner, const void* w, const float* bias, float* y,
